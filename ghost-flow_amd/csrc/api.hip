@@ -1,0 +1,365 @@
+// api.hip -- the extern "C" boundary (include/ghostflow_hip.h).
+//
+// Every entry point validates its arguments on the host before touching the
+// device: sizes and leading dimensions first, then pointers (NULL, and -- with
+// pointer checks on -- that each buffer is device memory large enough for
+// the access), then lazy device init, then the launch on the caller's
+// stream.  No C++ exception crosses the boundary.  Status codes follow
+// GhostFlowError (ghostflow-ffi/src/lib.rs:27-35).
+#include <climits>
+#include <new>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+using namespace gfh;
+
+namespace {
+
+constexpr int64_t kMaxDim = INT32_MAX;
+
+bool mul_ok(int64_t a, int64_t b, int64_t *out) {
+    __int128 r = (__int128)a * (__int128)b;
+    if (r > (__int128)INT64_MAX / 8) return false;
+    *out = (int64_t)r;
+    return true;
+}
+
+// Elements spanned by a rows x cols matrix with leading dimension ld.
+bool extent2d(int64_t rows, int64_t cols, int64_t ld, int64_t *out) {
+    if (rows == 0 || cols == 0) {
+        *out = 0;
+        return true;
+    }
+    int64_t t;
+    if (!mul_ok(rows - 1, ld, &t)) return false;
+    *out = t + cols;
+    return true;
+}
+
+// Extent of `batch` slices `stride` apart, each `one` elements.
+bool extent_batched(int64_t one, int64_t batch, int64_t stride, int64_t *out) {
+    if (one == 0 || batch == 0) {
+        *out = 0;
+        return true;
+    }
+    int64_t t;
+    if (!mul_ok(batch - 1, stride, &t)) return false;
+    *out = t + one;
+    return true;
+}
+
+template <typename F>
+int guarded(F &&f) {
+    try {
+        return f();
+    } catch (const std::bad_alloc &) {
+        return set_error(GFH_ALLOCATION_FAILED, "host allocation failed");
+    } catch (...) {
+        return set_error(GFH_UNKNOWN, "unexpected C++ exception");
+    }
+}
+
+int sgemm_common(int trans_a, int trans_b, int64_t m, int64_t n, int64_t k, float alpha, const float *a,
+                 int64_t lda, int64_t stride_a, int64_t batch_a, const float *b, int64_t ldb, int64_t stride_b,
+                 int64_t batch_b, float beta, float *c, int64_t ldc, int64_t stride_c, int64_t batch,
+                 const float *bias, gfh_stream_t stream) {
+    if (m < 0 || n < 0 || k < 0 || m > kMaxDim || n > kMaxDim || k > kMaxDim)
+        return set_error(GFH_INVALID_SHAPE, "sgemm: dims must be in [0, 2^31): m=%lld n=%lld k=%lld", (long long)m,
+                         (long long)n, (long long)k);
+    if (batch < 0 || batch_a < 1 || batch_b < 1 || batch > 65535)
+        return set_error(GFH_INVALID_SHAPE, "sgemm: batch=%lld batch_a=%lld batch_b=%lld out of range",
+                         (long long)batch, (long long)batch_a, (long long)batch_b);
+    if (stride_a < 0 || stride_b < 0 || stride_c < 0)
+        return set_error(GFH_INVALID_SHAPE, "sgemm: negative stride");
+    const int64_t a_rows = trans_a ? k : m, a_cols = trans_a ? m : k;
+    const int64_t b_rows = trans_b ? n : k, b_cols = trans_b ? k : n;
+    if (lda < (a_cols > 0 ? a_cols : 1) || ldb < (b_cols > 0 ? b_cols : 1) || ldc < (n > 0 ? n : 1))
+        return set_error(GFH_INVALID_SHAPE, "sgemm: leading dimension too small (lda=%lld ldb=%lld ldc=%lld)",
+                         (long long)lda, (long long)ldb, (long long)ldc);
+    if (m == 0 || n == 0 || batch == 0) return GFH_SUCCESS;
+    int64_t ea, eb, ec, t;
+    if (!extent2d(a_rows, a_cols, lda, &t) || !extent_batched(t, batch < batch_a ? batch : batch_a, stride_a, &ea) ||
+        !extent2d(b_rows, b_cols, ldb, &t) || !extent_batched(t, batch < batch_b ? batch : batch_b, stride_b, &eb) ||
+        !extent2d(m, n, ldc, &t) || !extent_batched(t, batch, stride_c, &ec))
+        return set_error(GFH_INVALID_SHAPE, "sgemm: operand extent overflows");
+    if (k > 0) {
+        GFH_TRY(require_range(a, (size_t)ea * 4, "A"));
+        GFH_TRY(require_range(b, (size_t)eb * 4, "B"));
+    }
+    GFH_TRY(require_range(c, (size_t)ec * 4, "C"));
+    GFH_TRY(optional_range(bias, (size_t)n * 4, "bias"));
+    GFH_TRY(ensure_init());
+    SgemmDesc d;
+    d.trans_a = trans_a != 0;
+    d.trans_b = trans_b != 0;
+    d.m = m;
+    d.n = n;
+    d.k = k;
+    d.alpha = alpha;
+    d.beta = beta;
+    d.a = a;
+    d.lda = lda;
+    d.stride_a = stride_a;
+    d.batch_a = batch_a;
+    d.b = b;
+    d.ldb = ldb;
+    d.stride_b = stride_b;
+    d.batch_b = batch_b;
+    d.c = c;
+    d.ldc = ldc;
+    d.stride_c = stride_c;
+    d.batch = batch;
+    d.bias = bias;
+    return launch_sgemm(d, as_stream(stream));
+}
+
+}  // namespace
+
+extern "C" {
+
+GFH_API int gfh_init(void) {
+    return guarded([]() -> int { return ensure_init(); });
+}
+
+GFH_API int gfh_shutdown(void) { return GFH_SUCCESS; }
+
+GFH_API const char *gfh_last_error(void) { return last_error(); }
+
+GFH_API const char *gfh_version(void) { return "ghostflow-hip 0.1.0 (gfx950)"; }
+
+GFH_API int gfh_set_pointer_checks(int enabled) { return set_pointer_checks(enabled); }
+
+GFH_API int gfh_sgemm(int trans_a, int trans_b, int64_t m, int64_t n, int64_t k, float alpha, const float *a,
+                      int64_t lda, const float *b, int64_t ldb, float beta, float *c, int64_t ldc,
+                      const float *bias, gfh_stream_t stream) {
+    return guarded([&]() -> int {
+        return sgemm_common(trans_a, trans_b, m, n, k, alpha, a, lda, 0, 1, b, ldb, 0, 1, beta, c, ldc, 0, 1, bias,
+                            stream);
+    });
+}
+
+GFH_API int gfh_sgemm_strided_batched(int trans_a, int trans_b, int64_t m, int64_t n, int64_t k, float alpha,
+                                      const float *a, int64_t lda, int64_t stride_a, int64_t batch_a,
+                                      const float *b, int64_t ldb, int64_t stride_b, int64_t batch_b, float beta,
+                                      float *c, int64_t ldc, int64_t stride_c, int64_t batch, const float *bias,
+                                      gfh_stream_t stream) {
+    return guarded([&]() -> int {
+        return sgemm_common(trans_a, trans_b, m, n, k, alpha, a, lda, stride_a, batch_a, b, ldb, stride_b, batch_b,
+                            beta, c, ldc, stride_c, batch, bias, stream);
+    });
+}
+
+GFH_API int gfh_quantize_i8_per_channel(const float *x, int64_t rows, int64_t cols, int symmetric, int8_t *q,
+                                        float *scales, int8_t *zero_points, gfh_stream_t stream) {
+    return guarded([&]() -> int {
+        if (rows < 0 || cols < 0 || rows > kMaxDim || cols > kMaxDim)
+            return set_error(GFH_INVALID_SHAPE, "quantize_per_channel: rows=%lld cols=%lld out of range",
+                             (long long)rows, (long long)cols);
+        if (rows == 0) return GFH_SUCCESS;
+        int64_t numel;
+        if (!mul_ok(rows, cols, &numel)) return set_error(GFH_INVALID_SHAPE, "quantize_per_channel: overflow");
+        GFH_TRY(require_range(x, (size_t)numel * 4, "x"));
+        GFH_TRY(require_range(q, (size_t)numel, "q"));
+        GFH_TRY(require_range(scales, (size_t)rows * 4, "scales"));
+        GFH_TRY(require_range(zero_points, (size_t)rows, "zero_points"));
+        GFH_TRY(ensure_init());
+        return launch_quantize_per_channel(x, rows, cols, symmetric != 0, q, scales, zero_points,
+                                           as_stream(stream));
+    });
+}
+
+GFH_API size_t gfh_quantize_i8_per_tensor_workspace_size(int64_t n) {
+    return quantize_per_tensor_workspace(n < 0 ? 0 : n);
+}
+
+GFH_API int gfh_quantize_i8_per_tensor(const float *x, int64_t n, int symmetric, int8_t *q, float *scale,
+                                       int8_t *zero_point, void *workspace, size_t workspace_bytes,
+                                       gfh_stream_t stream) {
+    return guarded([&]() -> int {
+        if (n < 0 || n > ((int64_t)1 << 40))
+            return set_error(GFH_INVALID_SHAPE, "quantize_per_tensor: n=%lld out of range", (long long)n);
+        GFH_TRY(require_range(x, (size_t)n * 4, "x"));
+        GFH_TRY(require_range(q, (size_t)n, "q"));
+        GFH_TRY(require_range(scale, 4, "scale"));
+        GFH_TRY(require_range(zero_point, 1, "zero_point"));
+        GFH_TRY(ensure_init());
+        hipStream_t s = as_stream(stream);
+        Scratch ws;
+        GFH_TRY(ws.acquire(workspace, workspace_bytes, quantize_per_tensor_workspace(n), s));
+        return launch_quantize_per_tensor(x, n, symmetric != 0, q, scale, zero_point, ws.ptr(), s);
+    });
+}
+
+GFH_API int gfh_dequantize_i8(const int8_t *q, int64_t rows, int64_t cols, const float *scales,
+                              const int8_t *zero_points, int64_t nscales, float *out, gfh_stream_t stream) {
+    return guarded([&]() -> int {
+        if (rows < 0 || cols < 0 || rows > kMaxDim || cols > kMaxDim)
+            return set_error(GFH_INVALID_SHAPE, "dequantize: rows=%lld cols=%lld out of range", (long long)rows,
+                             (long long)cols);
+        if (nscales != 1 && nscales != rows)
+            return set_error(GFH_INVALID_SHAPE, "dequantize: nscales=%lld must be 1 or rows=%lld",
+                             (long long)nscales, (long long)rows);
+        if (rows == 0 || cols == 0) return GFH_SUCCESS;
+        int64_t numel;
+        if (!mul_ok(rows, cols, &numel)) return set_error(GFH_INVALID_SHAPE, "dequantize: overflow");
+        GFH_TRY(require_range(q, (size_t)numel, "q"));
+        GFH_TRY(require_range(scales, (size_t)nscales * 4, "scales"));
+        GFH_TRY(require_range(zero_points, (size_t)nscales, "zero_points"));
+        GFH_TRY(require_range(out, (size_t)numel * 4, "out"));
+        GFH_TRY(ensure_init());
+        return launch_dequantize(q, rows, cols, scales, zero_points, nscales, out, as_stream(stream));
+    });
+}
+
+GFH_API int gfh_qweight_rowsum(const int8_t *qw, int64_t n, int64_t k, int32_t *rowsum, gfh_stream_t stream) {
+    return guarded([&]() -> int {
+        if (n < 0 || k < 0 || n > kMaxDim || k > (1 << 24))
+            return set_error(GFH_INVALID_SHAPE, "qweight_rowsum: n=%lld k=%lld out of range", (long long)n,
+                             (long long)k);
+        if (n == 0) return GFH_SUCCESS;
+        GFH_TRY(require_range(qw, (size_t)n * (size_t)k, "qw"));
+        GFH_TRY(require_range(rowsum, (size_t)n * 4, "rowsum"));
+        GFH_TRY(ensure_init());
+        return launch_rowsum_i8(qw, n, k, rowsum, as_stream(stream));
+    });
+}
+
+GFH_API int gfh_qlinear_i8(const int8_t *qx, const float *sx, const int8_t *zx, int x_per_row, const int8_t *qw,
+                           const float *sw, const int32_t *w_rowsum, const float *bias, float *y, int32_t *acc_out,
+                           int64_t m, int64_t n, int64_t k, gfh_stream_t stream) {
+    return guarded([&]() -> int {
+        if (m < 0 || n < 0 || k < 0 || m > kMaxDim || n > kMaxDim || k > kMaxDim)
+            return set_error(GFH_INVALID_SHAPE, "qlinear: m=%lld n=%lld k=%lld out of range", (long long)m,
+                             (long long)n, (long long)k);
+        // |acc| <= 255 * 128 * k must stay below 2^31 for the exact int32 accumulator.
+        if (k > 65793)
+            return set_error(GFH_INVALID_SHAPE, "qlinear: k=%lld exceeds the exact-int32 bound (65793)",
+                             (long long)k);
+        if (!y && !acc_out) return set_error(GFH_NULL_POINTER, "qlinear: y and acc_out are both NULL");
+        if (zx && !w_rowsum)
+            return set_error(GFH_NULL_POINTER, "qlinear: w_rowsum is required when zero points are given");
+        if (m == 0 || n == 0) return GFH_SUCCESS;
+        const int64_t nx = x_per_row ? m : 1;
+        GFH_TRY(require_range(qx, (size_t)m * (size_t)k, "qx"));
+        GFH_TRY(require_range(qw, (size_t)n * (size_t)k, "qw"));
+        if (y) {
+            GFH_TRY(require_range(sx, (size_t)nx * 4, "sx"));
+            GFH_TRY(require_range(sw, (size_t)n * 4, "sw"));
+        }
+        GFH_TRY(optional_range(zx, (size_t)nx, "zx"));
+        GFH_TRY(optional_range(w_rowsum, (size_t)n * 4, "w_rowsum"));
+        GFH_TRY(optional_range(bias, (size_t)n * 4, "bias"));
+        GFH_TRY(optional_range(y, (size_t)m * (size_t)n * 4, "y"));
+        GFH_TRY(optional_range(acc_out, (size_t)m * (size_t)n * 4, "acc_out"));
+        GFH_TRY(ensure_init());
+        QLinearDesc d;
+        d.qx = qx;
+        d.sx = sx;
+        d.zx = zx;
+        d.x_per_row = x_per_row != 0;
+        d.qw = qw;
+        d.sw = sw;
+        d.w_rowsum = w_rowsum;
+        d.bias = bias;
+        d.y = y;
+        d.acc = acc_out;
+        d.m = m;
+        d.n = n;
+        d.k = k;
+        return launch_qlinear_i8(d, as_stream(stream));
+    });
+}
+
+GFH_API int gfh_gemv_f32(const float *x, const float *w, float *y, int64_t b, int64_t k, int64_t n,
+                         gfh_stream_t stream) {
+    return guarded([&]() -> int {
+        if (b < 0 || k < 0 || n < 0 || b > 64 || k > kMaxDim || n > kMaxDim)
+            return set_error(GFH_INVALID_SHAPE, "gemv_f32: b=%lld (<= 64) k=%lld n=%lld out of range",
+                             (long long)b, (long long)k, (long long)n);
+        if (b == 0 || n == 0) return GFH_SUCCESS;
+        GFH_TRY(require_range(x, (size_t)b * (size_t)k * 4, "x"));
+        GFH_TRY(require_range(w, (size_t)k * (size_t)n * 4, "w"));
+        GFH_TRY(require_range(y, (size_t)b * (size_t)n * 4, "y"));
+        GFH_TRY(ensure_init());
+        return launch_gemv_f32(x, w, y, b, k, n, as_stream(stream));
+    });
+}
+
+GFH_API int gfh_gemv_w8(const float *x, const int8_t *qw, const float *scales, const int8_t *zero_points, float *y,
+                        int64_t b, int64_t k, int64_t n, gfh_stream_t stream) {
+    return guarded([&]() -> int {
+        if (b < 0 || k < 0 || n < 0 || b > 64 || k > kMaxDim || n > kMaxDim)
+            return set_error(GFH_INVALID_SHAPE, "gemv_w8: b=%lld (<= 64) k=%lld n=%lld out of range",
+                             (long long)b, (long long)k, (long long)n);
+        if (b == 0 || n == 0) return GFH_SUCCESS;
+        GFH_TRY(require_range(x, (size_t)b * (size_t)k * 4, "x"));
+        GFH_TRY(require_range(qw, (size_t)k * (size_t)n, "qw"));
+        GFH_TRY(require_range(scales, (size_t)k * 4, "scales"));
+        GFH_TRY(optional_range(zero_points, (size_t)k, "zero_points"));
+        GFH_TRY(require_range(y, (size_t)b * (size_t)n * 4, "y"));
+        GFH_TRY(ensure_init());
+        return launch_gemv_w8(x, qw, scales, zero_points, y, b, k, n, as_stream(stream));
+    });
+}
+
+GFH_API int gfh_softmax_lastdim_f32(const float *x, float *y, int64_t rows, int64_t cols, gfh_stream_t stream) {
+    return guarded([&]() -> int {
+        if (rows < 0 || cols < 0 || rows > kMaxDim || cols > kMaxDim)
+            return set_error(GFH_INVALID_SHAPE, "softmax: rows=%lld cols=%lld out of range", (long long)rows,
+                             (long long)cols);
+        if (rows == 0 || cols == 0) return GFH_SUCCESS;
+        int64_t numel;
+        if (!mul_ok(rows, cols, &numel)) return set_error(GFH_INVALID_SHAPE, "softmax: overflow");
+        GFH_TRY(require_range(x, (size_t)numel * 4, "x"));
+        GFH_TRY(require_range(y, (size_t)numel * 4, "y"));
+        GFH_TRY(ensure_init());
+        return launch_softmax_lastdim(x, y, rows, cols, as_stream(stream));
+    });
+}
+
+GFH_API int gfh_sdpa_f32(const float *q, const float *k, const float *v, float *out, float *weights, int64_t b,
+                         int64_t h, int64_t sq, int64_t skv, int64_t d, float scale, int causal, const float *mask,
+                         int64_t mask_numel, gfh_stream_t stream) {
+    return guarded([&]() -> int {
+        if (b < 0 || h < 0 || sq < 0 || skv < 0 || d < 0 || b > 65535 || h > 65535 || sq > kMaxDim ||
+            skv > kMaxDim)
+            return set_error(GFH_INVALID_SHAPE, "sdpa: b=%lld h=%lld sq=%lld skv=%lld out of range", (long long)b,
+                             (long long)h, (long long)sq, (long long)skv);
+        if (d == 0 || d > 128 || d % 4 != 0)
+            return set_error(GFH_INVALID_SHAPE, "sdpa: head_dim %lld must be a multiple of 4 in [4, 128]",
+                             (long long)d);
+        if (causal && sq != skv)
+            return set_error(GFH_INVALID_SHAPE, "sdpa: causal attention needs sq == skv (got %lld, %lld)",
+                             (long long)sq, (long long)skv);
+        if (mask && mask_numel <= 0) return set_error(GFH_INVALID_SHAPE, "sdpa: mask_numel must be > 0");
+        if (b == 0 || h == 0 || sq == 0) return GFH_SUCCESS;
+        if (skv == 0) return set_error(GFH_INVALID_SHAPE, "sdpa: empty key sequence");
+        const size_t bh = (size_t)b * (size_t)h;
+        GFH_TRY(require_range(q, bh * (size_t)sq * (size_t)d * 4, "q"));
+        GFH_TRY(require_range(k, bh * (size_t)skv * (size_t)d * 4, "k"));
+        GFH_TRY(require_range(v, bh * (size_t)skv * (size_t)d * 4, "v"));
+        GFH_TRY(require_range(out, bh * (size_t)sq * (size_t)d * 4, "out"));
+        GFH_TRY(optional_range(weights, bh * (size_t)sq * (size_t)skv * 4, "weights"));
+        GFH_TRY(optional_range(mask, (size_t)mask_numel * 4, "mask"));
+        GFH_TRY(ensure_init());
+        SdpaDesc sd;
+        sd.q = q;
+        sd.k = k;
+        sd.v = v;
+        sd.out = out;
+        sd.weights = weights;
+        sd.b = b;
+        sd.h = h;
+        sd.sq = sq;
+        sd.skv = skv;
+        sd.d = d;
+        sd.scale = scale;
+        sd.causal = causal != 0;
+        sd.mask = mask;
+        sd.mask_numel = mask ? mask_numel : 0;
+        return launch_sdpa(sd, as_stream(stream));
+    });
+}
+
+}  // extern "C"

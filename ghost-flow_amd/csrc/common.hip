@@ -1,0 +1,149 @@
+// common.hip -- error state, lazy device init, pointer checks, scratch.
+#include "common.hpp"
+
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+namespace gfh {
+
+namespace {
+thread_local std::string g_last_error = "No error";
+std::atomic<int> g_pointer_checks{1};
+std::once_flag g_init_once;
+int g_init_status = GFH_UNKNOWN;
+std::string g_init_message;
+}  // namespace
+
+int set_error(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+void clear_error() { g_last_error = "No error"; }
+
+const char *last_error() { return g_last_error.c_str(); }
+
+int check_launch(const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return set_error(GFH_COMPUTATION_FAILED, "%s: launch failed: %s", what, hipGetErrorString(e));
+    return GFH_SUCCESS;
+}
+
+int ensure_init() {
+    std::call_once(g_init_once, [] {
+        int n = 0;
+        hipError_t e = hipGetDeviceCount(&n);
+        if (e != hipSuccess || n == 0) {
+            g_init_status = GFH_COMPUTATION_FAILED;
+            g_init_message = std::string("no HIP device available: ") +
+                             (e != hipSuccess ? hipGetErrorString(e) : "device count is 0");
+            return;
+        }
+        int dev = 0;
+        hipGetDevice(&dev);
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+            g_init_status = GFH_COMPUTATION_FAILED;
+            g_init_message = "hipGetDeviceProperties failed";
+            return;
+        }
+        if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+            g_init_status = GFH_COMPUTATION_FAILED;
+            g_init_message = std::string("kernels are built for gfx950, device is ") + prop.gcnArchName;
+            return;
+        }
+        g_init_status = GFH_SUCCESS;
+    });
+    if (g_init_status != GFH_SUCCESS) return set_error(g_init_status, "%s", g_init_message.c_str());
+    return GFH_SUCCESS;
+}
+
+int check_device_ptr(const void *p, const char *name) {
+    if (!g_pointer_checks.load(std::memory_order_relaxed)) return GFH_SUCCESS;
+    hipPointerAttribute_t attr;
+    hipError_t e = hipPointerGetAttributes(&attr, p);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();  // do not leave the lookup failure for the next launch check
+        return set_error(GFH_INVALID_DATA, "%s is not a device pointer (%s)", name, hipGetErrorString(e));
+    }
+    if (attr.type != hipMemoryTypeDevice && attr.type != hipMemoryTypeManaged)
+        return set_error(GFH_INVALID_DATA, "%s is not device memory (memory type %d)", name, (int)attr.type);
+    return GFH_SUCCESS;
+}
+
+int require_ptr(const void *p, const char *name) {
+    if (!p) return set_error(GFH_NULL_POINTER, "%s is NULL", name);
+    return check_device_ptr(p, name);
+}
+
+int require_range(const void *p, size_t bytes, const char *name) {
+    if (!p) {
+        if (bytes == 0) return GFH_SUCCESS;
+        return set_error(GFH_NULL_POINTER, "%s is NULL", name);
+    }
+    if (!g_pointer_checks.load(std::memory_order_relaxed)) return GFH_SUCCESS;
+    GFH_TRY(check_device_ptr(p, name));
+    hipDeviceptr_t base = nullptr;
+    size_t size = 0;
+    hipError_t e = hipMemGetAddressRange(&base, &size, const_cast<void *>(p));
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return set_error(GFH_INVALID_DATA, "%s: no device allocation contains this address (%s)", name,
+                         hipGetErrorString(e));
+    }
+    const uintptr_t lo = reinterpret_cast<uintptr_t>(base);
+    const uintptr_t hi = lo + size;
+    const uintptr_t at = reinterpret_cast<uintptr_t>(p);
+    if (at < lo || bytes > hi - at)
+        return set_error(GFH_INVALID_SHAPE, "%s: %zu bytes needed but only %zu remain in its allocation", name,
+                         bytes, (size_t)(hi - at));
+    return GFH_SUCCESS;
+}
+
+int optional_range(const void *p, size_t bytes, const char *name) {
+    if (!p) return GFH_SUCCESS;
+    return require_range(p, bytes, name);
+}
+
+Scratch::~Scratch() {
+    if (owned_ && p_) (void)hipFreeAsync(p_, s_);
+}
+
+int Scratch::acquire(void *user, size_t user_bytes, size_t need, hipStream_t s) {
+    if (need == 0) need = 16;
+    if (user) {
+        if (user_bytes < need)
+            return set_error(GFH_INVALID_SHAPE, "workspace of %zu bytes is smaller than the %zu required",
+                             user_bytes, need);
+        GFH_TRY(check_device_ptr(user, "workspace"));
+        p_ = user;
+        owned_ = false;
+        return GFH_SUCCESS;
+    }
+    hipError_t e = hipMallocAsync(&p_, need, s);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        p_ = nullptr;
+        return set_error(GFH_ALLOCATION_FAILED, "hipMallocAsync(%zu) failed: %s", need, hipGetErrorString(e));
+    }
+    owned_ = true;
+    s_ = s;
+    return GFH_SUCCESS;
+}
+
+int set_pointer_checks(int enabled) {
+    g_pointer_checks.store(enabled ? 1 : 0);
+    return GFH_SUCCESS;
+}
+
+}  // namespace gfh

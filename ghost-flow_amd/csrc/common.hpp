@@ -1,0 +1,72 @@
+// common.hpp -- shared host/device helpers of the gfx950 backend.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "ghostflow_hip.h"
+
+namespace gfh {
+
+// ---- error reporting (thread-local last error) ---------------------------
+int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+// hipGetLastError after a launch -> GFH_COMPUTATION_FAILED with its text.
+int check_launch(const char *what);
+// Lazily initializes the device table; returns GFH_SUCCESS or an error code.
+int ensure_init();
+
+// ---- argument validation --------------------------------------------------
+// Device-pointer check (hipPointerGetAttributes) when pointer checks are on;
+// `p` must be non-null.
+int check_device_ptr(const void *p, const char *name);
+// Null check + device check for a required pointer.
+int require_ptr(const void *p, const char *name);
+// Required pointer to `bytes` bytes of device memory: non-null (unless
+// bytes == 0), and, with pointer checks on, [p, p + bytes) inside one device
+// allocation (hipMemGetAddressRange), so an undersized or host buffer is an
+// error instead of a GPU memory fault.
+int require_range(const void *p, size_t bytes, const char *name);
+// Same for a nullable pointer: NULL is accepted.
+int optional_range(const void *p, size_t bytes, const char *name);
+int set_pointer_checks(int enabled);
+const char *last_error();
+// 16-byte alignment helper.
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ---- stream-ordered scratch ----------------------------------------------
+// Uses the caller's workspace when given (and large enough), otherwise
+// hipMallocAsync on the stream; releases with hipFreeAsync on destruction.
+class Scratch {
+  public:
+    Scratch() = default;
+    ~Scratch();
+    int acquire(void *user, size_t user_bytes, size_t need, hipStream_t s);
+    void *ptr() const { return p_; }
+
+  private:
+    void *p_ = nullptr;
+    bool owned_ = false;
+    hipStream_t s_ = nullptr;
+};
+
+inline hipStream_t as_stream(gfh_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+}  // namespace gfh
+
+// Propagate a non-zero status.
+#define GFH_TRY(expr)                  \
+    do {                               \
+        int gfh_rc__ = (expr);         \
+        if (gfh_rc__ != GFH_SUCCESS) { \
+            return gfh_rc__;           \
+        }                              \
+    } while (0)
+
+// ---- device-side vector types and MFMA wrappers --------------------------
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));

@@ -1,0 +1,71 @@
+// kernels.hpp -- host-side launchers of the gfx950 kernels.  Arguments are
+// validated by the C ABI layer (api.hip) before any of these is called.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace gfh {
+
+struct SgemmDesc {
+    bool trans_a = false, trans_b = false;
+    int64_t m = 0, n = 0, k = 0;
+    float alpha = 1.f, beta = 0.f;
+    const float *a = nullptr;
+    int64_t lda = 0, stride_a = 0, batch_a = 1;
+    const float *b = nullptr;
+    int64_t ldb = 0, stride_b = 0, batch_b = 1;
+    float *c = nullptr;
+    int64_t ldc = 0, stride_c = 0;
+    int64_t batch = 1;
+    const float *bias = nullptr;
+};
+int launch_sgemm(const SgemmDesc &d, hipStream_t s);
+
+// quant.hip
+int launch_quantize_per_channel(const float *x, int64_t rows, int64_t cols, bool symmetric, int8_t *q,
+                                float *scales, int8_t *zps, hipStream_t s);
+size_t quantize_per_tensor_workspace(int64_t n);
+int launch_quantize_per_tensor(const float *x, int64_t n, bool symmetric, int8_t *q, float *scale, int8_t *zp,
+                               void *ws, hipStream_t s);
+int launch_dequantize(const int8_t *q, int64_t rows, int64_t cols, const float *scales, const int8_t *zps,
+                      int64_t nscales, float *out, hipStream_t s);
+int launch_rowsum_i8(const int8_t *q, int64_t n, int64_t k, int32_t *rowsum, hipStream_t s);
+
+// qgemm.hip
+struct QLinearDesc {
+    const int8_t *qx = nullptr;
+    const float *sx = nullptr;
+    const int8_t *zx = nullptr;
+    bool x_per_row = false;
+    const int8_t *qw = nullptr;
+    const float *sw = nullptr;
+    const int32_t *w_rowsum = nullptr;
+    const float *bias = nullptr;
+    float *y = nullptr;
+    int32_t *acc = nullptr;
+    int64_t m = 0, n = 0, k = 0;
+};
+int launch_qlinear_i8(const QLinearDesc &d, hipStream_t s);
+
+// gemv.hip
+int launch_gemv_f32(const float *x, const float *w, float *y, int64_t b, int64_t k, int64_t n, hipStream_t s);
+int launch_gemv_w8(const float *x, const int8_t *qw, const float *scales, const int8_t *zps, float *y, int64_t b,
+                   int64_t k, int64_t n, hipStream_t s);
+
+// attention.hip
+int launch_softmax_lastdim(const float *x, float *y, int64_t rows, int64_t cols, hipStream_t s);
+struct SdpaDesc {
+    const float *q = nullptr, *k = nullptr, *v = nullptr;
+    float *out = nullptr;
+    float *weights = nullptr;
+    int64_t b = 0, h = 0, sq = 0, skv = 0, d = 0;
+    float scale = 1.f;
+    bool causal = false;
+    const float *mask = nullptr;
+    int64_t mask_numel = 0;
+};
+int launch_sdpa(const SdpaDesc &d, hipStream_t s);
+
+}  // namespace gfh

@@ -1,0 +1,303 @@
+// quant.hip -- int8 quantize / dequantize with the reference's scheme
+// (ghostflow-nn/src/quantization.rs:77-204), bit-exact:
+//   min/max folds ignore NaN (f32::min / f32::max  ->  fminf / fmaxf);
+//   symmetric : scale = max(|min|, |max|) / 127, zp = 0
+//   asymmetric: scale = (max - min) / 255, zp = ((-min / scale) - 128).round() as i8
+//   q = ((x / scale).round() as i32 + zp).clamp(-128, 127)
+// `/` is the correctly rounded IEEE f32 division (hipcc's default), `round`
+// is half away from zero, `as` casts saturate with NaN -> 0, and the i32 add
+// wraps as in a release build.  All kernels are HBM-bound elementwise or
+// reduction passes: 16-byte loads, grid sized to fill the 256 CUs.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace gfh {
+namespace {
+
+constexpr int kBlock = 256;
+
+__device__ __forceinline__ int32_t sat_f32_to_i32(float f) {
+    if (f != f) return 0;
+    if (f >= 2147483648.0f) return INT32_MAX;
+    if (f <= -2147483648.0f) return INT32_MIN;
+    return (int32_t)f;
+}
+
+__device__ __forceinline__ int8_t sat_f32_to_i8(float f) {
+    if (f != f) return 0;
+    if (f >= 127.0f) return 127;
+    if (f <= -128.0f) return -128;
+    return (int8_t)(int32_t)f;
+}
+
+__device__ __forceinline__ void quant_params(float mn, float mx, bool symmetric, float &scale, int8_t &zp) {
+    if (symmetric) {
+        const float absmax = fmaxf(fabsf(mn), fabsf(mx));
+        scale = absmax / 127.0f;
+        zp = 0;
+    } else {
+        scale = (mx - mn) / 255.0f;
+        const float t = (-mn) / scale - 128.0f;
+        zp = sat_f32_to_i8(roundf(t));
+    }
+}
+
+__device__ __forceinline__ int8_t quant_one(float x, float scale, int32_t zp) {
+    const uint32_t sum = (uint32_t)sat_f32_to_i32(roundf(x / scale)) + (uint32_t)zp;
+    int32_t q = (int32_t)sum;
+    q = q < -128 ? -128 : (q > 127 ? 127 : q);
+    return (int8_t)q;
+}
+
+__device__ __forceinline__ uint32_t quant4(f32x4 v, float scale, int32_t zp) {
+    const uint32_t b0 = (uint8_t)quant_one(v[0], scale, zp);
+    const uint32_t b1 = (uint8_t)quant_one(v[1], scale, zp);
+    const uint32_t b2 = (uint8_t)quant_one(v[2], scale, zp);
+    const uint32_t b3 = (uint8_t)quant_one(v[3], scale, zp);
+    return b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
+}
+
+// Block-wide (min, max) reduction: wave shuffles, then LDS across waves.
+__device__ __forceinline__ void block_minmax(float &mn, float &mx) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        mn = fminf(mn, __shfl_xor(mn, off));
+        mx = fmaxf(mx, __shfl_xor(mx, off));
+    }
+    __shared__ float smn[kBlock / 64], smx[kBlock / 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        smn[wave] = mn;
+        smx[wave] = mx;
+    }
+    __syncthreads();
+    mn = smn[0];
+    mx = smx[0];
+#pragma unroll
+    for (int w = 1; w < kBlock / 64; ++w) {
+        mn = fminf(mn, smn[w]);
+        mx = fmaxf(mx, smx[w]);
+    }
+    __syncthreads();
+}
+
+// ---- per channel: one workgroup per row --------------------------------------
+template <bool VEC>
+__global__ __launch_bounds__(kBlock) void quant_per_channel_kernel(const float *__restrict__ x, int64_t cols,
+                                                                  bool symmetric, int8_t *__restrict__ q,
+                                                                  float *__restrict__ scales,
+                                                                  int8_t *__restrict__ zps) {
+    const int64_t row = blockIdx.x;
+    const float *xr = x + row * cols;
+    int8_t *qr = q + row * cols;
+    float mn = INFINITY, mx = -INFINITY;
+    if (VEC) {
+        const int64_t nv = cols / 4;
+        for (int64_t i = threadIdx.x; i < nv; i += kBlock) {
+            const f32x4 v = reinterpret_cast<const f32x4 *>(xr)[i];
+            mn = fminf(fminf(mn, v[0]), fminf(fminf(v[1], v[2]), v[3]));
+            mx = fmaxf(fmaxf(mx, v[0]), fmaxf(fmaxf(v[1], v[2]), v[3]));
+        }
+    } else {
+        for (int64_t i = threadIdx.x; i < cols; i += kBlock) {
+            mn = fminf(mn, xr[i]);
+            mx = fmaxf(mx, xr[i]);
+        }
+    }
+    block_minmax(mn, mx);
+    float scale;
+    int8_t zp;
+    quant_params(mn, mx, symmetric, scale, zp);
+    if (threadIdx.x == 0) {
+        scales[row] = scale;
+        zps[row] = zp;
+    }
+    if (VEC) {
+        const int64_t nv = cols / 4;
+        for (int64_t i = threadIdx.x; i < nv; i += kBlock)
+            reinterpret_cast<uint32_t *>(qr)[i] = quant4(reinterpret_cast<const f32x4 *>(xr)[i], scale, zp);
+    } else {
+        for (int64_t i = threadIdx.x; i < cols; i += kBlock) qr[i] = quant_one(xr[i], scale, zp);
+    }
+}
+
+// ---- per tensor: partial min/max, then finalize + quantize ---------------------
+constexpr int kMaxPartials = 1024;
+constexpr int64_t kVecPerThread = 8;  // float4s per thread per partial block
+
+int per_tensor_blocks(int64_t n) {
+    const int64_t per_block = (int64_t)kBlock * 4 * kVecPerThread;
+    int64_t nb = (n + per_block - 1) / per_block;
+    if (nb < 1) nb = 1;
+    if (nb > kMaxPartials) nb = kMaxPartials;
+    return (int)nb;
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kBlock) void minmax_partial_kernel(const float *__restrict__ x, int64_t n,
+                                                               float2 *__restrict__ partials) {
+    float mn = INFINITY, mx = -INFINITY;
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    if (VEC) {
+        const int64_t nv = n / 4;
+        for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < nv; i += stride) {
+            const f32x4 v = reinterpret_cast<const f32x4 *>(x)[i];
+            mn = fminf(fminf(mn, v[0]), fminf(fminf(v[1], v[2]), v[3]));
+            mx = fmaxf(fmaxf(mx, v[0]), fmaxf(fmaxf(v[1], v[2]), v[3]));
+        }
+        for (int64_t i = nv * 4 + (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+            mn = fminf(mn, x[i]);
+            mx = fmaxf(mx, x[i]);
+        }
+    } else {
+        for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+            mn = fminf(mn, x[i]);
+            mx = fmaxf(mx, x[i]);
+        }
+    }
+    block_minmax(mn, mx);
+    if (threadIdx.x == 0) partials[blockIdx.x] = make_float2(mn, mx);
+}
+
+template <bool VEC>
+__global__ __launch_bounds__(kBlock) void quant_per_tensor_kernel(const float *__restrict__ x, int64_t n,
+                                                                 bool symmetric, const float2 *__restrict__ partials,
+                                                                 int npartials, int8_t *__restrict__ q,
+                                                                 float *__restrict__ scale_out,
+                                                                 int8_t *__restrict__ zp_out) {
+    // Every workgroup folds all partials (at most 1024 pairs) itself, so the
+    // parameters are identical everywhere without a grid-wide barrier.
+    float mn = INFINITY, mx = -INFINITY;
+    for (int i = threadIdx.x; i < npartials; i += kBlock) {
+        const float2 p = partials[i];
+        mn = fminf(mn, p.x);
+        mx = fmaxf(mx, p.y);
+    }
+    block_minmax(mn, mx);
+    float scale;
+    int8_t zp;
+    quant_params(mn, mx, symmetric, scale, zp);
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+        *scale_out = scale;
+        *zp_out = zp;
+    }
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    if (VEC) {
+        const int64_t nv = n / 4;
+        for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < nv; i += stride)
+            reinterpret_cast<uint32_t *>(q)[i] = quant4(reinterpret_cast<const f32x4 *>(x)[i], scale, zp);
+        for (int64_t i = nv * 4 + (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
+            q[i] = quant_one(x[i], scale, zp);
+    } else {
+        for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride)
+            q[i] = quant_one(x[i], scale, zp);
+    }
+}
+
+// ---- dequantize -------------------------------------------------------------------
+// out = ((float)q - (float)zp) * scale, per tensor (nscales == 1) or per row.
+template <bool VEC>
+__global__ __launch_bounds__(kBlock) void dequant_kernel(const int8_t *__restrict__ q, int64_t rows, int64_t cols,
+                                                        const float *__restrict__ scales,
+                                                        const int8_t *__restrict__ zps, bool per_row,
+                                                        float *__restrict__ out) {
+    const int64_t n = rows * cols;
+    const int64_t stride = (int64_t)gridDim.x * kBlock;
+    if (VEC) {  // cols % 4 == 0: a group of 4 never straddles two rows
+        const int64_t nv = n / 4;
+        for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < nv; i += stride) {
+            const int64_t g = per_row ? (i * 4) / cols : 0;
+            const float s = scales[g];
+            const float z = (float)zps[g];
+            const uint32_t packed = reinterpret_cast<const uint32_t *>(q)[i];
+            f32x4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = ((float)(int8_t)(packed >> (8 * e)) - z) * s;
+            reinterpret_cast<f32x4 *>(out)[i] = v;
+        }
+    } else {
+        for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+            const int64_t g = per_row ? i / cols : 0;
+            out[i] = ((float)q[i] - (float)zps[g]) * scales[g];
+        }
+    }
+}
+
+// ---- int8 row sums ------------------------------------------------------------------
+__global__ __launch_bounds__(kBlock) void rowsum_i8_kernel(const int8_t *__restrict__ q, int64_t n, int64_t k,
+                                                          int32_t *__restrict__ out) {
+    // one wave per row
+    const int64_t row = (int64_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= n) return;
+    const int8_t *r = q + row * k;
+    int32_t s = 0;
+    for (int64_t i = lane; i < k; i += 64) s += r[i];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+    if (lane == 0) out[row] = s;
+}
+
+int grid_for(int64_t work_items) {
+    int64_t g = (work_items + kBlock - 1) / kBlock;
+    if (g < 1) g = 1;
+    if (g > 8192) g = 8192;
+    return (int)g;
+}
+
+}  // namespace
+
+int launch_quantize_per_channel(const float *x, int64_t rows, int64_t cols, bool symmetric, int8_t *q,
+                                float *scales, int8_t *zps, hipStream_t s) {
+    const bool vec = (cols % 4 == 0) && aligned16(x) && ((reinterpret_cast<uintptr_t>(q) & 3u) == 0);
+    if (vec)
+        hipLaunchKernelGGL(quant_per_channel_kernel<true>, dim3((unsigned)rows), dim3(kBlock), 0, s, x, cols,
+                           symmetric, q, scales, zps);
+    else
+        hipLaunchKernelGGL(quant_per_channel_kernel<false>, dim3((unsigned)rows), dim3(kBlock), 0, s, x, cols,
+                           symmetric, q, scales, zps);
+    return check_launch("quantize_per_channel");
+}
+
+size_t quantize_per_tensor_workspace(int64_t n) { return sizeof(float2) * (size_t)per_tensor_blocks(n); }
+
+int launch_quantize_per_tensor(const float *x, int64_t n, bool symmetric, int8_t *q, float *scale, int8_t *zp,
+                               void *ws, hipStream_t s) {
+    const int nb = per_tensor_blocks(n);
+    float2 *partials = static_cast<float2 *>(ws);
+    const bool vec = aligned16(x) && ((reinterpret_cast<uintptr_t>(q) & 3u) == 0);
+    if (vec) {
+        hipLaunchKernelGGL(minmax_partial_kernel<true>, dim3(nb), dim3(kBlock), 0, s, x, n, partials);
+        GFH_TRY(check_launch("quantize_per_tensor/minmax"));
+        hipLaunchKernelGGL(quant_per_tensor_kernel<true>, dim3(nb), dim3(kBlock), 0, s, x, n, symmetric, partials,
+                           nb, q, scale, zp);
+    } else {
+        hipLaunchKernelGGL(minmax_partial_kernel<false>, dim3(nb), dim3(kBlock), 0, s, x, n, partials);
+        GFH_TRY(check_launch("quantize_per_tensor/minmax"));
+        hipLaunchKernelGGL(quant_per_tensor_kernel<false>, dim3(nb), dim3(kBlock), 0, s, x, n, symmetric,
+                           partials, nb, q, scale, zp);
+    }
+    return check_launch("quantize_per_tensor/quantize");
+}
+
+int launch_dequantize(const int8_t *q, int64_t rows, int64_t cols, const float *scales, const int8_t *zps,
+                      int64_t nscales, float *out, hipStream_t s) {
+    const bool per_row = nscales != 1;
+    const bool vec = (cols % 4 == 0) && aligned16(out) && ((reinterpret_cast<uintptr_t>(q) & 3u) == 0);
+    const int64_t n = rows * cols;
+    if (vec)
+        hipLaunchKernelGGL(dequant_kernel<true>, dim3(grid_for(n / 4)), dim3(kBlock), 0, s, q, rows, cols, scales,
+                           zps, per_row, out);
+    else
+        hipLaunchKernelGGL(dequant_kernel<false>, dim3(grid_for(n)), dim3(kBlock), 0, s, q, rows, cols, scales,
+                           zps, per_row, out);
+    return check_launch("dequantize");
+}
+
+int launch_rowsum_i8(const int8_t *q, int64_t n, int64_t k, int32_t *rowsum, hipStream_t s) {
+    const int64_t blocks = (n + (kBlock / 64) - 1) / (kBlock / 64);
+    hipLaunchKernelGGL(rowsum_i8_kernel, dim3((unsigned)blocks), dim3(kBlock), 0, s, q, n, k, rowsum);
+    return check_launch("qweight_rowsum");
+}
+
+}  // namespace gfh

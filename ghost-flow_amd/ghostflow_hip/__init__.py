@@ -1,0 +1,28 @@
+"""ghostflow_hip -- Python bindings of the gfx950 backend for GhostFlow's dense
+hot path (fp32 GEMM / Linear, int8 quantized linear, decode GEMV, SDPA).
+
+All compute goes through the C ABI of libghostflow_hip.so
+(include/ghostflow_hip.h); see ops.py.  The package lives in the
+`ghost-flow_amd/` directory; put that directory on sys.path to import it.
+"""
+from . import _lib  # noqa: F401
+from .ops import (  # noqa: F401
+    GhostFlowError,
+    dequantize,
+    gemv_f32,
+    gemv_w8,
+    init,
+    lib,
+    linear,
+    matmul,
+    qlinear,
+    quantize_per_channel,
+    quantize_per_tensor,
+    quantize_per_tensor_workspace_size,
+    qweight_rowsum,
+    sdpa,
+    set_pointer_checks,
+    sgemm,
+    softmax_lastdim,
+)
+from .synth import normal, uniform  # noqa: F401

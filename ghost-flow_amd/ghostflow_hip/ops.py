@@ -1,0 +1,244 @@
+"""Thin wrappers that call the C ABI on torch device tensors.
+
+torch only supplies device memory and the current HIP stream; every
+computation below is one call into libghostflow_hip.so.  Each wrapper checks
+dtype / contiguity / device on the host and raises GhostFlowError with the
+library's status code and thread-local message when a call fails.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+class GhostFlowError(RuntimeError):
+    """A non-zero status from the C ABI (GhostFlowError codes)."""
+
+    def __init__(self, status: int, message: str):
+        self.status = status
+        name = _lib.STATUS_NAMES.get(status, str(status))
+        super().__init__(f"{name}: {message}")
+
+
+def _check(rc: int) -> None:
+    if rc != _lib.SUCCESS:
+        msg = _lib.load().gfh_last_error()
+        raise GhostFlowError(rc, msg.decode() if msg else "")
+
+
+def _stream(dev=None) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _need(t, dtype, name):
+    if t is None:
+        return
+    if not t.is_cuda:
+        raise GhostFlowError(_lib.INVALID_DATA, f"{name} must be a device tensor")
+    if t.dtype != dtype:
+        raise GhostFlowError(_lib.INVALID_DATA, f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise GhostFlowError(_lib.INVALID_DATA, f"{name} must be contiguous")
+
+
+def lib():
+    return _lib.load()
+
+
+def init() -> None:
+    _check(lib().gfh_init())
+
+
+def set_pointer_checks(enabled: bool) -> None:
+    _check(lib().gfh_set_pointer_checks(1 if enabled else 0))
+
+
+# ---- fp32 GEMM --------------------------------------------------------------
+
+def sgemm(a, b, *, trans_a=False, trans_b=False, alpha=1.0, beta=0.0, bias=None, out=None):
+    """out = alpha * op(a) @ op(b) + beta * out (+ bias), 2-D row-major."""
+    _need(a, torch.float32, "a")
+    _need(b, torch.float32, "b")
+    _need(bias, torch.float32, "bias")
+    m, k = (a.shape[1], a.shape[0]) if trans_a else (a.shape[0], a.shape[1])
+    k2, n = (b.shape[1], b.shape[0]) if trans_b else (b.shape[0], b.shape[1])
+    if k != k2:
+        raise GhostFlowError(_lib.INVALID_SHAPE, f"ShapeMismatch expected [{m}, {k}] got [{k2}, {n}]")
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.float32, device=a.device)
+    _need(out, torch.float32, "out")
+    _check(lib().gfh_sgemm(int(trans_a), int(trans_b), m, n, k, float(alpha), a.data_ptr(),
+                           max(a.shape[1], 1), b.data_ptr(), max(b.shape[1], 1),
+                           float(beta), out.data_ptr(), max(n, 1), _ptr(bias), _stream(a.device)))
+    return out
+
+
+def matmul(a, b):
+    """Tensor::matmul (ghostflow-core/src/ops/matmul.rs:13-42): 2-D -> GEMM,
+    otherwise the batched form with modulo batch indexing (:122-170)."""
+    _need(a, torch.float32, "a")
+    _need(b, torch.float32, "b")
+    if a.dim() < 2 or b.dim() < 2:
+        raise GhostFlowError(_lib.INVALID_SHAPE, "matmul requires at least 2D tensors")
+    m, k = a.shape[-2:]
+    k2, n = b.shape[-2:]
+    if k != k2:
+        raise GhostFlowError(_lib.INVALID_SHAPE, f"ShapeMismatch expected [{m}, {k}] got [{k2}, {n}]")
+    if a.dim() == 2 and b.dim() == 2:
+        return sgemm(a, b)
+    batch_shape = torch.broadcast_shapes(a.shape[:-2], b.shape[:-2])
+    batch = 1
+    for s in batch_shape:
+        batch *= s
+    ba = 1
+    for s in a.shape[:-2]:
+        ba *= s
+    bb = 1
+    for s in b.shape[:-2]:
+        bb *= s
+    out = torch.empty(tuple(batch_shape) + (m, n), dtype=torch.float32, device=a.device)
+    _check(lib().gfh_sgemm_strided_batched(0, 0, m, n, k, 1.0, a.data_ptr(), k, m * k, max(ba, 1),
+                                           b.data_ptr(), n, k * n, max(bb, 1), 0.0, out.data_ptr(),
+                                           n, m * n, batch, None, _stream(a.device)))
+    return out
+
+
+def linear(x, weight, bias=None):
+    """Linear::forward (ghostflow-nn/src/linear.rs:56-69): x @ W^T + b."""
+    return sgemm(x, weight, trans_b=True, bias=bias)
+
+
+# ---- int8 quantization ---------------------------------------------------------
+
+def quantize_per_channel(x, symmetric=True):
+    _need(x, torch.float32, "x")
+    rows = x.shape[0]
+    cols = x.numel() // rows if rows else 0
+    q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    s = torch.empty(rows, dtype=torch.float32, device=x.device)
+    z = torch.empty(rows, dtype=torch.int8, device=x.device)
+    _check(lib().gfh_quantize_i8_per_channel(x.data_ptr(), rows, cols, int(bool(symmetric)),
+                                             q.data_ptr(), s.data_ptr(), z.data_ptr(),
+                                             _stream(x.device)))
+    return q, s, z
+
+
+def quantize_per_tensor(x, symmetric=False, workspace=None):
+    _need(x, torch.float32, "x")
+    q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    s = torch.empty(1, dtype=torch.float32, device=x.device)
+    z = torch.empty(1, dtype=torch.int8, device=x.device)
+    ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(), workspace.numel() * workspace.element_size())
+    _check(lib().gfh_quantize_i8_per_tensor(x.data_ptr(), x.numel(), int(bool(symmetric)),
+                                            q.data_ptr(), s.data_ptr(), z.data_ptr(),
+                                            ws_ptr, ws_bytes, _stream(x.device)))
+    return q, s, z
+
+
+def quantize_per_tensor_workspace_size(n: int) -> int:
+    return int(lib().gfh_quantize_i8_per_tensor_workspace_size(n))
+
+
+def dequantize(q, scales, zero_points):
+    _need(q, torch.int8, "q")
+    _need(scales, torch.float32, "scales")
+    _need(zero_points, torch.int8, "zero_points")
+    rows = q.shape[0] if q.dim() else 1
+    cols = q.numel() // rows if rows else 0
+    out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    _check(lib().gfh_dequantize_i8(q.data_ptr(), rows, cols, scales.data_ptr(), zero_points.data_ptr(),
+                                   scales.numel(), out.data_ptr(), _stream(q.device)))
+    return out
+
+
+def qweight_rowsum(qw):
+    _need(qw, torch.int8, "qw")
+    n, k = qw.shape
+    out = torch.empty(n, dtype=torch.int32, device=qw.device)
+    _check(lib().gfh_qweight_rowsum(qw.data_ptr(), n, k, out.data_ptr(), _stream(qw.device)))
+    return out
+
+
+def qlinear(qx, sx, zx, qw, sw, *, x_per_row=False, w_rowsum=None, bias=None, want_y=True,
+            want_acc=False):
+    _need(qx, torch.int8, "qx")
+    _need(qw, torch.int8, "qw")
+    _need(sx, torch.float32, "sx")
+    _need(sw, torch.float32, "sw")
+    _need(zx, torch.int8, "zx")
+    _need(w_rowsum, torch.int32, "w_rowsum")
+    _need(bias, torch.float32, "bias")
+    m, k = qx.shape
+    n = qw.shape[0]
+    if qw.shape[1] != k:
+        raise GhostFlowError(_lib.INVALID_SHAPE, f"ShapeMismatch expected [{m}, {k}] got [{qw.shape[1]}, {n}]")
+    if zx is not None and w_rowsum is None:
+        w_rowsum = qweight_rowsum(qw)
+    y = torch.empty((m, n), dtype=torch.float32, device=qx.device) if want_y else None
+    acc = torch.empty((m, n), dtype=torch.int32, device=qx.device) if want_acc else None
+    _check(lib().gfh_qlinear_i8(qx.data_ptr(), _ptr(sx), _ptr(zx), int(bool(x_per_row)), qw.data_ptr(),
+                                _ptr(sw), _ptr(w_rowsum), _ptr(bias), _ptr(y), _ptr(acc), m, n, k,
+                                _stream(qx.device)))
+    return y, acc
+
+
+# ---- GEMV ---------------------------------------------------------------------
+
+def gemv_f32(x, w, out=None):
+    _need(x, torch.float32, "x")
+    _need(w, torch.float32, "w")
+    b, k = x.shape
+    n = w.shape[1]
+    if w.shape[0] != k:
+        raise GhostFlowError(_lib.INVALID_SHAPE, f"ShapeMismatch expected [{b}, {k}] got [{w.shape[0]}, {n}]")
+    y = torch.empty((b, n), dtype=torch.float32, device=x.device) if out is None else out
+    _check(lib().gfh_gemv_f32(x.data_ptr(), w.data_ptr(), y.data_ptr(), b, k, n, _stream(x.device)))
+    return y
+
+
+def gemv_w8(x, qw, scales, zero_points=None, out=None):
+    _need(x, torch.float32, "x")
+    _need(qw, torch.int8, "qw")
+    _need(scales, torch.float32, "scales")
+    _need(zero_points, torch.int8, "zero_points")
+    b, k = x.shape
+    n = qw.shape[1]
+    if qw.shape[0] != k:
+        raise GhostFlowError(_lib.INVALID_SHAPE, f"ShapeMismatch expected [{b}, {k}] got [{qw.shape[0]}, {n}]")
+    y = torch.empty((b, n), dtype=torch.float32, device=x.device) if out is None else out
+    _check(lib().gfh_gemv_w8(x.data_ptr(), qw.data_ptr(), scales.data_ptr(), _ptr(zero_points),
+                             y.data_ptr(), b, k, n, _stream(x.device)))
+    return y
+
+
+# ---- attention ------------------------------------------------------------------
+
+def softmax_lastdim(x, out=None):
+    _need(x, torch.float32, "x")
+    cols = x.shape[-1]
+    rows = x.numel() // cols if cols else 0
+    y = torch.empty_like(x) if out is None else out
+    _check(lib().gfh_softmax_lastdim_f32(x.data_ptr(), y.data_ptr(), rows, cols, _stream(x.device)))
+    return y
+
+
+def sdpa(q, k, v, *, scale=None, causal=False, mask=None, want_weights=False, out=None):
+    """Fused scaled_dot_product_attention on [B, H, S, D] tensors."""
+    for t, nm in ((q, "q"), (k, "k"), (v, "v")):
+        _need(t, torch.float32, nm)
+    _need(mask, torch.float32, "mask")
+    b, h, sq, d = q.shape
+    skv = k.shape[2]
+    if scale is None:
+        scale = float(torch.tensor(1.0, dtype=torch.float32) / torch.sqrt(torch.tensor(float(d), dtype=torch.float32)))
+    o = torch.empty_like(q) if out is None else out
+    w = torch.empty((b, h, sq, skv), dtype=torch.float32, device=q.device) if want_weights else None
+    _check(lib().gfh_sdpa_f32(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), _ptr(w), b, h, sq,
+                              skv, d, float(scale), int(bool(causal)), _ptr(mask),
+                              0 if mask is None else mask.numel(), _stream(q.device)))
+    return (o, w) if want_weights else o

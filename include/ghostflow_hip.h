@@ -1,0 +1,205 @@
+/*
+ * ghostflow_hip.h -- C ABI of the MI355X (gfx950) backend for GhostFlow's
+ * dense hot path.
+ *
+ * This library takes the role of the reference's `ghostflow-cuda` crate
+ * (the L0 device backend): stream-ordered entry points over caller-owned
+ * device buffers, plain pointers and sizes, no C++ or HIP types in the
+ * signatures.  Citations are file:line in the reference checkout
+ * (choksi2212/ghost-flow).
+ *
+ * Conventions
+ *  - Status codes mirror `GhostFlowError` (ghostflow-ffi/src/lib.rs:27-35,
+ *    ghostflow-ffi/ghostflow.h:12-20).  On failure `gfh_last_error()` returns
+ *    a thread-local message (the reference's ghostflow_get_last_error always
+ *    returns "No error", ghostflow-ffi/src/lib.rs:334-337).
+ *  - All matrices are row-major and contiguous along their last dimension,
+ *    f32 / int8 / int32, as the reference's Tensor storage
+ *    (ghostflow-core/src/tensor.rs:19-32).
+ *  - Every pointer argument except `stream` and those marked nullable is a
+ *    device pointer (hipMalloc / pool memory).  The caller owns all buffers;
+ *    the library never frees caller memory (ghostflow-cuda/src/tensor.rs:27-45
+ *    holds raw device pointers the same way).
+ *  - `stream` is a hipStream_t passed as void* (NULL = the default stream).
+ *    Calls are asynchronous and ordered on that stream, like the reference's
+ *    launchers taking a cudaStream_t (ghostflow-cuda/src/ffi.rs:167-197);
+ *    the caller synchronizes.  Shapes, strides and pointers are validated on
+ *    the host before any launch; nothing is launched when a call fails.
+ *  - Entry points are re-entrant.  Calls that take `workspace` use only that
+ *    memory as scratch; when `workspace` is NULL they allocate stream-ordered
+ *    scratch (hipMallocAsync/hipFreeAsync) on `stream`.
+ */
+#ifndef GHOSTFLOW_HIP_H
+#define GHOSTFLOW_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GFH_API __attribute__((visibility("default")))
+
+typedef enum gfh_status {
+    GFH_SUCCESS = 0,
+    GFH_INVALID_SHAPE = 1,
+    GFH_INVALID_DATA = 2,
+    GFH_NULL_POINTER = 3,
+    GFH_ALLOCATION_FAILED = 4,
+    GFH_COMPUTATION_FAILED = 5,
+    GFH_UNKNOWN = 99
+} gfh_status;
+
+typedef void *gfh_stream_t;
+
+/* ---- library ----------------------------------------------------------- */
+
+/* Replaces ghostflow_init (ghostflow-ffi/src/lib.rs:60-64): checks that a
+ * gfx950 device is present and caches its properties.  Optional; every entry
+ * point initializes lazily. */
+GFH_API int gfh_init(void);
+/* Releases cached per-device state.  Caller buffers are untouched. */
+GFH_API int gfh_shutdown(void);
+/* Replaces ghostflow_get_last_error (ghostflow-ffi/src/lib.rs:332-337);
+ * thread-local, valid until the next failing call on this thread. */
+GFH_API const char *gfh_last_error(void);
+/* Replaces ghostflow_version (ghostflow-ffi/src/lib.rs:66-71); static. */
+GFH_API const char *gfh_version(void);
+/* 1: check that every data pointer is device memory before launching
+ * (hipPointerGetAttributes; default), 0: trust the caller. */
+GFH_API int gfh_set_pointer_checks(int enabled);
+
+/* ---- fp32 GEMM (Tensor::matmul, Linear) --------------------------------- */
+
+/* C[m,n] = alpha * op(A)[m,k] . op(B)[k,n] + beta * C[m,n] (+ bias[n])
+ *   op(A) = A            (trans_a = 0, A is [m, lda >= k])
+ *         = A^T          (trans_a = 1, A is [k, lda >= m])
+ *   op(B) = B            (trans_b = 0, B is [k, ldb >= n])
+ *         = B^T          (trans_b = 1, B is [n, ldb >= k])
+ * beta == 0 never reads C.  bias is nullable.  Row-major form of
+ * CuBlas::sgemm (ghostflow-cuda/src/blas.rs:70-133; CuBlas::matmul swaps
+ * operands to get row-major, :278-313) and of the reference's optional cblas
+ * branch (ghostflow-core/src/ops/matmul.rs:60-88).  Serves
+ *   Tensor::matmul 2-D   (matmul.rs:13-57, matmul_blocked :91-119): NN
+ *   Linear::forward      (ghostflow-nn/src/linear.rs:56-69): x . W^T + b, NT
+ *   launch_optimized_sgemm (ghostflow-cuda/src/ffi.rs:169-174). */
+GFH_API int gfh_sgemm(int trans_a, int trans_b, int64_t m, int64_t n, int64_t k,
+                      float alpha, const float *a, int64_t lda,
+                      const float *b, int64_t ldb, float beta, float *c,
+                      int64_t ldc, const float *bias, gfh_stream_t stream);
+
+/* Batched form with the reference's batch indexing: output batch i uses A
+ * slice (i % batch_a) and B slice (i % batch_b) (matmul.rs:122-170, :148-149),
+ * slices `stride_*` elements apart.  Replaces cublasSgemmBatched
+ * (ghostflow-cuda/src/ffi.rs:226-242). */
+GFH_API int gfh_sgemm_strided_batched(int trans_a, int trans_b, int64_t m,
+                                      int64_t n, int64_t k, float alpha,
+                                      const float *a, int64_t lda, int64_t stride_a,
+                                      int64_t batch_a, const float *b, int64_t ldb,
+                                      int64_t stride_b, int64_t batch_b, float beta,
+                                      float *c, int64_t ldc, int64_t stride_c,
+                                      int64_t batch, const float *bias,
+                                      gfh_stream_t stream);
+
+/* ---- int8 quantization (ghostflow-nn/src/quantization.rs) ---------------- */
+
+/* quantize_per_channel_int8 (quantization.rs:110-153): channel = dim 0, one
+ * (scale, zero_point) per contiguous row of `cols` elements; symmetric or
+ * asymmetric.  Codes, scales and zero points are bit-identical to the
+ * reference. */
+GFH_API int gfh_quantize_i8_per_channel(const float *x, int64_t rows, int64_t cols,
+                                        int symmetric, int8_t *q, float *scales,
+                                        int8_t *zero_points, gfh_stream_t stream);
+
+/* quantize_per_tensor_int8 (quantization.rs:77-108): one (scale, zero_point)
+ * over all n elements; DynamicQuantization::quantize_activation uses it with
+ * symmetric = 0 (quantization.rs:280-287).  `scale` / `zero_point` are device
+ * pointers to one element each.  Workspace: gfh_quantize_i8_per_tensor_
+ * workspace_size(n) bytes (nullable, see conventions). */
+GFH_API int gfh_quantize_i8_per_tensor(const float *x, int64_t n, int symmetric,
+                                       int8_t *q, float *scale, int8_t *zero_point,
+                                       void *workspace, size_t workspace_bytes,
+                                       gfh_stream_t stream);
+GFH_API size_t gfh_quantize_i8_per_tensor_workspace_size(int64_t n);
+
+/* dequantize_int8 (quantization.rs:173-204): nscales == 1 -> per tensor,
+ * nscales == rows -> per channel over dim 0; (q - zp) * scale. */
+GFH_API int gfh_dequantize_i8(const int8_t *q, int64_t rows, int64_t cols,
+                              const float *scales, const int8_t *zero_points,
+                              int64_t nscales, float *out, gfh_stream_t stream);
+
+/* Sum over k of qw[n, k] for every row n (int32), the zero-point correction
+ * term of gfh_qlinear_i8.  Weights are static, so this runs once per weight. */
+GFH_API int gfh_qweight_rowsum(const int8_t *qw, int64_t n, int64_t k,
+                               int32_t *rowsum, gfh_stream_t stream);
+
+/* INT8 linear.  The reference has no integer GEMM (its executable path is
+ * DynamicQuantization::get_weights -> dequantize -> fp32 matmul,
+ * quantization.rs:275-277); this computes the same layer on int8 MFMA:
+ *   acc[m,n] = sum_k (qx[m,k] - zx) * qw[n,k]          exact int32
+ *            = sum_k qx*qw - zx * rowsum[n]
+ *   y[m,n]   = (float)acc * (sx * sw[n]) (+ bias[n])   each step f32-rounded
+ * x_per_row = 0: sx, zx point to ONE element (per-tensor activation,
+ *   quantization.rs:280-287);  x_per_row = 1: sx[m], zx[m] per row
+ *   (QuantizationConfig::default, per-channel over dim 0, :28-36).
+ * zx and w_rowsum are nullable (zero points taken as 0; w_rowsum is required
+ * when zx is given).  qw is [n, k] with per-row scales sw[n]
+ * (quantize_per_channel_int8 of the Linear weight [out, in]).
+ * y and acc_out are nullable (at least one must be given); acc_out receives
+ * the exact int32 accumulators. */
+GFH_API int gfh_qlinear_i8(const int8_t *qx, const float *sx, const int8_t *zx,
+                           int x_per_row, const int8_t *qw, const float *sw,
+                           const int32_t *w_rowsum, const float *bias, float *y,
+                           int32_t *acc_out, int64_t m, int64_t n, int64_t k,
+                           gfh_stream_t stream);
+
+/* ---- decode GEMV --------------------------------------------------------- */
+
+/* y[b, n] = sum_k x[b, k] * W[k, n], W [k, n] row-major, b <= 64.
+ * Tensor::matmul with M = b (matmul.rs:91-119); Tensor::mv for b = 1
+ * (matmul.rs:222-250). */
+GFH_API int gfh_gemv_f32(const float *x, const float *w, float *y, int64_t b,
+                         int64_t k, int64_t n, gfh_stream_t stream);
+
+/* Weight-only int8 GEMV: W is QuantizedTensor data [k, n] quantized per
+ * channel over dim 0 (quantize_per_channel_int8, quantization.rs:110-153), so
+ * row k has scale s[k] and zero point zp[k] (zp nullable = 0):
+ *   y[b, n] = sum_k x[b, k] * ((q[k, n] - zp[k]) * s[k])
+ * i.e. DynamicQuantization::get_weights (dequantize_int8, :173-204) followed
+ * by Tensor::matmul, without materializing the fp32 weight. b <= 64. */
+GFH_API int gfh_gemv_w8(const float *x, const int8_t *qw, const float *scales,
+                        const int8_t *zero_points, float *y, int64_t b,
+                        int64_t k, int64_t n, gfh_stream_t stream);
+
+/* ---- attention ----------------------------------------------------------- */
+
+/* Row softmax over the last dimension (Tensor::softmax(-1),
+ * ghostflow-core/src/ops/activation.rs:165-216).  x and y may alias. */
+GFH_API int gfh_softmax_lastdim_f32(const float *x, float *y, int64_t rows,
+                                    int64_t cols, gfh_stream_t stream);
+
+/* Fused scaled-dot-product attention, Q [b,h,sq,d], K/V [b,h,skv,d],
+ * out [b,h,sq,d]:  softmax(mask(Q.K^T * scale)) . V
+ *   - scale multiplies the finished dot product (mul_scalar after the
+ *     matmul, ghostflow-nn/src/attention.rs:19-25);
+ *   - causal != 0 masks j > i (ghostflow-cuda/src/ops.rs:205-224; needs
+ *     sq == skv);
+ *   - mask (nullable, f32, mask_numel elements) is CYCLED over the flattened
+ *     scores, m > 0.5 keeps (apply_attention_mask, attention.rs:51-64);
+ *   - weights (nullable) receives the [b,h,sq,skv] softmax output, the
+ *     second value scaled_dot_product_attention returns (attention.rs:48).
+ * Replaces scaled_dot_product_attention (attention.rs:11-49),
+ * ops::attention::flash_attention (ghostflow-cuda/src/ops.rs:166-203) and
+ * launch_fused_attention (ghostflow-cuda/src/ffi.rs:190-196).  d <= 128 and
+ * d % 4 == 0. */
+GFH_API int gfh_sdpa_f32(const float *q, const float *k, const float *v, float *out,
+                         float *weights, int64_t b, int64_t h, int64_t sq,
+                         int64_t skv, int64_t d, float scale, int causal,
+                         const float *mask, int64_t mask_numel, gfh_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GHOSTFLOW_HIP_H */

@@ -1,0 +1,123 @@
+"""CPU tests of the C ABI: the library loads, exports every symbol the header
+declares, and rejects bad arguments on the host before touching a device."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ghostflow_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"GFH_API\s+[\w\s\*]+?\b(gfh_\w+)\s*\(", text)))
+
+
+def _lib():
+    from ghostflow_hip import _lib as L
+    return L.load()
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    for must in ("gfh_sgemm", "gfh_qlinear_i8", "gfh_gemv_f32", "gfh_gemv_w8", "gfh_sdpa_f32",
+                 "gfh_quantize_i8_per_channel", "gfh_quantize_i8_per_tensor", "gfh_dequantize_i8",
+                 "gfh_softmax_lastdim_f32", "gfh_last_error"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib()
+    missing = [n for n in _declared() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_python_signatures_cover_header():
+    from ghostflow_hip import _lib as L
+    assert sorted(L.SIGNATURES) == _declared()
+
+
+def test_version_and_last_error():
+    lib = _lib()
+    assert b"gfx950" in lib.gfh_version()
+    assert lib.gfh_last_error() is not None
+
+
+# Host-side validation: these fail before any device call, so they run on CPU.
+
+def _fake(n=4096):
+    """A host buffer address; never dereferenced because validation fails first."""
+    buf = (C.c_char * n)()
+    return C.cast(buf, C.c_void_p), buf
+
+
+def test_sgemm_rejects_negative_dims():
+    lib = _lib()
+    rc = lib.gfh_sgemm(0, 0, -1, 4, 4, 1.0, None, 4, None, 4, 0.0, None, 4, None, None)
+    assert rc == 1
+    assert b"dims" in lib.gfh_last_error()
+
+
+def test_sgemm_rejects_small_leading_dim():
+    lib = _lib()
+    rc = lib.gfh_sgemm(0, 0, 8, 8, 8, 1.0, None, 4, None, 8, 0.0, None, 8, None, None)
+    assert rc == 1
+    assert b"leading dimension" in lib.gfh_last_error()
+
+
+def test_sgemm_null_operands():
+    lib = _lib()
+    rc = lib.gfh_sgemm(0, 0, 8, 8, 8, 1.0, None, 8, None, 8, 0.0, None, 8, None, None)
+    assert rc == 3
+    assert b"NULL" in lib.gfh_last_error()
+
+
+def test_sgemm_empty_is_noop():
+    lib = _lib()
+    assert lib.gfh_sgemm(0, 0, 0, 8, 8, 1.0, None, 8, None, 8, 0.0, None, 8, None, None) == 0
+
+
+def test_sgemm_rejects_host_memory():
+    lib = _lib()
+    p, keep = _fake(8 * 8 * 4)
+    rc = lib.gfh_sgemm(0, 0, 8, 8, 8, 1.0, p, 8, p, 8, 0.0, p, 8, None, None)
+    assert rc in (2, 5)  # not device memory (InvalidData) / no device (ComputationFailed)
+
+
+def test_qlinear_k_bound_and_outputs():
+    lib = _lib()
+    assert lib.gfh_qlinear_i8(None, None, None, 0, None, None, None, None, None, None, 4, 4, 70000, None) == 1
+    assert lib.gfh_qlinear_i8(None, None, None, 0, None, None, None, None, None, None, 4, 4, 64, None) == 3
+
+
+def test_gemv_batch_limit():
+    lib = _lib()
+    assert lib.gfh_gemv_f32(None, None, None, 65, 16, 16, None) == 1
+    assert lib.gfh_gemv_w8(None, None, None, None, None, 65, 16, 16, None) == 1
+
+
+def test_sdpa_shape_rules():
+    lib = _lib()
+    # head_dim must be a multiple of 4 in [4,128]
+    assert lib.gfh_sdpa_f32(None, None, None, None, None, 1, 1, 8, 8, 130, 1.0, 0, None, 0, None) == 1
+    assert lib.gfh_sdpa_f32(None, None, None, None, None, 1, 1, 8, 8, 6, 1.0, 0, None, 0, None) == 1
+    # causal needs sq == skv
+    assert lib.gfh_sdpa_f32(None, None, None, None, None, 1, 1, 8, 9, 16, 1.0, 1, None, 0, None) == 1
+    # missing tensors
+    assert lib.gfh_sdpa_f32(None, None, None, None, None, 1, 1, 8, 8, 16, 1.0, 1, None, 0, None) == 3
+
+
+def test_dequantize_scale_count():
+    lib = _lib()
+    assert lib.gfh_dequantize_i8(None, 4, 4, None, None, 3, None, None) == 1
+
+
+def test_python_wrapper_shape_mismatch():
+    torch = pytest.importorskip("torch")
+    import ghostflow_hip as gh
+    from ghostflow_hip.ops import GhostFlowError
+    a = torch.zeros(2, 3)
+    with pytest.raises(GhostFlowError):
+        gh.matmul(a, torch.zeros(4, 2))

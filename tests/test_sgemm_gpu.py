@@ -1,0 +1,162 @@
+"""fp32 GEMM / Linear on the GPU against the oracle (matmul_blocked,
+Linear::forward, batched_matmul restated from the reference).
+
+Bars: bit-exact where every partial sum is exactly representable
+(integer-valued inputs, reference known answers); otherwise
+max|err| <= 1e-4 * sqrt(K) * max|a| * max|b| (the north-star GEMM bound).
+"""
+import numpy as np
+import pytest
+
+from _util import gemm_tol, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _gh():
+    import ghostflow_hip
+    return ghostflow_hip
+
+
+def _oracle():
+    from oracle import oracle
+    return oracle
+
+
+def test_reference_known_answers(torch_dev):
+    gh = _gh()
+    # ghostflow-core/src/ops/matmul.rs:331-352
+    a = np.arange(1, 7, dtype=np.float32).reshape(2, 3)
+    b = np.arange(1, 7, dtype=np.float32).reshape(3, 2)
+    c = to_np(gh.matmul(to_dev(a, torch_dev), to_dev(b, torch_dev)))
+    assert c.tolist() == [[22.0, 28.0], [49.0, 64.0]]
+    # ghostflow-core/tests/test_optimizations.rs:65-91
+    a = np.array([[1, 2], [3, 4]], np.float32)
+    b = np.array([[5, 6], [7, 8]], np.float32)
+    c = to_np(gh.matmul(to_dev(a, torch_dev), to_dev(b, torch_dev)))
+    assert c.reshape(-1).tolist() == [19.0, 22.0, 43.0, 50.0]
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (7, 3, 5), (33, 29, 17), (64, 64, 64), (128, 200, 96),
+                                   (257, 300, 131), (1024, 1024, 1024)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_integer_inputs_bit_exact(torch_dev, m, k, n, ta, tb):
+    """|a|,|b| <= 8 integers: every partial sum < 2^24 is exact, so the GPU
+    must equal the oracle bit for bit whatever the summation order."""
+    gh, O = _gh(), _oracle()
+    rng = np.random.default_rng(m * 1000003 + k * 1009 + n)
+    a = rng.integers(-8, 9, size=(m, k)).astype(np.float32)
+    b = rng.integers(-8, 9, size=(k, n)).astype(np.float32)
+    ref = O.matmul(a, b)
+    da = to_dev(a.T.copy() if ta else a, torch_dev)
+    db = to_dev(b.T.copy() if tb else b, torch_dev)
+    got = to_np(gh.sgemm(da, db, trans_a=bool(ta), trans_b=bool(tb)))
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_config1_1024_normal(torch_dev):
+    """Config 1: A, B [1024,1024] ~ N(0,1) from seed 0, full output vs oracle."""
+    gh, O = _gh(), _oracle()
+    a = gh.normal((1024, 1024), seed=0, tensor_id=0)
+    b = gh.normal((1024, 1024), seed=0, tensor_id=1)
+    ref = O.matmul(a, b)
+    got = to_np(gh.matmul(to_dev(a, torch_dev), to_dev(b, torch_dev)))
+    err = np.abs(got - ref).max()
+    assert err <= gemm_tol(1024, a, b), err
+
+
+@pytest.mark.parametrize("m,k,n", [(5, 7, 3), (100, 37, 130), (129, 64, 255)])
+def test_unaligned_leading_dims(torch_dev, m, k, n):
+    """Odd K / N: the scalar (non-16-byte) load path."""
+    gh, O = _gh(), _oracle()
+    rng = np.random.default_rng(7)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    got = to_np(gh.matmul(to_dev(a, torch_dev), to_dev(b, torch_dev)))
+    assert np.abs(got - O.matmul(a, b)).max() <= gemm_tol(k, a, b)
+
+
+def test_alpha_beta_bias(torch_dev):
+    gh, O = _gh(), _oracle()
+    rng = np.random.default_rng(11)
+    m, k, n = 70, 96, 150
+    a = rng.integers(-4, 5, size=(m, k)).astype(np.float32)
+    b = rng.integers(-4, 5, size=(k, n)).astype(np.float32)
+    c0 = rng.integers(-4, 5, size=(m, n)).astype(np.float32)
+    bias = rng.integers(-4, 5, size=(n,)).astype(np.float32)
+    dc = to_dev(c0, torch_dev)
+    gh.sgemm(to_dev(a, torch_dev), to_dev(b, torch_dev), alpha=2.0, beta=-1.0, bias=to_dev(bias, torch_dev), out=dc)
+    ref = 2.0 * O.matmul(a, b) - c0 + bias
+    np.testing.assert_array_equal(to_np(dc), ref.astype(np.float32))
+
+
+def test_beta_zero_ignores_nan_output(torch_dev):
+    """beta == 0 must not read C (NaN in C stays out of the result)."""
+    import torch
+    gh = _gh()
+    a = np.ones((40, 8), np.float32)
+    b = np.ones((8, 50), np.float32)
+    out = torch.full((40, 50), float("nan"), device=torch_dev)
+    gh.sgemm(to_dev(a, torch_dev), to_dev(b, torch_dev), out=out)
+    assert (to_np(out) == 8.0).all()
+
+
+def test_linear_known_small(torch_dev):
+    """Linear::forward restated: x W^T + b, integer data -> exact."""
+    gh, O = _gh(), _oracle()
+    rng = np.random.default_rng(3)
+    x = rng.integers(-5, 6, size=(16, 64)).astype(np.float32)
+    w = rng.integers(-5, 6, size=(48, 64)).astype(np.float32)
+    bias = rng.integers(-5, 6, size=(48,)).astype(np.float32)
+    got = to_np(gh.linear(to_dev(x, torch_dev), to_dev(w, torch_dev), to_dev(bias, torch_dev)))
+    np.testing.assert_array_equal(got, O.linear_forward(x, w, bias))
+
+
+def test_config2_linear_4096_sampled_rows(torch_dev):
+    """Config 2 at full size: x [4096,4096] ~ N(0,1), W, b ~ U(-1/64,1/64).
+    Output rows are independent, so 48 sampled rows are checked exactly
+    against the oracle's Linear::forward on those rows."""
+    gh, O = _gh(), _oracle()
+    x = gh.normal((4096, 4096), seed=0, tensor_id=0)
+    w = gh.uniform((4096, 4096), -1 / 64, 1 / 64, seed=0, tensor_id=1)
+    bias = gh.uniform((4096,), -1 / 64, 1 / 64, seed=0, tensor_id=2)
+    y = to_np(gh.linear(to_dev(x, torch_dev), to_dev(w, torch_dev), to_dev(bias, torch_dev)))
+    rows = np.random.default_rng(0).choice(4096, 48, replace=False)
+    rows = np.concatenate([[0, 4095], rows])
+    ref = O.linear_forward(x[rows], w, bias)
+    err = np.abs(y[rows] - ref).max()
+    assert err <= gemm_tol(4096, x, w), err
+
+
+def test_batched_modulo_semantics(torch_dev):
+    """batched_matmul takes batch slices modulo each operand's batch count
+    (matmul.rs:148-149): [2,3,m,k] @ [3,k,n] broadcasts B over dim 0."""
+    gh, O = _gh(), _oracle()
+    rng = np.random.default_rng(5)
+    a = rng.integers(-6, 7, size=(2, 3, 20, 24)).astype(np.float32)
+    b = rng.integers(-6, 7, size=(3, 24, 36)).astype(np.float32)
+    got = to_np(gh.matmul(to_dev(a, torch_dev), to_dev(b, torch_dev)))
+    ref = O.batched_matmul(a, b)
+    assert got.shape == (2, 3, 20, 36)
+    np.testing.assert_array_equal(got, ref)
+
+
+@pytest.mark.parametrize("n", [2048])
+def test_square_sweep_sampled_rows(torch_dev, n):
+    gh, O = _gh(), _oracle()
+    a = gh.normal((n, n), seed=0, tensor_id=0)
+    b = gh.normal((n, n), seed=0, tensor_id=1)
+    c = to_np(gh.matmul(to_dev(a, torch_dev), to_dev(b, torch_dev)))
+    rows = np.random.default_rng(1).choice(n, 32, replace=False)
+    ref = O.matmul(a[rows], b)
+    assert np.abs(c[rows] - ref).max() <= gemm_tol(n, a, b)
+
+
+def test_k_zero_gives_bias(torch_dev):
+    import torch
+    gh = _gh()
+    a = torch.empty((4, 0), device=torch_dev)
+    b = torch.empty((0, 6), device=torch_dev)
+    bias = torch.arange(6, dtype=torch.float32, device=torch_dev)
+    out = gh.sgemm(a, b, bias=bias)
+    assert to_np(out).tolist() == [list(range(6))] * 4
