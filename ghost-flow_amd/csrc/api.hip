@@ -322,7 +322,7 @@ GFH_API int gfh_sdpa_f32(const float *q, const float *k, const float *v, float *
                          int64_t h, int64_t sq, int64_t skv, int64_t d, float scale, int causal, const float *mask,
                          int64_t mask_numel, gfh_stream_t stream) {
     return guarded([&]() -> int {
-        if (b < 0 || h < 0 || sq < 0 || skv < 0 || d < 0 || b > 65535 || h > 65535 || sq > kMaxDim ||
+        if (b < 0 || h < 0 || sq < 0 || skv < 0 || d < 0 || b > 65535 || h > 65535 || sq > 65535 * 128 ||
             skv > kMaxDim)
             return set_error(GFH_INVALID_SHAPE, "sdpa: b=%lld h=%lld sq=%lld skv=%lld out of range", (long long)b,
                              (long long)h, (long long)sq, (long long)skv);

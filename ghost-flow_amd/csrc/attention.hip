@@ -1,0 +1,355 @@
+// attention.hip -- fused scaled-dot-product attention and row softmax on
+// CDNA4 f32 MFMA.
+//
+// Computes, per (batch, head) slice, softmax(mask(Q K^T * scale)) V -- the
+// work of scaled_dot_product_attention (ghostflow-nn/src/attention.rs:11-49)
+// and ops::attention::flash_attention (ghostflow-cuda/src/ops.rs:166-224) --
+// without materializing the score matrix, using the online-softmax
+// recurrence (running max m, running sum l, rescale by exp(m_old - m_new)),
+// the blockwise form of ghostflow-nn/src/flash_attention.rs:178-250.
+//
+// Semantics kept from the reference:
+//   * the scale multiplies the finished dot product (mul_scalar after the
+//     matmul, attention.rs:24-25);
+//   * causal masking is j > i -> -inf (ops.rs:205-224); an explicit mask is
+//     cycled over the flattened scores, m > 0.5 keeps (attention.rs:51-64);
+//   * a row whose scores are all -inf yields NaN, as softmax over all -inf
+//     does in the reference (max = -inf, exp(NaN)).
+//
+// Layout (one 256-thread workgroup = 4 wave64s per 128 queries of one
+// (b, h); K/V streamed in 32-key tiles through double-buffered LDS):
+//   * S^T = K . Q^T on v_mfma_f32_32x32x2_f32: keys are the MFMA rows and
+//     queries the columns, so lane l owns query l%32 and holds 16 of the 32
+//     keys of a tile (the other 16 sit in lane l^32).  Row max / row sum are
+//     in-register folds plus one cross-half shuffle.
+//   * Q for the wave's 32 queries stays in registers for the whole key loop
+//     (one 16-byte fragment per 8 head dims).
+//   * O^T = V^T . P^T on the same MFMA: the B operand of step r is exactly
+//     accumulator register r of S^T (same key, same query), so P never moves;
+//     the A operand is one conflict-free ds_read_b32 of V per step.
+//   * O accumulators (head_dim/32 blocks of 16 registers) are per-lane per
+//     query, so the online-softmax rescale is a per-lane multiply.
+//   * Causal: key tiles above the diagonal are skipped (per workgroup and per
+//     wave), and workgroups are issued heaviest query block first.  The
+//     (b,h) index is the fastest grid dimension, so all query blocks of one
+//     (b,h) land on the same XCD and share its K/V in that L2.
+#include <cmath>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace gfh {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kBQ = 128;  // queries per workgroup (32 per wave)
+constexpr int kBKV = 32;  // keys per LDS tile
+
+struct SdpaParams {
+    const float *q, *k, *v;
+    float *out;
+    float *weights;
+    const float *mask;
+    int64_t mask_numel;
+    int64_t sq, skv, d;
+    int64_t bh;
+    float scale;
+    int nqb;
+};
+
+__device__ __forceinline__ int key_of(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+
+// One 32-key x DMAX tile of K or V: DMAX*8 float4 per tile, DMAX/32 per thread.
+template <int DMAX>
+struct KvStage {
+    static constexpr int kPer = kBKV * DMAX / 4 / kThreads;
+    static constexpr int kStride = DMAX + 4;
+    f32x4 r[kPer];
+
+    __device__ __forceinline__ void load(const float *__restrict__ base, int64_t key0, int64_t nkeys, int64_t d,
+                                         int tid) {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int idx = tid + i * kThreads;
+            const int key = idx / (DMAX / 4);
+            const int dim = (idx % (DMAX / 4)) * 4;
+            f32x4 v = {0.f, 0.f, 0.f, 0.f};
+            if (key0 + key < nkeys && dim < d) v = *reinterpret_cast<const f32x4 *>(base + (key0 + key) * d + dim);
+            r[i] = v;
+        }
+    }
+    __device__ __forceinline__ void store(float *lds, int tid) const {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int idx = tid + i * kThreads;
+            const int key = idx / (DMAX / 4);
+            const int dim = (idx % (DMAX / 4)) * 4;
+            *reinterpret_cast<f32x4 *>(lds + key * kStride + dim) = r[i];
+        }
+    }
+};
+
+// Scaled, masked scores of one 32-key tile for this lane's query.
+template <int DMAX, bool CAUSAL, bool MASK>
+__device__ __forceinline__ void tile_scores(const SdpaParams &p, const float *ks, const f32x4 (&qf)[DMAX / 8],
+                                            int64_t k0, int64_t my_q, int lane, float (&sv)[16]) {
+    constexpr int NG = DMAX / 8;
+    constexpr int kStride = DMAX + 4;
+    const int c = lane & 31, h = lane >> 5;
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        const f32x4 kf = *reinterpret_cast<const f32x4 *>(ks + c * kStride + 8 * g + 4 * h);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[s], qf[g][s], acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int64_t key = k0 + key_of(r, h);
+        float v = acc[r] * p.scale;
+        bool keep = key < p.skv;
+        if (CAUSAL) keep = keep && key <= my_q;
+        if (MASK && keep) {
+            const int64_t f = ((int64_t)blockIdx.x * p.sq + my_q) * p.skv + key;
+            keep = p.mask[f % p.mask_numel] > 0.5f;
+        }
+        sv[r] = keep ? v : -INFINITY;
+    }
+}
+
+template <int DMAX, bool CAUSAL, bool MASK, bool WEIGHTS>
+__global__ __launch_bounds__(kThreads) void sdpa_fwd_kernel(SdpaParams p) {
+    constexpr int NG = DMAX / 8, ND = DMAX / 32;
+    constexpr int kStride = DMAX + 4;
+    constexpr int kTile = kBKV * kStride;
+    __shared__ __attribute__((aligned(16))) float lds[4 * kTile];  // K0 K1 V0 V1
+    float *const lk = lds;
+    float *const lv = lds + 2 * kTile;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int c = lane & 31, h = lane >> 5;
+    const int64_t bh = blockIdx.x;
+    const int qb = CAUSAL ? (p.nqb - 1 - (int)blockIdx.y) : (int)blockIdx.y;
+    const int64_t q0 = (int64_t)qb * kBQ;
+    const int64_t wq0 = q0 + wave * 32;
+    const int64_t my_q = wq0 + c;
+    const float *Q = p.q + bh * p.sq * p.d;
+    const float *K = p.k + bh * p.skv * p.d;
+    const float *V = p.v + bh * p.skv * p.d;
+
+    f32x4 qf[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        const int dim = 8 * g + 4 * h;
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        if (my_q < p.sq && dim < p.d) v = *reinterpret_cast<const f32x4 *>(Q + my_q * p.d + dim);
+        qf[g] = v;
+    }
+
+    f32x16 o[ND];
+#pragma unroll
+    for (int j = 0; j < ND; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[j][r] = 0.f;
+    float m = -INFINITY, l = 0.f;
+
+    const int64_t kv_end = CAUSAL ? min(p.skv, q0 + kBQ) : p.skv;
+    const int64_t ntiles = (kv_end + kBKV - 1) / kBKV;
+
+    KvStage<DMAX> gk, gv;
+    if (ntiles > 0) {
+        gk.load(K, 0, p.skv, p.d, tid);
+        gv.load(V, 0, p.skv, p.d, tid);
+        gk.store(lk, tid);
+        gv.store(lv, tid);
+    }
+    __syncthreads();
+
+    for (int64_t t = 0; t < ntiles; ++t) {
+        const int cur = t & 1;
+        const bool more = t + 1 < ntiles;
+        if (more) {
+            gk.load(K, (t + 1) * kBKV, p.skv, p.d, tid);
+            gv.load(V, (t + 1) * kBKV, p.skv, p.d, tid);
+        }
+        const int64_t k0 = t * kBKV;
+        // A wave whose last query precedes the tile's first key has nothing to do.
+        const bool active = !CAUSAL || k0 <= wq0 + 31;
+        if (active) {
+            float sv[16];
+            tile_scores<DMAX, CAUSAL, MASK>(p, lk + cur * kTile, qf, k0, my_q, lane, sv);
+            float mb = sv[0];
+#pragma unroll
+            for (int r = 1; r < 16; ++r) mb = fmaxf(mb, sv[r]);
+            mb = fmaxf(mb, __shfl_xor(mb, 32));
+            const float m_new = fmaxf(m, mb);
+            const bool dead = (m_new == -INFINITY);  // every score so far masked
+            const float alpha = dead ? 1.f : __expf(m - m_new);
+            float psum = 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                sv[r] = dead ? 0.f : __expf(sv[r] - m_new);
+                psum += sv[r];
+            }
+            psum += __shfl_xor(psum, 32);
+            l = l * alpha + psum;
+            m = m_new;
+#pragma unroll
+            for (int j = 0; j < ND; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[j][r] *= alpha;
+            const float *vt = lv + cur * kTile;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float *vrow = vt + key_of(r, h) * kStride + c;
+#pragma unroll
+                for (int j = 0; j < ND; ++j)
+                    o[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * j], sv[r], o[j], 0, 0, 0);
+            }
+        }
+        if (more) {
+            gk.store(lk + (cur ^ 1) * kTile, tid);
+            gv.store(lv + (cur ^ 1) * kTile, tid);
+        }
+        __syncthreads();
+    }
+
+    // O = O / l.  Lane (query c, half h), register r of block j holds head
+    // dim 32j + 8(r/4) + 4h + r%4: four consecutive dims per 16-byte store.
+    if (my_q < p.sq) {
+        const float inv_l = 1.0f / l;
+        float *orow = p.out + (bh * p.sq + my_q) * p.d;
+#pragma unroll
+        for (int j = 0; j < ND; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int dim = 32 * j + 8 * i + 4 * h;
+                if (dim < p.d) {
+                    f32x4 v = {o[j][4 * i] * inv_l, o[j][4 * i + 1] * inv_l, o[j][4 * i + 2] * inv_l,
+                               o[j][4 * i + 3] * inv_l};
+                    *reinterpret_cast<f32x4 *>(orow + dim) = v;
+                }
+            }
+    }
+
+    if constexpr (WEIGHTS) {
+        // Second pass: the normalized probabilities exp(s - m) / l for every
+        // key (masked ones come out as 0), written as the [sq, skv] weights.
+        const int64_t wtiles = (p.skv + kBKV - 1) / kBKV;
+        const float inv_l = 1.0f / l;
+        float *wrow = p.weights + (bh * p.sq + (my_q < p.sq ? my_q : 0)) * p.skv;
+        __syncthreads();
+        for (int64_t t = 0; t < wtiles; ++t) {
+            gk.load(K, t * kBKV, p.skv, p.d, tid);
+            gk.store(lk, tid);
+            __syncthreads();
+            float sv[16];
+            tile_scores<DMAX, CAUSAL, MASK>(p, lk, qf, t * kBKV, my_q, lane, sv);
+            if (my_q < p.sq) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int64_t key = t * kBKV + 8 * i + 4 * h;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (key + e < p.skv) wrow[key + e] = __expf(sv[4 * i + e] - m) * inv_l;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// ---- row softmax (Tensor::softmax(-1)) ---------------------------------------
+// One workgroup per row: max fold, sum of exp, then exp(x - max) / sum with a
+// true division, as activation.rs:188-212.  expf is ROCm's full-precision
+// device expf.
+__global__ __launch_bounds__(kThreads) void softmax_rows_kernel(const float *__restrict__ x, float *__restrict__ y,
+                                                               int64_t cols) {
+    __shared__ float red[kThreads / 64];
+    const int64_t row = blockIdx.x;
+    const float *xr = x + row * cols;
+    float *yr = y + row * cols;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+
+    float mx = -INFINITY;
+    for (int64_t i = threadIdx.x; i < cols; i += kThreads) mx = fmaxf(mx, xr[i]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+
+    float sum = 0.f;
+    for (int64_t i = threadIdx.x; i < cols; i += kThreads) sum += expf(xr[i] - mx);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+    if (lane == 0) red[wave] = sum;
+    __syncthreads();
+    sum = (red[0] + red[1]) + (red[2] + red[3]);
+
+    for (int64_t i = threadIdx.x; i < cols; i += kThreads) yr[i] = expf(xr[i] - mx) / sum;
+}
+
+template <int DMAX, bool CAUSAL, bool MASK>
+void launch_sdpa_variant(const SdpaParams &p, dim3 grid, bool weights, hipStream_t s) {
+    if (weights)
+        hipLaunchKernelGGL((sdpa_fwd_kernel<DMAX, CAUSAL, MASK, true>), grid, dim3(kThreads), 0, s, p);
+    else
+        hipLaunchKernelGGL((sdpa_fwd_kernel<DMAX, CAUSAL, MASK, false>), grid, dim3(kThreads), 0, s, p);
+}
+
+template <int DMAX>
+void launch_sdpa_d(const SdpaParams &p, dim3 grid, bool causal, bool mask, bool weights, hipStream_t s) {
+    if (causal) {
+        if (mask)
+            launch_sdpa_variant<DMAX, true, true>(p, grid, weights, s);
+        else
+            launch_sdpa_variant<DMAX, true, false>(p, grid, weights, s);
+    } else {
+        if (mask)
+            launch_sdpa_variant<DMAX, false, true>(p, grid, weights, s);
+        else
+            launch_sdpa_variant<DMAX, false, false>(p, grid, weights, s);
+    }
+}
+
+}  // namespace
+
+int launch_softmax_lastdim(const float *x, float *y, int64_t rows, int64_t cols, hipStream_t s) {
+    hipLaunchKernelGGL(softmax_rows_kernel, dim3((unsigned)rows), dim3(kThreads), 0, s, x, y, cols);
+    return check_launch("softmax_lastdim");
+}
+
+int launch_sdpa(const SdpaDesc &d, hipStream_t s) {
+    if (!aligned16(d.q) || !aligned16(d.k) || !aligned16(d.v) || !aligned16(d.out))
+        return set_error(GFH_INVALID_DATA, "sdpa: q, k, v and out must be 16-byte aligned");
+    SdpaParams p{};
+    p.q = d.q;
+    p.k = d.k;
+    p.v = d.v;
+    p.out = d.out;
+    p.weights = d.weights;
+    p.mask = d.mask;
+    p.mask_numel = d.mask_numel;
+    p.sq = d.sq;
+    p.skv = d.skv;
+    p.d = d.d;
+    p.bh = d.b * d.h;
+    p.scale = d.scale;
+    p.nqb = (int)((d.sq + kBQ - 1) / kBQ);
+    dim3 grid((unsigned)p.bh, (unsigned)p.nqb);
+    const bool mask = d.mask != nullptr, weights = d.weights != nullptr;
+    if (d.d <= 32)
+        launch_sdpa_d<32>(p, grid, d.causal, mask, weights, s);
+    else if (d.d <= 64)
+        launch_sdpa_d<64>(p, grid, d.causal, mask, weights, s);
+    else
+        launch_sdpa_d<128>(p, grid, d.causal, mask, weights, s);
+    return check_launch("sdpa");
+}
+
+}  // namespace gfh

@@ -1,0 +1,230 @@
+// qgemm.hip -- INT8 linear on CDNA4 i8 MFMA (v_mfma_i32_32x32x32_i8).
+//
+//   raw[m,n] = sum_k qx[m,k] * qw[n,k]                       (exact int32)
+//   acc[m,n] = raw - zx * rowsum[n]                          (exact int32)
+//   y[m,n]   = (float)acc * (sx * sw[n]) (+ bias[n])         (f32 roundings)
+//
+// The reference quantizes with quantization.rs:77-153 and computes the layer
+// as dequantize + fp32 matmul (quantization.rs:275-277); the integer form
+// above is that layer's int32-accumulate equivalent.  The zero-point term is
+// folded out of the inner loop through rowsum[n] = sum_k qw[n,k], so the
+// MFMA loop multiplies raw codes only.
+//
+// Design: one 256-thread workgroup (4 wave64s, 2 x 2) per 128 x 128 output
+// tile; each wave holds 2 x 2 32x32 int32 accumulators.  Both operands are
+// K-contiguous ([m,k] and [n,k]), so both are staged into LDS as
+// [rows][BK + 16] byte tiles (16-byte pad keeps the 16-byte fragment reads
+// of 8 consecutive rows on distinct banks) and read with one ds_read_b128
+// per lane per MFMA: lane l supplies row l%32 and bytes k0 + 16*(l/32) ..
+// +15 for A and the same k range for B, so every product pairs matching k
+// (the integer sum is exact in any order).  Two LDS stages, global loads for
+// stage t+1 issued before the MFMAs of stage t, one barrier per stage, and
+// the same XCD-contiguous / GROUP_M tile order as the fp32 GEMM.
+#include "common.hpp"
+#include "kernels.hpp"
+
+// Every multiply and add below is its own f32 rounding, as in the reference
+// (rustc never contracts a*b+c into an FMA); the MFMA accumulation itself is
+// not affected by this pragma.
+#pragma clang fp contract(off)
+
+namespace gfh {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kBM = 128, kBN = 128, kBK = 128;
+constexpr int kWM = 64, kWN = 64;
+constexpr int kPadB = 16;
+constexpr int kStride = kBK + kPadB;  // bytes per LDS row
+constexpr int kTileBytes = kBM * kStride;
+constexpr int kGroupM = 8;
+
+struct QParams {
+    const int8_t *qx;
+    const float *sx;
+    const int8_t *zx;
+    const int8_t *qw;
+    const float *sw;
+    const int32_t *rowsum;
+    const float *bias;
+    float *y;
+    int32_t *acc;
+    int64_t m, n, k;
+    int x_per_row;
+    int tiles_m, tiles_n;
+};
+
+// One 128 x BK byte stage of a K-contiguous int8 operand: 1024 16-byte
+// vectors, 4 per thread.
+template <bool VEC>
+struct I8Stage {
+    static constexpr int kVecs = kBM * kBK / 16;
+    static constexpr int kPer = kVecs / kThreads;
+    i32x4 r[kPer];
+
+    __device__ __forceinline__ void load(const int8_t *__restrict__ base, int64_t row0, int64_t rows_total,
+                                         int64_t k0, int64_t k_total, int tid) {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int idx = tid + i * kThreads;
+            const int64_t row = row0 + idx / (kBK / 16);
+            const int64_t kk = k0 + (idx % (kBK / 16)) * 16;
+            const int8_t *p = base + row * k_total + kk;
+            if (VEC && row < rows_total && kk + 15 < k_total) {
+                r[i] = *reinterpret_cast<const i32x4 *>(p);
+            } else {
+                uint32_t w[4] = {0u, 0u, 0u, 0u};
+                if (row < rows_total) {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        if (kk + e < k_total) w[e >> 2] |= (uint32_t)(uint8_t)p[e] << (8 * (e & 3));
+                }
+                r[i] = i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(int8_t *lds, int tid) const {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int idx = tid + i * kThreads;
+            const int row = idx / (kBK / 16);
+            const int kb = (idx % (kBK / 16)) * 16;
+            *reinterpret_cast<i32x4 *>(lds + row * kStride + kb) = r[i];
+        }
+    }
+};
+
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void qlinear_mfma_kernel(QParams p) {
+    constexpr int FM = kWM / 32, FN = kWN / 32;
+    __shared__ __attribute__((aligned(16))) int8_t lds[4 * kTileBytes];  // A0 A1 B0 B1
+    int8_t *const lds_a = lds;
+    int8_t *const lds_b = lds + 2 * kTileBytes;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm0 = (wave >> 1) * kWM;
+    const int wn0 = (wave & 1) * kWN;
+
+    const int nblk = p.tiles_m * p.tiles_n;
+    int bid = blockIdx.x;
+    if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+    const int group_size = kGroupM * p.tiles_n;
+    const int group = bid / group_size;
+    const int first_m = group * kGroupM;
+    const int gm = min(p.tiles_m - first_m, kGroupM);
+    const int in_group = bid - group * group_size;
+    const int64_t m0 = (int64_t)(first_m + in_group % gm) * kBM;
+    const int64_t n0 = (int64_t)(in_group / gm) * kBN;
+
+    i32x16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+    I8Stage<VEC> ga, gb;
+    const int64_t nst = (p.k + kBK - 1) / kBK;
+    if (nst > 0) {
+        ga.load(p.qx, m0, p.m, 0, p.k, tid);
+        gb.load(p.qw, n0, p.n, 0, p.k, tid);
+        ga.store(lds_a, tid);
+        gb.store(lds_b, tid);
+    }
+    __syncthreads();
+
+    const int frag_row = lane & 31;
+    const int frag_k = 16 * (lane >> 5);
+    for (int64_t st = 0; st < nst; ++st) {
+        const int cur = st & 1;
+        const bool more = st + 1 < nst;
+        if (more) {
+            ga.load(p.qx, m0, p.m, (st + 1) * kBK, p.k, tid);
+            gb.load(p.qw, n0, p.n, (st + 1) * kBK, p.k, tid);
+        }
+        const int8_t *la = lds_a + cur * kTileBytes;
+        const int8_t *lb = lds_b + cur * kTileBytes;
+#pragma unroll
+        for (int ks = 0; ks < kBK / 32; ++ks) {
+            i32x4 af[FM], bf[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+                af[i] = *reinterpret_cast<const i32x4 *>(la + (wm0 + i * 32 + frag_row) * kStride + ks * 32 + frag_k);
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                bf[j] = *reinterpret_cast<const i32x4 *>(lb + (wn0 + j * 32 + frag_row) * kStride + ks * 32 + frag_k);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        if (more) {
+            ga.store(lds_a + (cur ^ 1) * kTileBytes, tid);
+            gb.store(lds_b + (cur ^ 1) * kTileBytes, tid);
+        }
+        __syncthreads();
+    }
+
+    // Epilogue: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4, col l%32.
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        const int64_t col = n0 + wn0 + j * 32 + (lane & 31);
+        if (col >= p.n) continue;
+        const int32_t rs = p.zx ? p.rowsum[col] : 0;
+        const float swc = p.y ? p.sw[col] : 0.f;
+        const float bc = p.bias ? p.bias[col] : 0.f;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (row >= p.m) continue;
+                const int64_t g = p.x_per_row ? row : 0;
+                int32_t a = acc[i][j][r];
+                if (p.zx) a = (int32_t)((uint32_t)a - (uint32_t)((int32_t)p.zx[g] * rs));
+                if (p.acc) p.acc[row * p.n + col] = a;
+                if (p.y) {
+                    const float s = p.sx[g] * swc;
+                    float v = (float)a * s;
+                    if (p.bias) v = v + bc;
+                    p.y[row * p.n + col] = v;
+                }
+            }
+        }
+    }
+}
+
+}  // namespace
+
+int launch_qlinear_i8(const QLinearDesc &d, hipStream_t s) {
+    QParams p{};
+    p.qx = d.qx;
+    p.sx = d.sx;
+    p.zx = d.zx;
+    p.qw = d.qw;
+    p.sw = d.sw;
+    p.rowsum = d.w_rowsum;
+    p.bias = d.bias;
+    p.y = d.y;
+    p.acc = d.acc;
+    p.m = d.m;
+    p.n = d.n;
+    p.k = d.k;
+    p.x_per_row = d.x_per_row ? 1 : 0;
+    p.tiles_m = (int)((d.m + kBM - 1) / kBM);
+    p.tiles_n = (int)((d.n + kBN - 1) / kBN);
+    const bool vec = (d.k % 16 == 0) && aligned16(d.qx) && aligned16(d.qw);
+    dim3 grid((unsigned)(p.tiles_m * p.tiles_n));
+    if (vec)
+        hipLaunchKernelGGL(qlinear_mfma_kernel<true>, grid, dim3(kThreads), 0, s, p);
+    else
+        hipLaunchKernelGGL(qlinear_mfma_kernel<false>, grid, dim3(kThreads), 0, s, p);
+    return check_launch("qlinear_i8");
+}
+
+}  // namespace gfh

@@ -11,6 +11,11 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+// Every multiply and add below is its own f32 rounding, as in the reference
+// (rustc never contracts a*b+c into an FMA); the MFMA accumulation itself is
+// not affected by this pragma.
+#pragma clang fp contract(off)
+
 namespace gfh {
 namespace {
 

@@ -1,0 +1,95 @@
+"""Decode GEMV (fp32 and int8 weights) on the GPU against the oracle
+(Tensor::matmul at M = B; int8 = dequantize_int8 then matmul).  Bar: the
+north-star GEMM bound max|err| <= 1e-4 * sqrt(K) * max|x| * max|w|;
+bit-exact on integer-valued inputs."""
+import numpy as np
+import pytest
+
+from _util import gemm_tol, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _gh():
+    import ghostflow_hip
+    return ghostflow_hip
+
+
+def _O():
+    from oracle import oracle
+    return oracle
+
+
+@pytest.mark.parametrize("b,k,n", [(1, 1, 1), (3, 64, 80), (1, 300, 999), (8, 1024, 1024), (5, 77, 1030),
+                                   (13, 256, 512), (64, 128, 260)])
+def test_gemv_f32_integer_exact(torch_dev, b, k, n):
+    gh, O = _gh(), _O()
+    rng = np.random.default_rng(b * 7 + k + n)
+    x = rng.integers(-8, 9, size=(b, k)).astype(np.float32)
+    w = rng.integers(-8, 9, size=(k, n)).astype(np.float32)
+    got = to_np(gh.gemv_f32(to_dev(x, torch_dev), to_dev(w, torch_dev)))
+    np.testing.assert_array_equal(got, O.matmul(x, w))
+
+
+def test_mv_reference_known_answer(torch_dev):
+    """Tensor::mv [[1,2],[3,4]] . [1,2] = [5, 11] (matmul.rs:363-371), as
+    x [1,2] . W^T with W^T = [[1,3],[2,4]]."""
+    gh = _gh()
+    x = np.array([[1, 2]], np.float32)
+    wt = np.array([[1, 3], [2, 4]], np.float32)
+    assert to_np(gh.gemv_f32(to_dev(x, torch_dev), to_dev(wt, torch_dev))).tolist() == [[5.0, 11.0]]
+
+
+@pytest.mark.parametrize("b", [1, 4, 8])
+def test_config4_fp32(torch_dev, b):
+    """Config 4: W [4096,14336] ~ N(0,0.02), x [B,4096] ~ N(0,1)."""
+    gh, O = _gh(), _O()
+    k, n = 4096, 14336
+    w = gh.normal((k, n), 0.0, 0.02, seed=0, tensor_id=1)
+    x = gh.normal((b, k), seed=0, tensor_id=0)
+    got = to_np(gh.gemv_f32(to_dev(x, torch_dev), to_dev(w, torch_dev)))
+    ref = O.matmul(x, w)
+    assert np.abs(got - ref).max() <= gemm_tol(k, x, w)
+
+
+@pytest.mark.parametrize("b", [1, 4, 8])
+@pytest.mark.parametrize("symmetric", [True, False])
+def test_config4_int8(torch_dev, b, symmetric):
+    """Config 4 int8: W [4096,14336] quantized per channel over dim 0 (one
+    scale per k row); y vs dequantize(W) then matmul (the reference's path)."""
+    gh, O = _gh(), _O()
+    k, n = 4096, 14336
+    w = gh.normal((k, n), 0.0, 0.02, seed=0, tensor_id=1)
+    x = gh.normal((b, k), seed=0, tensor_id=0)
+    q, s, z = gh.quantize_per_channel(to_dev(w, torch_dev), symmetric)
+    got = to_np(gh.gemv_w8(to_dev(x, torch_dev), q, s, z))
+    rq, rs, rz = O.quantize_per_channel(w, symmetric)
+    np.testing.assert_array_equal(to_np(q), rq)
+    dw = O.dequantize(rq, rs, rz)
+    ref = O.matmul(x, dw)
+    assert np.abs(got - ref).max() <= gemm_tol(k, x, dw)
+
+
+@pytest.mark.parametrize("b,k,n", [(2, 64, 80), (7, 333, 1001), (9, 1024, 2048)])
+def test_gemv_w8_integer_exact(torch_dev, b, k, n):
+    """Scales that are powers of two and small integer x: every product and
+    partial sum is exact, so the result must match bit for bit."""
+    gh, O = _gh(), _O()
+    rng = np.random.default_rng(k + n)
+    q = rng.integers(-128, 128, size=(k, n)).astype(np.int8)
+    s = (2.0 ** rng.integers(-3, 2, size=k)).astype(np.float32)
+    z = rng.integers(-5, 6, size=k).astype(np.int8)
+    x = rng.integers(-4, 5, size=(b, k)).astype(np.float32)
+    got = to_np(gh.gemv_w8(to_dev(x, torch_dev), to_dev(q, torch_dev), to_dev(s, torch_dev), to_dev(z, torch_dev)))
+    ref = O.matmul(x, O.dequantize(q, s, z))
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_gemv_w8_without_zero_points(torch_dev):
+    gh, O = _gh(), _O()
+    rng = np.random.default_rng(1)
+    q = rng.integers(-128, 128, size=(200, 300)).astype(np.int8)
+    s = (2.0 ** rng.integers(-3, 2, size=200)).astype(np.float32)
+    x = rng.integers(-4, 5, size=(3, 200)).astype(np.float32)
+    got = to_np(gh.gemv_w8(to_dev(x, torch_dev), to_dev(q, torch_dev), to_dev(s, torch_dev)))
+    np.testing.assert_array_equal(got, O.matmul(x, O.dequantize(q, s, np.zeros(200, np.int8))))

@@ -1,0 +1,219 @@
+"""int8 quantization, INT8 linear and dequantization on the GPU against the
+oracle (quantization.rs restated).  Codes, scales, zero points and int32
+accumulators must be bit-exact; the fp32 output of the INT8 linear must equal
+the oracle's epilogue bit for bit and stay within the GEMM bound of the
+reference's executable composite (dequantize both operands, fp32 matmul)."""
+import numpy as np
+import pytest
+
+from _util import gemm_tol, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _gh():
+    import ghostflow_hip
+    return ghostflow_hip
+
+
+def _O():
+    from oracle import oracle
+    return oracle
+
+
+def _same_f32(a, b):
+    """Bitwise equality of float32 arrays (NaN-aware)."""
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+
+REF_INPUTS = [
+    # (data, shape, per_channel, symmetric): the reference's own test inputs
+    # (ghostflow-nn/src/quantization.rs:300-428)
+    ([1, 2, 3, 4, 5, 6], (2, 3), False, True),
+    ([1, 2, 3, 10, 20, 30], (2, 3), True, True),
+    ([-5, -3, -1, 1, 3, 5], (6,), False, False),
+    ([0.5, 1.5, 2.5], (3,), False, False),
+    ([1, 2, 3, 4], (4,), True, True),
+    ([1, 2, 3, 4], (2, 2), True, True),
+]
+
+
+@pytest.mark.parametrize("data,shape,per_channel,symmetric", REF_INPUTS)
+def test_reference_inputs_bit_exact(torch_dev, data, shape, per_channel, symmetric):
+    gh, O = _gh(), _O()
+    x = np.array(data, np.float32).reshape(shape)
+    if per_channel:
+        q, s, z = gh.quantize_per_channel(to_dev(x, torch_dev), symmetric)
+        rq, rs, rz = O.quantize_per_channel(x, symmetric)
+    else:
+        q, s, z = gh.quantize_per_tensor(to_dev(x, torch_dev), symmetric)
+        rq, rs, rz = O.quantize_per_tensor(x, symmetric)
+    np.testing.assert_array_equal(to_np(q), rq)
+    assert _same_f32(to_np(s).reshape(-1), np.atleast_1d(rs))
+    np.testing.assert_array_equal(to_np(z).reshape(-1), np.atleast_1d(rz))
+    deq = to_np(gh.dequantize(q, s, z))
+    assert _same_f32(deq, O.dequantize(rq, rs, rz))
+
+
+def test_hand_derived_codes(torch_dev):
+    """Exact values worked out by hand from quantization.rs:77-108 (the
+    asymmetric case is a half-away-from-zero tie: zp = round(-0.5) = -1)."""
+    gh = _gh()
+    x = np.array([-5, -3, -1, 1, 3, 5], np.float32)
+    q, s, z = gh.quantize_per_tensor(to_dev(x, torch_dev), False)
+    assert to_np(q).tolist() == [-128, -78, -27, 25, 76, 126]
+    assert int(to_np(z)[0]) == -1
+    x = np.array([0.5, 1.5, 2.5], np.float32)
+    q, s, z = gh.quantize_per_tensor(to_dev(x, torch_dev), False)
+    assert to_np(q).tolist() == [-64, 63, 127]
+    assert int(to_np(z)[0]) == -128
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (37, 129), (64, 4096), (11008, 4096)])
+@pytest.mark.parametrize("symmetric", [True, False])
+def test_per_channel_random(torch_dev, rows, cols, symmetric):
+    gh, O = _gh(), _O()
+    x = gh.normal((rows, cols), 0.0, 0.02, seed=0, tensor_id=1)
+    q, s, z = gh.quantize_per_channel(to_dev(x, torch_dev), symmetric)
+    rq, rs, rz = O.quantize_per_channel(x, symmetric)
+    np.testing.assert_array_equal(to_np(q), rq)
+    assert _same_f32(to_np(s), rs)
+    np.testing.assert_array_equal(to_np(z), rz)
+
+
+@pytest.mark.parametrize("n", [1, 5, 1000, 4096 * 256 + 3, 4096 * 4096])
+@pytest.mark.parametrize("symmetric", [True, False])
+def test_per_tensor_random(torch_dev, n, symmetric):
+    gh, O = _gh(), _O()
+    x = gh.normal((n,), seed=0, tensor_id=0)
+    q, s, z = gh.quantize_per_tensor(to_dev(x, torch_dev), symmetric)
+    rq, rs, rz = O.quantize_per_tensor(x, symmetric)
+    np.testing.assert_array_equal(to_np(q), rq)
+    assert _same_f32(to_np(s), np.atleast_1d(rs))
+    assert int(to_np(z)[0]) == int(rz)
+
+
+def test_per_tensor_unaligned_view(torch_dev):
+    """An offset (non 16-byte aligned) input takes the scalar path."""
+    gh, O = _gh(), _O()
+    base = gh.normal((1001,), seed=3, tensor_id=0)
+    d = to_dev(base, torch_dev)[1:]
+    q, s, z = gh.quantize_per_tensor(d, False)
+    rq, rs, rz = O.quantize_per_tensor(base[1:], False)
+    np.testing.assert_array_equal(to_np(q), rq)
+    assert _same_f32(to_np(s), np.atleast_1d(rs))
+
+
+def test_special_values(torch_dev):
+    """NaN is ignored by the min/max folds and quantizes to zp; all-zero
+    input gives scale 0 and code 0 (0/0 = NaN -> 0); infinities saturate."""
+    gh, O = _gh(), _O()
+    for data in ([0.0, 0.0, 0.0, 0.0], [1.0, np.nan, -2.0, 3.0], [np.inf, 1.0, -1.0, 2.0],
+                 [-np.inf, 1.0, 0.5, 0.25], [7.0, 7.0, 7.0, 7.0], [-3.0, -3.0, -3.0, -3.0]):
+        x = np.array(data, np.float32)
+        for sym in (True, False):
+            q, s, z = gh.quantize_per_tensor(to_dev(x, torch_dev), sym)
+            rq, rs, rz = O.quantize_per_tensor(x, sym)
+            np.testing.assert_array_equal(to_np(q), rq, err_msg=f"{data} sym={sym}")
+            assert _same_f32(to_np(s), np.atleast_1d(rs)), (data, sym)
+            assert int(to_np(z)[0]) == int(rz), (data, sym)
+            qc, sc, zc = gh.quantize_per_channel(to_dev(x.reshape(2, 2), torch_dev), sym)
+            rqc, rsc, rzc = O.quantize_per_channel(x.reshape(2, 2), sym)
+            np.testing.assert_array_equal(to_np(qc), rqc)
+            assert _same_f32(to_np(sc), rsc)
+
+
+def test_dequantize_per_channel_large(torch_dev):
+    gh, O = _gh(), _O()
+    w = gh.normal((512, 1000), 0.0, 0.02, seed=0, tensor_id=1)
+    rq, rs, rz = O.quantize_per_channel(w, False)
+    got = to_np(gh.dequantize(to_dev(rq, torch_dev), to_dev(rs, torch_dev), to_dev(rz, torch_dev)))
+    assert _same_f32(got, O.dequantize(rq, rs, rz))
+
+
+def test_qweight_rowsum(torch_dev):
+    gh = _gh()
+    rng = np.random.default_rng(0)
+    q = rng.integers(-128, 128, size=(300, 777)).astype(np.int8)
+    got = to_np(gh.qweight_rowsum(to_dev(q, torch_dev)))
+    np.testing.assert_array_equal(got, q.astype(np.int64).sum(1).astype(np.int32))
+
+
+def _qlinear_case(torch_dev, m, n, k, x_per_row, with_zp, with_bias, seed=0):
+    gh, O = _gh(), _O()
+    x = gh.normal((m, k), seed=seed, tensor_id=0)
+    w = gh.normal((n, k), 0.0, 0.02, seed=seed, tensor_id=1)
+    bias = gh.uniform((n,), -1 / 64, 1 / 64, seed=seed, tensor_id=2) if with_bias else None
+    qw, sw, _ = O.quantize_per_channel(w, True)
+    if x_per_row:
+        qx, sx, zx = O.quantize_per_channel(x, not with_zp)
+    else:
+        qx, sx, zx = O.quantize_per_tensor(x, not with_zp)
+    zx_arg = np.atleast_1d(zx) if with_zp else None
+    ry, racc = O.qlinear_i8(qx, sx, zx_arg, x_per_row, qw, sw, bias)
+    d = lambda a: None if a is None else to_dev(np.ascontiguousarray(np.atleast_1d(a)), torch_dev)  # noqa: E731
+    y, acc = gh.qlinear(d(qx), d(sx), d(zx_arg), d(qw), d(sw), x_per_row=x_per_row, bias=d(bias),
+                        want_acc=True)
+    np.testing.assert_array_equal(to_np(acc), racc)
+    assert _same_f32(to_np(y), ry)
+    # Within the GEMM bound of the reference composite: dequantize + matmul.
+    dx = O.dequantize(qx.reshape(m, k), np.atleast_1d(sx), np.atleast_1d(zx))
+    dw = O.dequantize(qw, sw, np.zeros(n, np.int8))
+    comp = O.matmul(dx, O.transpose_last2(dw))
+    if bias is not None:
+        comp = comp + bias
+    assert np.abs(to_np(y) - comp).max() <= gemm_tol(k, dx, dw) + 1e-6
+    return x, w
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 48, 64), (5, 48, 64), (16, 1000, 256), (130, 257, 320), (256, 512, 4096)])
+@pytest.mark.parametrize("x_per_row,with_zp", [(False, True), (True, False), (False, False)])
+def test_qlinear_bit_exact(torch_dev, m, n, k, x_per_row, with_zp):
+    _qlinear_case(torch_dev, m, n, k, x_per_row, with_zp, with_bias=(m % 2 == 1))
+
+
+def test_qlinear_unaligned_k(torch_dev):
+    """K not a multiple of 16: the byte-gather load path."""
+    _qlinear_case(torch_dev, 33, 70, 77, False, True, True)
+
+
+def test_qlinear_config3_w11008_sampled(torch_dev):
+    """Config 3: W [11008,4096] ~ N(0,0.02) per-channel symmetric, x [M,4096]
+    per-tensor asymmetric (DynamicQuantization::quantize_activation); int32
+    accumulators of every row checked against an exact fp64 integer GEMM."""
+    gh, O = _gh(), _O()
+    n, k = 11008, 4096
+    w = gh.normal((n, k), 0.0, 0.02, seed=0, tensor_id=1)
+    dw = to_dev(w, torch_dev)
+    qw, sw, zw = gh.quantize_per_channel(dw, True)
+    rqw, rsw, _ = O.quantize_per_channel(w, True)
+    np.testing.assert_array_equal(to_np(qw), rqw)
+    for m in (1, 16, 256):
+        x = gh.normal((m, k), seed=0, tensor_id=0)
+        qx, sx, zx = gh.quantize_per_tensor(to_dev(x, torch_dev), False)
+        rqx, rsx, rzx = O.quantize_per_tensor(x, False)
+        np.testing.assert_array_equal(to_np(qx), rqx)
+        y, acc = gh.qlinear(qx, sx, zx, qw, sw, want_acc=True)
+        exact = (rqx.astype(np.float64) - float(rzx)) @ rqw.astype(np.float64).T
+        np.testing.assert_array_equal(to_np(acc), exact.astype(np.int64).astype(np.int32))
+        rows = np.arange(m) if m <= 16 else np.random.default_rng(m).choice(m, 16, replace=False)
+        ry, _ = O.qlinear_i8(rqx[rows], rsx, np.atleast_1d(rzx), False, rqw, rsw)
+        assert _same_f32(to_np(y)[rows], ry)
+
+
+def test_qlinear_4096_cube_sampled(torch_dev):
+    """The 4096^3 int8 GEMM target shape: sampled rows of the int32
+    accumulators against exact integer products."""
+    gh, O = _gh(), _O()
+    k = 4096
+    x = gh.normal((4096, k), seed=0, tensor_id=0)
+    w = gh.normal((4096, k), 0.0, 0.02, seed=0, tensor_id=1)
+    qx, sx, zx = gh.quantize_per_channel(to_dev(x, torch_dev), True)
+    qw, sw, _ = gh.quantize_per_channel(to_dev(w, torch_dev), True)
+    y, acc = gh.qlinear(qx, sx, None, qw, sw, x_per_row=True, want_acc=True)
+    rows = np.random.default_rng(4).choice(4096, 24, replace=False)
+    hqx, hqw = to_np(qx), to_np(qw)
+    exact = hqx[rows].astype(np.float64) @ hqw.astype(np.float64).T
+    np.testing.assert_array_equal(to_np(acc)[rows], exact.astype(np.int32))
+    ry, _ = O.qlinear_i8(hqx[rows], to_np(sx)[rows], None, True, hqw, to_np(sw))
+    assert _same_f32(to_np(y)[rows], ry)
