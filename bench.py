@@ -1,0 +1,388 @@
+#!/usr/bin/env python3
+"""bench.py -- throughput of GhostFlow's dense hot path on one MI355X.
+
+Headline (the one JSON line on stdout): the fp32 Linear forward
+y = x W^T + b at x [4096, 4096], W [4096, 4096], b [4096] -- the
+configuration BASELINE.json's metric is quoted on (Linear::forward,
+ghostflow-nn/src/linear.rs:56-69, served by gfh_sgemm NT + bias).  One step
+is one Linear forward over that batch, i.e. one sgemm kernel launch, with
+every input already resident in HBM.
+
+The same line carries
+  * "roofline": the sgemm kernel's algorithmic FLOP per launch (2*M*N*K,
+    bias excluded) over its average launch duration, timed with HIP events
+    on the stream the kernel runs on, against the f32 MFMA peak;
+  * "cpu_baseline": the reference CPU path (the oracle's restatement of
+    Linear::forward -> data_f32 gather of W^T + matmul_blocked + broadcast
+    bias add, single-threaded as the reference is) timed on this host on a
+    bounded row sample and extrapolated to the full layer;
+  * "components": the other north-star kernels at their BASELINE shapes
+    (square fp32 GEMM, int8 linear, decode GEMV fp32 / int8, causal SDPA),
+    each with its own roofline fraction.  These are supplementary numbers,
+    not the headline.
+
+Only 1 GPU is supported: --gpus N with N > 1 exits with an error.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "ghost-flow_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "GEMM TFLOPS (fp32) / TOPS (int8) + decode GEMV GB/s, % roofline, 1×MI355X"
+PEAK_F32 = 157.3e12   # dense f32 MFMA, FLOP/s
+PEAK_I8 = 5.0e15      # dense i8 MFMA, OP/s
+PEAK_HBM = 8.0e12     # HBM3E, B/s
+MALL_BYTES = 256 << 20  # Infinity Cache; HBM-bound timings cycle > 2x this
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-components", action="store_true",
+                    help="skip the supplementary per-kernel numbers")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-rows", type=int, default=768,
+                    help="rows of x in the CPU-baseline sample (of 4096)")
+    ap.add_argument("--only", default="",
+                    help="comma list of components to run (sgemm,qlinear,gemv,sdpa); "
+                         "used for focused profiling")
+    ap.add_argument("--detail", default="", help="also write the full result JSON to this file")
+    return ap.parse_args()
+
+
+class Lib:
+    """Direct ctypes calls into libghostflow_hip.so (no per-call Python checks)."""
+
+    def __init__(self):
+        import ghostflow_hip
+        self.L = ghostflow_hip.lib()
+        self.gh = ghostflow_hip
+
+    def check(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what}: status {rc}: {self.L.gfh_last_error().decode()}")
+
+
+def event_time_ms(torch, fn, reps, warmup=3):
+    """Average ms per call of fn() over `reps` back-to-back calls, timed
+    with events on torch's current stream (the stream every call uses)."""
+    for _ in range(warmup):
+        fn(0)
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record()
+    for i in range(reps):
+        fn(i)
+    e.record()
+    e.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+# ---------------------------------------------------------------------------
+# headline: fp32 Linear 4096^3
+# ---------------------------------------------------------------------------
+
+def bench_linear(lib, torch, args):
+    M = N = K = 4096
+    g = lib.gh
+    dev = torch.device("cuda:0")
+    x = torch.from_numpy(g.normal((M, K), seed=0, tensor_id=0)).to(dev)
+    w = torch.from_numpy(g.uniform((N, K), -1 / 64, 1 / 64, seed=0, tensor_id=1)).to(dev)
+    b = torch.from_numpy(g.uniform((N,), -1 / 64, 1 / 64, seed=0, tensor_id=2)).to(dev)
+    y = torch.empty((M, N), dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    L = lib.L
+    xp, wp, bp, yp = x.data_ptr(), w.data_ptr(), b.data_ptr(), y.data_ptr()
+
+    def step():
+        rc = L.gfh_sgemm(0, 1, M, N, K, 1.0, xp, K, wp, K, 0.0, yp, N, bp, stream)
+        if rc:
+            lib.check(rc, "gfh_sgemm")
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(args.steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ev_ms = ev0.elapsed_time(ev1) / args.steps
+    flops = 2.0 * M * N * K
+    # sanity: one sampled output element against a float64 dot product
+    xs = x[17].double().cpu()
+    ws = w[1234].double().cpu()
+    ref = float((xs * ws).sum() + b[1234].double().cpu())
+    got = float(y[17, 1234].cpu())
+    if abs(got - ref) > 1e-3:
+        raise RuntimeError(f"linear sanity check failed: {got} vs {ref}")
+    return {
+        "wall_s": wall,
+        "ms_per_step": wall * 1e3 / args.steps,
+        "kernel_ms": ev_ms,
+        "flops": flops,
+        "value": flops / (wall / args.steps) / 1e12,
+        "achieved": flops / (ev_ms * 1e-3) / 1e12,
+    }
+
+
+def cpu_baseline_linear(rows):
+    """Reference CPU path of Linear::forward at [4096,4096]x[4096,4096]^T,
+    timed on a row sample: the W^T gather (data_f32 of the t() view) is timed
+    once in full, matmul_blocked and the bias add on `rows` rows of x, then
+    scaled to 4096 rows (rows of the output are independent, identical work)."""
+    import numpy as np
+    from ghostflow_hip import synth
+    from oracle import oracle as O
+    M = N = K = 4096
+    L = O.lib()
+    x = synth.normal((rows, K), seed=0, tensor_id=0)
+    w = synth.uniform((N, K), -1 / 64, 1 / 64, seed=0, tensor_id=1)
+    b = synth.uniform((N,), -1 / 64, 1 / 64, seed=0, tensor_id=2)
+    wt = np.empty((K, N), np.float32)
+    t0 = time.perf_counter()
+    L.gfo_transpose_last2(w, wt, 1, N, K)
+    t_gather = time.perf_counter() - t0
+    y = np.empty((rows, N), np.float32)
+    t0 = time.perf_counter()
+    L.gfo_matmul_blocked(x, wt, y, rows, K, N)
+    t_mm = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    L.gfo_add_row_bias(y, b, rows, N)
+    t_bias = time.perf_counter() - t0
+    scale = M / rows
+    t_full = t_gather + (t_mm + t_bias) * scale
+    return {
+        "value": 2.0 * M * N * K / t_full / 1e12,
+        "unit": "TFLOP/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"oracle Linear::forward restatement (gather W^T in full {t_gather:.2f}s; "
+                   f"matmul_blocked + bias on {rows}/4096 rows {t_mm + t_bias:.2f}s), "
+                   f"extrapolated to 4096 rows: {t_full:.1f}s per forward"),
+        "seconds_measured": t_gather + t_mm + t_bias,
+    }
+
+
+# ---------------------------------------------------------------------------
+# supplementary components
+# ---------------------------------------------------------------------------
+
+def comp_sgemm(lib, torch, n):
+    dev = torch.device("cuda:0")
+    a = torch.randn((n, n), device=dev)
+    b = torch.randn((n, n), device=dev)
+    c = torch.empty((n, n), device=dev)
+    s = torch.cuda.current_stream(dev).cuda_stream
+    L = lib.L
+    ap, bp, cp = a.data_ptr(), b.data_ptr(), c.data_ptr()
+
+    def f(_):
+        L.gfh_sgemm(0, 0, n, n, n, 1.0, ap, n, bp, n, 0.0, cp, n, None, s)
+    reps = int(min(200, max(5, 1.0 / (2.0 * n ** 3 / 50e12))))  # about 1 s of GPU time
+    ms = event_time_ms(torch, f, reps)
+    fl = 2.0 * n ** 3
+    return {"name": f"sgemm_nn_{n}", "ms": ms, "value": fl / ms / 1e9, "unit": "TFLOP/s",
+            "frac": fl / ms / 1e9 / (PEAK_F32 / 1e12), "bound": "mfma_f32"}
+
+
+def comp_qlinear(lib, torch, m, n, k, per_tensor=True):
+    dev = torch.device("cuda:0")
+    qx = torch.randint(-128, 128, (m, k), dtype=torch.int8, device=dev)
+    sx = torch.full((1 if per_tensor else m,), 0.02, device=dev)
+    zx = torch.full((1 if per_tensor else m,), -3, dtype=torch.int8, device=dev)
+    # rotate weight copies when the working set would sit in the MALL
+    wbytes = n * k
+    ncopy = max(1, min(16, -(-2 * MALL_BYTES // wbytes))) if m <= 256 else 1
+    qws = [torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev) for _ in range(ncopy)]
+    sw = torch.rand((n,), device=dev) * 1e-3
+    rs = [lib.gh.qweight_rowsum(q) for q in qws]
+    y = torch.empty((m, n), device=dev)
+    s = torch.cuda.current_stream(dev).cuda_stream
+    L = lib.L
+    ptrs = [(q.data_ptr(), r.data_ptr()) for q, r in zip(qws, rs)]
+
+    def f(i):
+        qp, rp = ptrs[i % ncopy]
+        L.gfh_qlinear_i8(qx.data_ptr(), sx.data_ptr(), zx.data_ptr(), 0 if per_tensor else 1, qp,
+                         sw.data_ptr(), rp, None, y.data_ptr(), None, m, n, k, s)
+    ops = 2.0 * m * n * k
+    reps = 200 if ops < 5e10 else 100
+    ms = event_time_ms(torch, f, reps)
+    byts = m * k + n * k + 4 * m * n + 8 * n
+    tops = ops / ms / 1e9
+    gbs = byts / ms / 1e6
+    attain = min(PEAK_I8, ops / byts * PEAK_HBM)
+    return {"name": f"qlinear_i8_m{m}_n{n}_k{k}", "ms": ms, "value": tops, "unit": "TOP/s",
+            "gbps": gbs, "frac": ops / (ms * 1e-3) / attain,
+            "bound": "mfma_i8" if attain == PEAK_I8 else "hbm", "weight_copies": ncopy}
+
+
+def comp_gemv(lib, torch, bsz, int8):
+    dev = torch.device("cuda:0")
+    K, N = 4096, 14336
+    wbytes = K * N * (1 if int8 else 4)
+    ncopy = max(3, -(-2 * MALL_BYTES // wbytes) + 1)
+    x = torch.randn((bsz, K), device=dev)
+    y = torch.empty((bsz, N), device=dev)
+    if int8:
+        ws = [torch.randint(-127, 128, (K, N), dtype=torch.int8, device=dev) for _ in range(ncopy)]
+        sc = torch.rand((K,), device=dev) * 1e-3
+    else:
+        ws = [torch.randn((K, N), device=dev) * 0.02 for _ in range(ncopy)]
+    s = torch.cuda.current_stream(dev).cuda_stream
+    L = lib.L
+    wp = [t.data_ptr() for t in ws]
+    if int8:
+        def f(i):
+            L.gfh_gemv_w8(x.data_ptr(), wp[i % ncopy], sc.data_ptr(), None, y.data_ptr(), bsz, K, N, s)
+    else:
+        def f(i):
+            L.gfh_gemv_f32(x.data_ptr(), wp[i % ncopy], y.data_ptr(), bsz, K, N, s)
+    ms = event_time_ms(torch, f, 300)
+    byts = wbytes + 4 * bsz * K + 4 * bsz * N + (4 * K if int8 else 0)
+    gbs = byts / ms / 1e6
+    del ws
+    return {"name": f"gemv_{'w8' if int8 else 'f32'}_b{bsz}", "ms": ms, "value": gbs, "unit": "GB/s",
+            "frac": gbs * 1e9 / PEAK_HBM, "bound": "hbm", "weight_copies": ncopy}
+
+
+def comp_sdpa(lib, torch, S):
+    dev = torch.device("cuda:0")
+    B, H, D = 4, 32, 128
+    q = torch.randn((B, H, S, D), device=dev)
+    k = torch.randn((B, H, S, D), device=dev)
+    v = torch.randn((B, H, S, D), device=dev)
+    o = torch.empty_like(q)
+    s = torch.cuda.current_stream(dev).cuda_stream
+    L = lib.L
+    scale = float(1.0 / (128.0 ** 0.5))
+
+    def f(_):
+        L.gfh_sdpa_f32(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), None, B, H, S, S, D,
+                       scale, 1, None, 0, s)
+    ms = event_time_ms(torch, f, 50 if S <= 512 else 10)
+    fl = 4.0 * B * H * S * S * D * 0.5
+    return {"name": f"sdpa_causal_b4_h32_s{S}_d128", "ms": ms, "value": fl / ms / 1e9, "unit": "TFLOP/s",
+            "frac": fl / ms / 1e9 / (PEAK_F32 / 1e12), "bound": "mfma_f32"}
+
+
+def run_components(lib, torch, only):
+    want = set(filter(None, only.split(","))) or {"sgemm", "qlinear", "gemv", "sdpa"}
+    out = []
+
+    def add(fn, *a, **kw):
+        try:
+            r = fn(lib, torch, *a, **kw)
+        except Exception as e:  # report, keep going
+            r = {"name": fn.__name__ + repr(a), "error": str(e)}
+        log("  " + json.dumps(r))
+        out.append(r)
+        torch.cuda.empty_cache()
+
+    if "sgemm" in want:
+        for n in (1024, 2048, 4096, 8192):
+            add(comp_sgemm, n)
+    if "qlinear" in want:
+        add(comp_qlinear, 4096, 4096, 4096)
+        for m in (1, 16, 256, 4096):
+            add(comp_qlinear, m, 11008, 4096)
+    if "gemv" in want:
+        for int8 in (False, True):
+            for bsz in (1, 4, 8):
+                add(comp_gemv, bsz, int8)
+    if "sdpa" in want:
+        for S in (512, 2048):
+            add(comp_sdpa, S)
+    return out
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on exactly one GPU; --gpus {args.gpus} is not supported "
+              "(multi-GPU sharding is a design note only)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    lib = Lib()
+    lib.check(lib.L.gfh_init(), "gfh_init")
+    # The timed loops call the C ABI back to back; the per-call pointer
+    # validation (hipPointerGetAttributes / hipMemGetAddressRange) is host
+    # work that a serving loop with known-good buffers switches off.
+    lib.L.gfh_set_pointer_checks(0)
+
+    log(f"bench: fp32 Linear 4096^3, warmup {args.warmup}, steps {args.steps}")
+    h = bench_linear(lib, torch, args)
+    log(f"bench: {h['ms_per_step']:.3f} ms/step, {h['value']:.2f} TFLOP/s "
+        f"(kernel {h['kernel_ms']:.3f} ms, {h['achieved']:.2f} TFLOP/s)")
+
+    components = []
+    if not args.no_components:
+        log("bench: components")
+        components = run_components(lib, torch, args.only)
+
+    cpu = None
+    if not args.no_cpu:
+        log(f"bench: CPU baseline on {args.cpu_rows} rows")
+        cpu = cpu_baseline_linear(args.cpu_rows)
+        log(f"bench: CPU {cpu['value'] * 1e3:.3f} GFLOP/s ({cpu['sample']})")
+
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", "sgemm_linear4096_traffic.json")
+    if os.path.exists(tfile):
+        with open(tfile) as fh:
+            traffic = json.load(fh).get("bytes_per_launch")
+
+    line = {
+        "metric": METRIC,
+        "value": round(h["value"], 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(h["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (counter-based seed-0 generator: x ~ N(0,1), W, b ~ U(-1/64, 1/64))",
+        "config": {"workload": "fp32 Linear forward y = x W^T + b (Linear::forward via gfh_sgemm NT+bias)",
+                   "m": 4096, "k": 4096, "n": 4096, "bias": True, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(h["achieved"], 3), "peak": PEAK_F32 / 1e12,
+                     "unit": "TFLOP/s", "frac": round(h["achieved"] / (PEAK_F32 / 1e12), 4),
+                     "traffic": traffic},
+        "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
+        "components": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in c.items()}
+                       for c in components],
+    }
+    if args.detail:
+        with open(args.detail, "w") as fh:
+            json.dump(line, fh, indent=1)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
