@@ -62,6 +62,9 @@ def parse_args():
                     help="comma list of components to run (sgemm,qlinear,gemv,sdpa); "
                          "used for focused profiling")
     ap.add_argument("--detail", default="", help="also write the full result JSON to this file")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="only run a plain 1 GiB device-to-device copy `steps` times (the known-size "
+                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
     return ap.parse_args()
 
 
@@ -317,6 +320,21 @@ def run_components(lib, torch, only):
     return out
 
 
+def calib_copy(torch, steps):
+    """A plain copy of 1 GiB: reads 2^30 bytes and writes 2^30 bytes per
+    launch, so its FETCH_SIZE / WRITE_SIZE per dispatch give the counters'
+    scale factors."""
+    dev = torch.device("cuda:0")
+    nbytes = 1 << 30
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calib_copy_bytes_read": nbytes, "calib_copy_bytes_written": nbytes,
+                      "launches": steps}), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -327,6 +345,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.calib_copy:
+        calib_copy(torch, args.steps)
+        return
     lib = Lib()
     lib.check(lib.L.gfh_init(), "gfh_init")
     # The timed loops call the C ABI back to back; the per-call pointer
@@ -350,11 +371,16 @@ def main():
         cpu = cpu_baseline_linear(args.cpu_rows)
         log(f"bench: CPU {cpu['value'] * 1e3:.3f} GFLOP/s ({cpu['sample']})")
 
+    # HBM bytes per launch of the Linear kernel, measured with rocprofv3
+    # FETCH_SIZE / WRITE_SIZE and scaled by a plain copy of known size; the
+    # summary (with its commands) lives beside the other profiles.
     traffic = None
-    tfile = os.path.join(ROOT, "profiles", "sgemm_linear4096_traffic.json")
+    tfile = os.path.join(ROOT, "profiles", "sgemm_linear4096_traffic.md")
     if os.path.exists(tfile):
         with open(tfile) as fh:
-            traffic = json.load(fh).get("bytes_per_launch")
+            for ln in fh:
+                if ln.startswith("bytes_per_launch:"):
+                    traffic = int(ln.split(":", 1)[1])
 
     line = {
         "metric": METRIC,
