@@ -199,6 +199,202 @@ __global__ __launch_bounds__(kThreads) void qlinear_mfma_kernel(QParams p) {
     }
 }
 
+
+// ---- large tiles: 256 x 256 per workgroup, direct-to-LDS loads -------------------
+//
+// For M >= 1024 (compute-bound) each workgroup owns a 256 x 256 output tile
+// and each of its 4 waves a 128 x 128 sub-tile: 4 x 4 v_mfma_i32_32x32x32_i8
+// accumulators (256 registers per lane), so every 16-byte LDS fragment
+// feeds 4 MFMAs and the LDS read rate stays at half the MFMA rate.
+// Operands stream through a 4-deep ring of BK = 64 byte stages filled with
+// global_load_lds_dwordx4 (global memory straight into LDS, no VGPR
+// staging).  Rows of a stage are 64 bytes = 4 chunks of 16; chunk c of row
+// r is stored at position c ^ swz(r), which spreads the 16-byte fragment
+// reads of 8 (or 16) consecutive rows over distinct banks.  Each lane of a
+// load instruction fetches the chunk that lands at its own LDS slot, so the
+// swizzle costs nothing on the load side.  Rows past M / N are clamped to
+// the last row (their products are never stored); K must be a multiple of 64.
+namespace big {
+
+constexpr int kBM = 256, kBN = 256, kBK = 64, kStages = 4;
+constexpr int kStageBytes = kBM * kBK;  // one operand, one stage (16 KB)
+constexpr int kGroupM = 4;
+
+typedef __attribute__((address_space(3))) void *lds_ptr;
+typedef __attribute__((address_space(1))) void *glb_ptr;
+
+__device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
+// s_waitcnt with only vmcnt constrained (expcnt / lgkmcnt left at maximum).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Waits until at most 8 * n of this wave's stage loads are in flight.
+__device__ __forceinline__ void wait_stages(int n) {
+    if (n >= 3)
+        wait_vmcnt<24>();
+    else if (n == 2)
+        wait_vmcnt<16>();
+    else if (n == 1)
+        wait_vmcnt<8>();
+    else
+        wait_vmcnt<0>();
+}
+
+template <bool X_PER_ROW, bool WANT_ACC>
+__global__ __launch_bounds__(kThreads, 1) void qlinear_tile256_kernel(QParams p) {
+    __shared__ __attribute__((aligned(1024))) int8_t lds[kStages * 2 * kStageBytes];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm0 = (wave >> 1) * 128;
+    const int wn0 = (wave & 1) * 128;
+
+    const int nblk = p.tiles_m * p.tiles_n;
+    int bid = blockIdx.x;
+    if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+    const int group_size = kGroupM * p.tiles_n;
+    const int group = bid / group_size;
+    const int first_m = group * kGroupM;
+    const int gm = min(p.tiles_m - first_m, kGroupM);
+    const int in_group = bid - group * group_size;
+    const int64_t m0 = (int64_t)(first_m + in_group % gm) * kBM;
+    const int64_t n0 = (int64_t)(in_group / gm) * kBN;
+
+    // Per-lane source addresses of this wave's 4 A and 4 B load
+    // instructions: instruction j covers tile rows wave*64 + 16j .. +15;
+    // lane l fills LDS slot l of that 1 KB run (row l/4, physical chunk l%4).
+    const int8_t *a_src[4];
+    const int8_t *b_src[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int r = wave * 64 + j * 16 + (lane >> 2);
+        const int c = (lane & 3) ^ swz(r);
+        a_src[j] = p.qx + min(m0 + r, p.m - 1) * p.k + c * 16;
+        b_src[j] = p.qw + min(n0 + r, p.n - 1) * p.k + c * 16;
+    }
+    const int nk = (int)(p.k / kBK);
+
+    auto issue = [&](int t) {
+        int8_t *la = lds + (t % kStages) * 2 * kStageBytes + wave * 64 * kBK;
+        int8_t *lb = la + kStageBytes;
+        const int64_t k0 = (int64_t)t * kBK;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            __builtin_amdgcn_global_load_lds((glb_ptr)(a_src[j] + k0), (lds_ptr)(la + j * 16 * kBK), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((glb_ptr)(b_src[j] + k0), (lds_ptr)(lb + j * 16 * kBK), 16, 0, 0);
+        }
+    };
+
+    // Fragment address inside a stage: lane l reads row l%32 of a 32-row
+    // block, logical chunk 2*ks + l/32.
+    const int frow = lane & 31;
+    const int foff0 = frow * kBK + (((lane >> 5) ^ swz(frow)) * 16);
+    const int foff1 = frow * kBK + (((2 + (lane >> 5)) ^ swz(frow)) * 16);
+
+    i32x4 af[2][4], bf[2][4];
+    auto load_frags = [&](int buf, int t, int ks) {
+        const int8_t *la = lds + (t % kStages) * 2 * kStageBytes;
+        const int8_t *lb = la + kStageBytes;
+        const int fo = ks ? foff1 : foff0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) af[buf][i] = *reinterpret_cast<const i32x4 *>(la + (wm0 + i * 32) * kBK + fo);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bf[buf][j] = *reinterpret_cast<const i32x4 *>(lb + (wn0 + j * 32) * kBK + fo);
+    };
+
+    i32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+    auto mfmas = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[buf][i], bf[buf][j], acc[i][j], 0, 0, 0);
+    };
+
+    // Ring of 4 stages, all in flight at once: stage t+4 is issued into
+    // stage t's buffer as soon as every wave holds stage t's fragments.
+    const int pre = min(kStages, nk);
+    for (int t = 0; t < pre; ++t) issue(t);
+    wait_stages(pre - 1);
+    __builtin_amdgcn_s_barrier();
+    load_frags(0, 0, 0);
+
+    for (int t = 0; t < nk; ++t) {
+        load_frags(1, t, 1);
+        mfmas(0);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_lgkm0();  // this wave's reads of stage t are done
+        if (t + 1 < nk) {
+            // stage t+1 landed: stages t+2, t+3 may still be in flight
+            wait_stages(min(2, nk - t - 2));
+            __builtin_amdgcn_s_barrier();
+            if (t + kStages < nk) issue(t + kStages);
+            load_frags(0, t + 1, 0);
+        }
+        mfmas(1);
+    }
+
+    // Epilogue: lane l, register r of block (i, j) holds
+    // row 8*(r/4) + 4*(l/32) + r%4, column l%32 of that 32 x 32 block.
+    // Per-tensor activation parameters are uniform; per-row ones are read
+    // once per row.
+    const bool full = (m0 + kBM <= p.m) && (n0 + kBN <= p.n);
+    const int64_t ldo = p.n;
+    const int zx0 = (!X_PER_ROW && p.zx) ? (int)p.zx[0] : 0;
+    const float sx0 = (!X_PER_ROW && p.y) ? p.sx[0] : 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t col = n0 + wn0 + j * 32 + (lane & 31);
+        const bool col_ok = col < p.n;
+        const int64_t colc = col_ok ? col : p.n - 1;
+        const int32_t rs = p.zx ? p.rowsum[colc] : 0;
+        const float swc = p.y ? p.sw[colc] : 0.f;
+        const float bc = p.bias ? p.bias[colc] : 0.f;
+        const float sc0 = sx0 * swc;
+        const int32_t zr0 = zx0 * rs;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t rowb = m0 + wm0 + i * 32 + 4 * (lane >> 5);
+            const int64_t ob = rowb * ldo + col;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int ro = 8 * (r >> 2) + (r & 3);
+                if (!full && (!col_ok || rowb + ro >= p.m)) continue;
+                int32_t a = acc[i][j][r];
+                float sc = sc0;
+                if (X_PER_ROW) {
+                    const int64_t row = rowb + ro;
+                    if (p.zx) a = (int32_t)((uint32_t)a - (uint32_t)((int32_t)p.zx[row] * rs));
+                    if (p.y) sc = p.sx[row] * swc;
+                } else {
+                    a = (int32_t)((uint32_t)a - (uint32_t)zr0);
+                }
+                if (WANT_ACC) p.acc[ob + ro * ldo] = a;
+                if (p.y) {
+                    float v = (float)a * sc;
+                    if (p.bias) v = v + bc;
+                    p.y[ob + ro * ldo] = v;
+                }
+            }
+        }
+    }
+}
+
+}  // namespace big
+
 }  // namespace
 
 int launch_qlinear_i8(const QLinearDesc &d, hipStream_t s) {
@@ -216,6 +412,23 @@ int launch_qlinear_i8(const QLinearDesc &d, hipStream_t s) {
     p.n = d.n;
     p.k = d.k;
     p.x_per_row = d.x_per_row ? 1 : 0;
+    if (d.m >= 1024 && d.k % big::kBK == 0 && d.k > 0 && aligned16(d.qx) && aligned16(d.qw)) {
+        p.tiles_m = (int)((d.m + big::kBM - 1) / big::kBM);
+        p.tiles_n = (int)((d.n + big::kBN - 1) / big::kBN);
+        const dim3 grid((unsigned)(p.tiles_m * p.tiles_n));
+        if (d.x_per_row) {
+            if (d.acc)
+                hipLaunchKernelGGL((big::qlinear_tile256_kernel<true, true>), grid, dim3(kThreads), 0, s, p);
+            else
+                hipLaunchKernelGGL((big::qlinear_tile256_kernel<true, false>), grid, dim3(kThreads), 0, s, p);
+        } else {
+            if (d.acc)
+                hipLaunchKernelGGL((big::qlinear_tile256_kernel<false, true>), grid, dim3(kThreads), 0, s, p);
+            else
+                hipLaunchKernelGGL((big::qlinear_tile256_kernel<false, false>), grid, dim3(kThreads), 0, s, p);
+        }
+        return check_launch("qlinear_i8");
+    }
     p.tiles_m = (int)((d.m + kBM - 1) / kBM);
     p.tiles_n = (int)((d.n + kBN - 1) / kBN);
     const bool vec = (d.k % 16 == 0) && aligned16(d.qx) && aligned16(d.qw);

@@ -217,3 +217,35 @@ def test_qlinear_4096_cube_sampled(torch_dev):
     np.testing.assert_array_equal(to_np(acc)[rows], exact.astype(np.int32))
     ry, _ = O.qlinear_i8(hqx[rows], to_np(sx)[rows], None, True, hqw, to_np(sw))
     assert _same_f32(to_np(y)[rows], ry)
+
+
+@pytest.mark.parametrize("m,n,k", [(1024, 256, 64), (1030, 300, 128), (1300, 777, 320), (2048, 384, 1024)])
+@pytest.mark.parametrize("x_per_row,with_zp", [(False, True), (True, False), (True, True)])
+def test_qlinear_large_tile_bit_exact(torch_dev, m, n, k, x_per_row, with_zp):
+    """M >= 1024 with K % 64 == 0 takes the 256 x 256 tile kernel: ragged
+    edge tiles in M and N, every activation-scale variant, int32
+    accumulators and fp32 outputs bit-exact to the oracle."""
+    _qlinear_case(torch_dev, m, n, k, x_per_row, with_zp, with_bias=(n % 2 == 1 or x_per_row))
+
+
+@pytest.mark.parametrize("x_per_row", [False, True])
+def test_qlinear_large_tile_y_only(torch_dev, x_per_row):
+    """The output-only variant (no int32 accumulator buffer) of the large
+    tile kernel equals the oracle bit for bit."""
+    gh, O = _gh(), _O()
+    m, n, k = 1280, 520, 256
+    x = gh.normal((m, k), seed=9, tensor_id=0)
+    w = gh.normal((n, k), 0.0, 0.02, seed=9, tensor_id=1)
+    bias = gh.uniform((n,), -0.1, 0.1, seed=9, tensor_id=2)
+    qw, sw, _ = O.quantize_per_channel(w, True)
+    if x_per_row:
+        qx, sx, zx = O.quantize_per_channel(x, False)
+    else:
+        qx, sx, zx = O.quantize_per_tensor(x, False)
+    sx, zx = np.atleast_1d(sx), np.atleast_1d(zx)
+    ry, _ = O.qlinear_i8(qx, sx, zx, x_per_row, qw, sw, bias)
+    y, acc = gh.qlinear(to_dev(qx, torch_dev), to_dev(sx, torch_dev), to_dev(zx, torch_dev),
+                        to_dev(qw, torch_dev), to_dev(sw, torch_dev), x_per_row=x_per_row,
+                        bias=to_dev(bias, torch_dev), want_acc=False)
+    assert acc is None
+    assert _same_f32(to_np(y), ry)
