@@ -210,7 +210,7 @@ __global__ __launch_bounds__(kThreads) void qlinear_mfma_kernel(QParams p) {
 // global_load_lds_dwordx4 (global memory straight into LDS, no VGPR
 // staging).  Rows of a stage are 64 bytes = 4 chunks of 16; chunk c of row
 // r is stored at position c ^ swz(r), which spreads the 16-byte fragment
-// reads of 8 (or 16) consecutive rows over distinct banks.  Each lane of a
+// reads over distinct banks.  Each lane of a
 // load instruction fetches the chunk that lands at its own LDS slot, so the
 // swizzle costs nothing on the load side.  Rows past M / N are clamped to
 // the last row (their products are never stored); K must be a multiple of 64.
@@ -219,11 +219,19 @@ namespace big {
 constexpr int kBM = 256, kBN = 256, kBK = 64, kStages = 4;
 constexpr int kStageBytes = kBM * kBK;  // one operand, one stage (16 KB)
 constexpr int kGroupM = 4;
+constexpr int kOutStride = 136;  // floats per row of a wave's output staging area
+constexpr int kLdsBytes = (kStages * 2 * kStageBytes > 4 * 64 * kOutStride * 4) ? kStages * 2 * kStageBytes
+                                                                                 : 4 * 64 * kOutStride * 4;
 
 typedef __attribute__((address_space(3))) void *lds_ptr;
 typedef __attribute__((address_space(1))) void *glb_ptr;
 
-__device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+// Chunk swizzle of a 64-byte row.  A wave's fragment read has lanes 0-31 on
+// rows 0-31 of a block at one logical chunk (lanes 32-63 at the next); with
+// chunk ^ ((row >> 2) & 3) those 16-byte reads are conflict-free on gfx950's
+// 64-bank LDS (measured: 4.3 clk per ds_read_b128 per CU, against 8.3 for
+// chunk ^ ((row >> 1) ^ (row >> 3)) & 3 and 15.8 unswizzled).
+__device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
 
 // s_waitcnt with only vmcnt constrained (expcnt / lgkmcnt left at maximum).
 template <int N>
@@ -247,7 +255,7 @@ __device__ __forceinline__ void wait_stages(int n) {
 
 template <bool X_PER_ROW, bool WANT_ACC>
 __global__ __launch_bounds__(kThreads, 1) void qlinear_tile256_kernel(QParams p) {
-    __shared__ __attribute__((aligned(1024))) int8_t lds[kStages * 2 * kStageBytes];
+    __shared__ __attribute__((aligned(1024))) int8_t lds[kLdsBytes];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -351,43 +359,94 @@ __global__ __launch_bounds__(kThreads, 1) void qlinear_tile256_kernel(QParams p)
     // row 8*(r/4) + 4*(l/32) + r%4, column l%32 of that 32 x 32 block.
     // Per-tensor activation parameters are uniform; per-row ones are read
     // once per row.
-    const bool full = (m0 + kBM <= p.m) && (n0 + kBN <= p.n);
-    const int64_t ldo = p.n;
     const int zx0 = (!X_PER_ROW && p.zx) ? (int)p.zx[0] : 0;
     const float sx0 = (!X_PER_ROW && p.y) ? p.sx[0] : 0.f;
+    int32_t rs[4];
+    float swc[4], bc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int64_t col = n0 + wn0 + j * 32 + (lane & 31);
-        const bool col_ok = col < p.n;
-        const int64_t colc = col_ok ? col : p.n - 1;
-        const int32_t rs = p.zx ? p.rowsum[colc] : 0;
-        const float swc = p.y ? p.sw[colc] : 0.f;
-        const float bc = p.bias ? p.bias[colc] : 0.f;
-        const float sc0 = sx0 * swc;
-        const int32_t zr0 = zx0 * rs;
+        const int64_t col = min(n0 + wn0 + j * 32 + (lane & 31), p.n - 1);
+        rs[j] = p.zx ? p.rowsum[col] : 0;
+        swc[j] = p.y ? p.sw[col] : 0.f;
+        bc[j] = p.bias ? p.bias[col] : 0.f;
+    }
+    // The dequantized value of accumulator register r of block (i, j), and
+    // its exact int32 accumulator (zero-point term removed).
+    auto finish = [&](int i, int j, int r, int32_t &a) -> float {
+        a = acc[i][j][r];
+        float sc;
+        if (X_PER_ROW) {
+            const int64_t row = min(m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), p.m - 1);
+            if (p.zx) a = (int32_t)((uint32_t)a - (uint32_t)((int32_t)p.zx[row] * rs[j]));
+            sc = p.y ? p.sx[row] * swc[j] : 0.f;
+        } else {
+            a = (int32_t)((uint32_t)a - (uint32_t)(zx0 * rs[j]));
+            sc = sx0 * swc[j];
+        }
+        float v = (float)a * sc;
+        if (p.bias) v = v + bc[j];
+        return v;
+    };
+
+    if (WANT_ACC) {
+        // Parity/debug variant: int32 accumulators and outputs stored
+        // straight from registers.
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int64_t rowb = m0 + wm0 + i * 32 + 4 * (lane >> 5);
-            const int64_t ob = rowb * ldo + col;
+        for (int j = 0; j < 4; ++j) {
+            const int64_t col = n0 + wn0 + j * 32 + (lane & 31);
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int ro = 8 * (r >> 2) + (r & 3);
-                if (!full && (!col_ok || rowb + ro >= p.m)) continue;
-                int32_t a = acc[i][j][r];
-                float sc = sc0;
-                if (X_PER_ROW) {
-                    const int64_t row = rowb + ro;
-                    if (p.zx) a = (int32_t)((uint32_t)a - (uint32_t)((int32_t)p.zx[row] * rs));
-                    if (p.y) sc = p.sx[row] * swc;
-                } else {
-                    a = (int32_t)((uint32_t)a - (uint32_t)zr0);
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int64_t row = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    int32_t a;
+                    const float v = finish(i, j, r, a);
+                    if (col < p.n && row < p.m) {
+                        p.acc[row * p.n + col] = a;
+                        if (p.y) p.y[row * p.n + col] = v;
+                    }
                 }
-                if (WANT_ACC) p.acc[ob + ro * ldo] = a;
-                if (p.y) {
-                    float v = (float)a * sc;
-                    if (p.bias) v = v + bc;
-                    p.y[ob + ro * ldo] = v;
+        }
+        return;
+    }
+
+    // Output tile through LDS: each wave converts 64 rows x 128 columns at a
+    // time into its own region (row stride 136 floats keeps the two row
+    // groups of one ds_write_b32 on disjoint banks), then writes whole
+    // 512-byte row runs with 16-byte stores.
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();  // every wave is done with the operand ring
+    float *lt = reinterpret_cast<float *>(lds) + wave * (64 * kOutStride);
+    const bool vec_out = (p.n % 4) == 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    int32_t a;
+                    const float v = finish(2 * h + ii, j, r, a);
+                    const int lr = ii * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    lt[lr * kOutStride + j * 32 + (lane & 31)] = v;
                 }
+        // each read covers 2 rows x 128 columns: lane l -> row 2q + l/32,
+        // columns 4*(l%32) .. +3
+        const int64_t col = n0 + wn0 + 4 * (lane & 31);
+#pragma unroll
+        for (int q = 0; q < 32; ++q) {
+            const int lr = 2 * q + (lane >> 5);
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(lt + lr * kOutStride + 4 * (lane & 31));
+            const int64_t row = m0 + wm0 + h * 64 + lr;
+            if (row >= p.m) continue;
+            float *dst = p.y + row * p.n + col;
+            if (vec_out && col + 3 < p.n) {
+                *reinterpret_cast<f32x4 *>(dst) = v;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (col + e < p.n) dst[e] = v[e];
             }
         }
     }
