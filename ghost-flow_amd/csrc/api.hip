@@ -122,7 +122,12 @@ GFH_API int gfh_init(void) {
     return guarded([]() -> int { return ensure_init(); });
 }
 
-GFH_API int gfh_shutdown(void) { return GFH_SUCCESS; }
+GFH_API int gfh_shutdown(void) {
+    return guarded([]() -> int {
+        release_stream_state();
+        return GFH_SUCCESS;
+    });
+}
 
 GFH_API const char *gfh_last_error(void) { return last_error(); }
 

@@ -5,8 +5,11 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
+#include <utility>
+#include <vector>
 
 namespace gfh {
 
@@ -50,7 +53,11 @@ int ensure_init() {
             return;
         }
         int dev = 0;
-        hipGetDevice(&dev);
+        if (hipGetDevice(&dev) != hipSuccess) {
+            g_init_status = GFH_COMPUTATION_FAILED;
+            g_init_message = "hipGetDevice failed";
+            return;
+        }
         hipDeviceProp_t prop;
         if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {
             g_init_status = GFH_COMPUTATION_FAILED;
@@ -139,6 +146,85 @@ int Scratch::acquire(void *user, size_t user_bytes, size_t need, hipStream_t s) 
     owned_ = true;
     s_ = s;
     return GFH_SUCCESS;
+}
+
+namespace {
+struct StreamState {
+    int *counters = nullptr;
+    size_t ncounters = 0;
+    void *ws = nullptr;
+    size_t ws_bytes = 0;
+};
+std::mutex g_state_mu;
+std::map<std::pair<int, hipStream_t>, StreamState> g_states;
+std::vector<void *> g_retired;  // outgrown buffers (maybe still in use by queued work), freed at shutdown
+
+int current_state(hipStream_t s, StreamState **out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return set_error(GFH_COMPUTATION_FAILED, "hipGetDevice failed");
+    }
+    *out = &g_states[std::make_pair(dev, s)];
+    return GFH_SUCCESS;
+}
+}  // namespace
+
+int stream_counters(hipStream_t s, size_t count, int **out) {
+    std::lock_guard<std::mutex> lock(g_state_mu);
+    StreamState *st = nullptr;
+    GFH_TRY(current_state(s, &st));
+    if (st->ncounters < count) {
+        size_t want = 4096;
+        while (want < count) want *= 2;
+        int *p = nullptr;
+        hipError_t e = hipMallocAsync(reinterpret_cast<void **>(&p), want * sizeof(int), s);
+        if (e == hipSuccess) e = hipMemsetAsync(p, 0, want * sizeof(int), s);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            return set_error(GFH_ALLOCATION_FAILED, "counter buffer allocation failed: %s", hipGetErrorString(e));
+        }
+        if (st->counters) g_retired.push_back(st->counters);
+        st->counters = p;
+        st->ncounters = want;
+    }
+    *out = st->counters;
+    return GFH_SUCCESS;
+}
+
+int stream_workspace(hipStream_t s, size_t bytes, void **out) {
+    std::lock_guard<std::mutex> lock(g_state_mu);
+    StreamState *st = nullptr;
+    GFH_TRY(current_state(s, &st));
+    if (st->ws_bytes < bytes) {
+        size_t want = (size_t)1 << 20;
+        while (want < bytes) want *= 2;
+        void *p = nullptr;
+        hipError_t e = hipMallocAsync(&p, want, s);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            return set_error(GFH_ALLOCATION_FAILED, "workspace allocation (%zu bytes) failed: %s", want,
+                             hipGetErrorString(e));
+        }
+        if (st->ws) g_retired.push_back(st->ws);
+        st->ws = p;
+        st->ws_bytes = want;
+    }
+    *out = st->ws;
+    return GFH_SUCCESS;
+}
+
+void release_stream_state() {
+    std::lock_guard<std::mutex> lock(g_state_mu);
+    if (g_states.empty() && g_retired.empty()) return;
+    (void)hipDeviceSynchronize();
+    for (auto &kv : g_states) {
+        if (kv.second.counters) (void)hipFree(kv.second.counters);
+        if (kv.second.ws) (void)hipFree(kv.second.ws);
+    }
+    for (void *p : g_retired) (void)hipFree(p);
+    g_states.clear();
+    g_retired.clear();
 }
 
 int set_pointer_checks(int enabled) {

@@ -54,6 +54,19 @@ class Scratch {
 
 inline hipStream_t as_stream(gfh_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Per (device, stream) device state owned by the library, reused by every
+// call on that stream (calls on one stream are serialized by the stream, so
+// they can share it; other streams get their own):
+//  * int32 counters that are all zero whenever no kernel of the stream is
+//    running -- a kernel that counts arrivals in them must leave every
+//    counter it used at 0;
+//  * a scratch buffer for partial results.
+// Both are allocated (and the counters zeroed) stream-ordered on first use,
+// grow on demand, and are released at shutdown.
+int stream_counters(hipStream_t s, size_t count, int **out);
+int stream_workspace(hipStream_t s, size_t bytes, void **out);
+void release_stream_state();
+
 }  // namespace gfh
 
 // Propagate a non-zero status.

@@ -93,3 +93,29 @@ def test_gemv_w8_without_zero_points(torch_dev):
     x = rng.integers(-4, 5, size=(3, 200)).astype(np.float32)
     got = to_np(gh.gemv_w8(to_dev(x, torch_dev), to_dev(q, torch_dev), to_dev(s, torch_dev)))
     np.testing.assert_array_equal(got, O.matmul(x, O.dequantize(q, s, np.zeros(200, np.int8))))
+
+
+def test_split_k_counters_reset_across_calls_and_streams(torch_dev):
+    """K is split over workgroups for the int8 GEMV; the last workgroup of
+    each strip sums the slices and returns its arrival counter to zero.
+    Repeated calls on the default stream and on a second stream must give
+    identical (deterministic) results."""
+    import torch
+    gh = _gh()
+    b, k, n = 3, 4096, 2048 + 96
+    x = gh.normal((b, k), seed=12, tensor_id=0)
+    w = gh.normal((k, n), 0.0, 0.02, seed=12, tensor_id=1)
+    O = _O()
+    qw, s, z = O.quantize_per_channel(w, False)
+    dx, dq, ds, dz = (to_dev(a, torch_dev) for a in (x, qw, s, z))
+    first = to_np(gh.gemv_w8(dx, dq, ds, dz))
+    ref = O.matmul(x, O.dequantize(qw, s, z))
+    assert np.abs(first - ref).max() <= gemm_tol(k, x, np.abs(w).max() * 1.01)
+    for _ in range(3):
+        np.testing.assert_array_equal(to_np(gh.gemv_w8(dx, dq, ds, dz)), first)
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            y2 = gh.gemv_w8(dx, dq, ds, dz)
+    side.synchronize()
+    np.testing.assert_array_equal(to_np(y2), first)
