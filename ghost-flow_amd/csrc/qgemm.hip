@@ -20,6 +20,8 @@
 // (the integer sum is exact in any order).  Two LDS stages, global loads for
 // stage t+1 issued before the MFMAs of stage t, one barrier per stage, and
 // the same XCD-contiguous / GROUP_M tile order as the fp32 GEMM.
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -454,6 +456,200 @@ __global__ __launch_bounds__(kThreads, 1) void qlinear_tile256_kernel(QParams p)
 
 }  // namespace big
 
+
+// ---- skinny M (decode): weights streamed from HBM straight into MFMA ----------
+//
+// For M <= 64 the layer is HBM-bound (the weight is read once, 45 MB at the
+// BASELINE shape).  W [N, K] is K-contiguous, which is exactly the per-lane
+// operand layout of v_mfma_i32_16x16x64_i8 (lane l: row / column l % 16,
+// 16 consecutive k bytes), so weight fragments are plain 16-byte global
+// loads straight into registers, and so are the fragments of x (at most
+// 64 x K bytes, cache-resident).
+//  * A workgroup owns 16 output columns; its 4 waves split the K range
+//    four ways and their exact int32 accumulators are added through LDS at
+//    the end, so the waves never wait for one another.
+//  * One weight load instruction covers 16 rows x 64 contiguous bytes;
+//    kU k-steps per lane are in flight (512 contiguous bytes per row).
+//  * With fewer than ~512 column blocks, K is also split over workgroups:
+//    each publishes its int32 partial tile with agent-scope stores and
+//    counts its arrival; the last one of the column block sums the slices
+//    (integer, so exact in any order) and runs the dequantizing epilogue.
+namespace skinny {
+
+constexpr int kCols = 16;  // output columns per workgroup
+constexpr int kWaves = kThreads / 64;
+constexpr int kU = 8;
+
+struct SkParams {
+    QParams q;
+    int64_t kslice, slices, nblk;
+    int32_t *part;  // [slices][m][n] partial accumulators (slices > 1)
+    int *counters;  // one per column block, zero at rest (slices > 1)
+};
+
+template <int MB>
+__global__ __launch_bounds__(kThreads) void qlinear_skinny_kernel(SkParams sp) {
+    const QParams &p = sp.q;
+    __shared__ i32x4 red[kWaves - 1][MB][64];
+    __shared__ int last_flag;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t blk = blockIdx.x % sp.nblk, slice = blockIdx.x / sp.nblk;
+    const int64_t n0 = blk * kCols;
+    // This wave's k-steps (64 bytes each) inside the slice.
+    const int64_t k_lo = slice * sp.kslice;
+    const int kl = (int)min(sp.kslice, p.k - k_lo);  // a multiple of 16
+    const int nsteps = (kl + 63) / 64;
+    const int per = (nsteps + kWaves - 1) / kWaves;
+    const int st0 = min(wave * per, nsteps), st1 = min(st0 + per, nsteps);
+
+    // Fragment sources: lane l -> weight row n0 + l % 16 (clamped; such
+    // columns are never stored) / x row l % 16 + 16 mb, bytes 16 * (l / 16)
+    // of each 64-byte k-step.
+    const int kb = 16 * (lane >> 4);
+    const int8_t *wsrc = p.qw + min(n0 + (lane & 15), p.n - 1) * p.k + k_lo + kb;
+    const int8_t *xsrc = p.qx + k_lo + kb;
+
+    i32x4 acc[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = i32x4{0, 0, 0, 0};
+    for (int s0 = st0; s0 < st1; s0 += kU) {
+        i32x4 w[kU], xf[kU][MB];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            const int off = (s0 + u) * 64;
+            const bool ok = s0 + u < st1 && off + kb < kl;
+            w[u] = ok ? *reinterpret_cast<const i32x4 *>(wsrc + off) : i32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                const int64_t row = mb * 16 + (lane & 15);
+                xf[u][mb] = (ok && row < p.m) ? *reinterpret_cast<const i32x4 *>(xsrc + row * p.k + off)
+                                              : i32x4{0, 0, 0, 0};
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u)
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+                acc[mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xf[u][mb], w[u], acc[mb], 0, 0, 0);
+    }
+
+    // Add the four waves' accumulators (exact int32) in wave 0.
+    if (wave > 0) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) red[wave - 1][mb][lane] = acc[mb];
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int w2 = 0; w2 < kWaves - 1; ++w2) acc[mb] += red[w2][mb][lane];
+
+    // 16x16 accumulator layout: lane l, register r -> row 4 * (l / 16) + r,
+    // column l % 16 of the block.
+    const int64_t col = n0 + (lane & 15);
+    const bool col_ok = col < p.n;
+    auto row_of = [&](int mb, int r) -> int64_t { return (int64_t)mb * 16 + 4 * (lane >> 4) + r; };
+    auto epilogue = [&](int64_t row, int32_t raw) {
+        const int64_t g = p.x_per_row ? row : 0;
+        int32_t a = raw;
+        if (p.zx) a = (int32_t)((uint32_t)a - (uint32_t)((int32_t)p.zx[g] * p.rowsum[col]));
+        if (p.acc) p.acc[row * p.n + col] = a;
+        if (p.y) {
+            const float sc = p.sx[g] * p.sw[col];
+            float v = (float)a * sc;
+            if (p.bias) v = v + p.bias[col];
+            p.y[row * p.n + col] = v;
+        }
+    };
+
+    if (sp.slices == 1) {
+        if (!col_ok) return;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t row = row_of(mb, r);
+                if (row < p.m) epilogue(row, acc[mb][r]);
+            }
+        return;
+    }
+
+    // Publish the partial tile with agent-scope stores (they go to the
+    // device coherence point, so no cache writeback is needed), wait for
+    // them to complete, then count this workgroup's arrival (wave 0 only).
+    if (col_ok) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t row = row_of(mb, r);
+                if (row < p.m)
+                    __hip_atomic_store(sp.part + (slice * p.m + row) * p.n + col, acc[mb][r], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            }
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    int last = 0;
+    if (lane == 0)
+        last = __hip_atomic_fetch_add(sp.counters + blk, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               (int)sp.slices - 1;
+    last = __shfl(last, 0);
+    if (!last) return;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (col_ok) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t row = row_of(mb, r);
+                if (row >= p.m) continue;
+                const int32_t *src = sp.part + row * p.n + col;
+                // integer sum: exact whatever the order; wrapping as int32
+                uint32_t a = 0;
+                for (int64_t j = 0; j < sp.slices; ++j)
+                    a += (uint32_t)__hip_atomic_load(src + j * p.m * p.n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                epilogue(row, (int32_t)a);
+            }
+    }
+    if (lane == 0) __hip_atomic_store(sp.counters + blk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// K bytes per workgroup: all of K when there are at least ~512 column
+// blocks, otherwise enough slices for ~512 workgroups, each at least 1024
+// bytes (4 waves x 4 k-steps), a multiple of 64.
+int64_t choose_kslice(int64_t nblk, int64_t k) {
+    int64_t s = (512 + nblk - 1) / nblk;
+    s = std::max<int64_t>(1, std::min<int64_t>(s, k / 1024));
+    int64_t ks = (k + s - 1) / s;
+    return (ks + 63) & ~(int64_t)63;
+}
+
+int launch(const QParams &p, hipStream_t s) {
+    SkParams sp{};
+    sp.q = p;
+    sp.nblk = (p.n + kCols - 1) / kCols;
+    sp.kslice = choose_kslice(sp.nblk, p.k);
+    sp.slices = (p.k + sp.kslice - 1) / sp.kslice;
+    if (sp.slices > 1) {
+        void *ws = nullptr;
+        GFH_TRY(stream_workspace(s, sizeof(int32_t) * (size_t)(sp.slices * p.m * p.n), &ws));
+        sp.part = static_cast<int32_t *>(ws);
+        GFH_TRY(stream_counters(s, (size_t)sp.nblk, &sp.counters));
+    }
+    const dim3 grid((unsigned)(sp.nblk * sp.slices)), block(kThreads);
+    if (p.m <= 16)
+        hipLaunchKernelGGL(qlinear_skinny_kernel<1>, grid, block, 0, s, sp);
+    else if (p.m <= 32)
+        hipLaunchKernelGGL(qlinear_skinny_kernel<2>, grid, block, 0, s, sp);
+    else
+        hipLaunchKernelGGL(qlinear_skinny_kernel<4>, grid, block, 0, s, sp);
+    return check_launch("qlinear_i8 (skinny)");
+}
+
+}  // namespace skinny
+
 }  // namespace
 
 int launch_qlinear_i8(const QLinearDesc &d, hipStream_t s) {
@@ -471,6 +667,7 @@ int launch_qlinear_i8(const QLinearDesc &d, hipStream_t s) {
     p.n = d.n;
     p.k = d.k;
     p.x_per_row = d.x_per_row ? 1 : 0;
+    if (d.m <= 64 && d.k % 16 == 0 && d.k > 0 && aligned16(d.qx) && aligned16(d.qw)) return skinny::launch(p, s);
     if (d.m >= 1024 && d.k % big::kBK == 0 && d.k > 0 && aligned16(d.qx) && aligned16(d.qw)) {
         p.tiles_m = (int)((d.m + big::kBM - 1) / big::kBM);
         p.tiles_n = (int)((d.n + big::kBN - 1) / big::kBN);

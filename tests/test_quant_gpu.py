@@ -249,3 +249,14 @@ def test_qlinear_large_tile_y_only(torch_dev, x_per_row):
                         bias=to_dev(bias, torch_dev), want_acc=False)
     assert acc is None
     assert _same_f32(to_np(y), ry)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1000, 4096), (7, 130, 1088), (16, 520, 2048), (17, 300, 4096),
+                                   (33, 1000, 2048), (64, 130, 1088)])
+@pytest.mark.parametrize("x_per_row,with_zp", [(False, True), (True, False), (True, True)])
+def test_qlinear_skinny_bit_exact(torch_dev, m, n, k, x_per_row, with_zp):
+    """M <= 64 with K % 16 == 0 streams the weight straight into i8 MFMA and
+    splits K over workgroups (exact int32 partials, summed by the last
+    workgroup of each column block): ragged N, 1-4 accumulator blocks,
+    every activation-scale variant, bit-exact to the oracle."""
+    _qlinear_case(torch_dev, m, n, k, x_per_row, with_zp, with_bias=(n % 2 == 0))
