@@ -260,3 +260,29 @@ def test_qlinear_skinny_bit_exact(torch_dev, m, n, k, x_per_row, with_zp):
     workgroup of each column block): ragged N, 1-4 accumulator blocks,
     every activation-scale variant, bit-exact to the oracle."""
     _qlinear_case(torch_dev, m, n, k, x_per_row, with_zp, with_bias=(n % 2 == 0))
+
+
+@pytest.mark.parametrize("m,n,k", [(1024, 128, 64), (1030, 300, 128), (1300, 777, 320), (2048, 384, 1024),
+                                   (2304, 1152, 4096), (1024, 4096, 640)])
+@pytest.mark.parametrize("x_per_row,with_zp", [(False, True), (True, False), (True, True)])
+def test_qlinear_large_tile_y_variants_bit_exact(torch_dev, m, n, k, x_per_row, with_zp):
+    """Output-only calls with M >= 1024 (the 256 x 256 tile kernel's
+    LDS-staged output path): ragged edges, short and long K, every
+    activation-scale variant -- fp32 outputs bit-exact to the oracle."""
+    gh, O = _gh(), _O()
+    x = gh.normal((m, k), seed=m + n, tensor_id=0)
+    w = gh.normal((n, k), 0.0, 0.02, seed=m + n, tensor_id=1)
+    bias = gh.uniform((n,), -0.1, 0.1, seed=m + n, tensor_id=2) if n % 2 == 0 else None
+    qw, sw, _ = O.quantize_per_channel(w, True)
+    if x_per_row:
+        qx, sx, zx = O.quantize_per_channel(x, not with_zp)
+    else:
+        qx, sx, zx = O.quantize_per_tensor(x, not with_zp)
+    sx, zx = np.atleast_1d(sx), np.atleast_1d(zx)
+    zx_arg = zx if with_zp else None
+    ry, _ = O.qlinear_i8(qx, sx, zx_arg, x_per_row, qw, sw, bias, want_acc=False)
+    d = lambda a: None if a is None else to_dev(a, torch_dev)  # noqa: E731
+    y, acc = gh.qlinear(d(qx), d(sx), d(zx_arg), d(qw), d(sw), x_per_row=x_per_row, bias=d(bias),
+                        want_acc=False)
+    assert acc is None
+    assert _same_f32(to_np(y), ry)
