@@ -202,68 +202,100 @@ __global__ __launch_bounds__(kThreads) void qlinear_mfma_kernel(QParams p) {
 }
 
 
-// ---- large tiles: 256 x 256 per workgroup, direct-to-LDS loads -------------------
+// ---- MFMA tiles fed by direct-to-LDS loads (M > 64) ------------------------------
 //
-// For M >= 1024 (compute-bound) each workgroup owns a 256 x 256 output tile
-// and each of its 4 waves a 128 x 128 sub-tile: 4 x 4 v_mfma_i32_32x32x32_i8
-// accumulators (256 registers per lane), so every 16-byte LDS fragment
-// feeds 4 MFMAs and the LDS read rate stays at half the MFMA rate.
-// Operands stream through a 4-deep ring of BK = 64 byte stages filled with
-// global_load_lds_dwordx4 (global memory straight into LDS, no VGPR
-// staging).  Rows of a stage are 64 bytes = 4 chunks of 16; chunk c of row
-// r is stored at position c ^ swz(r), which spreads the 16-byte fragment
-// reads over distinct banks.  Each lane of a
-// load instruction fetches the chunk that lands at its own LDS slot, so the
-// swizzle costs nothing on the load side.  Rows past M / N are clamped to
-// the last row (their products are never stored); K must be a multiple of 64.
+// A workgroup owns a BM x BN output tile; its 4 waves form a 2 x 2 grid of
+// (BM/2) x (BN/2) sub-tiles held as v_mfma_i32_32x32x32_i8 accumulators.
+// 256 x 256 (M >= 1024): 4 x 4 accumulators per wave (256 registers), so
+// every 16-byte LDS fragment feeds 4 MFMAs.  128 x 128 (64 < M < 1024):
+// 2 x 2 per wave.
+// Operands stream through a ring of STAGES stages of BK bytes of K, filled
+// with global_load_lds_dwordx4 (global memory straight into LDS, no VGPR
+// staging); all stages but the one being consumed are in flight.  One load
+// instruction fills 1 KB of LDS = 1024/BK rows of BK bytes.  BK = 128 makes
+// every row run a whole 128-byte line, which measured 1.6-1.8x the ingest
+// rate per CU of BK = 64 (half lines); BK = 64 serves K % 128 == 64.  Chunk
+// c (16 bytes) of row r is stored at position c ^ swz(r), which spreads the
+// 16-byte fragment reads over distinct banks; each lane of a load fetches
+// the chunk that lands at its own LDS slot, so the swizzle costs nothing on
+// the load side.  Rows past M / N are clamped to the last row (their
+// products are never stored).
 namespace big {
 
-constexpr int kBM = 256, kBN = 256, kBK = 64, kStages = 4;
-constexpr int kStageBytes = kBM * kBK;  // one operand, one stage (16 KB)
 constexpr int kGroupM = 4;
-constexpr int kOutStride = 136;  // floats per row of a wave's output staging area
-constexpr int kLdsBytes = (kStages * 2 * kStageBytes > 4 * 64 * kOutStride * 4) ? kStages * 2 * kStageBytes
-                                                                                 : 4 * 64 * kOutStride * 4;
 
 typedef __attribute__((address_space(3))) void *lds_ptr;
 typedef __attribute__((address_space(1))) void *glb_ptr;
 
-// Chunk swizzle of a 64-byte row.  A wave's fragment read has lanes 0-31 on
-// rows 0-31 of a block at one logical chunk (lanes 32-63 at the next); with
-// chunk ^ ((row >> 2) & 3) those 16-byte reads are conflict-free on gfx950's
-// 64-bank LDS (measured: 4.3 clk per ds_read_b128 per CU, against 8.3 for
-// chunk ^ ((row >> 1) ^ (row >> 3)) & 3 and 15.8 unswizzled).
-__device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
+// Chunk swizzle of a BK-byte LDS row.  A wave's fragment read has lanes 0-31
+// on rows 0-31 of a block at one logical chunk (lanes 32-63 at the next);
+// gfx950's LDS serves a ds_read_b128 16 lanes at a time over 64 banks, and
+// these swizzles put those 16 lanes on 16 distinct 4-bank groups (measured
+// conflict-free: 4.3 clk per ds_read_b128 per CU, against 15.8 unswizzled).
+template <int BK>
+__device__ __forceinline__ int swz(int r) {
+    return BK == 64 ? ((r >> 2) & 3) : ((r >> 1) & 7);
+}
 
 // s_waitcnt with only vmcnt constrained (expcnt / lgkmcnt left at maximum).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
     __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
 }
 
 __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
-// Waits until at most 8 * n of this wave's stage loads are in flight.
-__device__ __forceinline__ void wait_stages(int n) {
-    if (n >= 3)
-        wait_vmcnt<24>();
-    else if (n == 2)
-        wait_vmcnt<16>();
-    else if (n == 1)
-        wait_vmcnt<8>();
-    else
-        wait_vmcnt<0>();
+// Scheduling groups for one k-step: NM MFMAs, with NV global loads and ND
+// LDS fragment reads spread evenly between them, so that LDS latency and
+// load issue hide behind the MFMA pipe instead of stalling it.
+template <int NV, int ND, int NM, int G = 0>
+__device__ __forceinline__ void interleave() {
+    if constexpr (G < NM) {
+        constexpr int v = (G + 1) * NV / NM - G * NV / NM;
+        constexpr int d = (G + 1) * ND / NM - G * ND / NM;
+        if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x010, v, 0);  // VMEM
+        if constexpr (d > 0) __builtin_amdgcn_sched_group_barrier(0x100, d, 0);  // DS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                       // MFMA
+        interleave<NV, ND, NM, G + 1>();
+    }
 }
 
-template <bool X_PER_ROW, bool WANT_ACC>
-__global__ __launch_bounds__(kThreads, 1) void qlinear_tile256_kernel(QParams p) {
-    __shared__ __attribute__((aligned(1024))) int8_t lds[kLdsBytes];
+template <int BM, int BN, int BK, int STAGES>
+struct Tile {
+    static_assert(BK == 64 || BK == 128, "stage depth in K");
+    static constexpr int kWM = BM / 2, kWN = BN / 2;         // wave sub-tile
+    static constexpr int kFM = kWM / 32, kFN = kWN / 32;     // accumulators per wave
+    static constexpr int kSteps = BK / 32;                   // MFMA k-steps per stage
+    static constexpr int kChunks = BK / 16;                  // 16-byte chunks per row
+    static constexpr int kRowsPerLoad = 1024 / BK;           // rows filled by one load instruction
+    static constexpr int kLA = BM * BK / 4096, kLB = BN * BK / 4096;  // load instructions per wave per stage
+    static constexpr int kLPS = kLA + kLB;
+    static constexpr int kABytes = BM * BK, kBBytes = BN * BK;
+    static constexpr int kStageBytes = kABytes + kBBytes;
+    static constexpr int kRing = STAGES * kStageBytes;
+    // Output staging: each wave converts half of its sub-tile (kWM/2 rows x
+    // kWN columns) at a time; row stride kWN + 8 floats keeps the two row
+    // groups of one ds_write_b32 on disjoint banks.
+    static constexpr int kOutStride = kWN + 8;
+    static constexpr int kOut = 4 * (kWM / 2) * kOutStride * 4;
+    static constexpr int kLds = kRing > kOut ? kRing : kOut;
+    static_assert(kLds <= 160 * 1024, "LDS per workgroup");
+};
+
+template <int BM, int BN, int BK, int STAGES, bool X_PER_ROW, bool WANT_ACC>
+__global__ __launch_bounds__(kThreads, ((Tile<BM, BN, BK, STAGES>::kLds > 80 * 1024) ? 1 : 2)) void qlinear_tile_kernel(
+    QParams p) {
+    using T = Tile<BM, BN, BK, STAGES>;
+    constexpr int FM = T::kFM, FN = T::kFN, WM = T::kWM, WN = T::kWN;
+    constexpr int RPL = T::kRowsPerLoad, CPR = T::kChunks;
+    __shared__ __attribute__((aligned(1024))) int8_t lds[T::kLds];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm0 = (wave >> 1) * 128;
-    const int wn0 = (wave & 1) * 128;
+    const int wm0 = (wave >> 1) * WM;
+    const int wn0 = (wave & 1) * WN;
 
     const int nblk = p.tiles_m * p.tiles_n;
     int bid = blockIdx.x;
@@ -273,89 +305,116 @@ __global__ __launch_bounds__(kThreads, 1) void qlinear_tile256_kernel(QParams p)
     const int first_m = group * kGroupM;
     const int gm = min(p.tiles_m - first_m, kGroupM);
     const int in_group = bid - group * group_size;
-    const int64_t m0 = (int64_t)(first_m + in_group % gm) * kBM;
-    const int64_t n0 = (int64_t)(in_group / gm) * kBN;
+    const int64_t m0 = (int64_t)(first_m + in_group % gm) * BM;
+    const int64_t n0 = (int64_t)(in_group / gm) * BN;
 
-    // Per-lane source addresses of this wave's 4 A and 4 B load
-    // instructions: instruction j covers tile rows wave*64 + 16j .. +15;
-    // lane l fills LDS slot l of that 1 KB run (row l/4, physical chunk l%4).
-    const int8_t *a_src[4];
-    const int8_t *b_src[4];
+    // Byte offsets, relative to the tile's first row, of this wave's load
+    // instructions: A instruction j covers tile rows wave*(BM/4) + j*RPL ..
+    // +RPL-1; lane l fills LDS slot l of that 1 KB run (row l / CPR, physical
+    // chunk l % CPR) from logical chunk (l % CPR) ^ swz(row).  The host
+    // guarantees BM * K < 2^32.
+    const int8_t *a_base = p.qx + m0 * p.k;
+    const int8_t *b_base = p.qw + n0 * p.k;
+    uint32_t a_off[T::kLA], b_off[T::kLB];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int r = wave * 64 + j * 16 + (lane >> 2);
-        const int c = (lane & 3) ^ swz(r);
-        a_src[j] = p.qx + min(m0 + r, p.m - 1) * p.k + c * 16;
-        b_src[j] = p.qw + min(n0 + r, p.n - 1) * p.k + c * 16;
+    for (int j = 0; j < T::kLA; ++j) {
+        const int r = wave * (BM / 4) + j * RPL + lane / CPR;
+        a_off[j] = (uint32_t)((min(m0 + r, p.m - 1) - m0) * p.k) + (uint32_t)(((lane % CPR) ^ swz<BK>(r)) * 16);
     }
-    const int nk = (int)(p.k / kBK);
+#pragma unroll
+    for (int j = 0; j < T::kLB; ++j) {
+        const int r = wave * (BN / 4) + j * RPL + lane / CPR;
+        b_off[j] = (uint32_t)((min(n0 + r, p.n - 1) - n0) * p.k) + (uint32_t)(((lane % CPR) ^ swz<BK>(r)) * 16);
+    }
+    const int nk = (int)(p.k / BK);
 
     auto issue = [&](int t) {
-        int8_t *la = lds + (t % kStages) * 2 * kStageBytes + wave * 64 * kBK;
-        int8_t *lb = la + kStageBytes;
-        const int64_t k0 = (int64_t)t * kBK;
+        int8_t *la = lds + (t % STAGES) * T::kStageBytes;
+        int8_t *lb = la + T::kABytes;
+        const int8_t *ga = a_base + (int64_t)t * BK;
+        const int8_t *gb = b_base + (int64_t)t * BK;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            __builtin_amdgcn_global_load_lds((glb_ptr)(a_src[j] + k0), (lds_ptr)(la + j * 16 * kBK), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds((glb_ptr)(b_src[j] + k0), (lds_ptr)(lb + j * 16 * kBK), 16, 0, 0);
-        }
+        for (int j = 0; j < T::kLA; ++j)
+            __builtin_amdgcn_global_load_lds((glb_ptr)(ga + a_off[j]), (lds_ptr)(la + (wave * (BM / 4) + j * RPL) * BK),
+                                             16, 0, 0);
+#pragma unroll
+        for (int j = 0; j < T::kLB; ++j)
+            __builtin_amdgcn_global_load_lds((glb_ptr)(gb + b_off[j]), (lds_ptr)(lb + (wave * (BN / 4) + j * RPL) * BK),
+                                             16, 0, 0);
     };
 
     // Fragment address inside a stage: lane l reads row l%32 of a 32-row
-    // block, logical chunk 2*ks + l/32.
+    // block, logical chunk 2*ks + l/32.  Blocks start at multiples of 32
+    // rows, so the swizzle depends on l only, and logical chunk 2*ks + h
+    // lands at offset foff0 ^ (ks * 32).
     const int frow = lane & 31;
-    const int foff0 = frow * kBK + (((lane >> 5) ^ swz(frow)) * 16);
-    const int foff1 = frow * kBK + (((2 + (lane >> 5)) ^ swz(frow)) * 16);
+    const int foff0 = frow * BK + (((lane >> 5) ^ swz<BK>(frow)) * 16);
 
-    i32x4 af[2][4], bf[2][4];
+    i32x4 af[2][FM], bf[2][FN];
     auto load_frags = [&](int buf, int t, int ks) {
-        const int8_t *la = lds + (t % kStages) * 2 * kStageBytes;
-        const int8_t *lb = la + kStageBytes;
-        const int fo = ks ? foff1 : foff0;
+        const int8_t *la = lds + (t % STAGES) * T::kStageBytes;
+        const int8_t *lb = la + T::kABytes;
+        const int fo = foff0 ^ (ks << 5);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) af[buf][i] = *reinterpret_cast<const i32x4 *>(la + (wm0 + i * 32) * kBK + fo);
+        for (int i = 0; i < FM; ++i) af[buf][i] = *reinterpret_cast<const i32x4 *>(la + (wm0 + i * 32) * BK + fo);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) bf[buf][j] = *reinterpret_cast<const i32x4 *>(lb + (wn0 + j * 32) * kBK + fo);
+        for (int j = 0; j < FN; ++j) bf[buf][j] = *reinterpret_cast<const i32x4 *>(lb + (wn0 + j * 32) * BK + fo);
     };
 
-    i32x16 acc[4][4];
+    i32x16 acc[FM][FN];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < FN; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
     auto mfmas = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < FN; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[buf][i], bf[buf][j], acc[i][j], 0, 0, 0);
     };
 
-    // Ring of 4 stages, all in flight at once: stage t+4 is issued into
-    // stage t's buffer as soon as every wave holds stage t's fragments.
-    const int pre = min(kStages, nk);
-    for (int t = 0; t < pre; ++t) issue(t);
-    wait_stages(pre - 1);
+    // Stage t+STAGES is issued into stage t's buffer as soon as every wave
+    // holds the last fragments of stage t.  Within a stage, the fragments of
+    // k-step ks+1 are read while the MFMAs of k-step ks run.  The loop body
+    // has no branches so that the scheduler can interleave reads, loads and
+    // MFMAs across it: past the end of K the ring reloads the last stage
+    // into the buffer just freed (never read), which keeps the number of
+    // stages in flight, and so every wait count, constant.
+    for (int t = 0; t < STAGES; ++t) issue(min(t, nk - 1));
+    wait_vmcnt<(STAGES - 1) * T::kLPS>();
     __builtin_amdgcn_s_barrier();
     load_frags(0, 0, 0);
 
-    for (int t = 0; t < nk; ++t) {
-        load_frags(1, t, 1);
-        mfmas(0);
+    constexpr int NR = FM + FN, NM = FM * FN;
+    auto k_steps = [&](int t) {
+#pragma unroll
+        for (int ks = 0; ks + 1 < T::kSteps; ++ks) {
+            load_frags((ks + 1) & 1, t, ks + 1);
+            mfmas(ks & 1);
+            interleave<0, NR, NM>();
+        }
+    };
+    for (int t = 0; t + 1 < nk; ++t) {
+        k_steps(t);
         __builtin_amdgcn_sched_barrier(0);
         wait_lgkm0();  // this wave's reads of stage t are done
-        if (t + 1 < nk) {
-            // stage t+1 landed: stages t+2, t+3 may still be in flight
-            wait_stages(min(2, nk - t - 2));
-            __builtin_amdgcn_s_barrier();
-            if (t + kStages < nk) issue(t + kStages);
-            load_frags(0, t + 1, 0);
-        }
-        mfmas(1);
+        // stage t+1 landed: stages t+2 .. t+STAGES-1 may still be in flight
+        wait_vmcnt<(STAGES - 2) * T::kLPS>();
+        __builtin_amdgcn_s_barrier();
+        issue(min(t + STAGES, nk - 1));
+        load_frags(0, t + 1, 0);
+        mfmas((T::kSteps - 1) & 1);
+        interleave<T::kLPS, NR, NM>();
+        __builtin_amdgcn_sched_barrier(0);
     }
+    k_steps(nk - 1);
+    mfmas((T::kSteps - 1) & 1);
+    // No load may still be writing the ring when the workgroup moves on.
+    wait_vmcnt<0>();
 
     // Epilogue: lane l, register r of block (i, j) holds
     // row 8*(r/4) + 4*(l/32) + r%4, column l%32 of that 32 x 32 block.
@@ -363,10 +422,10 @@ __global__ __launch_bounds__(kThreads, 1) void qlinear_tile256_kernel(QParams p)
     // once per row.
     const int zx0 = (!X_PER_ROW && p.zx) ? (int)p.zx[0] : 0;
     const float sx0 = (!X_PER_ROW && p.y) ? p.sx[0] : 0.f;
-    int32_t rs[4];
-    float swc[4], bc[4];
+    int32_t rs[FN];
+    float swc[FN], bc[FN];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < FN; ++j) {
         const int64_t col = min(n0 + wn0 + j * 32 + (lane & 31), p.n - 1);
         rs[j] = p.zx ? p.rowsum[col] : 0;
         swc[j] = p.y ? p.sw[col] : 0.f;
@@ -394,10 +453,10 @@ __global__ __launch_bounds__(kThreads, 1) void qlinear_tile256_kernel(QParams p)
         // Parity/debug variant: int32 accumulators and outputs stored
         // straight from registers.
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < FN; ++j) {
             const int64_t col = n0 + wn0 + j * 32 + (lane & 31);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int64_t row = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
@@ -412,35 +471,35 @@ __global__ __launch_bounds__(kThreads, 1) void qlinear_tile256_kernel(QParams p)
         return;
     }
 
-    // Output tile through LDS: each wave converts 64 rows x 128 columns at a
-    // time into its own region (row stride 136 floats keeps the two row
-    // groups of one ds_write_b32 on disjoint banks), then writes whole
-    // 512-byte row runs with 16-byte stores.
+    // Output tile through LDS: each wave converts half of its sub-tile at a
+    // time into its own region, then writes whole row runs (WN floats) with
+    // 16-byte stores.
+    constexpr int LPR = WN / 4;       // lanes per output row
+    constexpr int RPI = 64 / LPR;     // rows per read instruction
+    constexpr int HALF = WM / 2;      // rows per half
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();  // every wave is done with the operand ring
-    float *lt = reinterpret_cast<float *>(lds) + wave * (64 * kOutStride);
+    float *lt = reinterpret_cast<float *>(lds) + wave * (HALF * T::kOutStride);
     const bool vec_out = (p.n % 4) == 0;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
 #pragma unroll
-        for (int ii = 0; ii < 2; ++ii)
+        for (int ii = 0; ii < FM / 2; ++ii)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < FN; ++j)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     int32_t a;
-                    const float v = finish(2 * h + ii, j, r, a);
+                    const float v = finish(h * (FM / 2) + ii, j, r, a);
                     const int lr = ii * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    lt[lr * kOutStride + j * 32 + (lane & 31)] = v;
+                    lt[lr * T::kOutStride + j * 32 + (lane & 31)] = v;
                 }
-        // each read covers 2 rows x 128 columns: lane l -> row 2q + l/32,
-        // columns 4*(l%32) .. +3
-        const int64_t col = n0 + wn0 + 4 * (lane & 31);
+        const int64_t col = n0 + wn0 + 4 * (lane % LPR);
 #pragma unroll
-        for (int q = 0; q < 32; ++q) {
-            const int lr = 2 * q + (lane >> 5);
-            const f32x4 v = *reinterpret_cast<const f32x4 *>(lt + lr * kOutStride + 4 * (lane & 31));
-            const int64_t row = m0 + wm0 + h * 64 + lr;
+        for (int q = 0; q < HALF / RPI; ++q) {
+            const int lr = RPI * q + lane / LPR;
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(lt + lr * T::kOutStride + 4 * (lane % LPR));
+            const int64_t row = m0 + wm0 + h * HALF + lr;
             if (row >= p.m) continue;
             float *dst = p.y + row * p.n + col;
             if (vec_out && col + 3 < p.n) {
@@ -452,6 +511,25 @@ __global__ __launch_bounds__(kThreads, 1) void qlinear_tile256_kernel(QParams p)
             }
         }
     }
+}
+
+template <int BM, int BN, int BK, int STAGES>
+int launch_tiles(QParams p, hipStream_t s) {
+    p.tiles_m = (int)((p.m + BM - 1) / BM);
+    p.tiles_n = (int)((p.n + BN - 1) / BN);
+    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n)), block(kThreads);
+    if (p.x_per_row) {
+        if (p.acc)
+            hipLaunchKernelGGL((qlinear_tile_kernel<BM, BN, BK, STAGES, true, true>), grid, block, 0, s, p);
+        else
+            hipLaunchKernelGGL((qlinear_tile_kernel<BM, BN, BK, STAGES, true, false>), grid, block, 0, s, p);
+    } else {
+        if (p.acc)
+            hipLaunchKernelGGL((qlinear_tile_kernel<BM, BN, BK, STAGES, false, true>), grid, block, 0, s, p);
+        else
+            hipLaunchKernelGGL((qlinear_tile_kernel<BM, BN, BK, STAGES, false, false>), grid, block, 0, s, p);
+    }
+    return check_launch("qlinear_i8");
 }
 
 }  // namespace big
@@ -668,22 +746,14 @@ int launch_qlinear_i8(const QLinearDesc &d, hipStream_t s) {
     p.k = d.k;
     p.x_per_row = d.x_per_row ? 1 : 0;
     if (d.m <= 64 && d.k % 16 == 0 && d.k > 0 && aligned16(d.qx) && aligned16(d.qw)) return skinny::launch(p, s);
-    if (d.m >= 1024 && d.k % big::kBK == 0 && d.k > 0 && aligned16(d.qx) && aligned16(d.qw)) {
-        p.tiles_m = (int)((d.m + big::kBM - 1) / big::kBM);
-        p.tiles_n = (int)((d.n + big::kBN - 1) / big::kBN);
-        const dim3 grid((unsigned)(p.tiles_m * p.tiles_n));
-        if (d.x_per_row) {
-            if (d.acc)
-                hipLaunchKernelGGL((big::qlinear_tile256_kernel<true, true>), grid, dim3(kThreads), 0, s, p);
-            else
-                hipLaunchKernelGGL((big::qlinear_tile256_kernel<true, false>), grid, dim3(kThreads), 0, s, p);
-        } else {
-            if (d.acc)
-                hipLaunchKernelGGL((big::qlinear_tile256_kernel<false, true>), grid, dim3(kThreads), 0, s, p);
-            else
-                hipLaunchKernelGGL((big::qlinear_tile256_kernel<false, false>), grid, dim3(kThreads), 0, s, p);
-        }
-        return check_launch("qlinear_i8");
+    // Direct-to-LDS tiles need 16-byte aligned rows (K % 64 == 0) and 32-bit
+    // row offsets inside a tile (256 * K < 2^32).
+    const bool ring_ok = d.k > 0 && d.k % 64 == 0 && d.k <= (int64_t(1) << 24) && aligned16(d.qx) && aligned16(d.qw);
+    if (ring_ok) {
+        const bool bk128 = d.k % 128 == 0;
+        if (d.m >= 1024)
+            return bk128 ? big::launch_tiles<256, 256, 128, 2>(p, s) : big::launch_tiles<256, 256, 64, 4>(p, s);
+        return bk128 ? big::launch_tiles<128, 128, 128, 3>(p, s) : big::launch_tiles<128, 128, 64, 4>(p, s);
     }
     p.tiles_m = (int)((d.m + kBM - 1) / kBM);
     p.tiles_n = (int)((d.n + kBN - 1) / kBN);
