@@ -3,7 +3,7 @@
 
 Headline (the one JSON line on stdout): the fp32 Linear forward
 y = x W^T + b at x [4096, 4096], W [4096, 4096], b [4096] -- the
-configuration BASELINE.json's metric is quoted on (Linear::forward,
+configuration the headline metric is quoted on (Linear::forward,
 ghostflow-nn/src/linear.rs:56-69, served by gfh_sgemm NT + bias).  One step
 is one Linear forward over that batch, i.e. one sgemm kernel launch, with
 every input already resident in HBM.
@@ -16,7 +16,7 @@ The same line carries
     Linear::forward -> data_f32 gather of W^T + matmul_blocked + broadcast
     bias add, single-threaded as the reference is) timed on this host on a
     bounded row sample and extrapolated to the full layer;
-  * "components": the other north-star kernels at their BASELINE shapes
+  * "components": the other hot-path kernels at their benchmark shapes
     (square fp32 GEMM, int8 linear, decode GEMV fp32 / int8, causal SDPA),
     each with its own roofline fraction.  These are supplementary numbers,
     not the headline.

@@ -5,29 +5,27 @@
 // The int8 form is DynamicQuantization::get_weights -> Tensor::matmul
 // (ghostflow-nn/src/quantization.rs:173-204, :275-277) without ever
 // materializing the fp32 weight:
-//   y[b,n] = sum_k x[b,k] * ((q[k,n] - zp[k]) * s[k])
-//          = sum_k xs[b,k] * q[k,n]  -  sum_k xs[b,k] * zp[k],   xs = x * s[k]
-// so each weight costs one sign-extending convert and one FMA per batch row;
-// the zero-point term is the same for every column and is subtracted once.
-// (The products are regrouped, so the result is within the fp32 GEMM bound
-// of the reference, not bit-identical to it.)
+//   y[b,n] = sum_k x[b,k] * ((q[k,n] - zp[k]) * s[k]) = sum_k xs[b,k] * (q[k,n] - zp[k]),
+// xs = x * s[k].  (The products are regrouped, so the result is within the
+// fp32 GEMM bound of the reference, not bit-identical to it.)
 //
-// Layout of the work (one kernel per call):
+// Layout of the work (one kernel per group of up to 8 batch rows):
 //  * A workgroup (4 wave64) owns a strip of 256 bytes of every W row (64
-//    fp32 or 256 int8 columns) over one K-slice; lane l reads 16 bytes of
-//    row (l / 16) of a 4-row group, so one load instruction covers 4 rows x
-//    256 contiguous bytes and U of them per lane are in flight.  HBM streams
-//    256-byte row runs at about 6 TB/s; 128-byte runs only reach ~5.
-//  * Each wave walks a quarter of the slice; partial sums are reduced over
-//    the 4 row lanes with xor shuffles, then over the 4 waves through LDS in
-//    a fixed order.
-//  * fp32 has 224 strips at N = 14336, enough workgroups to keep HBM busy,
-//    so the slice is all of K and the workgroup writes y directly.  int8 has
-//    only 56 strips, so K is split into S slices: every workgroup writes its
-//    partial strip to a workspace, and the last of the S to finish (an
-//    agent-scope arrival counter) adds the S partials in slice order and
-//    writes y -- deterministic, one launch.  The counter is returned to 0
-//    by that last workgroup.
+//    fp32 or 256 int8 columns) over one K-slice; every load instruction
+//    covers 4 rows x 256 contiguous bytes (HBM streams 256-byte row runs at
+//    about 6 TB/s; 128-byte runs only reach ~5).  The slice's activations
+//    are staged in LDS once per workgroup.
+//  * fp32 (gemv_f32_kernel): lane l reads 16 bytes of row l/16 of a 4-row
+//    group and the b multiply-adds run on the VALU; partial sums are reduced
+//    over the 4 row lanes with xor shuffles, then over the waves in LDS.
+//  * int8 (w8mf::gemv_w8_mfma_kernel): the weights become exact f16 and the
+//    multiply-adds run on the matrix cores (v_mfma_f32_16x16x32_f16), so
+//    batches of 1-8 rows cost the same.
+//  * K is split into S slices when the strips alone are too few workgroups:
+//    every workgroup writes its partial strip to a workspace, and the last
+//    of the S to finish (an agent-scope arrival counter) adds the S
+//    partials in slice order and writes y -- deterministic, one launch.  The
+//    counter is returned to 0 by that last workgroup.
 #include <algorithm>
 
 #include "common.hpp"
@@ -56,20 +54,96 @@ struct GemvParams {
 
 constexpr int kMaxSlice = 1024;
 
-template <typename WT, int MAXB, int U, bool VEC>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
-    constexpr bool INT8 = sizeof(WT) == 1;
-    constexpr int EPL = 16 / sizeof(WT);  // weights per lane per load
-    constexpr int SCOLS = kStripBytes / sizeof(WT);
-    // x of this slice's rows (int8: x * s[k]), [row][batch]
-    __shared__ __attribute__((aligned(16))) float xs[kMaxSlice * MAXB];
+// Writes this workgroup's strip -- value(bi, c) for batch row bi < nb and
+// strip column c -- to y when K is not split.  Otherwise publishes it as the
+// slice's partial strip and counts arrivals; the last workgroup of the strip
+// to arrive sums the slices in order.  Every access to data shared between
+// workgroups (partials, counter) is an agent-scope atomic: such loads and
+// stores go to the device coherence point instead of an XCD's L2, so no L2
+// writeback or invalidate is needed -- only that the partial stores have
+// completed (vmcnt 0) before the arrival is counted.  The counter is
+// returned to 0 by that last workgroup.
+template <int MAXB, int SCOLS, typename F>
+__device__ __forceinline__ void store_strip(const GemvParams &p, int64_t strip, int64_t slice, int64_t nb,
+                                            int64_t col0, int *last_flag, F value) {
+    if (p.slices == 1) {
+        for (int t = threadIdx.x; t < MAXB * SCOLS; t += kThreads) {
+            const int bi = t / SCOLS, c = t % SCOLS;
+            if (bi >= nb || col0 + c >= p.n) continue;
+            p.y[bi * p.n + col0 + c] = value(bi, c);
+        }
+        return;
+    }
+
+    for (int t = threadIdx.x; t < MAXB * SCOLS; t += kThreads) {
+        const int bi = t / SCOLS, c = t % SCOLS;
+        if (bi >= nb || col0 + c >= p.n) continue;
+        __hip_atomic_store(p.part + (slice * nb + bi) * p.n + col0 + c, value(bi, c), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial stores are complete
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int old = __hip_atomic_fetch_add(p.counters + strip, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *last_flag = (old == (int)p.slices - 1);
+    }
+    __syncthreads();
+    if (!*last_flag) return;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    // Each thread requests the partials of all its outputs, for a group of
+    // slices at a time, before adding any of them, so the loads overlap
+    // instead of paying one memory latency per output or slice; each output
+    // is still summed in slice order.
+    constexpr int kOut = (MAXB * SCOLS + kThreads - 1) / kThreads;  // outputs per thread
+    constexpr int kGroup = kOut >= 32 ? 1 : 32 / kOut;                // slices per group
+    const float *src[kOut];
+    float v[kOut];
+#pragma unroll
+    for (int o = 0; o < kOut; ++o) {
+        const int t = threadIdx.x + o * kThreads;
+        const int bi = t / SCOLS, c = t % SCOLS;
+        const bool ok = t < MAXB * SCOLS && bi < nb && col0 + c < p.n;
+        src[o] = ok ? p.part + bi * p.n + col0 + c : nullptr;
+        v[o] = 0.f;
+    }
+    for (int64_t j0 = 0; j0 < p.slices; j0 += kGroup) {
+        float pv[kOut][kGroup];
+#pragma unroll
+        for (int o = 0; o < kOut; ++o)
+#pragma unroll
+            for (int j = 0; j < kGroup; ++j)
+                pv[o][j] = (src[o] && j0 + j < p.slices)
+                               ? __hip_atomic_load(src[o] + (j0 + j) * nb * p.n, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT)
+                               : 0.f;
+#pragma unroll
+        for (int o = 0; o < kOut; ++o)
+#pragma unroll
+            for (int j = 0; j < kGroup; ++j)
+                if (j0 + j < p.slices) v[o] = (j0 + j == 0) ? pv[o][j] : v[o] + pv[o][j];
+    }
+#pragma unroll
+    for (int o = 0; o < kOut; ++o)
+        if (src[o]) {
+            const int t = threadIdx.x + o * kThreads;
+            p.y[(t / SCOLS) * p.n + col0 + t % SCOLS] = v[o];
+        }
+    if (threadIdx.x == 0) __hip_atomic_store(p.counters + strip, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int MAXB, int U, bool VEC>
+__global__ __launch_bounds__(kThreads) void gemv_f32_kernel(GemvParams p) {
+    constexpr int EPL = 4;                    // floats per lane per load
+    constexpr int SCOLS = kStripBytes / 4;    // strip columns
+    constexpr int kStep = 4 * U;              // rows per wave step
+    __shared__ __attribute__((aligned(16))) float xs[kMaxSlice * MAXB];  // this slice's x, [row][batch]
     __shared__ float red[kWaves][MAXB][SCOLS];
-    __shared__ float zred[kWaves][MAXB];
     __shared__ int last_flag;
 
-    const WT *__restrict__ W = static_cast<const WT *>(p.w);
+    const float *__restrict__ W = static_cast<const float *>(p.w);
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t strip = blockIdx.x % p.nstrips;
     const int64_t slice = blockIdx.x / p.nstrips;
     const int64_t col0 = strip * SCOLS;
@@ -78,108 +152,105 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
     const int64_t nb = p.b < MAXB ? p.b : MAXB;
     const int64_t s_lo = slice * p.kslice;
     const int rows = (int)min(p.kslice, p.k - s_lo);
+    if (rows <= 0) {  // K == 0: y = 0, and no row may be read
+        store_strip<MAXB, SCOLS>(p, strip, slice, nb, col0, &last_flag, [](int, int) { return 0.f; });
+        return;
+    }
+    const int rows_s = (rows + kStep - 1) / kStep * kStep;
+
+    // Activations first, from clamped in-range indices: loads complete in
+    // issue order, so the staging below waits only for these while the
+    // first weight batch (issued next) streams in behind them.
+    constexpr int kRowsPerThread = kMaxSlice / kThreads;
+    float xv[kRowsPerThread][MAXB];
+#pragma unroll
+    for (int i = 0; i < kRowsPerThread; ++i) {
+        const int rr = min((int)threadIdx.x + kThreads * i, rows - 1);
+#pragma unroll
+        for (int bi = 0; bi < MAXB; ++bi) xv[i][bi] = p.x[min<int64_t>(bi, nb - 1) * p.k + s_lo + rr];
+    }
+
+    // Each wave walks whole steps of its quarter of the slice.  Loads are
+    // unconditional: rows past the slice read its last row (their x is
+    // zero); with VEC (N % 4 == 0, aligned W) a lane's 4 columns lie all
+    // inside N or all outside it, and lanes past N read the strip's first
+    // columns (never stored).  Without VEC every column is checked.
+    const int per = ((rows_s / kStep + kWaves - 1) / kWaves) * kStep;
+    const int wb = min(wave * per, rows_s), we = min(wb + per, rows_s);
+    const int64_t lcol = (VEC && col >= p.n) ? col0 : col;
+    const float *base = W + s_lo * p.n + lcol;
+    auto load_step = [&](int r0, i32x4 (&w)[U]) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int r = max(min(r0 + 4 * u + rsub, rows - 1), 0);
+            const float *src = base + (int64_t)r * p.n;
+            if constexpr (VEC) {
+                w[u] = *reinterpret_cast<const i32x4 *>(src);
+            } else {
+                float tmp[EPL];
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) tmp[e] = (col + e < p.n) ? src[e] : 0.f;
+                __builtin_memcpy(&w[u], tmp, 16);
+            }
+        }
+    };
+    __builtin_amdgcn_sched_barrier(0);
+    i32x4 wa[U], wn[U];
+    load_step(wb, wa);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // Stage x, zero past the slice and the batch (a mask, not a select: a
+    // value used only under a condition lets the compiler sink its load into
+    // a branch, which then waits for everything issued before it).
+#pragma unroll
+    for (int i = 0; i < kRowsPerThread; ++i) {
+        const int r = threadIdx.x + kThreads * i;
+        if (r >= rows_s) continue;
+#pragma unroll
+        for (int bi = 0; bi < MAXB; ++bi) {
+            const uint32_t keep = (r < rows && bi < nb) ? 0xffffffffu : 0u;
+            xs[r * MAXB + bi] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, xv[i][bi]) & keep);
+        }
+    }
+    __syncthreads();
 
     float acc[MAXB][EPL];
 #pragma unroll
     for (int bi = 0; bi < MAXB; ++bi)
 #pragma unroll
         for (int e = 0; e < EPL; ++e) acc[bi][e] = 0.f;
-
-    // Rows of this wave: a quarter of the slice, a multiple of 4.
-    const int per = (((int)p.kslice + kWaves - 1) / kWaves + 3) & ~3;
-    const int wb = min(wave * per, rows), we = min(wb + per, rows);
-    const bool full_cols = VEC && (col + EPL - 1 < p.n);
-    const WT *base = W + (s_lo + rsub) * p.n + col;
     auto fma_row = [&](const i32x4 &wv, int r) {
-        float xv[MAXB];
+        float x[MAXB];
 #pragma unroll
-        for (int bi = 0; bi < MAXB; ++bi) xv[bi] = xs[r * MAXB + bi];
-        if constexpr (INT8) {
+        for (int bi = 0; bi < MAXB; ++bi) x[bi] = xs[r * MAXB + bi];
+        const f32x4 wf = __builtin_bit_cast(f32x4, wv);
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const float q = (float)(int8_t)(wv[e >> 2] >> (8 * (e & 3)));
+        for (int bi = 0; bi < MAXB; ++bi)
 #pragma unroll
-                for (int bi = 0; bi < MAXB; ++bi) acc[bi][e] += xv[bi] * q;
-            }
-        } else {
-            const f32x4 wf = __builtin_bit_cast(f32x4, wv);
-#pragma unroll
-            for (int bi = 0; bi < MAXB; ++bi)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) acc[bi][e] += xv[bi] * wf[e];
-        }
+            for (int e = 0; e < EPL; ++e) acc[bi][e] += x[bi] * wf[e];
     };
-    int r0 = wb;
-    // The first batch of weights does not depend on x: request it before
-    // staging x, so the staging latency hides under the weight loads.
-    const bool first_full = full_cols && wb + 4 * U <= we;
-    i32x4 w0[U];
-    if (first_full) {
+    // The next step is requested before the current one is used.  Every
+    // branch is wave-uniform and every block issues its loads
+    // unconditionally, so the wait for a step never covers the next one.
+    auto fma_step = [&](const i32x4 (&w)[U], int r0) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) w0[u] = *reinterpret_cast<const i32x4 *>(base + (int64_t)(wb + 4 * u) * p.n);
-    }
-    // Stage this slice's x (times the row scale for int8); for int8 with
-    // zero points also sum xs * zp over the slice per batch row -- the
-    // column-independent zero-point term.
-    float zpart[MAXB];
-#pragma unroll
-    for (int bi = 0; bi < MAXB; ++bi) zpart[bi] = 0.f;
-    for (int r = threadIdx.x; r < rows; r += kThreads) {
-        const float sr = INT8 ? p.scales[s_lo + r] : 1.f;
-        const float zr = (INT8 && p.zps) ? (float)p.zps[s_lo + r] : 0.f;
-#pragma unroll
-        for (int bi = 0; bi < MAXB; ++bi) {
-            const float v = bi < nb ? (INT8 ? p.x[bi * p.k + s_lo + r] * sr : p.x[bi * p.k + s_lo + r]) : 0.f;
-            xs[r * MAXB + bi] = v;
-            zpart[bi] += v * zr;
+        for (int u = 0; u < U; ++u) fma_row(w[u], r0 + 4 * u + rsub);
+    };
+    for (int r0 = wb; r0 < we;) {
+        if (r0 + kStep >= we) {
+            fma_step(wa, r0);
+            break;
         }
-    }
-    if (INT8) {
-#pragma unroll
-        for (int bi = 0; bi < MAXB; ++bi) {
-            float v = zpart[bi];
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-            if (lane == 0) zred[wave][bi] = v;
+        load_step(r0 + kStep, wn);
+        fma_step(wa, r0);
+        r0 += kStep;
+        if (r0 + kStep >= we) {
+            fma_step(wn, r0);
+            break;
         }
-    }
-    __syncthreads();
-    if (first_full) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) fma_row(w0[u], wb + 4 * u + rsub);
-        r0 += 4 * U;
-        // Whole batches: no per-row checks.
-        for (; r0 + 4 * U <= we; r0 += 4 * U) {
-            i32x4 w[U];
-#pragma unroll
-            for (int u = 0; u < U; ++u) w[u] = *reinterpret_cast<const i32x4 *>(base + (int64_t)(r0 + 4 * u) * p.n);
-#pragma unroll
-            for (int u = 0; u < U; ++u) fma_row(w[u], r0 + 4 * u + rsub);
-        }
-    }
-    // Remaining rows, ragged columns or unaligned rows: checked loads.
-    for (; r0 < we; r0 += 4 * U) {
-        i32x4 w[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int r = r0 + 4 * u;  // this lane's row is r + rsub
-            i32x4 v = {0, 0, 0, 0};
-            if (r + rsub < we) {
-                const WT *src = base + (int64_t)r * p.n;
-                if (full_cols) {
-                    v = *reinterpret_cast<const i32x4 *>(src);
-                } else {
-                    WT tmp[EPL];
-#pragma unroll
-                    for (int e = 0; e < EPL; ++e) tmp[e] = (col + e < p.n) ? src[e] : WT(0);
-                    __builtin_memcpy(&v, tmp, 16);
-                }
-            }
-            w[u] = v;
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-            if (r0 + 4 * u + rsub < we) fma_row(w[u], r0 + 4 * u + rsub);
+        load_step(r0 + kStep, wa);
+        fma_step(wn, r0);
+        r0 += kStep;
     }
 
     // Reduce over the 4 row lanes of each column group, then over waves.
@@ -190,98 +261,309 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvParams p) {
             float v = acc[bi][e];
             v += __shfl_xor(v, 16);
             v += __shfl_xor(v, 32);
-            acc[bi][e] = v;
+            if (lane < 16) red[wave][bi][lane * EPL + e] = v;
         }
-    if (lane < 16) {
-#pragma unroll
-        for (int bi = 0; bi < MAXB; ++bi)
-#pragma unroll
-            for (int e = 0; e < EPL; ++e) red[wave][bi][lane * EPL + e] = acc[bi][e];
-    }
     __syncthreads();
     auto strip_value = [&](int bi, int c) {
         float v = red[0][bi][c];
 #pragma unroll
         for (int w2 = 1; w2 < kWaves; ++w2) v = v + red[w2][bi][c];
-        if (INT8) v = v - ((zred[0][bi] + zred[1][bi]) + (zred[2][bi] + zred[3][bi]));
         return v;
     };
+    store_strip<MAXB, SCOLS>(p, strip, slice, nb, col0, &last_flag, strip_value);
+}
 
-    if (p.slices == 1) {
-        for (int t = threadIdx.x; t < MAXB * SCOLS; t += kThreads) {
-            const int bi = t / SCOLS, c = t % SCOLS;
-            if (bi >= nb || col0 + c >= p.n) continue;
-            p.y[bi * p.n + col0 + c] = strip_value(bi, c);
-        }
+// ---- int8 weights on the matrix cores -------------------------------------------
+//
+// y[b,n] = sum_k xs[b,k] * (q[k,n] - zp[k]) with xs = x * s[k] runs as
+// v_mfma_f32_16x16x32_f16 with W as the A operand (m = column, k = row) and
+// the split activations as B (k = row, n = split column):
+//  * A: lane l holds 8 consecutive rows of one column.  Lane (g = l/16,
+//    c = l%16) loads rows 8g..8g+7 of a 32-row block, 16 bytes each
+//    (columns 16c..16c+15 of the 256-byte strip), so every load instruction
+//    still reads 4 rows x 256 contiguous bytes.  Column 16c + j of those 8
+//    rows is then the A operand of MFMA j.
+//  * int8 -> f16 is exact and cheap: with u = q ^ 0x80 (= q + 128 as an
+//    unsigned byte) the f16 with bits 0x64uu is 1024 + u = 1152 + q, built by
+//    two byte permutes per pair of weights; one packed f16 add of
+//    -(1152 + zp) per pair of rows leaves q - zp, exact (|q - zp| <= 255).
+//  * B: each workgroup scales its slice of xs by a power of two 2^e so that
+//    max |xs| 2^e lies in [2^14, 2^15), then splits it into two f16, hi =
+//    f16(xs 2^e) and lo = f16(xs 2^e - hi): hi + lo carries 22 significant
+//    bits, and hi * w, lo * w are exact in the fp32 accumulators.  Split
+//    column n = b holds hi of batch row b and n = 8 + b its lo, so 8 batch
+//    rows fill the 16 columns of one MFMA.
+// Sums are fp32 in a fixed order, as in the VALU form; the result is within
+// the fp32 GEMM bound of the reference, not bit-identical to it.
+namespace w8mf {
+
+constexpr int kBlockRows = 32;           // rows per MFMA step of a wave
+constexpr int kXStride = kMaxSlice + 8;  // f16 per split column: +16 bytes keeps B reads conflict-free
+constexpr int kXBytes = 16 * kXStride * 2;
+// Wave partials [wave][batch][column], aliased onto the split activations:
+// 2 words of padding per 64 columns and a 264-word row put the 32 lanes
+// that store together on 32 distinct banks.
+constexpr int kRedStride = 264;
+constexpr int kRedBytes = kWaves * 8 * kRedStride * 4;
+constexpr int kLdsBytes = kXBytes > kRedBytes ? kXBytes : kRedBytes;
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int red_index(int w, int b, int col) { return (w * 8 + b) * kRedStride + col + 2 * (col >> 6); }
+
+template <int MAXB, bool VEC>
+__global__ __launch_bounds__(kThreads, VEC ? 2 : 1) void gemv_w8_mfma_kernel(GemvParams p) {
+    constexpr int SCOLS = kStripBytes;
+    __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
+    __shared__ __attribute__((aligned(16))) uint32_t zph[kMaxSlice / 2];  // -(1152 + zp) of row pairs, f16x2
+    __shared__ float amax_red[kWaves];
+    __shared__ int last_flag;
+    _Float16 *xsh = reinterpret_cast<_Float16 *>(lds);
+
+    const int8_t *__restrict__ W = static_cast<const int8_t *>(p.w);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, c = lane & 15;
+    const int64_t strip = blockIdx.x % p.nstrips;
+    const int64_t slice = blockIdx.x / p.nstrips;
+    const int64_t col0 = strip * SCOLS;
+    const int64_t nb = p.b < MAXB ? p.b : MAXB;
+    const int64_t s_lo = slice * p.kslice;
+    const int rows = (int)min(p.kslice, p.k - s_lo);
+    const int rows32 = (rows + kBlockRows - 1) & ~(kBlockRows - 1);
+    if (rows <= 0) {  // K == 0: y = 0, and no row may be read
+        store_strip<MAXB, SCOLS>(p, strip, slice, nb, col0, &last_flag, [](int, int) { return 0.f; });
         return;
     }
 
-    // Split K: publish this slice's partial strip, count arrivals; the last
-    // workgroup of the strip sums the slices in order.  Every access to data
-    // shared between workgroups (partials, counter) is an agent-scope atomic:
-    // such loads and stores go to the device coherence point instead of an
-    // XCD's L2, so no L2 writeback or invalidate is needed -- only that the
-    // partial stores have completed (vmcnt 0) before the arrival is counted.
-    for (int t = threadIdx.x; t < MAXB * SCOLS; t += kThreads) {
-        const int bi = t / SCOLS, c = t % SCOLS;
-        if (bi >= nb || col0 + c >= p.n) continue;
-        __hip_atomic_store(p.part + (slice * nb + bi) * p.n + col0 + c, strip_value(bi, c), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial stores are complete
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int old = __hip_atomic_fetch_add(p.counters + strip, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last_flag = (old == (int)p.slices - 1);
-    }
-    __syncthreads();
-    if (!last_flag) return;
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    // All slice partials are requested before the first is added, in
-    // groups of kSumGroup, so the loads overlap instead of paying one memory
-    // latency per slice; the sum itself runs in slice order.
-    constexpr int kSumGroup = 16;
-    for (int t = threadIdx.x; t < MAXB * SCOLS; t += kThreads) {
-        const int bi = t / SCOLS, c = t % SCOLS;
-        if (bi >= nb || col0 + c >= p.n) continue;
-        const float *src = p.part + bi * p.n + col0 + c;
-        float v = 0.f;
-        for (int64_t j0 = 0; j0 < p.slices; j0 += kSumGroup) {
-            float pv[kSumGroup];
+    // Activations first: loads complete in issue order, so the staging below
+    // waits only for these, while the first weight blocks (issued next)
+    // stream in behind them.  Each thread owns rows threadIdx.x + 256 i.
+    // The loads are unconditional, from clamped in-range indices, and the
+    // values are selected afterwards: a load under a lane condition would be
+    // waited for before the branches rejoin, one memory latency per load.
+    constexpr int kRowsPerThread = kMaxSlice / kThreads;
+    float xv[kRowsPerThread][MAXB], sv[kRowsPerThread];
 #pragma unroll
-            for (int j = 0; j < kSumGroup; ++j)
-                pv[j] = (j0 + j < p.slices)
-                            ? __hip_atomic_load(src + (j0 + j) * nb * p.n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                            : 0.f;
+    for (int i = 0; i < kRowsPerThread; ++i) {
+        const int rr = min((int)threadIdx.x + kThreads * i, rows - 1);
+        sv[i] = p.scales[s_lo + rr];
 #pragma unroll
-            for (int j = 0; j < kSumGroup; ++j)
-                if (j0 + j < p.slices) v = (j0 + j == 0) ? pv[j] : v + pv[j];
+        for (int bi = 0; bi < MAXB; ++bi) xv[i][bi] = p.x[min<int64_t>(bi, nb - 1) * p.k + s_lo + rr];
+    }
+    // Zero points of row pairs threadIdx.x + 256 u.  Without zero points
+    // the (ignored) bytes come from the scales, so that no branch guards
+    // these loads either.
+    constexpr int kPairsPerThread = kMaxSlice / 2 / kThreads;
+    const int8_t *zsrc = p.zps ? p.zps : reinterpret_cast<const int8_t *>(p.scales);
+    int zr[kPairsPerThread][2];
+#pragma unroll
+    for (int u = 0; u < kPairsPerThread; ++u)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) zr[u][h] = zsrc[s_lo + min(2 * ((int)threadIdx.x + kThreads * u) + h, rows - 1)];
+
+    const int per = ((rows32 / kBlockRows + kWaves - 1) / kWaves) * kBlockRows;
+    const int wb = min(wave * per, rows32), we = min(wb + per, rows32);
+    const int64_t col = col0 + 16 * c;
+    // Loads are unconditional so that the wait for a block never has to wait
+    // for the prefetch of the next one.  Rows past the slice read its last
+    // row (their activations are zero); with VEC (N % 16 == 0, aligned W) a
+    // lane's 16 columns lie all inside N or all outside it, and lanes past
+    // N read the strip's first columns (never stored).  Without VEC every
+    // byte is checked.
+    const int64_t lcol = (VEC && col >= p.n) ? col0 : col;
+    const int8_t *base = W + s_lo * p.n + lcol;
+    auto load_block = [&](int r0, i32x4 (&R)[8]) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = max(min(r0 + 8 * g + i, rows - 1), 0);  // row within the slice
+            const int8_t *src = base + (int64_t)r * p.n;
+            if constexpr (VEC) {
+                R[i] = *reinterpret_cast<const i32x4 *>(src);
+            } else {
+                int8_t tmp[16];
+#pragma unroll
+                for (int e = 0; e < 16; ++e) tmp[e] = (col + e < p.n) ? src[e] : int8_t(0);
+                __builtin_memcpy(&R[i], tmp, 16);
+            }
         }
-        p.y[bi * p.n + col0 + c] = v;
+    };
+    // Unconditional as well (a wave without rows re-reads the slice's last
+    // row): a branch here would make the staging below wait for these loads.
+    // The scheduling barriers keep the issue order: activations, weights,
+    // then the staging arithmetic.
+    __builtin_amdgcn_sched_barrier(0);
+    i32x4 Ra[8], Rb[8];
+    load_block(wb, Ra);
+    load_block(min(wb + kBlockRows, max(we - kBlockRows, wb)), Rb);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // Masks rather than selects: a value that is only used under a
+    // condition lets the compiler sink its load into a branch again.
+#pragma unroll
+    for (int i = 0; i < kRowsPerThread; ++i) {
+        const int r = threadIdx.x + kThreads * i;
+#pragma unroll
+        for (int bi = 0; bi < MAXB; ++bi) {
+            const uint32_t keep = (r < rows && bi < nb) ? 0xffffffffu : 0u;
+            xv[i][bi] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, xv[i][bi] * sv[i]) & keep);
+        }
     }
-    if (threadIdx.x == 0) __hip_atomic_store(p.counters + strip, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int u = 0; u < kPairsPerThread; ++u)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            zr[u][h] &= (p.zps && 2 * ((int)threadIdx.x + kThreads * u) + h < rows) ? -1 : 0;
+
+    // Stage: power-of-two prescale, f16 hi/lo split into columns [n][row]
+    // (zero past the slice), and the zero-point pairs.  Split columns of
+    // batch rows past MAXB are never written: an MFMA output column depends
+    // only on its own B column, and those are not stored.
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < kRowsPerThread; ++i)
+#pragma unroll
+        for (int bi = 0; bi < MAXB; ++bi) amax = fmaxf(amax, fabsf(xv[i][bi]));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    if (lane == 0) amax_red[wave] = amax;
+#pragma unroll
+    for (int u = 0; u < kPairsPerThread; ++u) {
+        const int pr = (int)threadIdx.x + kThreads * u;
+        if (2 * pr < rows32) {
+            const half2 z = {(_Float16)(-(1152 + zr[u][0])), (_Float16)(-(1152 + zr[u][1]))};
+            zph[pr] = __builtin_bit_cast(uint32_t, z);
+        }
+    }
+    __syncthreads();
+    amax = fmaxf(fmaxf(amax_red[0], amax_red[1]), fmaxf(amax_red[2], amax_red[3]));
+    int ex = 0;
+    if (amax > 0.f && amax <= 3.4e38f) {
+        (void)frexpf(amax, &ex);  // amax = f 2^ex, f in [0.5, 1)
+        ex = 15 - ex;
+    }
+#pragma unroll
+    for (int i = 0; i < kRowsPerThread; ++i) {
+        const int r = threadIdx.x + kThreads * i;
+        if (r >= rows32) continue;
+#pragma unroll
+        for (int bi = 0; bi < MAXB; ++bi) {
+            const float X = ldexpf(xv[i][bi], ex);
+            const _Float16 hi = (_Float16)X;
+            xsh[bi * kXStride + r] = hi;
+            xsh[(8 + bi) * kXStride + r] = (_Float16)(X - (float)hi);
+        }
+    }
+    __syncthreads();
+
+    // Stream the weights in 32-row blocks, two blocks in flight.
+    f32x4 acc[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto compute_block = [&](const i32x4 (&R)[8], int r0) {
+        const half8 bx = *reinterpret_cast<const half8 *>(xsh + c * kXStride + r0 + 8 * g);
+        const u32x4 zq = *reinterpret_cast<const u32x4 *>(zph + (r0 + 8 * g) / 2);
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            u32x4 a[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t lo_r = (uint32_t)R[2 * i][d] ^ 0x80808080u;
+                const uint32_t hi_r = (uint32_t)R[2 * i + 1][d] ^ 0x80808080u;
+                const uint32_t t0 = __builtin_amdgcn_perm(hi_r, lo_r, 0x05010400u);  // columns 4d, 4d+1
+                const uint32_t t1 = __builtin_amdgcn_perm(hi_r, lo_r, 0x07030602u);  // columns 4d+2, 4d+3
+                // (a vector element is copied to a scalar before the bit cast:
+                // this compiler casts an element lvalue from the vector start)
+                const uint32_t zi = zq[i];
+                const half2 z = __builtin_bit_cast(half2, zi);
+                a[0][i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, __builtin_amdgcn_perm(t0, 0x64646464u, 0x00050004u)) + z);
+                a[1][i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, __builtin_amdgcn_perm(t0, 0x64646464u, 0x00070006u)) + z);
+                a[2][i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, __builtin_amdgcn_perm(t1, 0x64646464u, 0x00050004u)) + z);
+                a[3][i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, __builtin_amdgcn_perm(t1, 0x64646464u, 0x00070006u)) + z);
+            }
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+                acc[4 * d + jj] =
+                    __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a[jj]), bx, acc[4 * d + jj], 0, 0, 0);
+        }
+    };
+    // A buffer is refilled with the block after next as soon as it has been
+    // consumed.  The prefetch past the wave's last block re-reads that block
+    // (an L2 hit) instead of branching around the loads: a load under a
+    // branch would make the wait for the current block cover it too.
+    for (int r0 = wb; r0 < we; r0 += 2 * kBlockRows) {
+        compute_block(Ra, r0);
+        if (r0 + kBlockRows >= we) break;
+        load_block(min(r0 + 2 * kBlockRows, we - kBlockRows), Ra);
+        compute_block(Rb, r0 + kBlockRows);
+        if (r0 + 2 * kBlockRows >= we) break;
+        load_block(min(r0 + 3 * kBlockRows, we - kBlockRows), Rb);
+    }
+
+    // acc[j][i] of lane (g, c) is column 16 (4g + i) + j for split column c;
+    // hi (c) and lo (c + 8) of batch row c meet with a rotation by 8 lanes
+    // within each row of 16 (DPP row_ror:8).
+    __syncthreads();  // every wave is done with the split activations
+    float *red = reinterpret_cast<float *>(lds);
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float v = acc[j][i];
+            const float o = __builtin_bit_cast(
+                float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
+            if (c < MAXB) red[red_index(wave, c, 16 * (4 * g + i) + j)] = v + o;
+        }
+    __syncthreads();
+    auto strip_value = [&](int bi, int cc) {
+        const float s = (red[red_index(0, bi, cc)] + red[red_index(1, bi, cc)]) +
+                        (red[red_index(2, bi, cc)] + red[red_index(3, bi, cc)]);
+        return ldexpf(s, -ex);
+    };
+    store_strip<MAXB, SCOLS>(p, strip, slice, nb, col0, &last_flag, strip_value);
 }
 
-template <typename WT, int MAXB>
-void launch_one(const GemvParams &p, bool vec, hipStream_t s) {
-    // int8 at b >= 4 is VALU-heavy (b FMAs per weight): fewer rows per
-    // batch keep registers low enough for two waves per SIMD.
-    constexpr int U = (sizeof(WT) == 1 && MAXB >= 4) ? 4 : 8;
+template <int MAXB>
+void launch(const GemvParams &q, bool vec, hipStream_t s) {
+    const dim3 grid((unsigned)(q.nstrips * q.slices)), block(kThreads);
+    if (vec)
+        hipLaunchKernelGGL((gemv_w8_mfma_kernel<MAXB, true>), grid, block, 0, s, q);
+    else
+        hipLaunchKernelGGL((gemv_w8_mfma_kernel<MAXB, false>), grid, block, 0, s, q);
+}
+
+}  // namespace w8mf
+
+template <int MAXB>
+void launch_f32(const GemvParams &p, bool vec, hipStream_t s) {
+    constexpr int U = 8;
     const dim3 grid((unsigned)(p.nstrips * p.slices)), block(kThreads);
     if (vec)
-        hipLaunchKernelGGL((gemv_kernel<WT, MAXB, U, true>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((gemv_f32_kernel<MAXB, U, true>), grid, block, 0, s, p);
     else
-        hipLaunchKernelGGL((gemv_kernel<WT, MAXB, U, false>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((gemv_f32_kernel<MAXB, U, false>), grid, block, 0, s, p);
 }
 
-// Rows per K-slice: 512 (measured best at the BASELINE shapes for both
-// weight types: each wave then runs 4 whole batches of 32 rows), halved
+// Rows per K-slice of the int8 MFMA kernel: the longest slice, up to
+// kMaxSlice, that still gives at least 192 workgroups.  Its fixed cost per
+// workgroup (staging the activations, reducing the waves, publishing the
+// partial) favours long slices: at [4096, 14336] 1024 rows measured
+// 17-19 us for 1-8 batch rows against 18-21 us at 512 and 26-41 us at 128.
+int64_t choose_kslice_w8(int64_t nstrips, int64_t k) {
+    int64_t ks = kMaxSlice;
+    while (ks > 128 && nstrips * ((k + ks - 1) / ks) < 192) ks /= 2;
+    return ks;
+}
+
+// Rows per K-slice of the fp32 kernel: 512 (best measured at W [4096, 14336]:
+// 44.8 us at 1 batch row, against 46.6 at 256 and 45.3 at 1024), halved
 // while there would be fewer than ~448 workgroups (each CU streams only
 // ~30-45 GB/s, so all CUs must take part), at least 128 rows, a multiple of
 // 128 -- and enlarged so the partial strips written and read back stay
-// under ~10% of the weight bytes (5% for groups of 8 batch rows, whose
-// VALU-heavy slices gain more from fewer, longer slices), up to kMaxSlice.
+// under ~10% of the weight bytes (5% for groups of 8 batch rows), up to
+// kMaxSlice.
 int64_t choose_kslice(int64_t nstrips, int64_t k, int64_t b, size_t wsize) {
     int64_t ks = 512;
     while (ks > 128 && nstrips * ((k + ks - 1) / ks) < 448) ks /= 2;
@@ -306,7 +588,10 @@ int launch_gemv(const float *x, const void *w, const float *scales, const int8_t
     p.k = k;
     p.n = n;
     p.nstrips = (n + SCOLS - 1) / SCOLS;
-    p.kslice = k > 0 ? choose_kslice(p.nstrips, k, b, sizeof(WT)) : 16;
+    if constexpr (sizeof(WT) == 1)
+        p.kslice = k > 0 ? choose_kslice_w8(p.nstrips, k) : 128;
+    else
+        p.kslice = k > 0 ? choose_kslice(p.nstrips, k, b, sizeof(WT)) : 16;
     p.slices = k > 0 ? (k + p.kslice - 1) / p.kslice : 1;
     if (p.slices > 1) {
         const int64_t gb = b < 8 ? b : 8;
@@ -324,14 +609,23 @@ int launch_gemv(const float *x, const void *w, const float *scales, const int8_t
         q.x = x + b0 * k;
         q.y = y + b0 * n;
         q.b = nbg;
-        if (nbg == 1)
-            launch_one<WT, 1>(q, vec, s);
+        if constexpr (sizeof(WT) == 1) {
+            if (nbg == 1)
+                w8mf::launch<1>(q, vec, s);
+            else if (nbg == 2)
+                w8mf::launch<2>(q, vec, s);
+            else if (nbg <= 4)
+                w8mf::launch<4>(q, vec, s);
+            else
+                w8mf::launch<8>(q, vec, s);
+        } else if (nbg == 1)
+            launch_f32<1>(q, vec, s);
         else if (nbg == 2)
-            launch_one<WT, 2>(q, vec, s);
+            launch_f32<2>(q, vec, s);
         else if (nbg <= 4)
-            launch_one<WT, 4>(q, vec, s);
+            launch_f32<4>(q, vec, s);
         else
-            launch_one<WT, 8>(q, vec, s);
+            launch_f32<8>(q, vec, s);
         GFH_TRY(check_launch(sizeof(WT) == 1 ? "gemv_w8" : "gemv_f32"));
     }
     return GFH_SUCCESS;

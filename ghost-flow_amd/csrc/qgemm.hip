@@ -537,8 +537,8 @@ int launch_tiles(QParams p, hipStream_t s) {
 
 // ---- skinny M (decode): weights streamed from HBM straight into MFMA ----------
 //
-// For M <= 64 the layer is HBM-bound (the weight is read once, 45 MB at the
-// BASELINE shape).  W [N, K] is K-contiguous, which is exactly the per-lane
+// For M <= 64 the layer is HBM-bound (the weight is read once, 45 MB for
+// W [11008, 4096]).  W [N, K] is K-contiguous, which is exactly the per-lane
 // operand layout of v_mfma_i32_16x16x64_i8 (lane l: row / column l % 16,
 // 16 consecutive k bytes), so weight fragments are plain 16-byte global
 // loads straight into registers, and so are the fragments of x (at most
