@@ -248,15 +248,27 @@ __global__ __launch_bounds__(kThreads) void sgemm_mfma_kernel(SgemmParams p) {
         }
 }
 
-template <bool TA, bool TB, bool VEC>
-int launch_variant(const SgemmParams &p0, int64_t batch, hipStream_t s) {
-    constexpr int BM = 128, BN = 128, BK = 32, WM = 64, WN = 64;
+template <int BM, int BN, int BK, int WM, int WN, bool TA, bool TB, bool VEC>
+int launch_tiles(const SgemmParams &p0, int64_t batch, hipStream_t s) {
     SgemmParams p = p0;
     p.tiles_m = (int)((p.m + BM - 1) / BM);
     p.tiles_n = (int)((p.n + BN - 1) / BN);
     dim3 grid((unsigned)(p.tiles_m * p.tiles_n), 1, (unsigned)batch);
     hipLaunchKernelGGL((sgemm_mfma_kernel<BM, BN, BK, WM, WN, TA, TB, VEC>), grid, dim3(kThreads), 0, s, p);
     return check_launch("sgemm");
+}
+
+// Tile size by problem size: 128 x 128 tiles (64 x 64 per wave) give the
+// most MFMA work per LDS byte, but a launch needs hundreds of workgroups to
+// keep all 1024 SIMDs busy.  Measured (square, NN): 1024^3 88.7 us at
+// 128x128 (64 workgroups), 50.4 at 128x64, 30.9 at 64x64 with BK = 64;
+// 2048^3 170 / 159 / 173 us; 4096^3 1104 / 1221 / 1318 us.
+template <bool TA, bool TB, bool VEC>
+int launch_variant(const SgemmParams &p, int64_t batch, hipStream_t s) {
+    const int64_t t128 = ((p.m + 127) / 128) * ((p.n + 127) / 128) * batch;
+    if (t128 >= 512) return launch_tiles<128, 128, 32, 64, 64, TA, TB, VEC>(p, batch, s);
+    if (t128 >= 128) return launch_tiles<128, 64, 32, 64, 32, TA, TB, VEC>(p, batch, s);
+    return launch_tiles<64, 64, 64, 32, 32, TA, TB, VEC>(p, batch, s);
 }
 
 }  // namespace

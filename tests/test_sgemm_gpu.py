@@ -38,11 +38,13 @@ def test_reference_known_answers(torch_dev):
 
 
 @pytest.mark.parametrize("m,k,n", [(1, 1, 1), (7, 3, 5), (33, 29, 17), (64, 64, 64), (128, 200, 96),
-                                   (257, 300, 131), (1024, 1024, 1024)])
+                                   (257, 300, 131), (1024, 1024, 1024), (1500, 300, 1300), (2048, 96, 2048)])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_integer_inputs_bit_exact(torch_dev, m, k, n, ta, tb):
     """|a|,|b| <= 8 integers: every partial sum < 2^24 is exact, so the GPU
-    must equal the oracle bit for bit whatever the summation order."""
+    must equal the oracle bit for bit whatever the summation order.  The
+    shapes cover all three tilings (64x64 below 128 tiles of 128x128,
+    128x64 up to 512 of them, 128x128 beyond) with ragged edges."""
     gh, O = _gh(), _oracle()
     rng = np.random.default_rng(m * 1000003 + k * 1009 + n)
     a = rng.integers(-8, 9, size=(m, k)).astype(np.float32)
