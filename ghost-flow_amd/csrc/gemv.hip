@@ -52,7 +52,15 @@ struct GemvParams {
     int64_t kslice;  // rows per slice: a multiple of 16, at most kMaxSlice
 };
 
-constexpr int kMaxSlice = 1024;
+constexpr int kMaxSlice = 1024;  // int8 kernel
+
+// Rows per slice the fp32 kernel can stage: its activations take
+// rows x MAXB floats of LDS (static, so it also bounds the workgroups per
+// CU).  4096 rows (16 per thread) up to 4 batch rows -- one slice for
+// K = 4096 -- and 1024 for 8 batch rows, whose slices are split anyway:
+// 2048 rows there (64 KB) measured 55.1 us against 50.8 at 1024 (32 KB).
+template <int MAXB>
+constexpr int f32_max_rows() { return MAXB >= 8 ? 1024 : 4096; }
 
 // Writes this workgroup's strip -- value(bi, c) for batch row bi < nb and
 // strip column c -- to y when K is not split.  Otherwise publishes it as the
@@ -137,7 +145,8 @@ __global__ __launch_bounds__(kThreads) void gemv_f32_kernel(GemvParams p) {
     constexpr int EPL = 4;                    // floats per lane per load
     constexpr int SCOLS = kStripBytes / 4;    // strip columns
     constexpr int kStep = 4 * U;              // rows per wave step
-    __shared__ __attribute__((aligned(16))) float xs[kMaxSlice * MAXB];  // this slice's x, [row][batch]
+    constexpr int kMaxRows = f32_max_rows<MAXB>();
+    __shared__ __attribute__((aligned(16))) float xs[kMaxRows * MAXB];  // this slice's x, [row][batch]
     __shared__ float red[kWaves][MAXB][SCOLS];
     __shared__ int last_flag;
 
@@ -161,7 +170,7 @@ __global__ __launch_bounds__(kThreads) void gemv_f32_kernel(GemvParams p) {
     // Activations first, from clamped in-range indices: loads complete in
     // issue order, so the staging below waits only for these while the
     // first weight batch (issued next) streams in behind them.
-    constexpr int kRowsPerThread = kMaxSlice / kThreads;
+    constexpr int kRowsPerThread = kMaxRows / kThreads;
     float xv[kRowsPerThread][MAXB];
 #pragma unroll
     for (int i = 0; i < kRowsPerThread; ++i) {
@@ -557,76 +566,53 @@ int64_t choose_kslice_w8(int64_t nstrips, int64_t k) {
     return ks;
 }
 
-// Rows per K-slice of the fp32 kernel: 512 (best measured at W [4096, 14336]:
-// 44.8 us at 1 batch row, against 46.6 at 256 and 45.3 at 1024), halved
-// while there would be fewer than ~448 workgroups (each CU streams only
-// ~30-45 GB/s, so all CUs must take part), at least 128 rows, a multiple of
-// 128 -- and enlarged so the partial strips written and read back stay
-// under ~10% of the weight bytes (5% for groups of 8 batch rows), up to
-// kMaxSlice.
-int64_t choose_kslice(int64_t nstrips, int64_t k, int64_t b, size_t wsize) {
+// Rows per K-slice of the fp32 kernel.  All of K in one slice (up to
+// f32_max_rows) when the strips alone give at least 192 workgroups: no
+// partial strips, no arrival count, no last-arriver sum.  Measured at
+// W [4096, 14336] (224 strips), 1 batch row: 41.5 us in one slice against
+// 44.1 / 46.1 / 46.7 us in 2 / 4 / 8.  Otherwise 512 rows, halved while
+// there would be fewer than ~448 workgroups (each CU streams only ~30-45
+// GB/s, so all CUs must take part), at least 128 rows, a multiple of 128 --
+// and enlarged so the partial strips written and read back stay under ~10%
+// of the weight bytes (5% for groups of 8 batch rows), up to max_rows.
+int64_t choose_kslice_f32(int64_t nstrips, int64_t k, int64_t nb, int64_t max_rows) {
+    if (nstrips >= 192 && k <= max_rows) return k;
     int64_t ks = 512;
     while (ks > 128 && nstrips * ((k + ks - 1) / ks) < 448) ks /= 2;
-    const int64_t nb = b < 8 ? b : 8;
     const double cap = nb >= 8 ? 0.05 : 0.10;
-    const int64_t max_slices = (int64_t)(cap * (double)k * (double)wsize / (8.0 * (double)nb));
+    const int64_t max_slices = (int64_t)(cap * (double)k * 4.0 / (8.0 * (double)nb));
     if (max_slices >= 1) ks = std::max(ks, (k + max_slices - 1) / max_slices);
     else ks = k;
     ks = (ks + 127) & ~(int64_t)127;
-    return std::min<int64_t>(ks, kMaxSlice);
+    return std::min<int64_t>(ks, max_rows);
 }
 
-template <typename WT>
-int launch_gemv(const float *x, const void *w, const float *scales, const int8_t *zps, float *y, int64_t b,
-                int64_t k, int64_t n, hipStream_t s) {
-    constexpr int SCOLS = kStripBytes / sizeof(WT);
-    GemvParams p{};
-    p.x = x;
-    p.w = w;
-    p.scales = scales;
-    p.zps = zps;
-    p.k = k;
-    p.n = n;
-    p.nstrips = (n + SCOLS - 1) / SCOLS;
-    if constexpr (sizeof(WT) == 1)
-        p.kslice = k > 0 ? choose_kslice_w8(p.nstrips, k) : 128;
-    else
-        p.kslice = k > 0 ? choose_kslice(p.nstrips, k, b, sizeof(WT)) : 16;
-    p.slices = k > 0 ? (k + p.kslice - 1) / p.kslice : 1;
-    if (p.slices > 1) {
-        const int64_t gb = b < 8 ? b : 8;
+// Sets the slicing of one batch group and, for more than one slice, its
+// per-stream partial workspace and arrival counters.  Groups of a call run
+// one after another on the stream, so they share the workspace.
+int set_slices(GemvParams &q, int64_t kslice, hipStream_t s) {
+    q.kslice = kslice;
+    q.slices = q.k > 0 ? (q.k + kslice - 1) / kslice : 1;
+    q.part = nullptr;
+    q.counters = nullptr;
+    if (q.slices > 1) {
         void *ws = nullptr;
-        GFH_TRY(stream_workspace(s, sizeof(float) * (size_t)(p.slices * gb * n), &ws));
-        p.part = static_cast<float *>(ws);
-        GFH_TRY(stream_counters(s, (size_t)p.nstrips, &p.counters));
+        GFH_TRY(stream_workspace(s, sizeof(float) * (size_t)(q.slices * q.b * q.n), &ws));
+        q.part = static_cast<float *>(ws);
+        GFH_TRY(stream_counters(s, (size_t)q.nstrips, &q.counters));
     }
-    const bool vec = (n * sizeof(WT)) % 16 == 0 && aligned16(w);
-    // The batch is processed in groups of at most 8 rows; groups run one
-    // after another on the stream, so they share the workspace.
+    return GFH_SUCCESS;
+}
+
+// The batch is processed in groups of at most 8 rows.
+template <typename F>
+int for_batch_groups(const GemvParams &p, const float *x, float *y, int64_t b, F launch_group) {
     for (int64_t b0 = 0; b0 < b; b0 += 8) {
         GemvParams q = p;
-        const int64_t nbg = (b - b0) < 8 ? (b - b0) : 8;
-        q.x = x + b0 * k;
-        q.y = y + b0 * n;
-        q.b = nbg;
-        if constexpr (sizeof(WT) == 1) {
-            if (nbg == 1)
-                w8mf::launch<1>(q, vec, s);
-            else if (nbg == 2)
-                w8mf::launch<2>(q, vec, s);
-            else if (nbg <= 4)
-                w8mf::launch<4>(q, vec, s);
-            else
-                w8mf::launch<8>(q, vec, s);
-        } else if (nbg == 1)
-            launch_f32<1>(q, vec, s);
-        else if (nbg == 2)
-            launch_f32<2>(q, vec, s);
-        else if (nbg <= 4)
-            launch_f32<4>(q, vec, s);
-        else
-            launch_f32<8>(q, vec, s);
-        GFH_TRY(check_launch(sizeof(WT) == 1 ? "gemv_w8" : "gemv_f32"));
+        q.x = x + b0 * p.k;
+        q.y = y + b0 * p.n;
+        q.b = (b - b0) < 8 ? (b - b0) : 8;
+        GFH_TRY(launch_group(q));
     }
     return GFH_SUCCESS;
 }
@@ -634,12 +620,53 @@ int launch_gemv(const float *x, const void *w, const float *scales, const int8_t
 }  // namespace
 
 int launch_gemv_f32(const float *x, const float *w, float *y, int64_t b, int64_t k, int64_t n, hipStream_t s) {
-    return launch_gemv<float>(x, w, nullptr, nullptr, y, b, k, n, s);
+    GemvParams p{};
+    p.w = w;
+    p.k = k;
+    p.n = n;
+    p.nstrips = (n + kStripBytes / 4 - 1) / (kStripBytes / 4);
+    const bool vec = n % 4 == 0 && aligned16(w);
+    return for_batch_groups(p, x, y, b, [&](GemvParams &q) {
+        const int maxb = q.b == 1 ? 1 : q.b == 2 ? 2 : q.b <= 4 ? 4 : 8;
+        const int64_t max_rows = maxb == 1   ? f32_max_rows<1>()
+                                 : maxb == 2 ? f32_max_rows<2>()
+                                 : maxb == 4 ? f32_max_rows<4>()
+                                             : f32_max_rows<8>();
+        GFH_TRY(set_slices(q, k > 0 ? choose_kslice_f32(q.nstrips, k, q.b, max_rows) : 32, s));
+        if (maxb == 1)
+            launch_f32<1>(q, vec, s);
+        else if (maxb == 2)
+            launch_f32<2>(q, vec, s);
+        else if (maxb == 4)
+            launch_f32<4>(q, vec, s);
+        else
+            launch_f32<8>(q, vec, s);
+        return check_launch("gemv_f32");
+    });
 }
 
 int launch_gemv_w8(const float *x, const int8_t *qw, const float *scales, const int8_t *zps, float *y, int64_t b,
                    int64_t k, int64_t n, hipStream_t s) {
-    return launch_gemv<int8_t>(x, qw, scales, zps, y, b, k, n, s);
+    GemvParams p{};
+    p.w = qw;
+    p.scales = scales;
+    p.zps = zps;
+    p.k = k;
+    p.n = n;
+    p.nstrips = (n + kStripBytes - 1) / kStripBytes;
+    const bool vec = n % 16 == 0 && aligned16(qw);
+    return for_batch_groups(p, x, y, b, [&](GemvParams &q) {
+        GFH_TRY(set_slices(q, k > 0 ? choose_kslice_w8(q.nstrips, k) : 128, s));
+        if (q.b == 1)
+            w8mf::launch<1>(q, vec, s);
+        else if (q.b == 2)
+            w8mf::launch<2>(q, vec, s);
+        else if (q.b <= 4)
+            w8mf::launch<4>(q, vec, s);
+        else
+            w8mf::launch<8>(q, vec, s);
+        return check_launch("gemv_w8");
+    });
 }
 
 }  // namespace gfh
