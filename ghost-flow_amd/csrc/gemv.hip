@@ -27,6 +27,7 @@
 //    partials in slice order and writes y -- deterministic, one launch.  The
 //    counter is returned to 0 by that last workgroup.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -71,11 +72,11 @@ constexpr int f32_max_rows() { return MAXB >= 8 ? 1024 : 4096; }
 // writeback or invalidate is needed -- only that the partial stores have
 // completed (vmcnt 0) before the arrival is counted.  The counter is
 // returned to 0 by that last workgroup.
-template <int MAXB, int SCOLS, typename F>
+template <int MAXB, int SCOLS, int NT = kThreads, typename F>
 __device__ __forceinline__ void store_strip(const GemvParams &p, int64_t strip, int64_t slice, int64_t nb,
                                             int64_t col0, int *last_flag, F value) {
     if (p.slices == 1) {
-        for (int t = threadIdx.x; t < MAXB * SCOLS; t += kThreads) {
+        for (int t = threadIdx.x; t < MAXB * SCOLS; t += NT) {
             const int bi = t / SCOLS, c = t % SCOLS;
             if (bi >= nb || col0 + c >= p.n) continue;
             p.y[bi * p.n + col0 + c] = value(bi, c);
@@ -83,7 +84,7 @@ __device__ __forceinline__ void store_strip(const GemvParams &p, int64_t strip, 
         return;
     }
 
-    for (int t = threadIdx.x; t < MAXB * SCOLS; t += kThreads) {
+    for (int t = threadIdx.x; t < MAXB * SCOLS; t += NT) {
         const int bi = t / SCOLS, c = t % SCOLS;
         if (bi >= nb || col0 + c >= p.n) continue;
         __hip_atomic_store(p.part + (slice * nb + bi) * p.n + col0 + c, value(bi, c), __ATOMIC_RELAXED,
@@ -103,13 +104,13 @@ __device__ __forceinline__ void store_strip(const GemvParams &p, int64_t strip, 
     // slices at a time, before adding any of them, so the loads overlap
     // instead of paying one memory latency per output or slice; each output
     // is still summed in slice order.
-    constexpr int kOut = (MAXB * SCOLS + kThreads - 1) / kThreads;  // outputs per thread
+    constexpr int kOut = (MAXB * SCOLS + NT - 1) / NT;  // outputs per thread
     constexpr int kGroup = kOut >= 32 ? 1 : 32 / kOut;                // slices per group
     const float *src[kOut];
     float v[kOut];
 #pragma unroll
     for (int o = 0; o < kOut; ++o) {
-        const int t = threadIdx.x + o * kThreads;
+        const int t = threadIdx.x + o * NT;
         const int bi = t / SCOLS, c = t % SCOLS;
         const bool ok = t < MAXB * SCOLS && bi < nb && col0 + c < p.n;
         src[o] = ok ? p.part + bi * p.n + col0 + c : nullptr;
@@ -134,7 +135,7 @@ __device__ __forceinline__ void store_strip(const GemvParams &p, int64_t strip, 
 #pragma unroll
     for (int o = 0; o < kOut; ++o)
         if (src[o]) {
-            const int t = threadIdx.x + o * kThreads;
+            const int t = threadIdx.x + o * NT;
             p.y[(t / SCOLS) * p.n + col0 + t % SCOLS] = v[o];
         }
     if (threadIdx.x == 0) __hip_atomic_store(p.counters + strip, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -313,8 +314,10 @@ constexpr int kXBytes = 16 * kXStride * 2;
 // 2 words of padding per 64 columns and a 264-word row put the 32 lanes
 // that store together on 32 distinct banks.
 constexpr int kRedStride = 264;
-constexpr int kRedBytes = kWaves * 8 * kRedStride * 4;
-constexpr int kLdsBytes = kXBytes > kRedBytes ? kXBytes : kRedBytes;
+template <int NW>
+constexpr int lds_bytes() {
+    return kXBytes > NW * 8 * kRedStride * 4 ? kXBytes : NW * 8 * kRedStride * 4;
+}
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half2 __attribute__((ext_vector_type(2)));
@@ -322,12 +325,13 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int red_index(int w, int b, int col) { return (w * 8 + b) * kRedStride + col + 2 * (col >> 6); }
 
-template <int MAXB, bool VEC>
-__global__ __launch_bounds__(kThreads, VEC ? 2 : 1) void gemv_w8_mfma_kernel(GemvParams p) {
+template <int MAXB, bool VEC, int NW>
+__global__ __launch_bounds__(64 * NW, (VEC && NW == 4) ? 2 : 1) void gemv_w8_mfma_kernel(GemvParams p) {
     constexpr int SCOLS = kStripBytes;
-    __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsBytes];
+    constexpr int NT = 64 * NW;
+    __shared__ __attribute__((aligned(16))) unsigned char lds[lds_bytes<NW>()];
     __shared__ __attribute__((aligned(16))) uint32_t zph[kMaxSlice / 2];  // -(1152 + zp) of row pairs, f16x2
-    __shared__ float amax_red[kWaves];
+    __shared__ float amax_red[NW];
     __shared__ int last_flag;
     _Float16 *xsh = reinterpret_cast<_Float16 *>(lds);
 
@@ -343,7 +347,7 @@ __global__ __launch_bounds__(kThreads, VEC ? 2 : 1) void gemv_w8_mfma_kernel(Gem
     const int rows = (int)min(p.kslice, p.k - s_lo);
     const int rows32 = (rows + kBlockRows - 1) & ~(kBlockRows - 1);
     if (rows <= 0) {  // K == 0: y = 0, and no row may be read
-        store_strip<MAXB, SCOLS>(p, strip, slice, nb, col0, &last_flag, [](int, int) { return 0.f; });
+        store_strip<MAXB, SCOLS, NT>(p, strip, slice, nb, col0, &last_flag, [](int, int) { return 0.f; });
         return;
     }
 
@@ -353,11 +357,11 @@ __global__ __launch_bounds__(kThreads, VEC ? 2 : 1) void gemv_w8_mfma_kernel(Gem
     // The loads are unconditional, from clamped in-range indices, and the
     // values are selected afterwards: a load under a lane condition would be
     // waited for before the branches rejoin, one memory latency per load.
-    constexpr int kRowsPerThread = kMaxSlice / kThreads;
+    constexpr int kRowsPerThread = kMaxSlice / NT;
     float xv[kRowsPerThread][MAXB], sv[kRowsPerThread];
 #pragma unroll
     for (int i = 0; i < kRowsPerThread; ++i) {
-        const int rr = min((int)threadIdx.x + kThreads * i, rows - 1);
+        const int rr = min((int)threadIdx.x + NT * i, rows - 1);
         sv[i] = p.scales[s_lo + rr];
 #pragma unroll
         for (int bi = 0; bi < MAXB; ++bi) xv[i][bi] = p.x[min<int64_t>(bi, nb - 1) * p.k + s_lo + rr];
@@ -365,15 +369,15 @@ __global__ __launch_bounds__(kThreads, VEC ? 2 : 1) void gemv_w8_mfma_kernel(Gem
     // Zero points of row pairs threadIdx.x + 256 u.  Without zero points
     // the (ignored) bytes come from the scales, so that no branch guards
     // these loads either.
-    constexpr int kPairsPerThread = kMaxSlice / 2 / kThreads;
+    constexpr int kPairsPerThread = kMaxSlice / 2 / NT;
     const int8_t *zsrc = p.zps ? p.zps : reinterpret_cast<const int8_t *>(p.scales);
     int zr[kPairsPerThread][2];
 #pragma unroll
     for (int u = 0; u < kPairsPerThread; ++u)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) zr[u][h] = zsrc[s_lo + min(2 * ((int)threadIdx.x + kThreads * u) + h, rows - 1)];
+        for (int h = 0; h < 2; ++h) zr[u][h] = zsrc[s_lo + min(2 * ((int)threadIdx.x + NT * u) + h, rows - 1)];
 
-    const int per = ((rows32 / kBlockRows + kWaves - 1) / kWaves) * kBlockRows;
+    const int per = ((rows32 / kBlockRows + NW - 1) / NW) * kBlockRows;
     const int wb = min(wave * per, rows32), we = min(wb + per, rows32);
     const int64_t col = col0 + 16 * c;
     // Loads are unconditional so that the wait for a block never has to wait
@@ -413,7 +417,7 @@ __global__ __launch_bounds__(kThreads, VEC ? 2 : 1) void gemv_w8_mfma_kernel(Gem
     // condition lets the compiler sink its load into a branch again.
 #pragma unroll
     for (int i = 0; i < kRowsPerThread; ++i) {
-        const int r = threadIdx.x + kThreads * i;
+        const int r = threadIdx.x + NT * i;
 #pragma unroll
         for (int bi = 0; bi < MAXB; ++bi) {
             const uint32_t keep = (r < rows && bi < nb) ? 0xffffffffu : 0u;
@@ -424,7 +428,7 @@ __global__ __launch_bounds__(kThreads, VEC ? 2 : 1) void gemv_w8_mfma_kernel(Gem
     for (int u = 0; u < kPairsPerThread; ++u)
 #pragma unroll
         for (int h = 0; h < 2; ++h)
-            zr[u][h] &= (p.zps && 2 * ((int)threadIdx.x + kThreads * u) + h < rows) ? -1 : 0;
+            zr[u][h] &= (p.zps && 2 * ((int)threadIdx.x + NT * u) + h < rows) ? -1 : 0;
 
     // Stage: power-of-two prescale, f16 hi/lo split into columns [n][row]
     // (zero past the slice), and the zero-point pairs.  Split columns of
@@ -440,14 +444,16 @@ __global__ __launch_bounds__(kThreads, VEC ? 2 : 1) void gemv_w8_mfma_kernel(Gem
     if (lane == 0) amax_red[wave] = amax;
 #pragma unroll
     for (int u = 0; u < kPairsPerThread; ++u) {
-        const int pr = (int)threadIdx.x + kThreads * u;
+        const int pr = (int)threadIdx.x + NT * u;
         if (2 * pr < rows32) {
             const half2 z = {(_Float16)(-(1152 + zr[u][0])), (_Float16)(-(1152 + zr[u][1]))};
             zph[pr] = __builtin_bit_cast(uint32_t, z);
         }
     }
     __syncthreads();
-    amax = fmaxf(fmaxf(amax_red[0], amax_red[1]), fmaxf(amax_red[2], amax_red[3]));
+    amax = amax_red[0];
+#pragma unroll
+    for (int w2 = 1; w2 < NW; ++w2) amax = fmaxf(amax, amax_red[w2]);
     int ex = 0;
     if (amax > 0.f && amax <= 3.4e38f) {
         (void)frexpf(amax, &ex);  // amax = f 2^ex, f in [0.5, 1)
@@ -455,7 +461,7 @@ __global__ __launch_bounds__(kThreads, VEC ? 2 : 1) void gemv_w8_mfma_kernel(Gem
     }
 #pragma unroll
     for (int i = 0; i < kRowsPerThread; ++i) {
-        const int r = threadIdx.x + kThreads * i;
+        const int r = threadIdx.x + NT * i;
         if (r >= rows32) continue;
 #pragma unroll
         for (int bi = 0; bi < MAXB; ++bi) {
@@ -527,20 +533,21 @@ __global__ __launch_bounds__(kThreads, VEC ? 2 : 1) void gemv_w8_mfma_kernel(Gem
         }
     __syncthreads();
     auto strip_value = [&](int bi, int cc) {
-        const float s = (red[red_index(0, bi, cc)] + red[red_index(1, bi, cc)]) +
-                        (red[red_index(2, bi, cc)] + red[red_index(3, bi, cc)]);
+        float s = red[red_index(0, bi, cc)];
+#pragma unroll
+        for (int w2 = 1; w2 < NW; ++w2) s += red[red_index(w2, bi, cc)];
         return ldexpf(s, -ex);
     };
-    store_strip<MAXB, SCOLS>(p, strip, slice, nb, col0, &last_flag, strip_value);
+    store_strip<MAXB, SCOLS, NT>(p, strip, slice, nb, col0, &last_flag, strip_value);
 }
 
-template <int MAXB>
+template <int MAXB, int NW = 4>
 void launch(const GemvParams &q, bool vec, hipStream_t s) {
-    const dim3 grid((unsigned)(q.nstrips * q.slices)), block(kThreads);
+    const dim3 grid((unsigned)(q.nstrips * q.slices)), block(64 * NW);
     if (vec)
-        hipLaunchKernelGGL((gemv_w8_mfma_kernel<MAXB, true>), grid, block, 0, s, q);
+        hipLaunchKernelGGL((gemv_w8_mfma_kernel<MAXB, true, NW>), grid, block, 0, s, q);
     else
-        hipLaunchKernelGGL((gemv_w8_mfma_kernel<MAXB, false>), grid, block, 0, s, q);
+        hipLaunchKernelGGL((gemv_w8_mfma_kernel<MAXB, false, NW>), grid, block, 0, s, q);
 }
 
 }  // namespace w8mf
@@ -657,14 +664,27 @@ int launch_gemv_w8(const float *x, const int8_t *qw, const float *scales, const 
     const bool vec = n % 16 == 0 && aligned16(qw);
     return for_batch_groups(p, x, y, b, [&](GemvParams &q) {
         GFH_TRY(set_slices(q, k > 0 ? choose_kslice_w8(q.nstrips, k) : 128, s));
+        // At most one workgroup per CU: 8 waves each, so that twice the weight
+        // blocks are in flight while the activations are staged (at
+        // [4096, 14336] and 1024-row slices, 1-8 batch rows: 16.6-18.2 us
+        // against 17.0-19.4 with 4 waves; with two workgroups per CU, 4
+        // waves are faster).
+        const bool wide = q.nstrips * q.slices <= 256;
+        auto go = [&](auto maxb) {
+            constexpr int MB = decltype(maxb)::value;
+            if (wide)
+                w8mf::launch<MB, 8>(q, vec, s);
+            else
+                w8mf::launch<MB, 4>(q, vec, s);
+        };
         if (q.b == 1)
-            w8mf::launch<1>(q, vec, s);
+            go(std::integral_constant<int, 1>{});
         else if (q.b == 2)
-            w8mf::launch<2>(q, vec, s);
+            go(std::integral_constant<int, 2>{});
         else if (q.b <= 4)
-            w8mf::launch<4>(q, vec, s);
+            go(std::integral_constant<int, 4>{});
         else
-            w8mf::launch<8>(q, vec, s);
+            go(std::integral_constant<int, 8>{});
         return check_launch("gemv_w8");
     });
 }
