@@ -210,16 +210,29 @@ def comp_sgemm(lib, torch, n):
 
 
 def comp_qlinear(lib, torch, m, n, k, per_tensor=True):
+    """Config 3: W ~ N(0, 0.02) quantized per channel (symmetric), x ~ N(0, 1)
+    quantized per tensor (asymmetric), as DynamicQuantization does, with this
+    library's own quantize kernels (torch only draws the normal samples)."""
     dev = torch.device("cuda:0")
-    qx = torch.randint(-128, 128, (m, k), dtype=torch.int8, device=dev)
-    sx = torch.full((1 if per_tensor else m,), 0.02, device=dev)
-    zx = torch.full((1 if per_tensor else m,), -3, dtype=torch.int8, device=dev)
+    gh = lib.gh
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    x = torch.randn((m, k), device=dev, generator=g)
+    if per_tensor:
+        qx, sx, zx = gh.quantize_per_tensor(x, symmetric=False)
+    else:
+        qx, sx, zx = gh.quantize_per_channel(x, symmetric=True)
+    del x
     # rotate weight copies when the working set would sit in the MALL
     wbytes = n * k
     ncopy = max(1, min(16, -(-2 * MALL_BYTES // wbytes))) if m <= 256 else 1
-    qws = [torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev) for _ in range(ncopy)]
-    sw = torch.rand((n,), device=dev) * 1e-3
-    rs = [lib.gh.qweight_rowsum(q) for q in qws]
+    qws = []
+    for _ in range(ncopy):
+        w = torch.randn((n, k), device=dev, generator=g) * 0.02
+        qw, sw, _zw = gh.quantize_per_channel(w, symmetric=True)
+        qws.append(qw)
+        del w
+    rs = [gh.qweight_rowsum(q) for q in qws]
     y = torch.empty((m, n), device=dev)
     s = torch.cuda.current_stream(dev).cuda_stream
     L = lib.L

@@ -204,11 +204,10 @@ __global__ __launch_bounds__(kThreads) void qlinear_mfma_kernel(QParams p) {
 
 // ---- MFMA tiles fed by direct-to-LDS loads (M > 64) ------------------------------
 //
-// A workgroup owns a BM x BN output tile; its 4 waves form a 2 x 2 grid of
-// (BM/2) x (BN/2) sub-tiles held as v_mfma_i32_32x32x32_i8 accumulators.
-// 256 x 256 (M >= 1024): 4 x 4 accumulators per wave (256 registers), so
-// every 16-byte LDS fragment feeds 4 MFMAs.  128 x 128 (64 < M < 1024):
-// 2 x 2 per wave.
+// A workgroup owns a BM x BN output tile; its NWM x NWN waves each hold a
+// (BM/NWM) x (BN/NWN) sub-tile as v_mfma_i32_32x32x32_i8 accumulators.
+// The dispatch runs 8 waves in a 2 x 4 grid: 256 x 256 tiles (M > 512)
+// give each wave 4 x 2 accumulators (128 registers), 128 x 128 tiles 2 x 1.
 // Operands stream through a ring of STAGES stages of BK bytes of K, filled
 // with global_load_lds_dwordx4 (global memory straight into LDS, no VGPR
 // staging); all stages but the one being consumed are in flight.  One load
@@ -261,15 +260,16 @@ __device__ __forceinline__ void interleave() {
     }
 }
 
-template <int BM, int BN, int BK, int STAGES>
+template <int BM, int BN, int BK, int STAGES, int NWM = 2, int NWN = 2>
 struct Tile {
     static_assert(BK == 64 || BK == 128, "stage depth in K");
-    static constexpr int kWM = BM / 2, kWN = BN / 2;         // wave sub-tile
+    static constexpr int kNW = NWM * NWN, kNT = 64 * kNW;   // waves, threads
+    static constexpr int kWM = BM / NWM, kWN = BN / NWN;     // wave sub-tile
     static constexpr int kFM = kWM / 32, kFN = kWN / 32;     // accumulators per wave
     static constexpr int kSteps = BK / 32;                   // MFMA k-steps per stage
     static constexpr int kChunks = BK / 16;                  // 16-byte chunks per row
     static constexpr int kRowsPerLoad = 1024 / BK;           // rows filled by one load instruction
-    static constexpr int kLA = BM * BK / 4096, kLB = BN * BK / 4096;  // load instructions per wave per stage
+    static constexpr int kLA = BM * BK / (1024 * kNW), kLB = BN * BK / (1024 * kNW);  // loads per wave per stage
     static constexpr int kLPS = kLA + kLB;
     static constexpr int kABytes = BM * BK, kBBytes = BN * BK;
     static constexpr int kStageBytes = kABytes + kBBytes;
@@ -278,15 +278,17 @@ struct Tile {
     // kWN columns) at a time; row stride kWN + 8 floats keeps the two row
     // groups of one ds_write_b32 on disjoint banks.
     static constexpr int kOutStride = kWN + 8;
-    static constexpr int kOut = 4 * (kWM / 2) * kOutStride * 4;
+    static constexpr int kOut = kNW * (kWM / 2) * kOutStride * 4;
     static constexpr int kLds = kRing > kOut ? kRing : kOut;
     static_assert(kLds <= 160 * 1024, "LDS per workgroup");
 };
 
-template <int BM, int BN, int BK, int STAGES, bool X_PER_ROW, bool WANT_ACC>
-__global__ __launch_bounds__(kThreads, ((Tile<BM, BN, BK, STAGES>::kLds > 80 * 1024) ? 1 : 2)) void qlinear_tile_kernel(
+template <int BM, int BN, int BK, int STAGES, int NWM, int NWN, bool X_PER_ROW, bool WANT_ACC>
+__global__ __launch_bounds__((Tile<BM, BN, BK, STAGES, NWM, NWN>::kNT),
+                             ((Tile<BM, BN, BK, STAGES, NWM, NWN>::kLds > 80 * 1024) ? 1 : 2)) void qlinear_tile_kernel(
     QParams p) {
-    using T = Tile<BM, BN, BK, STAGES>;
+    using T = Tile<BM, BN, BK, STAGES, NWM, NWN>;
+    constexpr int NW = T::kNW;
     constexpr int FM = T::kFM, FN = T::kFN, WM = T::kWM, WN = T::kWN;
     constexpr int RPL = T::kRowsPerLoad, CPR = T::kChunks;
     __shared__ __attribute__((aligned(1024))) int8_t lds[T::kLds];
@@ -294,8 +296,8 @@ __global__ __launch_bounds__(kThreads, ((Tile<BM, BN, BK, STAGES>::kLds > 80 * 1
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm0 = (wave >> 1) * WM;
-    const int wn0 = (wave & 1) * WN;
+    const int wm0 = (wave / NWN) * WM;
+    const int wn0 = (wave % NWN) * WN;
 
     const int nblk = p.tiles_m * p.tiles_n;
     int bid = blockIdx.x;
@@ -309,7 +311,7 @@ __global__ __launch_bounds__(kThreads, ((Tile<BM, BN, BK, STAGES>::kLds > 80 * 1
     const int64_t n0 = (int64_t)(in_group / gm) * BN;
 
     // Byte offsets, relative to the tile's first row, of this wave's load
-    // instructions: A instruction j covers tile rows wave*(BM/4) + j*RPL ..
+    // instructions: A instruction j covers tile rows wave*(BM/NW) + j*RPL ..
     // +RPL-1; lane l fills LDS slot l of that 1 KB run (row l / CPR, physical
     // chunk l % CPR) from logical chunk (l % CPR) ^ swz(row).  The host
     // guarantees BM * K < 2^32.
@@ -318,12 +320,12 @@ __global__ __launch_bounds__(kThreads, ((Tile<BM, BN, BK, STAGES>::kLds > 80 * 1
     uint32_t a_off[T::kLA], b_off[T::kLB];
 #pragma unroll
     for (int j = 0; j < T::kLA; ++j) {
-        const int r = wave * (BM / 4) + j * RPL + lane / CPR;
+        const int r = wave * (BM / NW) + j * RPL + lane / CPR;
         a_off[j] = (uint32_t)((min(m0 + r, p.m - 1) - m0) * p.k) + (uint32_t)(((lane % CPR) ^ swz<BK>(r)) * 16);
     }
 #pragma unroll
     for (int j = 0; j < T::kLB; ++j) {
-        const int r = wave * (BN / 4) + j * RPL + lane / CPR;
+        const int r = wave * (BN / NW) + j * RPL + lane / CPR;
         b_off[j] = (uint32_t)((min(n0 + r, p.n - 1) - n0) * p.k) + (uint32_t)(((lane % CPR) ^ swz<BK>(r)) * 16);
     }
     const int nk = (int)(p.k / BK);
@@ -335,11 +337,11 @@ __global__ __launch_bounds__(kThreads, ((Tile<BM, BN, BK, STAGES>::kLds > 80 * 1
         const int8_t *gb = b_base + (int64_t)t * BK;
 #pragma unroll
         for (int j = 0; j < T::kLA; ++j)
-            __builtin_amdgcn_global_load_lds((glb_ptr)(ga + a_off[j]), (lds_ptr)(la + (wave * (BM / 4) + j * RPL) * BK),
+            __builtin_amdgcn_global_load_lds((glb_ptr)(ga + a_off[j]), (lds_ptr)(la + (wave * (BM / NW) + j * RPL) * BK),
                                              16, 0, 0);
 #pragma unroll
         for (int j = 0; j < T::kLB; ++j)
-            __builtin_amdgcn_global_load_lds((glb_ptr)(gb + b_off[j]), (lds_ptr)(lb + (wave * (BN / 4) + j * RPL) * BK),
+            __builtin_amdgcn_global_load_lds((glb_ptr)(gb + b_off[j]), (lds_ptr)(lb + (wave * (BN / NW) + j * RPL) * BK),
                                              16, 0, 0);
     };
 
@@ -513,21 +515,21 @@ __global__ __launch_bounds__(kThreads, ((Tile<BM, BN, BK, STAGES>::kLds > 80 * 1
     }
 }
 
-template <int BM, int BN, int BK, int STAGES>
+template <int BM, int BN, int BK, int STAGES, int NWM = 2, int NWN = 2>
 int launch_tiles(QParams p, hipStream_t s) {
     p.tiles_m = (int)((p.m + BM - 1) / BM);
     p.tiles_n = (int)((p.n + BN - 1) / BN);
-    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n)), block(kThreads);
+    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n)), block(Tile<BM, BN, BK, STAGES, NWM, NWN>::kNT);
     if (p.x_per_row) {
         if (p.acc)
-            hipLaunchKernelGGL((qlinear_tile_kernel<BM, BN, BK, STAGES, true, true>), grid, block, 0, s, p);
+            hipLaunchKernelGGL((qlinear_tile_kernel<BM, BN, BK, STAGES, NWM, NWN, true, true>), grid, block, 0, s, p);
         else
-            hipLaunchKernelGGL((qlinear_tile_kernel<BM, BN, BK, STAGES, true, false>), grid, block, 0, s, p);
+            hipLaunchKernelGGL((qlinear_tile_kernel<BM, BN, BK, STAGES, NWM, NWN, true, false>), grid, block, 0, s, p);
     } else {
         if (p.acc)
-            hipLaunchKernelGGL((qlinear_tile_kernel<BM, BN, BK, STAGES, false, true>), grid, block, 0, s, p);
+            hipLaunchKernelGGL((qlinear_tile_kernel<BM, BN, BK, STAGES, NWM, NWN, false, true>), grid, block, 0, s, p);
         else
-            hipLaunchKernelGGL((qlinear_tile_kernel<BM, BN, BK, STAGES, false, false>), grid, block, 0, s, p);
+            hipLaunchKernelGGL((qlinear_tile_kernel<BM, BN, BK, STAGES, NWM, NWN, false, false>), grid, block, 0, s, p);
     }
     return check_launch("qlinear_i8");
 }
@@ -749,11 +751,21 @@ int launch_qlinear_i8(const QLinearDesc &d, hipStream_t s) {
     // Direct-to-LDS tiles need 16-byte aligned rows (K % 64 == 0) and 32-bit
     // row offsets inside a tile (256 * K < 2^32).
     const bool ring_ok = d.k > 0 && d.k % 64 == 0 && d.k <= (int64_t(1) << 24) && aligned16(d.qx) && aligned16(d.qw);
+    // 8 waves per workgroup (a 2 x 4 wave grid, two waves per SIMD): one
+    // wave's MFMAs run while the other waits on LDS or a barrier.  Measured
+    // against 4 waves: 4096^3 76.7 -> 69.5 us, 4096 x 11008 x 4096 234.7 ->
+    // 209.4 us; at N = 11008, K = 4096: M = 768 74.8 -> 60.8 us (256 x 256),
+    // M = 512 50.5 -> 42.5 us (128 x 128, two workgroups per CU), M = 256
+    // 27.2 -> 25.6 us (128 x 128, one per CU with a 3-deep ring).
     if (ring_ok) {
         const bool bk128 = d.k % 128 == 0;
-        if (d.m >= 1024)
-            return bk128 ? big::launch_tiles<256, 256, 128, 2>(p, s) : big::launch_tiles<256, 256, 64, 4>(p, s);
-        return bk128 ? big::launch_tiles<128, 128, 128, 3>(p, s) : big::launch_tiles<128, 128, 64, 4>(p, s);
+        if (d.m > 512)
+            return bk128 ? big::launch_tiles<256, 256, 128, 2, 2, 4>(p, s)
+                         : big::launch_tiles<256, 256, 64, 4, 2, 4>(p, s);
+        const int64_t tiles = ((d.m + 127) / 128) * ((d.n + 127) / 128);
+        if (!bk128) return big::launch_tiles<128, 128, 64, 4, 2, 4>(p, s);
+        return tiles <= 256 ? big::launch_tiles<128, 128, 128, 3, 2, 4>(p, s)
+                            : big::launch_tiles<128, 128, 128, 2, 2, 4>(p, s);
     }
     p.tiles_m = (int)((d.m + kBM - 1) / kBM);
     p.tiles_n = (int)((d.n + kBN - 1) / kBN);
