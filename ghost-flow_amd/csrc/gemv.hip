@@ -377,8 +377,15 @@ __global__ __launch_bounds__(64 * NW, (VEC && NW == 4) ? 2 : 1) void gemv_w8_mfm
 #pragma unroll
         for (int h = 0; h < 2; ++h) zr[u][h] = zsrc[s_lo + min(2 * ((int)threadIdx.x + NT * u) + h, rows - 1)];
 
-    const int per = ((rows32 / kBlockRows + NW - 1) / NW) * kBlockRows;
-    const int wb = min(wave * per, rows32), we = min(wb + per, rows32);
+    // Blocks of 32 rows go to the waves round-robin (wave w takes blocks w,
+    // w + NW, ...): a read-only probe of this pattern streamed the
+    // [4096, 14336] weight in 11.6 us against 12.8 us with contiguous row
+    // ranges per wave, whose waves also finished further apart.
+    const int nblk = rows32 / kBlockRows;
+    const int cnt = wave < nblk ? (nblk - wave + NW - 1) / NW : 0;
+    // First row of the wave's i-th block; past the last block it repeats
+    // that block (a wave without blocks gets rows that the loads clamp).
+    auto block_row = [&](int i) { return (wave + NW * min(i, max(cnt - 1, 0))) * kBlockRows; };
     const int64_t col = col0 + 16 * c;
     // Loads are unconditional so that the wait for a block never has to wait
     // for the prefetch of the next one.  Rows past the slice read its last
@@ -403,14 +410,19 @@ __global__ __launch_bounds__(64 * NW, (VEC && NW == 4) ? 2 : 1) void gemv_w8_mfm
             }
         }
     };
-    // Unconditional as well (a wave without rows re-reads the slice's last
-    // row): a branch here would make the staging below wait for these loads.
-    // The scheduling barriers keep the issue order: activations, weights,
-    // then the staging arithmetic.
+    // The wave's first kBufs blocks are requested before the staging.
+    // Unconditional as well (past the wave's blocks they re-read its last
+    // block): a branch here would make the staging below wait for these
+    // loads.  The scheduling barriers keep the issue order: activations,
+    // weights, then the staging arithmetic.  Measured at [4096, 14336] and
+    // 1024-row slices, 3 or 4 buffers were no faster than 2 with 4 waves and
+    // 1-2 us slower with 8; waiting for the activations before requesting
+    // any weights changed nothing either.
+    constexpr int kBufs = 2;
     __builtin_amdgcn_sched_barrier(0);
-    i32x4 Ra[8], Rb[8];
-    load_block(wb, Ra);
-    load_block(min(wb + kBlockRows, max(we - kBlockRows, wb)), Rb);
+    i32x4 R[kBufs][8];
+#pragma unroll
+    for (int j = 0; j < kBufs; ++j) load_block(block_row(j), R[j]);
     __builtin_amdgcn_sched_barrier(0);
 
     // Masks rather than selects: a value that is only used under a
@@ -473,7 +485,7 @@ __global__ __launch_bounds__(64 * NW, (VEC && NW == 4) ? 2 : 1) void gemv_w8_mfm
     }
     __syncthreads();
 
-    // Stream the weights in 32-row blocks, two blocks in flight.
+    // Stream the weights in 32-row blocks, kBufs blocks in flight.
     f32x4 acc[16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -504,18 +516,24 @@ __global__ __launch_bounds__(64 * NW, (VEC && NW == 4) ? 2 : 1) void gemv_w8_mfm
                     __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a[jj]), bx, acc[4 * d + jj], 0, 0, 0);
         }
     };
-    // A buffer is refilled with the block after next as soon as it has been
-    // consumed.  The prefetch past the wave's last block re-reads that block
-    // (an L2 hit) instead of branching around the loads: a load under a
-    // branch would make the wait for the current block cover it too.
-    for (int r0 = wb; r0 < we; r0 += 2 * kBlockRows) {
-        compute_block(Ra, r0);
-        if (r0 + kBlockRows >= we) break;
-        load_block(min(r0 + 2 * kBlockRows, we - kBlockRows), Ra);
-        compute_block(Rb, r0 + kBlockRows);
-        if (r0 + 2 * kBlockRows >= we) break;
-        load_block(min(r0 + 3 * kBlockRows, we - kBlockRows), Rb);
+    // While more than kBufs blocks remain, a buffer is refilled with the
+    // block kBufs ahead as soon as it has been consumed; the refills of the
+    // last such pass may re-read the wave's last block (an L2 hit) rather
+    // than branch around the loads, since a load under a branch would make
+    // the wait for the current block cover it too.  The last kBufs buffers
+    // are then consumed without refills (the conditions are wave-uniform and
+    // guard no loads).
+    int i = 0;
+    for (; i + kBufs < cnt; i += kBufs) {
+#pragma unroll
+        for (int j = 0; j < kBufs; ++j) {
+            compute_block(R[j], block_row(i + j));
+            load_block(block_row(i + j + kBufs), R[j]);
+        }
     }
+#pragma unroll
+    for (int j = 0; j < kBufs; ++j)
+        if (i + j < cnt) compute_block(R[j], block_row(i + j));
 
     // acc[j][i] of lane (g, c) is column 16 (4g + i) + j for split column c;
     // hi (c) and lo (c + 8) of batch row c meet with a rotation by 8 lanes
@@ -541,12 +559,13 @@ __global__ __launch_bounds__(64 * NW, (VEC && NW == 4) ? 2 : 1) void gemv_w8_mfm
     store_strip<MAXB, SCOLS, NT>(p, strip, slice, nb, col0, &last_flag, strip_value);
 }
 
+// NW = 8 exists only with VEC (the caller never asks for it without).
 template <int MAXB, int NW = 4>
 void launch(const GemvParams &q, bool vec, hipStream_t s) {
     const dim3 grid((unsigned)(q.nstrips * q.slices)), block(64 * NW);
     if (vec)
         hipLaunchKernelGGL((gemv_w8_mfma_kernel<MAXB, true, NW>), grid, block, 0, s, q);
-    else
+    else if constexpr (NW == 4)
         hipLaunchKernelGGL((gemv_w8_mfma_kernel<MAXB, false, NW>), grid, block, 0, s, q);
 }
 
@@ -669,7 +688,8 @@ int launch_gemv_w8(const float *x, const int8_t *qw, const float *scales, const 
         // [4096, 14336] and 1024-row slices, 1-8 batch rows: 16.6-18.2 us
         // against 17.0-19.4 with 4 waves; with two workgroups per CU, 4
         // waves are faster).
-        const bool wide = q.nstrips * q.slices <= 256;
+        // (Without VEC, 8 waves would spill registers.)
+        const bool wide = vec && q.nstrips * q.slices <= 256;
         auto go = [&](auto maxb) {
             constexpr int MB = decltype(maxb)::value;
             if (wide)

@@ -85,6 +85,26 @@ def test_gemv_w8_integer_exact(torch_dev, b, k, n):
     np.testing.assert_array_equal(got, ref)
 
 
+@pytest.mark.parametrize("b,k,n", [(2, 1677, 33024), (3, 4136, 10000)])
+def test_gemv_w8_refill_ring_integer_exact(torch_dev, b, k, n):
+    """Shapes whose waves stream more weight blocks than they hold in
+    registers.  [1677, 33024]: 129 strips x 2 slices, 4 waves per workgroup;
+    the 1024-row slice gives 8 blocks per wave (one refill pass of the
+    4-buffer ring), the 653-row slice 6, 6, 6 and 3 (refills that re-read
+    the last block, and a wave with fewer blocks than buffers).  [4136,
+    10000]: N % 16 != 0, so the byte-checked loads and their 2-buffer ring,
+    8 blocks per wave."""
+    gh, O = _gh(), _O()
+    rng = np.random.default_rng(k * 3 + n)
+    q = rng.integers(-128, 128, size=(k, n)).astype(np.int8)
+    s = (2.0 ** rng.integers(-3, 2, size=k)).astype(np.float32)
+    z = rng.integers(-5, 6, size=k).astype(np.int8)
+    x = rng.integers(-4, 5, size=(b, k)).astype(np.float32)
+    got = to_np(gh.gemv_w8(to_dev(x, torch_dev), to_dev(q, torch_dev), to_dev(s, torch_dev), to_dev(z, torch_dev)))
+    ref = O.matmul(x, O.dequantize(q, s, z))
+    np.testing.assert_array_equal(got, ref)
+
+
 def test_gemv_w8_without_zero_points(torch_dev):
     gh, O = _gh(), _O()
     rng = np.random.default_rng(1)
