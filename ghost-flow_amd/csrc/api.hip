@@ -367,4 +367,69 @@ GFH_API int gfh_sdpa_f32(const float *q, const float *k, const float *v, float *
     });
 }
 
+GFH_API int gfh_kv_attention_f32(const float *q, int64_t ldq, const float *k, const float *v, int64_t capacity,
+                                 int64_t ldkv, float *out, int64_t ldo, float *weights, int64_t b, int64_t h,
+                                 int64_t sq, int64_t kv_len, int64_t d, float scale, int causal, const float *mask,
+                                 int64_t mask_numel, gfh_stream_t stream) {
+    return guarded([&]() -> int {
+        if (b < 0 || h < 0 || sq < 0 || kv_len < 0 || capacity < 0 || b > 65535 || h > 65535 || sq > kMaxDim ||
+            kv_len > kMaxDim || capacity > kMaxDim)
+            return set_error(GFH_INVALID_SHAPE, "kv_attention: b=%lld h=%lld sq=%lld kv_len=%lld out of range",
+                             (long long)b, (long long)h, (long long)sq, (long long)kv_len);
+        if (d <= 0 || d > 128 || d % 4 != 0)
+            return set_error(GFH_INVALID_SHAPE, "kv_attention: head_dim %lld must be a multiple of 4 in [4, 128]",
+                             (long long)d);
+        if (kv_len > capacity)
+            return set_error(GFH_INVALID_SHAPE, "kv_attention: kv_len %lld exceeds the cache capacity %lld",
+                             (long long)kv_len, (long long)capacity);
+        const int64_t hd = h * d;
+        if (ldq < hd || ldkv < hd || ldo < hd || ldq % 4 || ldkv % 4 || ldo % 4)
+            return set_error(GFH_INVALID_SHAPE,
+                             "kv_attention: ldq=%lld ldkv=%lld ldo=%lld must be multiples of 4 and >= h*d=%lld",
+                             (long long)ldq, (long long)ldkv, (long long)ldo, (long long)hd);
+        if (causal && kv_len < sq)
+            return set_error(GFH_INVALID_SHAPE, "kv_attention: causal needs kv_len >= sq (got %lld < %lld)",
+                             (long long)kv_len, (long long)sq);
+        if (mask && mask_numel <= 0) return set_error(GFH_INVALID_SHAPE, "kv_attention: mask_numel must be > 0");
+        if (b == 0 || h == 0 || sq == 0) return GFH_SUCCESS;
+        if (kv_len == 0) return set_error(GFH_INVALID_SHAPE, "kv_attention: empty key sequence");
+        int64_t bs, bhs, eq, ekv, eo, ew, t;
+        if (!mul_ok(b, sq, &bs) || !mul_ok(bs, h, &bhs) || !extent2d(bs, hd, ldq, &eq) ||
+            !extent2d(bs, hd, ldo, &eo) || !mul_ok(capacity, ldkv, &t) ||
+            !extent_batched((kv_len - 1) * ldkv + hd, b, t, &ekv) || !mul_ok(bhs, kv_len, &ew))
+            return set_error(GFH_INVALID_SHAPE, "kv_attention: operand extent overflows");
+        GFH_TRY(require_range(q, (size_t)eq * 4, "q"));
+        GFH_TRY(require_range(k, (size_t)ekv * 4, "k"));
+        GFH_TRY(require_range(v, (size_t)ekv * 4, "v"));
+        GFH_TRY(require_range(out, (size_t)eo * 4, "out"));
+        GFH_TRY(optional_range(weights, (size_t)ew * 4, "weights"));
+        GFH_TRY(optional_range(mask, (size_t)mask_numel * 4, "mask"));
+        if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(out))
+            return set_error(GFH_INVALID_DATA, "kv_attention: q, k, v and out must be 16-byte aligned");
+        GFH_TRY(ensure_init());
+        KvAttnDesc kd;
+        kd.q = q;
+        kd.k = k;
+        kd.v = v;
+        kd.out = out;
+        kd.weights = weights;
+        kd.mask = mask;
+        kd.mask_numel = mask ? mask_numel : 0;
+        kd.q_bs = sq * ldq;
+        kd.q_rs = ldq;
+        kd.kv_bs = t;
+        kd.kv_rs = ldkv;
+        kd.o_bs = sq * ldo;
+        kd.o_rs = ldo;
+        kd.b = b;
+        kd.h = h;
+        kd.sq = sq;
+        kd.kv_len = kv_len;
+        kd.d = d;
+        kd.scale = scale;
+        kd.causal = causal != 0;
+        return launch_kv_attention(kd, as_stream(stream));
+    });
+}
+
 }  // extern "C"

@@ -1,0 +1,212 @@
+// gemv_nt.hip -- Linear::forward at decode sizes: y = alpha * x . W^T (+ beta y)
+// (+ bias) with x [m <= 8, k] and W [n, k] row-major, the reference's
+// [out, in] weight (ghostflow-nn/src/linear.rs:56-69).  HBM-bound: every
+// weight byte is read once, and the m rows of x are re-read from L2.
+//
+// A weight row is contiguous in k, so the natural split is the row dot
+// product: a wave owns R consecutive rows and its 64 lanes stride over k in
+// 16-byte pieces (lane l takes k = 4l + 256t), each load instruction reading
+// 1 KB of one row.  The R x m partial sums of a lane are added over the wave
+// with xor shuffles at the end; no LDS, no barriers, no split-K.  The sums
+// are regrouped against the reference's sequential k order, so the result is
+// within the fp32 GEMM bound, not bit-identical.
+//
+// gfh_sgemm sends an NT call here when m <= 8 and the operands allow 16-byte
+// loads (k, lda, ldb multiples of 4; 16-byte aligned A and B); batched calls
+// keep the reference's modulo batch indexing (matmul.rs:147-149).
+#include <algorithm>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace gfh {
+namespace {
+
+constexpr int kNtWaves = 4;
+
+struct NtParams {
+    const float *x;  // [batch_a][m][lda]
+    const float *w;  // [batch_b][n][ldb]
+    float *y;        // [batch][m][ldc]
+    const float *bias;
+    int64_t lda, ldb, ldc;
+    int64_t stride_a, stride_b, stride_c;
+    int64_t batch_a, batch_b;
+    int64_t m, n, k;
+    float alpha, beta;
+};
+
+// MB: batch rows the kernel is compiled for (m <= MB); R: weight rows per
+// wave; U: 256-element k steps whose loads are issued together.
+template <int MB, int R, int U>
+__global__ __launch_bounds__(64 * kNtWaves) void gemv_nt_kernel(NtParams p) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t n0 = ((int64_t)blockIdx.x * kNtWaves + wave) * R;
+    if (n0 >= p.n) return;  // wave-uniform, and the kernel has no barrier
+    const int64_t z = blockIdx.y;
+    const float *xb = p.x + (z % p.batch_a) * p.stride_a;
+    const float *wb = p.w + (z % p.batch_b) * p.stride_b;
+    float *yb = p.y + z * p.stride_c;
+
+    // Rows past n read row n-1 and batch rows past m read row m-1: their
+    // sums are never stored, and the loads need no condition.
+    const float *wr[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) wr[r] = wb + std::min<int64_t>(n0 + r, p.n - 1) * p.ldb + 4 * lane;
+    const float *xr[MB];
+#pragma unroll
+    for (int b = 0; b < MB; ++b) xr[b] = xb + std::min<int64_t>(b, p.m - 1) * p.lda + 4 * lane;
+
+    float acc[R][MB];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int b = 0; b < MB; ++b) acc[r][b] = 0.f;
+    auto fma4 = [&](const f32x4 (&wv)[R], const f32x4 (&xv)[MB]) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int b = 0; b < MB; ++b)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[r][b] = fmaf(wv[r][e], xv[b][e], acc[r][b]);
+    };
+
+    // Whole 256-element steps, U at a time, then the remaining whole steps
+    // one at a time, then a partial step whose lanes past k contribute 0.
+    const int64_t full = p.k / 256;
+    int64_t t = 0;
+    for (; t + U <= full; t += U) {
+        f32x4 wv[U][R], xv[U][MB];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) wv[u][r] = *reinterpret_cast<const f32x4 *>(wr[r] + (t + u) * 256);
+#pragma unroll
+            for (int b = 0; b < MB; ++b) xv[u][b] = *reinterpret_cast<const f32x4 *>(xr[b] + (t + u) * 256);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) fma4(wv[u], xv[u]);
+    }
+    for (; t < full; ++t) {
+        f32x4 wv[R], xv[MB];
+#pragma unroll
+        for (int r = 0; r < R; ++r) wv[r] = *reinterpret_cast<const f32x4 *>(wr[r] + t * 256);
+#pragma unroll
+        for (int b = 0; b < MB; ++b) xv[b] = *reinterpret_cast<const f32x4 *>(xr[b] + t * 256);
+        fma4(wv, xv);
+    }
+    if (full * 256 < p.k) {
+        // k % 4 == 0, so a lane's 4 elements are all inside k or all past
+        // it.  Lanes past k read the row start and zero both operands (a
+        // zeroed x alone would turn an inf weight into NaN).
+        const bool in = full * 256 + 4 * lane < p.k;
+        const int64_t off = in ? full * 256 : -4 * (int64_t)lane;
+        const uint32_t keep = in ? 0xffffffffu : 0u;
+        f32x4 wv[R], xv[MB];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(wr[r] + off);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float ve = v[e];  // (a bit cast of the element lvalue would read element 0)
+                wv[r][e] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, ve) & keep);
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(xr[b] + off);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float ve = v[e];
+                xv[b][e] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, ve) & keep);
+            }
+        }
+        fma4(wv, xv);
+    }
+
+    // Sum over the wave; every lane ends with every total.
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+            float v = acc[r][b];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+            acc[r][b] = v;
+        }
+    // Lane r * MB + b stores output (b, n0 + r); same epilogue as the tile
+    // GEMM: alpha * acc, then + beta * y (beta != 0 only), then + bias.
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+            if (lane != r * MB + b) continue;
+            const int64_t col = n0 + r;
+            if (col >= p.n || b >= p.m) continue;
+            float *dst = yb + b * p.ldc + col;
+            float v = p.alpha * acc[r][b];
+            if (p.beta != 0.f) v = v + p.beta * *dst;
+            if (p.bias) v = v + p.bias[col];
+            *dst = v;
+        }
+}
+
+template <int MB>
+int launch_mb(const NtParams &p, int64_t batch, hipStream_t s) {
+    // Rows per wave: R = MB / 2 (at least 1), so that the x re-reads from L2
+    // stay at most twice the weight bytes, halved once if that leaves fewer
+    // than 256 workgroups.  Measured on [4096, 4096] / [12288, 4096]: m = 1
+    // 13.4 / 35.1 us at R = 1 against 17.3 / 41.8 at R = 4; m = 4 16.9 /
+    // 43.3 us at R = 2 against 21.1 / 58.9 at R = 1; m = 8 23.7 / 51.7 us at
+    // R = 4 against 32 / 89 at R = 1.  U: 4 steps in flight up to 2 rows of
+    // x, 2 beyond.
+    const dim3 block(64 * kNtWaves);
+    auto grid = [&](int r) { return dim3((unsigned)((p.n + kNtWaves * r - 1) / (kNtWaves * r)), (unsigned)batch); };
+    constexpr int U = MB <= 2 ? 4 : 2;
+    int r = MB >= 8 ? 4 : MB >= 4 ? 2 : 1;
+    if (r > 1 && (p.n + kNtWaves * r - 1) / (kNtWaves * r) < 256) r /= 2;
+    if (r == 4)
+        hipLaunchKernelGGL((gemv_nt_kernel<MB, 4, U>), grid(4), block, 0, s, p);
+    else if (r == 2)
+        hipLaunchKernelGGL((gemv_nt_kernel<MB, 2, U>), grid(2), block, 0, s, p);
+    else
+        hipLaunchKernelGGL((gemv_nt_kernel<MB, 1, U>), grid(1), block, 0, s, p);
+    return check_launch("sgemm (NT GEMV)");
+}
+
+}  // namespace
+
+bool gemv_nt_fits(const SgemmDesc &d) {
+    return !d.trans_a && d.trans_b && d.m >= 1 && d.m <= 8 && d.k > 0 && d.n > 0 && d.k % 4 == 0 &&
+           d.lda % 4 == 0 && d.ldb % 4 == 0 && aligned16(d.a) && aligned16(d.b) &&
+           (d.batch_a <= 1 || d.stride_a % 4 == 0) && (d.batch_b <= 1 || d.stride_b % 4 == 0) && d.batch <= 65535;
+}
+
+int launch_gemv_nt(const SgemmDesc &d, hipStream_t s) {
+    NtParams p{};
+    p.x = d.a;
+    p.w = d.b;
+    p.y = d.c;
+    p.bias = d.bias;
+    p.lda = d.lda;
+    p.ldb = d.ldb;
+    p.ldc = d.ldc;
+    p.stride_a = d.stride_a;
+    p.stride_b = d.stride_b;
+    p.stride_c = d.stride_c;
+    p.batch_a = std::max<int64_t>(d.batch_a, 1);
+    p.batch_b = std::max<int64_t>(d.batch_b, 1);
+    p.m = d.m;
+    p.n = d.n;
+    p.k = d.k;
+    p.alpha = d.alpha;
+    p.beta = d.beta;
+    const int64_t batch = std::max<int64_t>(d.batch, 1);
+    if (d.m == 1) return launch_mb<1>(p, batch, s);
+    if (d.m == 2) return launch_mb<2>(p, batch, s);
+    if (d.m <= 4) return launch_mb<4>(p, batch, s);
+    return launch_mb<8>(p, batch, s);
+}
+
+}  // namespace gfh

@@ -22,6 +22,10 @@ struct SgemmDesc {
     const float *bias = nullptr;
 };
 int launch_sgemm(const SgemmDesc &d, hipStream_t s);
+// gemv_nt.hip: the NT form at m <= 8 (Linear at decode sizes); launch_sgemm
+// uses it when gemv_nt_fits.
+bool gemv_nt_fits(const SgemmDesc &d);
+int launch_gemv_nt(const SgemmDesc &d, hipStream_t s);
 
 // quant.hip
 int launch_quantize_per_channel(const float *x, int64_t rows, int64_t cols, bool symmetric, int8_t *q,
@@ -67,5 +71,20 @@ struct SdpaDesc {
     int64_t mask_numel = 0;
 };
 int launch_sdpa(const SdpaDesc &d, hipStream_t s);
+
+// kv_attention.hip: a few queries over a K/V cache in [B, S, E] layout
+// (head h in columns h*d ..); strides in elements.
+struct KvAttnDesc {
+    const float *q = nullptr, *k = nullptr, *v = nullptr;
+    float *out = nullptr;
+    float *weights = nullptr;  // [b, h, sq, kv_len], nullable
+    const float *mask = nullptr;
+    int64_t mask_numel = 0;
+    int64_t q_bs = 0, q_rs = 0, kv_bs = 0, kv_rs = 0, o_bs = 0, o_rs = 0;
+    int64_t b = 0, h = 0, sq = 0, kv_len = 0, d = 0;
+    float scale = 1.f;
+    bool causal = false;
+};
+int launch_kv_attention(const KvAttnDesc &d, hipStream_t s);
 
 }  // namespace gfh

@@ -571,7 +571,6 @@ template <int MB>
 __global__ __launch_bounds__(kThreads) void qlinear_skinny_kernel(SkParams sp) {
     const QParams &p = sp.q;
     __shared__ i32x4 red[kWaves - 1][MB][64];
-    __shared__ int last_flag;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t blk = blockIdx.x % sp.nblk, slice = blockIdx.x / sp.nblk;
     const int64_t n0 = blk * kCols;

@@ -274,6 +274,9 @@ int launch_variant(const SgemmParams &p, int64_t batch, hipStream_t s) {
 }  // namespace
 
 int launch_sgemm(const SgemmDesc &d, hipStream_t s) {
+    // x . W^T with at most 8 rows of x: a tile of this kernel would leave
+    // most of its MFMA rows empty and its grid far too small to stream W.
+    if (gemv_nt_fits(d)) return launch_gemv_nt(d, s);
     SgemmParams p{};
     p.a = d.a;
     p.b = d.b;

@@ -12,6 +12,7 @@ from .ops import (  # noqa: F401
     gemv_f32,
     gemv_w8,
     init,
+    kv_attention,
     lib,
     linear,
     matmul,

@@ -56,6 +56,8 @@ SIGNATURES = {
     "gfh_gemv_w8": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "gfh_softmax_lastdim_f32": (_i, [_p, _p, _i64, _i64, _p]),
     "gfh_sdpa_f32": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f, _i, _p, _i64, _p]),
+    "gfh_kv_attention_f32": (_i, [_p, _i64, _p, _p, _i64, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _f,
+                                  _i, _p, _i64, _p]),
 }
 
 _lib = None

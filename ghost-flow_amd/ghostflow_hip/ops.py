@@ -235,10 +235,44 @@ def sdpa(q, k, v, *, scale=None, causal=False, mask=None, want_weights=False, ou
     b, h, sq, d = q.shape
     skv = k.shape[2]
     if scale is None:
-        scale = float(torch.tensor(1.0, dtype=torch.float32) / torch.sqrt(torch.tensor(float(d), dtype=torch.float32)))
+        scale = _inv_sqrt(d)
     o = torch.empty_like(q) if out is None else out
     w = torch.empty((b, h, sq, skv), dtype=torch.float32, device=q.device) if want_weights else None
     _check(lib().gfh_sdpa_f32(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), _ptr(w), b, h, sq,
                               skv, d, float(scale), int(bool(causal)), _ptr(mask),
                               0 if mask is None else mask.numel(), _stream(q.device)))
     return (o, w) if want_weights else o
+
+
+def kv_attention(q, k_cache, v_cache, kv_len, num_heads, *, scale=None, causal=False, mask=None,
+                 want_weights=False, out=None):
+    """Attention of q [B, Sq, E] over the first kv_len rows of the caches
+    [B, C, E] (head h = columns h*D .. h*D+D-1, D = E / num_heads): the
+    scaled_dot_product_attention step of MultiHeadAttention::
+    forward_with_cache (ghostflow-nn/src/attention.rs:100-144) with the
+    concatenated keys read in place.  Returns out [B, Sq, E] (and the
+    [B, H, Sq, kv_len] weights)."""
+    for t, nm in ((q, "q"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _need(t, torch.float32, nm)
+    _need(mask, torch.float32, "mask")
+    b, sq, e = q.shape
+    cap = k_cache.shape[1]
+    if tuple(k_cache.shape) != (b, cap, e) or tuple(v_cache.shape) != (b, cap, e):
+        raise GhostFlowError(_lib.INVALID_SHAPE, "k_cache / v_cache must be [B, C, E] like q")
+    if e % num_heads:
+        raise GhostFlowError(_lib.INVALID_SHAPE, "embed_dim must be divisible by num_heads")
+    d = e // num_heads
+    if scale is None:
+        scale = _inv_sqrt(d)
+    o = torch.empty_like(q) if out is None else out
+    w = torch.empty((b, num_heads, sq, kv_len), dtype=torch.float32, device=q.device) if want_weights else None
+    _check(lib().gfh_kv_attention_f32(q.data_ptr(), e, k_cache.data_ptr(), v_cache.data_ptr(), cap, e,
+                                      o.data_ptr(), e, _ptr(w), b, num_heads, sq, kv_len, d, float(scale),
+                                      int(bool(causal)), _ptr(mask), 0 if mask is None else mask.numel(),
+                                      _stream(q.device)))
+    return (o, w) if want_weights else o
+
+
+def _inv_sqrt(d):
+    """1.0f32 / (d as f32).sqrt() (attention.rs:19-20), in float32."""
+    return float(torch.tensor(1.0, dtype=torch.float32) / torch.sqrt(torch.tensor(float(d), dtype=torch.float32)))

@@ -198,6 +198,32 @@ GFH_API int gfh_sdpa_f32(const float *q, const float *k, const float *v, float *
                          int64_t skv, int64_t d, float scale, int causal,
                          const float *mask, int64_t mask_numel, gfh_stream_t stream);
 
+/* Attention of sq new queries over a key/value cache, in the reference's
+ * [B, S, E] layout with head hh in columns hh*d .. hh*d+d-1 (the storage of
+ * reshape_for_attention's [B, H, S, D] view, ghostflow-nn/src/attention.rs:
+ * 146-150):
+ *   q      [b, sq, ldq]           projected queries
+ *   k, v   [b, capacity, ldkv]    cache rows [0, kv_len) are attended to
+ *   out    [b, sq, ldo]           heads merged (reshape_from_attention, :152-157)
+ *   weights (nullable)            [b, h, sq, kv_len] softmax probabilities
+ * per (b, hh): softmax(mask(q . k^T * scale)) . v -- the
+ * scaled_dot_product_attention step (:11-49) of
+ * MultiHeadAttention::forward_with_cache (:100-144), reading the cache in
+ * place where the reference concatenates past and new keys (concat_tensors,
+ * :214-247).  mask (nullable) is cycled over the flattened
+ * [b, h, sq, kv_len] scores, m > 0.5 keeps (:51-64); causal != 0 keeps key j
+ * for query i when j <= kv_len - sq + i (needs kv_len >= sq).  A query with
+ * every key masked gets NaN, as in the reference.  d % 4 == 0, d <= 128;
+ * ldq, ldkv, ldo multiples of 4 and >= h*d; q, k, v, out 16-byte aligned.
+ * Meant for few queries (decode); long query runs are better served by
+ * gfh_sdpa_f32. */
+GFH_API int gfh_kv_attention_f32(const float *q, int64_t ldq, const float *k,
+                                 const float *v, int64_t capacity, int64_t ldkv,
+                                 float *out, int64_t ldo, float *weights, int64_t b,
+                                 int64_t h, int64_t sq, int64_t kv_len, int64_t d,
+                                 float scale, int causal, const float *mask,
+                                 int64_t mask_numel, gfh_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

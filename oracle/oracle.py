@@ -146,6 +146,50 @@ def sdpa(q, k, v, mask=None, want_weights=False):
     return (out, w) if want_weights else out
 
 
+def mha_forward_with_cache(query, key, value, wq, bq, wk, bk, wv, bv, wo, bo, num_heads,
+                           mask=None, past_key=None, past_value=None):
+    """MultiHeadAttention::forward_with_cache (ghostflow-nn/src/attention.rs:
+    100-144) with dropout off (p = 0 or eval mode, :37-43).
+
+    query [B, S, E], key/value [B, Sk, E]; weights [E, E] as [out, in],
+    biases [E] or None; past_key/past_value [B, P, E] (the layout
+    concat_tensors joins along dim 1, :214-247).  Returns (output [B, S, E],
+    attn_weights [B, H, S, P + Sk], k_new, v_new) where k_new/v_new are the
+    new projected keys/values only (:141-142), given as [B, Sk, E]: the
+    storage order of the reference's [B, H, Sk, D] view (reshape, then
+    transpose(1, 2), :146-150).
+
+    All arithmetic is in the C restatement: linear_forward (Linear::forward
+    on [B*S, E]; the batched 3-D form of :61 sums each element in the same
+    sequential-k order, matmul.rs:147-160) and sdpa (:11-49).  What numpy
+    does here is data movement only: the head split/merge of
+    reshape_for_attention / reshape_from_attention (:146-157) and the
+    concatenation.
+    """
+    query, key, value = _f32(query), _f32(key), _f32(value)
+    b, s, e = query.shape
+    sk = key.shape[1]
+    h = int(num_heads)
+    d = e // h
+    q = linear_forward(query.reshape(b * s, e), wq, bq).reshape(b, s, e)
+    k = linear_forward(key.reshape(b * sk, e), wk, bk).reshape(b, sk, e)
+    v = linear_forward(value.reshape(b * sk, e), wv, bv).reshape(b, sk, e)
+    if past_key is not None and past_value is not None:
+        kc = np.concatenate([_f32(past_key), k], axis=1)
+        vc = np.concatenate([_f32(past_value), v], axis=1)
+    else:
+        kc, vc = k, v
+    skv = kc.shape[1]
+
+    def heads(t, n):  # [B, n, E] -> [B, H, n, D]
+        return np.ascontiguousarray(t.reshape(b, n, h, d).transpose(0, 2, 1, 3))
+
+    out, w = sdpa(heads(q, s), heads(kc, skv), heads(vc, skv), mask=mask, want_weights=True)
+    attn = np.ascontiguousarray(out.transpose(0, 2, 1, 3)).reshape(b * s, e)
+    output = linear_forward(attn, wo, bo).reshape(b, s, e)
+    return output, w, k, v
+
+
 def flash_attention(q, k, v, scale, causal):
     """ghostflow-cuda ops::attention::flash_attention (ops.rs:166-224)."""
     q, k, v = _f32(q), _f32(k), _f32(v)

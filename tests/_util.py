@@ -14,3 +14,17 @@ def to_np(t):
 def gemm_tol(k, a, b):
     """fp32 GEMM bound: max|err| <= 1e-4 * sqrt(K) * max|a| * max|b|."""
     return 1e-4 * np.sqrt(max(k, 1)) * float(np.abs(a).max(initial=0)) * float(np.abs(b).max(initial=0))
+
+
+def assert_rel(got, ref, tol=1e-4):
+    """Attention bar: max|err| / max|ref| <= tol and, per element,
+    |err| <= tol * (|ref| + mean|ref|)."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert got.shape == ref.shape
+    err = np.abs(got - ref)
+    scale = np.abs(ref).max()
+    assert err.max() <= tol * scale + 1e-30, (err.max(), scale)
+    bound = tol * (np.abs(ref) + np.abs(ref).mean())
+    bad = err > bound
+    assert not bad.any(), (int(bad.sum()), float(err[bad].max()))

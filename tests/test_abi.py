@@ -121,3 +121,20 @@ def test_python_wrapper_shape_mismatch():
     a = torch.zeros(2, 3)
     with pytest.raises(GhostFlowError):
         gh.matmul(a, torch.zeros(4, 2))
+
+
+def test_kv_attention_rejects_bad_shapes():
+    lib = _lib()
+    p, _keep = _fake()
+    # head_dim not a multiple of 4
+    assert lib.gfh_kv_attention_f32(p, 12, p, p, 8, 12, p, 12, None, 1, 2, 1, 8, 6, 1.0, 0, None, 0, None) == 1
+    assert b"head_dim" in lib.gfh_last_error()
+    # kv_len beyond the cache capacity
+    assert lib.gfh_kv_attention_f32(p, 16, p, p, 8, 16, p, 16, None, 1, 2, 1, 9, 8, 1.0, 0, None, 0, None) == 1
+    assert b"capacity" in lib.gfh_last_error()
+    # leading dimension below h * d
+    assert lib.gfh_kv_attention_f32(p, 8, p, p, 8, 16, p, 16, None, 1, 2, 1, 8, 8, 1.0, 0, None, 0, None) == 1
+    assert b"ldq" in lib.gfh_last_error()
+    # causal with more queries than keys
+    assert lib.gfh_kv_attention_f32(p, 16, p, p, 8, 16, p, 16, None, 1, 2, 4, 3, 8, 1.0, 1, None, 0, None) == 1
+    assert b"causal" in lib.gfh_last_error()

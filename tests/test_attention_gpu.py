@@ -5,7 +5,7 @@ max|err| / max|ref| <= 1e-4 and |err| <= 1e-4 * (|ref| + mean|ref|) per element.
 import numpy as np
 import pytest
 
-from _util import to_dev, to_np
+from _util import assert_rel, to_dev, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -18,18 +18,6 @@ def _gh():
 def _O():
     from oracle import oracle
     return oracle
-
-
-def assert_rel(got, ref, tol=1e-4):
-    got = np.asarray(got, np.float64)
-    ref = np.asarray(ref, np.float64)
-    assert got.shape == ref.shape
-    err = np.abs(got - ref)
-    scale = np.abs(ref).max()
-    assert err.max() <= tol * scale + 1e-30, (err.max(), scale)
-    bound = tol * (np.abs(ref) + np.abs(ref).mean())
-    bad = err > bound
-    assert not bad.any(), (int(bad.sum()), float(err[bad].max()))
 
 
 def _scale(d):

@@ -1,0 +1,103 @@
+"""Linear::forward at decode sizes (x [m <= 8, k] . W^T, W [out, in]) on the
+GPU: gfh_sgemm sends these NT calls to the row-dot GEMV kernel.  Against
+the oracle's Linear::forward / matmul (ghostflow-nn/src/linear.rs:56-69,
+ghostflow-core/src/ops/matmul.rs:91-170).  Bars: bit-exact on
+integer-valued inputs (every partial sum exact in any order), otherwise the
+north-star GEMM bound."""
+import numpy as np
+import pytest
+
+from _util import gemm_tol, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _gh():
+    import ghostflow_hip
+    return ghostflow_hip
+
+
+def _O():
+    from oracle import oracle
+    return oracle
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 8])
+@pytest.mark.parametrize("k,n", [(4, 1), (256, 17), (260, 300), (1000, 4100), (4096, 16385)])
+def test_nt_gemv_integer_exact(torch_dev, m, k, n):
+    """k = 260 / 1000: a partial last 256-element step; n = 4100 / 16385:
+    the 2- and 4-row-per-wave tilings with a ragged last wave."""
+    gh, O = _gh(), _O()
+    rng = np.random.default_rng(m * 7919 + k * 31 + n)
+    x = rng.integers(-8, 9, size=(m, k)).astype(np.float32)
+    w = rng.integers(-8, 9, size=(n, k)).astype(np.float32)
+    bias = rng.integers(-8, 9, size=(n,)).astype(np.float32)
+    got = to_np(gh.linear(to_dev(x, torch_dev), to_dev(w, torch_dev), to_dev(bias, torch_dev)))
+    np.testing.assert_array_equal(got, O.linear_forward(x, w, bias))
+
+
+def test_nt_gemv_alpha_beta(torch_dev):
+    gh, O = _gh(), _O()
+    rng = np.random.default_rng(21)
+    m, k, n = 6, 520, 777
+    x = rng.integers(-4, 5, size=(m, k)).astype(np.float32)
+    w = rng.integers(-4, 5, size=(n, k)).astype(np.float32)
+    c0 = rng.integers(-4, 5, size=(m, n)).astype(np.float32)
+    bias = rng.integers(-4, 5, size=(n,)).astype(np.float32)
+    dc = to_dev(c0, torch_dev)
+    gh.sgemm(to_dev(x, torch_dev), to_dev(w, torch_dev), trans_b=True, alpha=2.0, beta=-1.0,
+             bias=to_dev(bias, torch_dev), out=dc)
+    ref = 2.0 * O.matmul(x, np.ascontiguousarray(w.T)) - c0 + bias
+    np.testing.assert_array_equal(to_np(dc), ref.astype(np.float32))
+
+
+def test_nt_gemv_strided_rows(torch_dev):
+    """lda > k and ldc > n (rows of a larger buffer, as when a projection
+    writes into a KV cache); the bytes between rows stay untouched."""
+    import torch
+    gh, O = _gh(), _O()
+    rng = np.random.default_rng(22)
+    m, k, n, lda, ldc = 4, 512, 300, 520, 1000
+    xa = rng.integers(-8, 9, size=(m, lda)).astype(np.float32)
+    w = rng.integers(-8, 9, size=(n, k)).astype(np.float32)
+    dx, dw = to_dev(xa, torch_dev), to_dev(w, torch_dev)
+    out = torch.full((m, ldc), 7.0, device=torch_dev)
+    rc = gh.lib().gfh_sgemm(0, 1, m, n, k, 1.0, dx.data_ptr(), lda, dw.data_ptr(), k, 0.0, out.data_ptr(), ldc,
+                            None, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    got = to_np(out)
+    np.testing.assert_array_equal(got[:, :n], O.linear_forward(np.ascontiguousarray(xa[:, :k]), w))
+    assert (got[:, n:] == 7.0).all()
+
+
+def test_nt_gemv_batched_modulo(torch_dev):
+    """Batched NT with one shared weight (batch_b = 1): every batch slice
+    uses W, as the reference's modulo indexing gives (matmul.rs:148-149)."""
+    import torch
+    gh, O = _gh(), _O()
+    rng = np.random.default_rng(23)
+    batch, m, k, n = 3, 2, 256, 129
+    x = rng.integers(-8, 9, size=(batch, m, k)).astype(np.float32)
+    w = rng.integers(-8, 9, size=(n, k)).astype(np.float32)
+    dx, dw = to_dev(x, torch_dev), to_dev(w, torch_dev)
+    out = torch.empty((batch, m, n), device=torch_dev)
+    rc = gh.lib().gfh_sgemm_strided_batched(0, 1, m, n, k, 1.0, dx.data_ptr(), k, m * k, batch, dw.data_ptr(), k,
+                                            0, 1, 0.0, out.data_ptr(), n, m * n, batch, None,
+                                            torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    ref = np.stack([O.linear_forward(x[i], w) for i in range(batch)])
+    np.testing.assert_array_equal(to_np(out), ref)
+
+
+@pytest.mark.parametrize("m", [1, 4, 8])
+
+def test_decode_linear_4096(torch_dev, m):
+    """x [m, 4096] ~ N(0,1), W [4096, 4096] and b ~ U(-1/64, 1/64) (the
+    config-2 layer at decode batch sizes), against the GEMM bound."""
+    gh, O = _gh(), _O()
+    x = gh.normal((m, 4096), seed=3, tensor_id=0)
+    w = gh.uniform((4096, 4096), -1 / 64, 1 / 64, seed=0, tensor_id=1)
+    bias = gh.uniform((4096,), -1 / 64, 1 / 64, seed=0, tensor_id=2)
+    got = to_np(gh.linear(to_dev(x, torch_dev), to_dev(w, torch_dev), to_dev(bias, torch_dev)))
+    ref = O.linear_forward(x, w, bias)
+    assert np.abs(got - ref).max() <= gemm_tol(4096, x, w)
