@@ -7,6 +7,7 @@
 // stream.  No C++ exception crosses the boundary.  Status codes follow
 // GhostFlowError (ghostflow-ffi/src/lib.rs:27-35).
 #include <climits>
+#include <cmath>
 #include <new>
 
 #include "common.hpp"
@@ -429,6 +430,99 @@ GFH_API int gfh_kv_attention_f32(const float *q, int64_t ldq, const float *k, co
         kd.scale = scale;
         kd.causal = causal != 0;
         return launch_kv_attention(kd, as_stream(stream));
+    });
+}
+
+GFH_API size_t gfh_mha_workspace_size(int64_t b, int64_t sq, int64_t e) {
+    if (b <= 0 || sq <= 0 || e <= 0 || b > 65535 || sq > kMaxDim || e > kMaxDim) return 0;
+    return mha_workspace_bytes(b, sq, e);
+}
+
+GFH_API int gfh_mha_forward_with_cache_f32(const float *query, const float *key, const float *value, const float *wq,
+                                           const float *bq, const float *wk, const float *bk, const float *wv,
+                                           const float *bv, const float *wo, const float *bo, float *k_cache,
+                                           float *v_cache, int64_t capacity, int64_t past_len, const float *mask,
+                                           int64_t mask_numel, int causal, float *out, float *weights, int64_t b,
+                                           int64_t sq, int64_t sk, int64_t e, int64_t h, void *workspace,
+                                           size_t workspace_bytes, gfh_stream_t stream) {
+    return guarded([&]() -> int {
+        if (b < 0 || sq < 0 || sk < 0 || e < 0 || h <= 0 || past_len < 0 || capacity < 0 || b > 65535 ||
+            h > 65535 || sq > kMaxDim || sk > kMaxDim || e > kMaxDim || past_len > kMaxDim || capacity > kMaxDim)
+            return set_error(GFH_INVALID_SHAPE,
+                             "mha: b=%lld sq=%lld sk=%lld e=%lld h=%lld past_len=%lld capacity=%lld out of range",
+                             (long long)b, (long long)sq, (long long)sk, (long long)e, (long long)h,
+                             (long long)past_len, (long long)capacity);
+        if (e % h != 0)
+            return set_error(GFH_INVALID_SHAPE, "mha: embed_dim %lld must be divisible by num_heads %lld",
+                             (long long)e, (long long)h);
+        const int64_t hd = e / h;
+        if (hd < 4 || hd > 128 || hd % 4 != 0)
+            return set_error(GFH_INVALID_SHAPE, "mha: head_dim %lld must be a multiple of 4 in [4, 128]",
+                             (long long)hd);
+        if (past_len + sk > capacity)
+            return set_error(GFH_INVALID_SHAPE, "mha: past_len %lld + %lld new keys exceed the cache capacity %lld",
+                             (long long)past_len, (long long)sk, (long long)capacity);
+        const int64_t kv_len = past_len + sk;
+        if (causal && kv_len < sq)
+            return set_error(GFH_INVALID_SHAPE, "mha: causal needs past_len + sk >= sq");
+        if (mask && mask_numel <= 0) return set_error(GFH_INVALID_SHAPE, "mha: mask_numel must be > 0");
+        if (b == 0 || sq == 0) return GFH_SUCCESS;
+        if (kv_len == 0) return set_error(GFH_INVALID_SHAPE, "mha: empty key sequence");
+        int64_t bsq, bsk, ww, cache, bh, bhs, wts;
+        if (!mul_ok(b * sq, e, &bsq) || !mul_ok(b * sk, e, &bsk) || !mul_ok(e, e, &ww) ||
+            !mul_ok(b * capacity, e, &cache) || !mul_ok(b, h, &bh) || !mul_ok(bh, sq, &bhs) ||
+            !mul_ok(bhs, kv_len, &wts))
+            return set_error(GFH_INVALID_SHAPE, "mha: operand extent overflows");
+        GFH_TRY(require_range(query, (size_t)bsq * 4, "query"));
+        GFH_TRY(require_range(key, (size_t)bsk * 4, "key"));
+        GFH_TRY(require_range(value, (size_t)bsk * 4, "value"));
+        GFH_TRY(require_range(wq, (size_t)ww * 4, "wq"));
+        GFH_TRY(require_range(wk, (size_t)ww * 4, "wk"));
+        GFH_TRY(require_range(wv, (size_t)ww * 4, "wv"));
+        GFH_TRY(require_range(wo, (size_t)ww * 4, "wo"));
+        GFH_TRY(optional_range(bq, (size_t)e * 4, "bq"));
+        GFH_TRY(optional_range(bk, (size_t)e * 4, "bk"));
+        GFH_TRY(optional_range(bv, (size_t)e * 4, "bv"));
+        GFH_TRY(optional_range(bo, (size_t)e * 4, "bo"));
+        GFH_TRY(require_range(k_cache, (size_t)cache * 4, "k_cache"));
+        GFH_TRY(require_range(v_cache, (size_t)cache * 4, "v_cache"));
+        GFH_TRY(require_range(out, (size_t)bsq * 4, "out"));
+        GFH_TRY(optional_range(weights, (size_t)wts * 4, "weights"));
+        GFH_TRY(optional_range(mask, (size_t)mask_numel * 4, "mask"));
+        if (!aligned16(k_cache) || !aligned16(v_cache) || (workspace && !aligned16(workspace)))
+            return set_error(GFH_INVALID_DATA, "mha: k_cache, v_cache and the workspace must be 16-byte aligned");
+        GFH_TRY(ensure_init());
+        hipStream_t s = as_stream(stream);
+        Scratch ws;
+        GFH_TRY(ws.acquire(workspace, workspace_bytes, mha_workspace_bytes(b, sq, e), s));
+        MhaDesc d;
+        d.query = query;
+        d.key = key;
+        d.value = value;
+        d.wq = wq;
+        d.bq = bq;
+        d.wk = wk;
+        d.bk = bk;
+        d.wv = wv;
+        d.bv = bv;
+        d.wo = wo;
+        d.bo = bo;
+        d.k_cache = k_cache;
+        d.v_cache = v_cache;
+        d.capacity = capacity;
+        d.past_len = past_len;
+        d.mask = mask;
+        d.mask_numel = mask ? mask_numel : 0;
+        d.causal = causal != 0;
+        d.out = out;
+        d.weights = weights;
+        d.b = b;
+        d.sq = sq;
+        d.sk = sk;
+        d.e = e;
+        d.h = h;
+        d.scale = 1.0f / sqrtf((float)hd);
+        return launch_mha_forward(d, ws.ptr(), s);
     });
 }
 

@@ -45,14 +45,22 @@ constexpr int kThreads = 256;
 constexpr int kBQ = 128;  // queries per workgroup (32 per wave)
 constexpr int kBKV = 32;  // keys per LDS tile
 
+// Element (b, h, i, d) of q is at q[b*q_bs + h*q_hs + i*q_rs + d] (K, V with
+// the kv_* strides, the output with o_*): [B, H, S, D] contiguous, or the
+// [B, S, E] projections with heads as column blocks (h stride D, row stride
+// E) that MultiHeadAttention attends over without a transpose.  weights is
+// always [B*H, sq, skv].
 struct SdpaParams {
     const float *q, *k, *v;
     float *out;
     float *weights;
     const float *mask;
     int64_t mask_numel;
+    int64_t q_bs, q_hs, q_rs, kv_bs, kv_hs, kv_rs, o_bs, o_hs, o_rs;
+    int64_t h;
     int64_t sq, skv, d;
     int64_t bh;
+    int64_t causal_off;  // causal keeps key j for query i when j <= i + causal_off
     float scale;
     int nqb;
 };
@@ -67,14 +75,14 @@ struct KvStage {
     f32x4 r[kPer];
 
     __device__ __forceinline__ void load(const float *__restrict__ base, int64_t key0, int64_t nkeys, int64_t d,
-                                         int tid) {
+                                         int64_t rs, int tid) {
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
             const int idx = tid + i * kThreads;
             const int key = idx / (DMAX / 4);
             const int dim = (idx % (DMAX / 4)) * 4;
             f32x4 v = {0.f, 0.f, 0.f, 0.f};
-            if (key0 + key < nkeys && dim < d) v = *reinterpret_cast<const f32x4 *>(base + (key0 + key) * d + dim);
+            if (key0 + key < nkeys && dim < d) v = *reinterpret_cast<const f32x4 *>(base + (key0 + key) * rs + dim);
             r[i] = v;
         }
     }
@@ -110,7 +118,7 @@ __device__ __forceinline__ void tile_scores(const SdpaParams &p, const float *ks
         const int64_t key = k0 + key_of(r, h);
         float v = acc[r] * p.scale;
         bool keep = key < p.skv;
-        if (CAUSAL) keep = keep && key <= my_q;
+        if (CAUSAL) keep = keep && key <= my_q + p.causal_off;
         if (MASK && keep) {
             const int64_t f = ((int64_t)blockIdx.x * p.sq + my_q) * p.skv + key;
             keep = p.mask[f % p.mask_numel] > 0.5f;
@@ -136,16 +144,17 @@ __global__ __launch_bounds__(kThreads) void sdpa_fwd_kernel(SdpaParams p) {
     const int64_t q0 = (int64_t)qb * kBQ;
     const int64_t wq0 = q0 + wave * 32;
     const int64_t my_q = wq0 + c;
-    const float *Q = p.q + bh * p.sq * p.d;
-    const float *K = p.k + bh * p.skv * p.d;
-    const float *V = p.v + bh * p.skv * p.d;
+    const int64_t bb = bh / p.h, hh = bh % p.h;
+    const float *Q = p.q + bb * p.q_bs + hh * p.q_hs;
+    const float *K = p.k + bb * p.kv_bs + hh * p.kv_hs;
+    const float *V = p.v + bb * p.kv_bs + hh * p.kv_hs;
 
     f32x4 qf[NG];
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
         const int dim = 8 * g + 4 * h;
         f32x4 v = {0.f, 0.f, 0.f, 0.f};
-        if (my_q < p.sq && dim < p.d) v = *reinterpret_cast<const f32x4 *>(Q + my_q * p.d + dim);
+        if (my_q < p.sq && dim < p.d) v = *reinterpret_cast<const f32x4 *>(Q + my_q * p.q_rs + dim);
         qf[g] = v;
     }
 
@@ -156,13 +165,13 @@ __global__ __launch_bounds__(kThreads) void sdpa_fwd_kernel(SdpaParams p) {
         for (int r = 0; r < 16; ++r) o[j][r] = 0.f;
     float m = -INFINITY, l = 0.f;
 
-    const int64_t kv_end = CAUSAL ? min(p.skv, q0 + kBQ) : p.skv;
+    const int64_t kv_end = CAUSAL ? min(p.skv, q0 + kBQ + p.causal_off) : p.skv;
     const int64_t ntiles = (kv_end + kBKV - 1) / kBKV;
 
     KvStage<DMAX> gk, gv;
     if (ntiles > 0) {
-        gk.load(K, 0, p.skv, p.d, tid);
-        gv.load(V, 0, p.skv, p.d, tid);
+        gk.load(K, 0, p.skv, p.d, p.kv_rs, tid);
+        gv.load(V, 0, p.skv, p.d, p.kv_rs, tid);
         gk.store(lk, tid);
         gv.store(lv, tid);
     }
@@ -172,12 +181,12 @@ __global__ __launch_bounds__(kThreads) void sdpa_fwd_kernel(SdpaParams p) {
         const int cur = t & 1;
         const bool more = t + 1 < ntiles;
         if (more) {
-            gk.load(K, (t + 1) * kBKV, p.skv, p.d, tid);
-            gv.load(V, (t + 1) * kBKV, p.skv, p.d, tid);
+            gk.load(K, (t + 1) * kBKV, p.skv, p.d, p.kv_rs, tid);
+            gv.load(V, (t + 1) * kBKV, p.skv, p.d, p.kv_rs, tid);
         }
         const int64_t k0 = t * kBKV;
         // A wave whose last query precedes the tile's first key has nothing to do.
-        const bool active = !CAUSAL || k0 <= wq0 + 31;
+        const bool active = !CAUSAL || k0 <= wq0 + 31 + p.causal_off;
         if (active) {
             float sv[16];
             tile_scores<DMAX, CAUSAL, MASK>(p, lk + cur * kTile, qf, k0, my_q, lane, sv);
@@ -221,7 +230,7 @@ __global__ __launch_bounds__(kThreads) void sdpa_fwd_kernel(SdpaParams p) {
     // dim 32j + 8(r/4) + 4h + r%4: four consecutive dims per 16-byte store.
     if (my_q < p.sq) {
         const float inv_l = 1.0f / l;
-        float *orow = p.out + (bh * p.sq + my_q) * p.d;
+        float *orow = p.out + bb * p.o_bs + hh * p.o_hs + my_q * p.o_rs;
 #pragma unroll
         for (int j = 0; j < ND; ++j)
 #pragma unroll
@@ -243,7 +252,7 @@ __global__ __launch_bounds__(kThreads) void sdpa_fwd_kernel(SdpaParams p) {
         float *wrow = p.weights + (bh * p.sq + (my_q < p.sq ? my_q : 0)) * p.skv;
         __syncthreads();
         for (int64_t t = 0; t < wtiles; ++t) {
-            gk.load(K, t * kBKV, p.skv, p.d, tid);
+            gk.load(K, t * kBKV, p.skv, p.d, p.kv_rs, tid);
             gk.store(lk, tid);
             __syncthreads();
             float sv[16];
@@ -338,7 +347,18 @@ int launch_sdpa(const SdpaDesc &d, hipStream_t s) {
     p.sq = d.sq;
     p.skv = d.skv;
     p.d = d.d;
+    p.h = d.h;
     p.bh = d.b * d.h;
+    if (d.strided) {
+        p.q_bs = d.q_bs, p.q_hs = d.q_hs, p.q_rs = d.q_rs;
+        p.kv_bs = d.kv_bs, p.kv_hs = d.kv_hs, p.kv_rs = d.kv_rs;
+        p.o_bs = d.o_bs, p.o_hs = d.o_hs, p.o_rs = d.o_rs;
+    } else {
+        p.q_hs = d.sq * d.d, p.q_bs = d.h * p.q_hs, p.q_rs = d.d;
+        p.kv_hs = d.skv * d.d, p.kv_bs = d.h * p.kv_hs, p.kv_rs = d.d;
+        p.o_hs = p.q_hs, p.o_bs = p.q_bs, p.o_rs = d.d;
+    }
+    p.causal_off = d.causal ? d.skv - d.sq : 0;
     p.scale = d.scale;
     p.nqb = (int)((d.sq + kBQ - 1) / kBQ);
     dim3 grid((unsigned)p.bh, (unsigned)p.nqb);

@@ -69,6 +69,11 @@ struct SdpaDesc {
     bool causal = false;
     const float *mask = nullptr;
     int64_t mask_numel = 0;
+    // Element strides (b, h, row) of q, k/v and out when `strided`;
+    // otherwise [b, h, s, d] contiguous.  causal keeps key j for query i
+    // when j <= i + skv - sq.
+    bool strided = false;
+    int64_t q_bs = 0, q_hs = 0, q_rs = 0, kv_bs = 0, kv_hs = 0, kv_rs = 0, o_bs = 0, o_hs = 0, o_rs = 0;
 };
 int launch_sdpa(const SdpaDesc &d, hipStream_t s);
 
@@ -86,5 +91,24 @@ struct KvAttnDesc {
     bool causal = false;
 };
 int launch_kv_attention(const KvAttnDesc &d, hipStream_t s);
+
+// mha.hip: MultiHeadAttention::forward_with_cache over a [b, capacity, e]
+// K/V cache; the workspace holds the projected queries and the attention
+// output (mha_workspace_bytes).
+struct MhaDesc {
+    const float *query = nullptr, *key = nullptr, *value = nullptr;
+    const float *wq = nullptr, *bq = nullptr, *wk = nullptr, *bk = nullptr;
+    const float *wv = nullptr, *bv = nullptr, *wo = nullptr, *bo = nullptr;
+    float *k_cache = nullptr, *v_cache = nullptr;
+    int64_t capacity = 0, past_len = 0;
+    const float *mask = nullptr;
+    int64_t mask_numel = 0;
+    bool causal = false;
+    float *out = nullptr, *weights = nullptr;
+    int64_t b = 0, sq = 0, sk = 0, e = 0, h = 0;
+    float scale = 1.f;
+};
+size_t mha_workspace_bytes(int64_t b, int64_t sq, int64_t e);
+int launch_mha_forward(const MhaDesc &d, void *workspace, hipStream_t s);
 
 }  // namespace gfh

@@ -16,6 +16,9 @@ from .ops import (  # noqa: F401
     lib,
     linear,
     matmul,
+    mha_forward_cached,
+    mha_forward_with_cache,
+    mha_workspace_size,
     qlinear,
     quantize_per_channel,
     quantize_per_tensor,
@@ -26,4 +29,5 @@ from .ops import (  # noqa: F401
     sgemm,
     softmax_lastdim,
 )
+from .nn import KVCache, MultiHeadAttention  # noqa: F401
 from .synth import normal, uniform  # noqa: F401

@@ -58,6 +58,9 @@ SIGNATURES = {
     "gfh_sdpa_f32": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f, _i, _p, _i64, _p]),
     "gfh_kv_attention_f32": (_i, [_p, _i64, _p, _p, _i64, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _f,
                                   _i, _p, _i64, _p]),
+    "gfh_mha_workspace_size": (_sz, [_i64, _i64, _i64]),
+    "gfh_mha_forward_with_cache_f32": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p,
+                                            _i64, _i, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _sz, _p]),
 }
 
 _lib = None

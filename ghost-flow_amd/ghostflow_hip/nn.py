@@ -1,0 +1,99 @@
+"""Module-level mirrors of the reference's attention layer on this library.
+
+MultiHeadAttention follows ghostflow-nn/src/attention.rs:66-170: four
+embed_dim x embed_dim Linear projections stored [out, in] with biases,
+forward_with_cache(query, key, value, mask, past_key, past_value) ->
+(output, attn_weights, k_cache, v_cache), and forward(input) as
+self-attention.  Dropout is not implemented on this path: in training mode
+with dropout > 0 (the reference's default mode is training) the calls
+raise, so use eval() or dropout 0.
+
+KVCache is the in-place form of the reference's past_key / past_value
+concatenation: preallocated [B, capacity, E] buffers that every step
+appends to, so a decode step costs no copy of the past.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+from .ops import GhostFlowError, mha_forward_cached, mha_forward_with_cache
+
+
+class KVCache:
+    """Keys and values of the positions seen so far, [B, capacity, E]."""
+
+    def __init__(self, batch: int, capacity: int, embed_dim: int, device="cuda"):
+        self.k = torch.empty((batch, capacity, embed_dim), dtype=torch.float32, device=device)
+        self.v = torch.empty_like(self.k)
+        self.length = 0
+
+    @property
+    def capacity(self) -> int:
+        return self.k.shape[1]
+
+    def reset(self) -> None:
+        self.length = 0
+
+
+class MultiHeadAttention:
+    """ghostflow-nn MultiHeadAttention (attention.rs:66-170) on the GPU."""
+
+    def __init__(self, embed_dim: int, num_heads: int, dropout: float = 0.0, device="cuda"):
+        if embed_dim % num_heads:
+            raise GhostFlowError(_lib.INVALID_SHAPE, "embed_dim must be divisible by num_heads")
+        self.embed_dim = embed_dim
+        self.num_heads = num_heads
+        self.head_dim = embed_dim // num_heads
+        self.dropout_p = dropout
+        self.training = True
+        # Linear::new's init (ghostflow-nn/src/linear.rs:23-33, init.rs:31-41):
+        # W ~ U(+-sqrt(6/in)), b ~ U(+-1/sqrt(in)); the reference draws from
+        # an unseeded RNG, so only the distribution is kept.
+        wb, bb = math.sqrt(6.0 / embed_dim), 1.0 / math.sqrt(embed_dim)
+        mk = lambda shape, bound: (torch.rand(shape, device=device) * 2 - 1) * bound  # noqa: E731
+        self.q_weight, self.k_weight, self.v_weight, self.out_weight = (
+            mk((embed_dim, embed_dim), wb) for _ in range(4))
+        self.q_bias, self.k_bias, self.v_bias, self.out_bias = (mk((embed_dim,), bb) for _ in range(4))
+
+    def _weights(self):
+        if self.training and self.dropout_p > 0:
+            raise GhostFlowError(_lib.INVALID_DATA, "attention dropout is not implemented on this path; "
+                                 "call eval() or use dropout 0")
+        return (self.q_weight, self.q_bias, self.k_weight, self.k_bias, self.v_weight, self.v_bias,
+                self.out_weight, self.out_bias)
+
+    def forward_with_cache(self, query, key, value, mask=None, past_key=None, past_value=None):
+        return mha_forward_with_cache(query, key, value, *self._weights(), self.num_heads, mask=mask,
+                                      past_key=past_key, past_value=past_value)
+
+    def forward(self, x):
+        return self.forward_with_cache(x, x, x)[0]
+
+    __call__ = forward
+
+    def step(self, x, cache: KVCache, *, mask=None, causal=False, want_weights=False):
+        """Self-attention of x [B, S, E] (new positions) over the cache plus
+        x, appending x's keys and values to the cache in place."""
+        s = x.shape[1]
+        if cache.length + s > cache.capacity:
+            raise GhostFlowError(_lib.INVALID_SHAPE, "KV cache is full")
+        r = mha_forward_cached(x, x, x, *self._weights(), self.num_heads, cache.k, cache.v, cache.length,
+                               mask=mask, causal=causal, want_weights=want_weights)
+        cache.length += s
+        return r
+
+    def parameters(self):
+        return [self.q_weight, self.q_bias, self.k_weight, self.k_bias, self.v_weight, self.v_bias,
+                self.out_weight, self.out_bias]
+
+    def train(self):
+        self.training = True
+
+    def eval(self):
+        self.training = False
+
+    def is_training(self) -> bool:
+        return self.training

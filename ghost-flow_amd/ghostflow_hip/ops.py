@@ -276,3 +276,65 @@ def kv_attention(q, k_cache, v_cache, kv_len, num_heads, *, scale=None, causal=F
 def _inv_sqrt(d):
     """1.0f32 / (d as f32).sqrt() (attention.rs:19-20), in float32."""
     return float(torch.tensor(1.0, dtype=torch.float32) / torch.sqrt(torch.tensor(float(d), dtype=torch.float32)))
+
+
+# ---- multi-head attention with a key/value cache ------------------------------------
+
+def mha_workspace_size(b: int, sq: int, e: int) -> int:
+    return int(lib().gfh_mha_workspace_size(b, sq, e))
+
+
+def mha_forward_cached(query, key, value, wq, bq, wk, bk, wv, bv, wo, bo, num_heads, k_cache, v_cache,
+                       past_len, *, mask=None, causal=False, want_weights=False, out=None, workspace=None):
+    """MultiHeadAttention::forward_with_cache on an in-place cache: writes
+    the projected key/value rows into k_cache / v_cache [B, C, E] at
+    [past_len, past_len + Sk) and attends over rows [0, past_len + Sk).
+    Returns out [B, Sq, E] (and the [B, H, Sq, past_len + Sk] weights)."""
+    for t, nm in ((query, "query"), (key, "key"), (value, "value"), (wq, "wq"), (wk, "wk"), (wv, "wv"),
+                  (wo, "wo"), (bq, "bq"), (bk, "bk"), (bv, "bv"), (bo, "bo"), (k_cache, "k_cache"),
+                  (v_cache, "v_cache"), (mask, "mask")):
+        _need(t, torch.float32, nm)
+    b, sq, e = query.shape
+    sk = key.shape[1]
+    if tuple(key.shape) != (b, sk, e) or tuple(value.shape) != (b, sk, e):
+        raise GhostFlowError(_lib.INVALID_SHAPE, "key / value must be [B, Sk, E] like query")
+    cap = k_cache.shape[1]
+    if tuple(k_cache.shape) != (b, cap, e) or tuple(v_cache.shape) != (b, cap, e):
+        raise GhostFlowError(_lib.INVALID_SHAPE, "k_cache / v_cache must be [B, C, E]")
+    kv_len = past_len + sk
+    o = torch.empty_like(query) if out is None else out
+    w = (torch.empty((b, num_heads, sq, kv_len), dtype=torch.float32, device=query.device)
+         if want_weights else None)
+    ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(),
+                                                             workspace.numel() * workspace.element_size())
+    _check(lib().gfh_mha_forward_with_cache_f32(
+        query.data_ptr(), key.data_ptr(), value.data_ptr(), wq.data_ptr(), _ptr(bq), wk.data_ptr(), _ptr(bk),
+        wv.data_ptr(), _ptr(bv), wo.data_ptr(), _ptr(bo), k_cache.data_ptr(), v_cache.data_ptr(), cap, past_len,
+        _ptr(mask), 0 if mask is None else mask.numel(), int(bool(causal)), o.data_ptr(), _ptr(w), b, sq, sk, e,
+        num_heads, ws_ptr, ws_bytes, _stream(query.device)))
+    return (o, w) if want_weights else o
+
+
+def mha_forward_with_cache(query, key, value, wq, bq, wk, bk, wv, bv, wo, bo, num_heads, mask=None,
+                           past_key=None, past_value=None):
+    """The reference's signature and results (attention.rs:100-144):
+    past_key / past_value [B, P, E] are concatenated before the new keys
+    along dim 1; returns (output [B, Sq, E], attn_weights
+    [B, H, Sq, P + Sk], k_cache, v_cache), the last two being the new
+    projected keys / values as [B, H, Sk, D] views, like
+    reshape_for_attention's (:146-150)."""
+    b, sq, e = query.shape
+    sk = key.shape[1]
+    have_past = past_key is not None and past_value is not None
+    p = past_key.shape[1] if have_past else 0
+    kc = torch.empty((b, p + sk, e), dtype=torch.float32, device=query.device)
+    vc = torch.empty_like(kc)
+    if p:
+        kc[:, :p].copy_(past_key)
+        vc[:, :p].copy_(past_value)
+    out, w = mha_forward_cached(query, key, value, wq, bq, wk, bk, wv, bv, wo, bo, num_heads, kc, vc, p,
+                                mask=mask, want_weights=True)
+    d = e // num_heads
+    k_new = kc[:, p:].reshape(b, sk, num_heads, d).transpose(1, 2)
+    v_new = vc[:, p:].reshape(b, sk, num_heads, d).transpose(1, 2)
+    return out, w, k_new, v_new

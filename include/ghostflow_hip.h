@@ -224,6 +224,38 @@ GFH_API int gfh_kv_attention_f32(const float *q, int64_t ldq, const float *k,
                                  float scale, int causal, const float *mask,
                                  int64_t mask_numel, gfh_stream_t stream);
 
+/* ---- multi-head attention with a key/value cache ------------------------ */
+
+/* MultiHeadAttention::forward_with_cache (ghostflow-nn/src/attention.rs:
+ * 100-144) with dropout off, on an in-place K/V cache:
+ *   query [b, sq, e], key / value [b, sk, e];
+ *   wq, wk, wv, wo [e, e] as Linear weights [out, in]; biases [e] nullable;
+ *   k_cache, v_cache [b, capacity, e]: rows [0, past_len) hold the earlier
+ *     projected keys/values (the reference's past_key / past_value); this
+ *     call writes key . Wk^T + bk and value . Wv^T + bv into rows
+ *     [past_len, past_len + sk) -- the concatenation along dim 1 of
+ *     concat_tensors (:214-247) without the copy, and the new k/v the
+ *     reference returns (:141-142, in [b, sk, e] storage order);
+ *   out [b, sq, e] = out_proj(attention(q, k_cache, v_cache));
+ *   weights (nullable) [b, h, sq, past_len + sk] softmax probabilities.
+ * scale = 1 / sqrt(e / h) (attention.rs:19-20); mask (nullable) is cycled
+ * over the flattened [b, h, sq, past_len + sk] scores (:51-64); causal != 0
+ * keeps key j for query i when j <= past_len + sk - sq + i, which equals
+ * passing the matching lower-triangular mask.  e / h must be a multiple of
+ * 4 in [4, 128]; k_cache and v_cache 16-byte aligned.  workspace (nullable,
+ * 16-byte aligned) of at least gfh_mha_workspace_size(b, sq, e) bytes holds
+ * the projected queries and the attention output; without one the call
+ * allocates stream-ordered. */
+GFH_API size_t gfh_mha_workspace_size(int64_t b, int64_t sq, int64_t e);
+GFH_API int gfh_mha_forward_with_cache_f32(
+    const float *query, const float *key, const float *value, const float *wq,
+    const float *bq, const float *wk, const float *bk, const float *wv,
+    const float *bv, const float *wo, const float *bo, float *k_cache,
+    float *v_cache, int64_t capacity, int64_t past_len, const float *mask,
+    int64_t mask_numel, int causal, float *out, float *weights, int64_t b,
+    int64_t sq, int64_t sk, int64_t e, int64_t h, void *workspace,
+    size_t workspace_bytes, gfh_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
