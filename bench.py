@@ -17,9 +17,11 @@ The same line carries
     bias add, single-threaded as the reference is) timed on this host on a
     bounded row sample and extrapolated to the full layer;
   * "components": the other hot-path kernels at their benchmark shapes
-    (square fp32 GEMM, int8 linear, decode GEMV fp32 / int8, causal SDPA),
-    each with its own roofline fraction.  These are supplementary numbers,
-    not the headline.
+    (square fp32 GEMM, int8 linear, decode GEMV fp32 / int8, causal SDPA)
+    and the decode path built on them (Linear at decode batch sizes,
+    attention over a KV cache, one MultiHeadAttention decode step), each
+    with its own roofline fraction.  These are supplementary numbers, not
+    the headline.
 
 Only 1 GPU is supported: --gpus N with N > 1 exits with an error.
 """
@@ -59,7 +61,7 @@ def parse_args():
     ap.add_argument("--cpu-rows", type=int, default=768,
                     help="rows of x in the CPU-baseline sample (of 4096)")
     ap.add_argument("--only", default="",
-                    help="comma list of components to run (sgemm,qlinear,gemv,sdpa); "
+                    help="comma list of components to run (sgemm,qlinear,gemv,sdpa,decode); "
                          "used for focused profiling")
     ap.add_argument("--detail", default="", help="also write the full result JSON to this file")
     ap.add_argument("--calib-copy", action="store_true",
@@ -303,8 +305,107 @@ def comp_sdpa(lib, torch, S):
             "frac": fl / ms / 1e9 / (PEAK_F32 / 1e12), "bound": "mfma_f32"}
 
 
+def comp_linear_decode(lib, torch, m):
+    """Linear::forward at decode batch sizes: x [m, 4096] . W^T + b with W
+    [4096, 4096] (gfh_sgemm NT -> the row-dot GEMV).  HBM-bound: bytes =
+    4*N*K + 4*m*K + 4*N (bias) + 4*m*N."""
+    dev = torch.device("cuda:0")
+    N = K = 4096
+    wbytes = 4 * N * K
+    ncopy = max(3, -(-2 * MALL_BYTES // wbytes) + 1)
+    ws = [torch.empty((N, K), device=dev).uniform_(-1 / 64, 1 / 64) for _ in range(ncopy)]
+    x = torch.randn((m, K), device=dev)
+    bias = torch.empty((N,), device=dev).uniform_(-1 / 64, 1 / 64)
+    y = torch.empty((m, N), device=dev)
+    s = torch.cuda.current_stream(dev).cuda_stream
+    L = lib.L
+    wp = [t.data_ptr() for t in ws]
+
+    def f(i):
+        L.gfh_sgemm(0, 1, m, N, K, 1.0, x.data_ptr(), K, wp[i % ncopy], K, 0.0, y.data_ptr(), N,
+                    bias.data_ptr(), s)
+    ms = event_time_ms(torch, f, 300)
+    byts = wbytes + 4 * m * K + 4 * N + 4 * m * N
+    gbs = byts / ms / 1e6
+    del ws
+    return {"name": f"linear_decode_m{m}_4096", "ms": ms, "value": gbs, "unit": "GB/s",
+            "frac": gbs * 1e9 / PEAK_HBM, "bound": "hbm", "weight_copies": ncopy}
+
+
+def _kv_sets(torch, dev, B, C, E, n):
+    return [(torch.randn((B, C, E), device=dev), torch.randn((B, C, E), device=dev)) for _ in range(n)]
+
+
+def comp_kv_attention(lib, torch, B=4, H=32, D=128, kv_len=2048):
+    """One decode step of attention over a [B, kv_len, E] cache
+    (gfh_kv_attention_f32, Sq = 1).  HBM-bound: bytes = 2*4*B*kv_len*E
+    (K and V) + 8*B*E (q, out)."""
+    dev = torch.device("cuda:0")
+    E = H * D
+    kvbytes = 2 * 4 * B * kv_len * E
+    ncopy = max(2, -(-2 * MALL_BYTES // kvbytes) + 1)
+    sets = _kv_sets(torch, dev, B, kv_len, E, ncopy)
+    q = torch.randn((B, 1, E), device=dev)
+    o = torch.empty_like(q)
+    s = torch.cuda.current_stream(dev).cuda_stream
+    L = lib.L
+    ptrs = [(k.data_ptr(), v.data_ptr()) for k, v in sets]
+    scale = float(1.0 / (D ** 0.5))
+
+    def f(i):
+        kp, vp = ptrs[i % ncopy]
+        L.gfh_kv_attention_f32(q.data_ptr(), E, kp, vp, kv_len, E, o.data_ptr(), E, None, B, H, 1, kv_len, D,
+                               scale, 0, None, 0, s)
+    ms = event_time_ms(torch, f, 200)
+    byts = kvbytes + 8 * B * E
+    gbs = byts / ms / 1e6
+    del sets
+    return {"name": f"kv_attention_b{B}_h{H}_d{D}_kv{kv_len}", "ms": ms, "value": gbs, "unit": "GB/s",
+            "frac": gbs * 1e9 / PEAK_HBM, "bound": "hbm", "cache_copies": ncopy}
+
+
+def comp_mha_decode(lib, torch, B=4, H=32, D=128, past=2047):
+    """One decode step of MultiHeadAttention::forward_with_cache: 1 new
+    token per sequence, E = 4096, 32 heads, `past` cached positions
+    (gfh_mha_forward_with_cache_f32: 4 projections + cache attention).
+    HBM-bound: bytes = 4 * 4*E*E (weights) + 2*4*B*(past+1)*E (cache) plus
+    the small activations."""
+    dev = torch.device("cuda:0")
+    E = H * D
+    C = past + 1
+    per_set = 4 * 4 * E * E + 2 * 4 * B * C * E
+    ncopy = max(2, -(-2 * MALL_BYTES // per_set) + 1)
+    sets = []
+    for _ in range(ncopy):
+        w = [torch.empty((E, E), device=dev).uniform_(-1 / 64, 1 / 64) for _ in range(4)]
+        kc, vc = _kv_sets(torch, dev, B, C, E, 1)[0]
+        sets.append((w, kc, vc))
+    bias = [torch.empty((E,), device=dev).uniform_(-1 / 64, 1 / 64) for _ in range(4)]
+    x = torch.randn((B, 1, E), device=dev)
+    out = torch.empty_like(x)
+    ws = torch.empty((int(lib.L.gfh_mha_workspace_size(B, 1, E)) + 3) // 4, device=dev)
+    s = torch.cuda.current_stream(dev).cuda_stream
+    L = lib.L
+    bp = [t.data_ptr() for t in bias]
+    ptrs = [([t.data_ptr() for t in w], kc.data_ptr(), vc.data_ptr()) for w, kc, vc in sets]
+
+    def f(i):
+        wp, kp, vp = ptrs[i % ncopy]
+        L.gfh_mha_forward_with_cache_f32(x.data_ptr(), x.data_ptr(), x.data_ptr(), wp[0], bp[0], wp[1], bp[1],
+                                         wp[2], bp[2], wp[3], bp[3], kp, vp, C, past, None, 0, 0,
+                                         out.data_ptr(), None, B, 1, 1, E, H, ws.data_ptr(),
+                                         ws.numel() * 4, s)
+    ms = event_time_ms(torch, f, 100)
+    byts = per_set + 4 * B * E * 6
+    gbs = byts / ms / 1e6
+    del sets
+    return {"name": f"mha_decode_step_b{B}_e{E}_h{H}_past{past}", "ms": ms, "value": gbs, "unit": "GB/s",
+            "tokens_per_s": B / (ms * 1e-3), "frac": gbs * 1e9 / PEAK_HBM, "bound": "hbm",
+            "set_copies": ncopy}
+
+
 def run_components(lib, torch, only):
-    want = set(filter(None, only.split(","))) or {"sgemm", "qlinear", "gemv", "sdpa"}
+    want = set(filter(None, only.split(","))) or {"sgemm", "qlinear", "gemv", "sdpa", "decode"}
     out = []
 
     def add(fn, *a, **kw):
@@ -330,6 +431,11 @@ def run_components(lib, torch, only):
     if "sdpa" in want:
         for S in (512, 2048):
             add(comp_sdpa, S)
+    if "decode" in want:
+        for m in (1, 4, 8):
+            add(comp_linear_decode, m)
+        add(comp_kv_attention)
+        add(comp_mha_decode)
     return out
 
 

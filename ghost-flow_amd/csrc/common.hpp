@@ -83,3 +83,36 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+// ---- cross-lane sums without LDS round trips ---------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float readlane_f(float x, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
+}
+// Sum over each row of 16 lanes, in every lane of the row: quad xor 1 and
+// xor 2 (DPP quad_perm), then rotations by 4 and 8 within the row.  Lanes of
+// a row may differ in the last bit (the rotations associate differently).
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_mov<0x124>(v);  // row_ror:4
+    v += dpp_mov<0x128>(v);  // row_ror:8
+    return v;
+}
+// Sum over the 64 lanes, bit-identical in every lane (row totals read out
+// with readlane and added in a fixed order).  A __shfl_xor ladder would be
+// six dependent ds_bpermute round trips.
+__device__ __forceinline__ float wave_sum(float v) {
+    v = row16_sum(v);
+    return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
+}
+// Sum over each half-wave (lanes 0-31, 32-63), bit-identical across it.
+__device__ __forceinline__ float half_wave_sum(float v) {
+    v = row16_sum(v);
+    const float lo = readlane_f(v, 0) + readlane_f(v, 16);
+    const float hi = readlane_f(v, 32) + readlane_f(v, 48);
+    return (threadIdx.x & 32) ? hi : lo;
+}

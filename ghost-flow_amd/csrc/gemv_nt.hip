@@ -4,12 +4,17 @@
 // weight byte is read once, and the m rows of x are re-read from L2.
 //
 // A weight row is contiguous in k, so the natural split is the row dot
-// product: a wave owns R consecutive rows and its 64 lanes stride over k in
-// 16-byte pieces (lane l takes k = 4l + 256t), each load instruction reading
-// 1 KB of one row.  The R x m partial sums of a lane are added over the wave
-// with xor shuffles at the end; no LDS, no barriers, no split-K.  The sums
-// are regrouped against the reference's sequential k order, so the result is
-// within the fp32 GEMM bound, not bit-identical.
+// product: lanes stride over k in 16-byte pieces (lane l takes k = 4l + 256t),
+// each load instruction reading 1 KB of one row, and the R x m partial sums
+// of a lane are added over the wave with xor shuffles at the end.  Two forms:
+//  * m <= 4 (gemv_nt_ksplit_kernel): a workgroup owns R rows and its 4
+//    waves take every 4th 256-element step of them, so a wave re-reads only
+//    its quarter of x for all R rows; the 4 wave totals are added in LDS in
+//    a fixed order.
+//  * m > 4 (gemv_nt_rows_kernel): a wave owns R rows and all of k; at 8
+//    rows of x the multiply-adds (8 per weight, VALU) bound the kernel.
+// The sums are regrouped against the reference's sequential k order, so the
+// result is within the fp32 GEMM bound, not bit-identical.
 //
 // gfh_sgemm sends an NT call here when m <= 8 and the operands allow 16-byte
 // loads (k, lda, ldb multiples of 4; 16-byte aligned A and B); batched calls
@@ -36,18 +41,32 @@ struct NtParams {
     float alpha, beta;
 };
 
+// Operands of batch slice blockIdx.y, with the reference's modulo indexing.
+// Batch counts are below 2^16, so 32-bit arithmetic suffices (a 64-bit
+// remainder expands to a long instruction sequence), and a single slice
+// skips it.
+__device__ __forceinline__ void batch_slices(const NtParams &p, const float *&xb, const float *&wb, float *&yb) {
+    const uint32_t z = blockIdx.y;
+    if (z == 0) {
+        xb = p.x, wb = p.w, yb = p.y;
+        return;
+    }
+    xb = p.x + (int64_t)(z % (uint32_t)p.batch_a) * p.stride_a;
+    wb = p.w + (int64_t)(z % (uint32_t)p.batch_b) * p.stride_b;
+    yb = p.y + (int64_t)z * p.stride_c;
+}
+
 // MB: batch rows the kernel is compiled for (m <= MB); R: weight rows per
 // wave; U: 256-element k steps whose loads are issued together.
 template <int MB, int R, int U>
-__global__ __launch_bounds__(64 * kNtWaves) void gemv_nt_kernel(NtParams p) {
+__global__ __launch_bounds__(64 * kNtWaves) void gemv_nt_rows_kernel(NtParams p) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t n0 = ((int64_t)blockIdx.x * kNtWaves + wave) * R;
     if (n0 >= p.n) return;  // wave-uniform, and the kernel has no barrier
-    const int64_t z = blockIdx.y;
-    const float *xb = p.x + (z % p.batch_a) * p.stride_a;
-    const float *wb = p.w + (z % p.batch_b) * p.stride_b;
-    float *yb = p.y + z * p.stride_c;
+    const float *xb, *wb;
+    float *yb;
+    batch_slices(p, xb, wb, yb);
 
     // Rows past n read row n-1 and batch rows past m read row m-1: their
     // sums are never stored, and the loads need no condition.
@@ -129,12 +148,7 @@ __global__ __launch_bounds__(64 * kNtWaves) void gemv_nt_kernel(NtParams p) {
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int b = 0; b < MB; ++b) {
-            float v = acc[r][b];
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-            acc[r][b] = v;
-        }
+        for (int b = 0; b < MB; ++b) acc[r][b] = wave_sum(acc[r][b]);
     // Lane r * MB + b stores output (b, n0 + r); same epilogue as the tile
     // GEMM: alpha * acc, then + beta * y (beta != 0 only), then + bias.
 #pragma unroll
@@ -152,26 +166,139 @@ __global__ __launch_bounds__(64 * kNtWaves) void gemv_nt_kernel(NtParams p) {
         }
 }
 
+// Same contract, K split over the workgroup's waves: wave w takes the
+// 256-element steps t = w, w + 4, ... of the workgroup's R rows (the partial
+// last step, if any, belongs to the wave whose turn it is).
+template <int MB, int R, int U>
+__global__ __launch_bounds__(64 * kNtWaves, 2) void gemv_nt_ksplit_kernel(NtParams p) {
+    __shared__ float red[kNtWaves][R * MB];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t n0 = (int64_t)blockIdx.x * R;
+    const float *xb, *wb;
+    float *yb;
+    batch_slices(p, xb, wb, yb);
+
+    const float *wr[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) wr[r] = wb + std::min<int64_t>(n0 + r, p.n - 1) * p.ldb + 4 * lane;
+    const float *xr[MB];
+#pragma unroll
+    for (int b = 0; b < MB; ++b) xr[b] = xb + std::min<int64_t>(b, p.m - 1) * p.lda + 4 * lane;
+
+    float acc[R][MB];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int b = 0; b < MB; ++b) acc[r][b] = 0.f;
+    auto fma4 = [&](const f32x4 (&wv)[R], const f32x4 (&xv)[MB]) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int b = 0; b < MB; ++b)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[r][b] = fmaf(wv[r][e], xv[b][e], acc[r][b]);
+    };
+
+    const int64_t full = p.k / 256;
+    int64_t t = wave;
+    for (; t + kNtWaves * (U - 1) < full; t += kNtWaves * U) {
+        f32x4 wv[U][R], xv[U][MB];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                wv[u][r] = *reinterpret_cast<const f32x4 *>(wr[r] + (t + kNtWaves * u) * 256);
+#pragma unroll
+            for (int b = 0; b < MB; ++b)
+                xv[u][b] = *reinterpret_cast<const f32x4 *>(xr[b] + (t + kNtWaves * u) * 256);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) fma4(wv[u], xv[u]);
+    }
+    for (; t < full; t += kNtWaves) {
+        f32x4 wv[R], xv[MB];
+#pragma unroll
+        for (int r = 0; r < R; ++r) wv[r] = *reinterpret_cast<const f32x4 *>(wr[r] + t * 256);
+#pragma unroll
+        for (int b = 0; b < MB; ++b) xv[b] = *reinterpret_cast<const f32x4 *>(xr[b] + t * 256);
+        fma4(wv, xv);
+    }
+    if (full * 256 < p.k && t == full) {  // the partial step is this wave's turn (wave-uniform)
+        const bool in = full * 256 + 4 * lane < p.k;
+        const int64_t off = in ? full * 256 : -4 * (int64_t)lane;
+        const uint32_t keep = in ? 0xffffffffu : 0u;
+        f32x4 wv[R], xv[MB];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(wr[r] + off);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float ve = v[e];  // (a bit cast of the element lvalue would read element 0)
+                wv[r][e] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, ve) & keep);
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < MB; ++b) {
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(xr[b] + off);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float ve = v[e];
+                xv[b][e] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, ve) & keep);
+            }
+        }
+        fma4(wv, xv);
+    }
+
+    // All the wave sums first, then the stores: a store under a lane
+    // condition between them would serialize the reductions.
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int b = 0; b < MB; ++b) acc[r][b] = wave_sum(acc[r][b]);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int b = 0; b < MB; ++b) red[wave][r * MB + b] = acc[r][b];
+    }
+    __syncthreads();
+    const int idx = threadIdx.x;
+    if (idx < R * MB) {
+        const int r = idx / MB, b = idx % MB;
+        const int64_t col = n0 + r;
+        if (col < p.n && b < p.m) {
+            float *dst = yb + b * p.ldc + col;
+            float v = p.alpha * ((red[0][idx] + red[1][idx]) + (red[2][idx] + red[3][idx]));
+            if (p.beta != 0.f) v = v + p.beta * *dst;
+            if (p.bias) v = v + p.bias[col];
+            *dst = v;
+        }
+    }
+}
+
 template <int MB>
 int launch_mb(const NtParams &p, int64_t batch, hipStream_t s) {
-    // Rows per wave: R = MB / 2 (at least 1), so that the x re-reads from L2
-    // stay at most twice the weight bytes, halved once if that leaves fewer
-    // than 256 workgroups.  Measured on [4096, 4096] / [12288, 4096]: m = 1
-    // 13.4 / 35.1 us at R = 1 against 17.3 / 41.8 at R = 4; m = 4 16.9 /
-    // 43.3 us at R = 2 against 21.1 / 58.9 at R = 1; m = 8 23.7 / 51.7 us at
-    // R = 4 against 32 / 89 at R = 1.  U: 4 steps in flight up to 2 rows of
-    // x, 2 beyond.
     const dim3 block(64 * kNtWaves);
-    auto grid = [&](int r) { return dim3((unsigned)((p.n + kNtWaves * r - 1) / (kNtWaves * r)), (unsigned)batch); };
-    constexpr int U = MB <= 2 ? 4 : 2;
-    int r = MB >= 8 ? 4 : MB >= 4 ? 2 : 1;
-    if (r > 1 && (p.n + kNtWaves * r - 1) / (kNtWaves * r) < 256) r /= 2;
-    if (r == 4)
-        hipLaunchKernelGGL((gemv_nt_kernel<MB, 4, U>), grid(4), block, 0, s, p);
-    else if (r == 2)
-        hipLaunchKernelGGL((gemv_nt_kernel<MB, 2, U>), grid(2), block, 0, s, p);
-    else
-        hipLaunchKernelGGL((gemv_nt_kernel<MB, 1, U>), grid(1), block, 0, s, p);
+    if constexpr (MB <= 4) {
+        // K split over the waves: 2 rows per workgroup up to 2 rows of x, 4
+        // rows at 3-4 (x re-read from L2 at most twice the weight bytes).
+        // Measured on [4096, 4096] / [12288, 4096]: m = 1 12.8 / 33.1 us,
+        // m = 4 15.2 / 38.4 us, against 13.4 / 35.1 and 16.9 / 43.3 us with
+        // one row group per wave.
+        constexpr int R = MB <= 2 ? 2 : 4;
+        constexpr int U = MB <= 2 ? 2 : 1;
+        const dim3 grid((unsigned)((p.n + R - 1) / R), (unsigned)batch);
+        hipLaunchKernelGGL((gemv_nt_ksplit_kernel<MB, R, U>), grid, block, 0, s, p);
+    } else {
+        // 4 rows per wave (2 when that gives fewer than 256 workgroups): at
+        // 8 rows of x, 23.7 / 51.7 us against 32 / 89 us at 1 row per wave.
+        auto grid = [&](int r) { return dim3((unsigned)((p.n + kNtWaves * r - 1) / (kNtWaves * r)), (unsigned)batch); };
+        if ((p.n + kNtWaves * 4 - 1) / (kNtWaves * 4) >= 256)
+            hipLaunchKernelGGL((gemv_nt_rows_kernel<MB, 4, 2>), grid(4), block, 0, s, p);
+        else
+            hipLaunchKernelGGL((gemv_nt_rows_kernel<MB, 2, 2>), grid(2), block, 0, s, p);
+    }
     return check_launch("sgemm (NT GEMV)");
 }
 
