@@ -526,4 +526,136 @@ GFH_API int gfh_mha_forward_with_cache_f32(const float *query, const float *key,
     });
 }
 
+GFH_API int gfh_silu_mul_f32(const float *gate, const float *up, float *out, int64_t n, gfh_stream_t stream) {
+    return guarded([&]() -> int {
+        if (n < 0 || n > ((int64_t)1 << 40))
+            return set_error(GFH_INVALID_SHAPE, "silu_mul: n=%lld out of range", (long long)n);
+        if (n == 0) return GFH_SUCCESS;
+        GFH_TRY(require_range(gate, (size_t)n * 4, "gate"));
+        GFH_TRY(require_range(up, (size_t)n * 4, "up"));
+        GFH_TRY(require_range(out, (size_t)n * 4, "out"));
+        GFH_TRY(ensure_init());
+        return launch_silu_mul(gate, up, out, n, as_stream(stream));
+    });
+}
+
+namespace {
+// Shape checks shared by both SwiGLU entry points.
+int swiglu_shapes(const char *what, int64_t m, int64_t hidden, int64_t inter, int64_t *mh, int64_t *mi,
+                  int64_t *wi) {
+    if (m < 0 || hidden < 0 || inter < 0 || m > kMaxDim || hidden > kMaxDim || inter > kMaxDim)
+        return set_error(GFH_INVALID_SHAPE, "%s: m=%lld hidden=%lld inter=%lld out of range", what, (long long)m,
+                         (long long)hidden, (long long)inter);
+    if (!mul_ok(m, hidden, mh) || !mul_ok(m, inter, mi) || !mul_ok(hidden, inter, wi))
+        return set_error(GFH_INVALID_SHAPE, "%s: operand extent overflows", what);
+    return GFH_SUCCESS;
+}
+}  // namespace
+
+GFH_API size_t gfh_swiglu_f32_workspace_size(int64_t m, int64_t inter) {
+    return swiglu_f32_workspace_bytes(m < 0 ? 0 : m, inter < 0 ? 0 : inter);
+}
+
+GFH_API int gfh_swiglu_f32(const float *x, int64_t m, int64_t hidden, int64_t inter, const float *wg,
+                           const float *bg, const float *wu, const float *bu, const float *wd, const float *bd,
+                           float *y, float *h, void *workspace, size_t workspace_bytes, gfh_stream_t stream) {
+    return guarded([&]() -> int {
+        int64_t mh, mi, wi;
+        GFH_TRY(swiglu_shapes("swiglu", m, hidden, inter, &mh, &mi, &wi));
+        if (m == 0 || hidden == 0) return GFH_SUCCESS;
+        GFH_TRY(require_range(x, (size_t)mh * 4, "x"));
+        GFH_TRY(require_range(wg, (size_t)wi * 4, "wg"));
+        GFH_TRY(require_range(wu, (size_t)wi * 4, "wu"));
+        GFH_TRY(require_range(wd, (size_t)wi * 4, "wd"));
+        GFH_TRY(optional_range(bg, (size_t)inter * 4, "bg"));
+        GFH_TRY(optional_range(bu, (size_t)inter * 4, "bu"));
+        GFH_TRY(optional_range(bd, (size_t)hidden * 4, "bd"));
+        GFH_TRY(require_range(y, (size_t)mh * 4, "y"));
+        GFH_TRY(optional_range(h, (size_t)mi * 4, "h"));
+        if (workspace && !aligned16(workspace))
+            return set_error(GFH_INVALID_DATA, "swiglu: the workspace must be 16-byte aligned");
+        GFH_TRY(ensure_init());
+        hipStream_t s = as_stream(stream);
+        Scratch ws;
+        GFH_TRY(ws.acquire(workspace, workspace_bytes, swiglu_f32_workspace_bytes(m, inter), s));
+        SwigluDesc d;
+        d.x = x;
+        d.m = m;
+        d.hidden = hidden;
+        d.inter = inter;
+        d.wg = wg;
+        d.bg = bg;
+        d.wu = wu;
+        d.bu = bu;
+        d.wd = wd;
+        d.bd = bd;
+        d.y = y;
+        d.h = h;
+        return launch_swiglu_f32(d, ws.ptr(), s);
+    });
+}
+
+GFH_API size_t gfh_swiglu_i8_workspace_size(int64_t m, int64_t hidden, int64_t inter) {
+    return swiglu_i8_workspace_bytes(m < 0 ? 0 : m, hidden < 0 ? 0 : hidden, inter < 0 ? 0 : inter);
+}
+
+GFH_API int gfh_swiglu_i8(const float *x, int64_t m, int64_t hidden, int64_t inter, const int8_t *qwg,
+                          const float *swg, const int32_t *rsg, const float *bg, const int8_t *qwu, const float *swu,
+                          const int32_t *rsu, const float *bu, const int8_t *qwd, const float *swd,
+                          const int32_t *rsd, const float *bd, float *y, float *h, void *workspace,
+                          size_t workspace_bytes, gfh_stream_t stream) {
+    return guarded([&]() -> int {
+        int64_t mh, mi, wi;
+        GFH_TRY(swiglu_shapes("swiglu_i8", m, hidden, inter, &mh, &mi, &wi));
+        if (hidden % 16 != 0 || inter % 16 != 0)
+            return set_error(GFH_INVALID_SHAPE, "swiglu_i8: hidden=%lld and inter=%lld must be multiples of 16",
+                             (long long)hidden, (long long)inter);
+        if (hidden > 65793 || inter > 65793)
+            return set_error(GFH_INVALID_SHAPE, "swiglu_i8: hidden / inter exceed the exact-int32 bound (65793)");
+        if (m == 0 || hidden == 0) return GFH_SUCCESS;
+        if (inter == 0) return set_error(GFH_INVALID_SHAPE, "swiglu_i8: inter must be > 0");
+        GFH_TRY(require_range(x, (size_t)mh * 4, "x"));
+        GFH_TRY(require_range(qwg, (size_t)wi, "qwg"));
+        GFH_TRY(require_range(qwu, (size_t)wi, "qwu"));
+        GFH_TRY(require_range(qwd, (size_t)wi, "qwd"));
+        GFH_TRY(require_range(swg, (size_t)inter * 4, "swg"));
+        GFH_TRY(require_range(swu, (size_t)inter * 4, "swu"));
+        GFH_TRY(require_range(swd, (size_t)hidden * 4, "swd"));
+        GFH_TRY(require_range(rsg, (size_t)inter * 4, "rsg"));
+        GFH_TRY(require_range(rsu, (size_t)inter * 4, "rsu"));
+        GFH_TRY(require_range(rsd, (size_t)hidden * 4, "rsd"));
+        GFH_TRY(optional_range(bg, (size_t)inter * 4, "bg"));
+        GFH_TRY(optional_range(bu, (size_t)inter * 4, "bu"));
+        GFH_TRY(optional_range(bd, (size_t)hidden * 4, "bd"));
+        GFH_TRY(require_range(y, (size_t)mh * 4, "y"));
+        GFH_TRY(optional_range(h, (size_t)mi * 4, "h"));
+        if (!aligned16(qwg) || !aligned16(qwu) || !aligned16(qwd) || (workspace && !aligned16(workspace)))
+            return set_error(GFH_INVALID_DATA, "swiglu_i8: weight codes and the workspace must be 16-byte aligned");
+        GFH_TRY(ensure_init());
+        hipStream_t s = as_stream(stream);
+        Scratch ws;
+        GFH_TRY(ws.acquire(workspace, workspace_bytes, swiglu_i8_workspace_bytes(m, hidden, inter), s));
+        SwigluDesc d;
+        d.x = x;
+        d.m = m;
+        d.hidden = hidden;
+        d.inter = inter;
+        d.qwg = qwg;
+        d.swg = swg;
+        d.rsg = rsg;
+        d.bg = bg;
+        d.qwu = qwu;
+        d.swu = swu;
+        d.rsu = rsu;
+        d.bu = bu;
+        d.qwd = qwd;
+        d.swd = swd;
+        d.rsd = rsd;
+        d.bd = bd;
+        d.y = y;
+        d.h = h;
+        return launch_swiglu_i8(d, ws.ptr(), s);
+    });
+}
+
 }  // extern "C"

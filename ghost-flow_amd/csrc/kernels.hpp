@@ -111,4 +111,22 @@ struct MhaDesc {
 size_t mha_workspace_bytes(int64_t b, int64_t sq, int64_t e);
 int launch_mha_forward(const MhaDesc &d, void *workspace, hipStream_t s);
 
+// swiglu.hip: SwiGLU::forward (llama.rs:276-286).  x [m, hidden]; gate / up
+// weights [inter, hidden], down weight [hidden, inter] (Linear [out, in]);
+// biases nullable; h (nullable) receives silu(gate) * up [m, inter].
+struct SwigluDesc {
+    const float *x = nullptr;
+    int64_t m = 0, hidden = 0, inter = 0;
+    const float *wg = nullptr, *bg = nullptr, *wu = nullptr, *bu = nullptr, *wd = nullptr, *bd = nullptr;
+    const int8_t *qwg = nullptr, *qwu = nullptr, *qwd = nullptr;
+    const float *swg = nullptr, *swu = nullptr, *swd = nullptr;
+    const int32_t *rsg = nullptr, *rsu = nullptr, *rsd = nullptr;
+    float *y = nullptr, *h = nullptr;
+};
+int launch_silu_mul(const float *g, const float *u, float *out, int64_t n, hipStream_t s);
+size_t swiglu_f32_workspace_bytes(int64_t m, int64_t inter);
+int launch_swiglu_f32(const SwigluDesc &d, void *workspace, hipStream_t s);
+size_t swiglu_i8_workspace_bytes(int64_t m, int64_t hidden, int64_t inter);
+int launch_swiglu_i8(const SwigluDesc &d, void *workspace, hipStream_t s);
+
 }  // namespace gfh

@@ -208,9 +208,12 @@ __global__ __launch_bounds__(kThreads) void qlinear_mfma_kernel(QParams p) {
 // (BM/NWM) x (BN/NWN) sub-tile as v_mfma_i32_32x32x32_i8 accumulators.
 // The dispatch runs 8 waves in a 2 x 4 grid: 256 x 256 tiles (M > 512)
 // give each wave 4 x 2 accumulators (128 registers), 128 x 128 tiles 2 x 1.
-// Operands stream through a ring of STAGES stages of BK bytes of K, filled
-// with global_load_lds_dwordx4 (global memory straight into LDS, no VGPR
-// staging); all stages but the one being consumed are in flight.  One load
+// Operands stream through rings of SA (A) and SB (B) slots of BK bytes of K,
+// filled with global_load_lds_dwordx4 (global memory straight into LDS, no
+// VGPR staging); all stages but the one being consumed are in flight.  At
+// 256 x 256 x 128 two full stages take 128 KB, so the remaining 32 KB of the
+// 160 KB LDS holds a third A slot: A stages are requested two stages ahead,
+// B stages one.  One load
 // instruction fills 1 KB of LDS = 1024/BK rows of BK bytes.  BK = 128 makes
 // every row run a whole 128-byte line, which measured 1.6-1.8x the ingest
 // rate per CU of BK = 64 (half lines); BK = 64 serves K % 128 == 64.  Chunk
@@ -260,9 +263,12 @@ __device__ __forceinline__ void interleave() {
     }
 }
 
-template <int BM, int BN, int BK, int STAGES, int NWM = 2, int NWN = 2>
+// SA / SB: ring slots of the A / B operand.  With SA == SB + 1, A stages
+// are requested one stage further ahead than B stages in the same LDS.
+template <int BM, int BN, int BK, int SA, int SB, int NWM = 2, int NWN = 2>
 struct Tile {
     static_assert(BK == 64 || BK == 128, "stage depth in K");
+    static_assert(SB >= 2 && (SA == SB || SA == SB + 1), "ring slots");
     static constexpr int kNW = NWM * NWN, kNT = 64 * kNW;   // waves, threads
     static constexpr int kWM = BM / NWM, kWN = BN / NWN;     // wave sub-tile
     static constexpr int kFM = kWM / 32, kFN = kWN / 32;     // accumulators per wave
@@ -272,8 +278,14 @@ struct Tile {
     static constexpr int kLA = BM * BK / (1024 * kNW), kLB = BN * BK / (1024 * kNW);  // loads per wave per stage
     static constexpr int kLPS = kLA + kLB;
     static constexpr int kABytes = BM * BK, kBBytes = BN * BK;
-    static constexpr int kStageBytes = kABytes + kBBytes;
-    static constexpr int kRing = STAGES * kStageBytes;
+    static constexpr int kRing = SA * kABytes + SB * kBBytes;
+    // Loads of this wave still allowed in flight when stage t+1 must have
+    // landed (end of stage t).  Stage s's B part is requested at the end of
+    // stage s - SB, its A part at the end of stage s - SA, each batch B
+    // first; in-order completion makes the count exact.
+    static constexpr int kWaitSteady = (SA - SB) * kLA + (SB - 2) * (kLA + kLB);
+    // The same before the first stage, after the prologue's requests.
+    static constexpr int kWaitFirst = (SB - 1) * (kLA + kLB) + (SA - SB) * kLA;
     // Output staging: each wave converts half of its sub-tile (kWM/2 rows x
     // kWN columns) at a time; row stride kWN + 8 floats keeps the two row
     // groups of one ds_write_b32 on disjoint banks.
@@ -283,11 +295,11 @@ struct Tile {
     static_assert(kLds <= 160 * 1024, "LDS per workgroup");
 };
 
-template <int BM, int BN, int BK, int STAGES, int NWM, int NWN, bool X_PER_ROW, bool WANT_ACC>
-__global__ __launch_bounds__((Tile<BM, BN, BK, STAGES, NWM, NWN>::kNT),
-                             ((Tile<BM, BN, BK, STAGES, NWM, NWN>::kLds > 80 * 1024) ? 1 : 2)) void qlinear_tile_kernel(
+template <int BM, int BN, int BK, int SA, int SB, int NWM, int NWN, bool X_PER_ROW, bool WANT_ACC>
+__global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
+                             ((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kLds > 80 * 1024) ? 1 : 2)) void qlinear_tile_kernel(
     QParams p) {
-    using T = Tile<BM, BN, BK, STAGES, NWM, NWN>;
+    using T = Tile<BM, BN, BK, SA, SB, NWM, NWN>;
     constexpr int NW = T::kNW;
     constexpr int FM = T::kFM, FN = T::kFN, WM = T::kWM, WN = T::kWN;
     constexpr int RPL = T::kRowsPerLoad, CPR = T::kChunks;
@@ -330,15 +342,20 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, STAGES, NWM, NWN>::kNT),
     }
     const int nk = (int)(p.k / BK);
 
-    auto issue = [&](int t) {
-        int8_t *la = lds + (t % STAGES) * T::kStageBytes;
-        int8_t *lb = la + T::kABytes;
+    // Ring slots: A stages at [0, SA * kABytes), B stages after them.
+    int8_t *const ring_b = lds + SA * T::kABytes;
+    // Request K stage t of A (of B) into ring slot `slot`.
+    auto issue_a = [&](int t, int slot) {
+        int8_t *la = lds + slot * T::kABytes;
         const int8_t *ga = a_base + (int64_t)t * BK;
-        const int8_t *gb = b_base + (int64_t)t * BK;
 #pragma unroll
         for (int j = 0; j < T::kLA; ++j)
             __builtin_amdgcn_global_load_lds((glb_ptr)(ga + a_off[j]), (lds_ptr)(la + (wave * (BM / NW) + j * RPL) * BK),
                                              16, 0, 0);
+    };
+    auto issue_b = [&](int t, int slot) {
+        int8_t *lb = ring_b + slot * T::kBBytes;
+        const int8_t *gb = b_base + (int64_t)t * BK;
 #pragma unroll
         for (int j = 0; j < T::kLB; ++j)
             __builtin_amdgcn_global_load_lds((glb_ptr)(gb + b_off[j]), (lds_ptr)(lb + (wave * (BN / NW) + j * RPL) * BK),
@@ -354,8 +371,8 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, STAGES, NWM, NWN>::kNT),
 
     i32x4 af[2][FM], bf[2][FN];
     auto load_frags = [&](int buf, int t, int ks) {
-        const int8_t *la = lds + (t % STAGES) * T::kStageBytes;
-        const int8_t *lb = la + T::kABytes;
+        const int8_t *la = lds + (t % SA) * T::kABytes;
+        const int8_t *lb = ring_b + (t % SB) * T::kBBytes;
         const int fo = foff0 ^ (ks << 5);
 #pragma unroll
         for (int i = 0; i < FM; ++i) af[buf][i] = *reinterpret_cast<const i32x4 *>(la + (wm0 + i * 32) * BK + fo);
@@ -379,15 +396,20 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, STAGES, NWM, NWN>::kNT),
                 acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[buf][i], bf[buf][j], acc[i][j], 0, 0, 0);
     };
 
-    // Stage t+STAGES is issued into stage t's buffer as soon as every wave
-    // holds the last fragments of stage t.  Within a stage, the fragments of
-    // k-step ks+1 are read while the MFMAs of k-step ks run.  The loop body
-    // has no branches so that the scheduler can interleave reads, loads and
-    // MFMAs across it: past the end of K the ring reloads the last stage
-    // into the buffer just freed (never read), which keeps the number of
-    // stages in flight, and so every wait count, constant.
-    for (int t = 0; t < STAGES; ++t) issue(min(t, nk - 1));
-    wait_vmcnt<(STAGES - 1) * T::kLPS>();
+    // Stages t+SB of B and t+SA of A are issued into stage t's slots as soon
+    // as every wave holds the last fragments of stage t.  Within a stage,
+    // the fragments of k-step ks+1 are read while the MFMAs of k-step ks
+    // run.  The loop body has no branches so that the scheduler can
+    // interleave reads, loads and MFMAs across it: past the end of K the
+    // ring reloads the last stage into the slot just freed (never read
+    // again), which keeps the number of loads in flight, and so every wait
+    // count, constant.
+    for (int t = 0; t < SB; ++t) {
+        issue_a(min(t, nk - 1), t);
+        issue_b(min(t, nk - 1), t);
+    }
+    for (int t = SB; t < SA; ++t) issue_a(min(t, nk - 1), t);
+    wait_vmcnt<T::kWaitFirst>();
     __builtin_amdgcn_s_barrier();
     load_frags(0, 0, 0);
 
@@ -404,10 +426,11 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, STAGES, NWM, NWN>::kNT),
         k_steps(t);
         __builtin_amdgcn_sched_barrier(0);
         wait_lgkm0();  // this wave's reads of stage t are done
-        // stage t+1 landed: stages t+2 .. t+STAGES-1 may still be in flight
-        wait_vmcnt<(STAGES - 2) * T::kLPS>();
+        // stage t+1 landed; later requests may still be in flight
+        wait_vmcnt<T::kWaitSteady>();
         __builtin_amdgcn_s_barrier();
-        issue(min(t + STAGES, nk - 1));
+        issue_b(min(t + SB, nk - 1), t % SB);
+        issue_a(min(t + SA, nk - 1), t % SA);
         load_frags(0, t + 1, 0);
         mfmas((T::kSteps - 1) & 1);
         interleave<T::kLPS, NR, NM>();
@@ -515,21 +538,21 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, STAGES, NWM, NWN>::kNT),
     }
 }
 
-template <int BM, int BN, int BK, int STAGES, int NWM = 2, int NWN = 2>
+template <int BM, int BN, int BK, int SA, int SB, int NWM = 2, int NWN = 2>
 int launch_tiles(QParams p, hipStream_t s) {
     p.tiles_m = (int)((p.m + BM - 1) / BM);
     p.tiles_n = (int)((p.n + BN - 1) / BN);
-    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n)), block(Tile<BM, BN, BK, STAGES, NWM, NWN>::kNT);
+    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n)), block(Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT);
     if (p.x_per_row) {
         if (p.acc)
-            hipLaunchKernelGGL((qlinear_tile_kernel<BM, BN, BK, STAGES, NWM, NWN, true, true>), grid, block, 0, s, p);
+            hipLaunchKernelGGL((qlinear_tile_kernel<BM, BN, BK, SA, SB, NWM, NWN, true, true>), grid, block, 0, s, p);
         else
-            hipLaunchKernelGGL((qlinear_tile_kernel<BM, BN, BK, STAGES, NWM, NWN, true, false>), grid, block, 0, s, p);
+            hipLaunchKernelGGL((qlinear_tile_kernel<BM, BN, BK, SA, SB, NWM, NWN, true, false>), grid, block, 0, s, p);
     } else {
         if (p.acc)
-            hipLaunchKernelGGL((qlinear_tile_kernel<BM, BN, BK, STAGES, NWM, NWN, false, true>), grid, block, 0, s, p);
+            hipLaunchKernelGGL((qlinear_tile_kernel<BM, BN, BK, SA, SB, NWM, NWN, false, true>), grid, block, 0, s, p);
         else
-            hipLaunchKernelGGL((qlinear_tile_kernel<BM, BN, BK, STAGES, NWM, NWN, false, false>), grid, block, 0, s, p);
+            hipLaunchKernelGGL((qlinear_tile_kernel<BM, BN, BK, SA, SB, NWM, NWN, false, false>), grid, block, 0, s, p);
     }
     return check_launch("qlinear_i8");
 }
@@ -759,12 +782,12 @@ int launch_qlinear_i8(const QLinearDesc &d, hipStream_t s) {
     if (ring_ok) {
         const bool bk128 = d.k % 128 == 0;
         if (d.m > 512)
-            return bk128 ? big::launch_tiles<256, 256, 128, 2, 2, 4>(p, s)
-                         : big::launch_tiles<256, 256, 64, 4, 2, 4>(p, s);
+            return bk128 ? big::launch_tiles<256, 256, 128, 3, 2, 2, 4>(p, s)
+                         : big::launch_tiles<256, 256, 64, 4, 4, 2, 4>(p, s);
         const int64_t tiles = ((d.m + 127) / 128) * ((d.n + 127) / 128);
-        if (!bk128) return big::launch_tiles<128, 128, 64, 4, 2, 4>(p, s);
-        return tiles <= 256 ? big::launch_tiles<128, 128, 128, 3, 2, 4>(p, s)
-                            : big::launch_tiles<128, 128, 128, 2, 2, 4>(p, s);
+        if (!bk128) return big::launch_tiles<128, 128, 64, 4, 4, 2, 4>(p, s);
+        return tiles <= 256 ? big::launch_tiles<128, 128, 128, 3, 3, 2, 4>(p, s)
+                            : big::launch_tiles<128, 128, 128, 2, 2, 2, 4>(p, s);
     }
     p.tiles_m = (int)((d.m + kBM - 1) / kBM);
     p.tiles_n = (int)((d.n + kBN - 1) / kBN);

@@ -1,5 +1,6 @@
 """ghostflow_hip -- Python bindings of the gfx950 backend for GhostFlow's dense
-hot path (fp32 GEMM / Linear, int8 quantized linear, decode GEMV, SDPA).
+hot path (fp32 GEMM / Linear, int8 quantized linear, decode GEMV, SDPA) and
+the layers built on it (MultiHeadAttention with a KV cache, SwiGLU).
 
 All compute goes through the C ABI of libghostflow_hip.so
 (include/ghostflow_hip.h); see ops.py.  The package lives in the
@@ -20,14 +21,17 @@ from .ops import (  # noqa: F401
     mha_forward_with_cache,
     mha_workspace_size,
     qlinear,
+    qswiglu,
     quantize_per_channel,
     quantize_per_tensor,
     quantize_per_tensor_workspace_size,
     qweight_rowsum,
     sdpa,
     set_pointer_checks,
+    silu_mul,
     sgemm,
     softmax_lastdim,
+    swiglu,
 )
-from .nn import KVCache, MultiHeadAttention  # noqa: F401
+from .nn import KVCache, MultiHeadAttention, QuantizedSwiGLU, SwiGLU  # noqa: F401
 from .synth import normal, uniform  # noqa: F401

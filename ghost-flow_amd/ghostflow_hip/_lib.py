@@ -61,6 +61,12 @@ SIGNATURES = {
     "gfh_mha_workspace_size": (_sz, [_i64, _i64, _i64]),
     "gfh_mha_forward_with_cache_f32": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p,
                                             _i64, _i, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _sz, _p]),
+    "gfh_silu_mul_f32": (_i, [_p, _p, _p, _i64, _p]),
+    "gfh_swiglu_f32_workspace_size": (_sz, [_i64, _i64]),
+    "gfh_swiglu_f32": (_i, [_p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p]),
+    "gfh_swiglu_i8_workspace_size": (_sz, [_i64, _i64, _i64]),
+    "gfh_swiglu_i8": (_i, [_p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
+                           _sz, _p]),
 }
 
 _lib = None

@@ -1,4 +1,4 @@
-"""Module-level mirrors of the reference's attention layer on this library.
+"""Module-level mirrors of the reference's attention and feed-forward layers.
 
 MultiHeadAttention follows ghostflow-nn/src/attention.rs:66-170: four
 embed_dim x embed_dim Linear projections stored [out, in] with biases,
@@ -11,6 +11,10 @@ raise, so use eval() or dropout 0.
 KVCache is the in-place form of the reference's past_key / past_value
 concatenation: preallocated [B, capacity, E] buffers that every step
 appends to, so a decode step costs no copy of the past.
+
+SwiGLU follows ghostflow-nn/src/llama.rs:259-287 (LLaMA / Mistral
+feed-forward); QuantizedSwiGLU is the same block with DynamicQuantization's
+int8 weights (ghostflow-nn/src/quantization.rs:251-288).
 """
 from __future__ import annotations
 
@@ -19,7 +23,8 @@ import math
 import torch
 
 from . import _lib
-from .ops import GhostFlowError, mha_forward_cached, mha_forward_with_cache
+from .ops import (GhostFlowError, mha_forward_cached, mha_forward_with_cache, qswiglu, quantize_per_channel,
+                  qweight_rowsum, swiglu)
 
 
 class KVCache:
@@ -97,3 +102,68 @@ class MultiHeadAttention:
 
     def is_training(self) -> bool:
         return self.training
+
+
+class SwiGLU:
+    """ghostflow-nn SwiGLU (llama.rs:259-287): gate_proj and up_proj
+    Linear(hidden, inter), down_proj Linear(inter, hidden), all with bias
+    (Linear::new), forward = down(silu(gate(x)) * up(x)) on the GPU."""
+
+    def __init__(self, hidden_size: int, intermediate_size: int, device="cuda"):
+        self.hidden_size = hidden_size
+        self.intermediate_size = intermediate_size
+
+        # Linear::new's init (linear.rs:23-33, init.rs:31-41) with an unseeded
+        # RNG in the reference, so only the distribution is kept.
+        def lin(n_in, n_out):
+            wb, bb = math.sqrt(6.0 / n_in), 1.0 / math.sqrt(n_in)
+            w = (torch.rand((n_out, n_in), device=device) * 2 - 1) * wb
+            b = (torch.rand((n_out,), device=device) * 2 - 1) * bb
+            return w, b
+
+        self.gate_weight, self.gate_bias = lin(hidden_size, intermediate_size)
+        self.up_weight, self.up_bias = lin(hidden_size, intermediate_size)
+        self.down_weight, self.down_bias = lin(intermediate_size, hidden_size)
+
+    def forward(self, x):
+        """x [..., hidden] -> [..., hidden]."""
+        lead = x.shape[:-1]
+        y = swiglu(x.reshape(-1, self.hidden_size).contiguous(), self.gate_weight, self.gate_bias,
+                   self.up_weight, self.up_bias, self.down_weight, self.down_bias)
+        return y.reshape(*lead, self.hidden_size)
+
+    __call__ = forward
+
+    def parameters(self):
+        return [self.gate_weight, self.gate_bias, self.up_weight, self.up_bias, self.down_weight,
+                self.down_bias]
+
+    def quantize(self) -> "QuantizedSwiGLU":
+        """DynamicQuantization of each projection (quantization.rs:251-288):
+        weights per-channel symmetric int8, biases kept in fp32."""
+        return QuantizedSwiGLU(self)
+
+
+class QuantizedSwiGLU:
+    """SwiGLU with DynamicQuantization's int8 weights: codes [out, in],
+    per-row scales, per-row code sums for the activation zero point.
+    Activations are quantized per tensor (asymmetric) on each call."""
+
+    def __init__(self, layer: SwiGLU):
+        self.hidden_size = layer.hidden_size
+        self.intermediate_size = layer.intermediate_size
+
+        def q(w, b):
+            codes, scales, _zp = quantize_per_channel(w, symmetric=True)
+            return codes, scales, qweight_rowsum(codes), b
+
+        self.gate = q(layer.gate_weight, layer.gate_bias)
+        self.up = q(layer.up_weight, layer.up_bias)
+        self.down = q(layer.down_weight, layer.down_bias)
+
+    def forward(self, x):
+        lead = x.shape[:-1]
+        y = qswiglu(x.reshape(-1, self.hidden_size).contiguous(), self.gate, self.up, self.down)
+        return y.reshape(*lead, self.hidden_size)
+
+    __call__ = forward

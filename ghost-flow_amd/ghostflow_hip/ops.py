@@ -338,3 +338,67 @@ def mha_forward_with_cache(query, key, value, wq, bq, wk, bk, wv, bv, wo, bo, nu
     k_new = kc[:, p:].reshape(b, sk, num_heads, d).transpose(1, 2)
     v_new = vc[:, p:].reshape(b, sk, num_heads, d).transpose(1, 2)
     return out, w, k_new, v_new
+
+
+# ---- SwiGLU feed-forward block (ghostflow-nn/src/llama.rs:259-287) -------------
+
+def silu_mul(gate, up, out=None):
+    """gate.silu().mul(&up): silu(v) = v / (1 + exp(-v)) (activation.rs:117-122)."""
+    _need(gate, torch.float32, "gate")
+    _need(up, torch.float32, "up")
+    if gate.shape != up.shape:
+        raise GhostFlowError(_lib.INVALID_SHAPE, f"ShapeMismatch {list(gate.shape)} vs {list(up.shape)}")
+    if out is None:
+        out = torch.empty_like(gate)
+    _need(out, torch.float32, "out")
+    _check(lib().gfh_silu_mul_f32(gate.data_ptr(), up.data_ptr(), out.data_ptr(), gate.numel(),
+                                  _stream(gate.device)))
+    return out
+
+
+def _swiglu_dims(x, w_gate, w_down):
+    if x.dim() != 2:
+        raise GhostFlowError(_lib.INVALID_SHAPE, "x must be [m, hidden]")
+    m, hidden = x.shape
+    inter = w_gate.shape[0]
+    if w_gate.shape[1] != hidden or tuple(w_down.shape) != (hidden, inter):
+        raise GhostFlowError(_lib.INVALID_SHAPE, f"ShapeMismatch x [{m}, {hidden}] with gate "
+                             f"{list(w_gate.shape)} and down {list(w_down.shape)}")
+    return m, hidden, inter
+
+
+def swiglu(x, wg, bg, wu, bu, wd, bd, *, want_h=False):
+    """SwiGLU::forward (llama.rs:276-286) in fp32; returns y, or (y, h) with
+    h = silu(gate) * up when want_h."""
+    for t, n in ((x, "x"), (wg, "wg"), (bg, "bg"), (wu, "wu"), (bu, "bu"), (wd, "wd"), (bd, "bd")):
+        _need(t, torch.float32, n)
+    m, hidden, inter = _swiglu_dims(x, wg, wd)
+    y = torch.empty((m, hidden), dtype=torch.float32, device=x.device)
+    h = torch.empty((m, inter), dtype=torch.float32, device=x.device) if want_h else None
+    _check(lib().gfh_swiglu_f32(x.data_ptr(), m, hidden, inter, wg.data_ptr(), _ptr(bg), wu.data_ptr(),
+                                _ptr(bu), wd.data_ptr(), _ptr(bd), y.data_ptr(), _ptr(h), None, 0,
+                                _stream(x.device)))
+    return (y, h) if want_h else y
+
+
+def qswiglu(x, gate, up, down, *, want_h=False):
+    """SwiGLU::forward with each Linear as the INT8 linear on
+    DynamicQuantization's scheme (quantization.rs:251-288).  gate / up / down
+    are (codes, scales, rowsums, bias-or-None) of per-channel symmetric
+    weights [out, in]; x and h are quantized per tensor (asymmetric) on the
+    device."""
+    _need(x, torch.float32, "x")
+    for name, (q, s, r, b) in (("gate", gate), ("up", up), ("down", down)):
+        _need(q, torch.int8, name + " codes")
+        _need(s, torch.float32, name + " scales")
+        _need(r, torch.int32, name + " rowsums")
+        _need(b, torch.float32, name + " bias")
+    m, hidden, inter = _swiglu_dims(x, gate[0], down[0])
+    y = torch.empty((m, hidden), dtype=torch.float32, device=x.device)
+    h = torch.empty((m, inter), dtype=torch.float32, device=x.device) if want_h else None
+    args = []
+    for q, s, r, b in (gate, up, down):
+        args += [q.data_ptr(), s.data_ptr(), r.data_ptr(), _ptr(b)]
+    _check(lib().gfh_swiglu_i8(x.data_ptr(), m, hidden, inter, *args, y.data_ptr(), _ptr(h), None, 0,
+                               _stream(x.device)))
+    return (y, h) if want_h else y

@@ -256,6 +256,49 @@ GFH_API int gfh_mha_forward_with_cache_f32(
     int64_t sq, int64_t sk, int64_t e, int64_t h, void *workspace,
     size_t workspace_bytes, gfh_stream_t stream);
 
+/* ---- SwiGLU feed-forward block ------------------------------------------ */
+
+/* out[i] = silu(gate[i]) * up[i], silu(v) = v / (1 + exp(-v)): the
+ * gate.silu().mul(&up) step of SwiGLU::forward (ghostflow-nn/src/llama.rs:
+ * 281-283; silu = ghostflow-core/src/ops/activation.rs:117-122, mul =
+ * arithmetic.rs:39-45).  out may alias gate or up. */
+GFH_API int gfh_silu_mul_f32(const float *gate, const float *up, float *out, int64_t n,
+                             gfh_stream_t stream);
+
+/* SwiGLU::forward (ghostflow-nn/src/llama.rs:276-286), fp32:
+ *   y = (silu(x . Wg^T + bg) * (x . Wu^T + bu)) . Wd^T + bd
+ * x [m, hidden]; wg, wu [inter, hidden] and wd [hidden, inter] as Linear
+ * weights [out, in]; biases nullable (Linear::new has them, linear.rs:18-20);
+ * y [m, hidden]; h (nullable) [m, inter] receives silu(gate) * up.
+ * workspace (nullable, 16-byte aligned) of at least
+ * gfh_swiglu_f32_workspace_size(m, inter) bytes; without one the call
+ * allocates stream-ordered. */
+GFH_API size_t gfh_swiglu_f32_workspace_size(int64_t m, int64_t inter);
+GFH_API int gfh_swiglu_f32(const float *x, int64_t m, int64_t hidden, int64_t inter,
+                           const float *wg, const float *bg, const float *wu, const float *bu,
+                           const float *wd, const float *bd, float *y, float *h,
+                           void *workspace, size_t workspace_bytes, gfh_stream_t stream);
+
+/* SwiGLU::forward with each Linear as the INT8 linear (gfh_qlinear_i8) on
+ * DynamicQuantization's scheme (ghostflow-nn/src/quantization.rs:251-288):
+ *   qwg, qwu [inter, hidden], qwd [hidden, inter]: per-channel symmetric
+ *     codes (quantize_per_channel_int8, :110-153) with scales swg / swu /
+ *     swd and row sums rsg / rsu / rsd (gfh_qweight_rowsum);
+ *   x and h = silu(gate) * up are quantized per tensor, asymmetric
+ *     (quantize_activation, :280-287) on the device;
+ *   gate, up and y are the dequantized fp32 outputs plus bias.
+ * h (nullable) [m, inter] receives silu(gate) * up.  workspace (nullable,
+ * 16-byte aligned) of at least gfh_swiglu_i8_workspace_size(m, hidden,
+ * inter) bytes.  hidden and inter must be multiples of 16. */
+GFH_API size_t gfh_swiglu_i8_workspace_size(int64_t m, int64_t hidden, int64_t inter);
+GFH_API int gfh_swiglu_i8(const float *x, int64_t m, int64_t hidden, int64_t inter,
+                          const int8_t *qwg, const float *swg, const int32_t *rsg,
+                          const float *bg, const int8_t *qwu, const float *swu,
+                          const int32_t *rsu, const float *bu, const int8_t *qwd,
+                          const float *swd, const int32_t *rsd, const float *bd, float *y,
+                          float *h, void *workspace, size_t workspace_bytes,
+                          gfh_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -29,6 +29,11 @@
  *   gfo_softmax_lastdim : rows sum to 1 (activation.rs:266-272,
  *       tests/test_optimizations.rs:51-62); constant row -> uniform;
  *       fp64 closed form within a few ulp; all -inf row -> NaN.
+ *   gfo_silu_mul : silu(0) = 0, silu(x) = x once exp(-x) < ulp(1)/2,
+ *       silu(-x) = -0 once exp(x) overflows; bit-exact against a float32
+ *       restatement on inputs whose expf is unambiguous, chosen so that
+ *       the plausible x * (1 / (1 + e)) form differs; fp64 closed form
+ *       within a few ulp.
  *   gfo_sdpa / gfo_flash_attention : causal row 0 == V[0] exactly;
  *       constant K -> prefix mean of V; fp64 brute force on tiny shapes;
  *       cycled [S,S] causal mask == causal flag path bit for bit.
@@ -205,6 +210,19 @@ GFO_API void gfo_softmax_lastdim(const float *x, float *y, size_t rows,
             sum = sum + e;
         }
         for (size_t j = 0; j < cols; ++j) yr[j] = yr[j] / sum;
+    }
+}
+
+/* activation.rs:117-122 `silu` = x / (1.0 + (-x).exp()) (negate, expf, add,
+ * true division: three roundings), then arithmetic.rs:39-45 `mul` of two
+ * same-shaped tensors (one rounding): the `gate.silu().mul(&up)` step of
+ * SwiGLU::forward (ghostflow-nn/src/llama.rs:276-286). */
+GFO_API void gfo_silu_mul(const float *gate, const float *up, float *out,
+                          size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        const float g = gate[i];
+        const float s = g / (1.0f + expf(-g));
+        out[i] = s * up[i];
     }
 }
 

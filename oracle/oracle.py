@@ -42,6 +42,7 @@ def lib():
         L.gfo_linear_forward.argtypes = [_f32p, _f32p, C.c_void_p, _f32p, _sz, _sz, _sz]
         L.gfo_linear_forward.restype = C.c_int
         L.gfo_softmax_lastdim.argtypes = [_f32p, _f32p, _sz, _sz]
+        L.gfo_silu_mul.argtypes = [_f32p, _f32p, _f32p, _sz]
         L.gfo_apply_mask_cycled.argtypes = [_f32p, _sz, _f32p, _sz]
         L.gfo_apply_causal.argtypes = [_f32p, _sz, _sz]
         L.gfo_sdpa.argtypes = [_f32p, _f32p, _f32p, C.c_void_p, _sz, _f32p, C.c_void_p,
@@ -119,6 +120,26 @@ def linear_forward(x, w, bias=None):
     if rc:
         raise MemoryError("oracle allocation failed")
     return y
+
+
+def silu_mul(gate, up):
+    """gate.silu().mul(&up) (activation.rs:117-122, arithmetic.rs:39-45)."""
+    g, u = _f32(gate), _f32(up)
+    if g.shape != u.shape:
+        raise ValueError("gate and up must have the same shape")
+    out = np.empty(g.shape, np.float32)
+    lib().gfo_silu_mul(g.reshape(-1), u.reshape(-1), out.reshape(-1), g.size)
+    return out
+
+
+def swiglu_forward(x, wg, bg, wu, bu, wd, bd):
+    """SwiGLU::forward (ghostflow-nn/src/llama.rs:276-286): three
+    Linear::forward calls and the silu * up product, composed from the
+    restated pieces.  Returns (y, h) with h = silu(gate) * up."""
+    gate = linear_forward(x, wg, bg)
+    up = linear_forward(x, wu, bu)
+    h = silu_mul(gate, up)
+    return linear_forward(h, wd, bd), h
 
 
 def softmax_lastdim(x):
@@ -248,6 +269,22 @@ def dequantize(q, scales, zps):
     lib().gfo_dequantize(q.reshape(-1), rows, cols, scales, zps, scales.size,
                          out.reshape(-1))
     return out
+
+
+def qswiglu_forward(x, qwg, swg, bg, qwu, swu, bu, qwd, swd, bd):
+    """SwiGLU::forward (llama.rs:276-286) with every Linear run as the INT8
+    linear on DynamicQuantization's scheme (quantization.rs:251-288):
+    weights per-channel symmetric codes + scales, activations quantized per
+    tensor, asymmetric (quantize_activation, :280-287) -- x before gate/up,
+    h = silu(gate) * up before down.  Returns a dict of every stage."""
+    qx, sx, zx = quantize_per_tensor(x, symmetric=False)
+    gate, _ = qlinear_i8(qx, sx, zx, False, qwg, swg, bg, want_acc=False)
+    up, _ = qlinear_i8(qx, sx, zx, False, qwu, swu, bu, want_acc=False)
+    h = silu_mul(gate, up)
+    qh, sh, zh = quantize_per_tensor(h, symmetric=False)
+    y, _ = qlinear_i8(qh, sh, zh, False, qwd, swd, bd, want_acc=False)
+    return {"qx": qx, "sx": sx, "zx": zx, "gate": gate, "up": up, "h": h, "qh": qh, "sh": sh, "zh": zh,
+            "y": y}
 
 
 def qlinear_i8(qx, sx, zx, x_per_row, qw, sw, bias=None, want_acc=True):

@@ -138,3 +138,30 @@ def test_kv_attention_rejects_bad_shapes():
     # causal with more queries than keys
     assert lib.gfh_kv_attention_f32(p, 16, p, p, 8, 16, p, 16, None, 1, 2, 4, 3, 8, 1.0, 1, None, 0, None) == 1
     assert b"causal" in lib.gfh_last_error()
+
+
+def test_swiglu_rejects_bad_shapes():
+    lib = _lib()
+    p, _keep = _fake()
+    assert lib.gfh_silu_mul_f32(p, p, p, -1, None) == 1
+    assert lib.gfh_silu_mul_f32(None, None, None, 0, None) == 0  # empty is a no-op
+    assert lib.gfh_swiglu_f32(p, -1, 16, 16, p, None, p, None, p, None, p, None, None, 0, None) == 1
+    assert b"out of range" in lib.gfh_last_error()
+    assert lib.gfh_swiglu_f32(None, 0, 16, 16, None, None, None, None, None, None, None, None, None, 0,
+                              None) == 0
+    # int8 rows must be whole 16-byte groups
+    args = [p] * 12
+    assert lib.gfh_swiglu_i8(p, 2, 24, 32, *args, p, None, None, 0, None) == 1
+    assert b"multiples of 16" in lib.gfh_last_error()
+    assert lib.gfh_swiglu_i8(p, 2, 16, 70000 * 16, *args, p, None, None, 0, None) == 1
+    assert b"exact-int32" in lib.gfh_last_error()
+    # host memory is not device memory
+    assert lib.gfh_swiglu_i8(p, 2, 16, 32, *args, p, None, None, 0, None) != 0
+
+
+def test_swiglu_workspace_sizes():
+    lib = _lib()
+    assert lib.gfh_swiglu_f32_workspace_size(4, 100) >= 2 * 4 * 100 * 4
+    n = lib.gfh_swiglu_i8_workspace_size(4, 64, 96)
+    assert n >= 4 * 64 + 2 * 4 * 96 * 4 + 4 * 96
+    assert lib.gfh_swiglu_i8_workspace_size(-1, -1, -1) >= 0
