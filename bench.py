@@ -61,7 +61,7 @@ def parse_args():
     ap.add_argument("--cpu-rows", type=int, default=768,
                     help="rows of x in the CPU-baseline sample (of 4096)")
     ap.add_argument("--only", default="",
-                    help="comma list of components to run (sgemm,qlinear,gemv,sdpa,decode); "
+                    help="comma list of components to run (sgemm,qlinear,gemv,sdpa,decode,swiglu); "
                          "used for focused profiling")
     ap.add_argument("--detail", default="", help="also write the full result JSON to this file")
     ap.add_argument("--calib-copy", action="store_true",
@@ -404,8 +404,64 @@ def comp_mha_decode(lib, torch, B=4, H=32, D=128, past=2047):
             "set_copies": ncopy}
 
 
+def comp_swiglu(lib, torch, m, int8, H=4096, I=11008):
+    """SwiGLU::forward (llama.rs:276-286) at the LLaMA-7B feed-forward shape,
+    hidden 4096, intermediate 11008, x [m, 4096] ~ N(0, 1).
+    * int8 (gfh_swiglu_i8): W ~ N(0, 0.02) per-channel symmetric codes; x
+      and h quantized per tensor on the device; gate/up as one fused launch.
+    * fp32 (gfh_swiglu_f32): W ~ U(+-sqrt(6/in)), b ~ U(+-1/sqrt(in)).
+    Work: 6*m*H*I ops (three GEMMs).  Algorithmic bytes: the three weights
+    (s_w*3*H*I) + x + y (8*m*H); the bound is min(MFMA peak, AI * HBM)."""
+    dev = torch.device("cuda:0")
+    gh = lib.gh
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    sw = 1 if int8 else 4
+    wbytes = 3 * H * I * sw
+    ncopy = max(1, -(-2 * MALL_BYTES // wbytes) + 1) if m <= 256 else 1
+    sets = []
+    for _ in range(ncopy):
+        layer = []
+        for n_out, n_in in ((I, H), (I, H), (H, I)):
+            if int8:
+                w = torch.randn((n_out, n_in), device=dev, generator=g) * 0.02
+                q, sc, _ = gh.quantize_per_channel(w, symmetric=True)
+                del w
+                b = (torch.rand((n_out,), device=dev, generator=g) * 2 - 1) / n_in ** 0.5
+                layer.append((q, sc, gh.qweight_rowsum(q), b))
+            else:
+                w = (torch.rand((n_out, n_in), device=dev, generator=g) * 2 - 1) * (6.0 / n_in) ** 0.5
+                b = (torch.rand((n_out,), device=dev, generator=g) * 2 - 1) / n_in ** 0.5
+                layer.append((w, b))
+        sets.append(layer)
+    x = torch.randn((m, H), device=dev, generator=g)
+    y = torch.empty((m, H), device=dev)
+    L = lib.L
+    nws = int(L.gfh_swiglu_i8_workspace_size(m, H, I) if int8 else L.gfh_swiglu_f32_workspace_size(m, I))
+    ws = torch.empty((nws + 3) // 4, device=dev)
+    s = torch.cuda.current_stream(dev).cuda_stream
+    ptrs = [[t.data_ptr() for part in layer for t in part] for layer in sets]
+
+    def f(i):
+        p = ptrs[i % ncopy]
+        if int8:
+            L.gfh_swiglu_i8(x.data_ptr(), m, H, I, *p, y.data_ptr(), None, ws.data_ptr(), nws, s)
+        else:
+            L.gfh_swiglu_f32(x.data_ptr(), m, H, I, *p, y.data_ptr(), None, ws.data_ptr(), nws, s)
+    ops = 6.0 * m * H * I
+    ms = event_time_ms(torch, f, 20 if ops > 1e12 else 100)
+    byts = wbytes + 8 * m * H
+    peak = PEAK_I8 if int8 else PEAK_F32
+    attain = min(peak, ops / byts * PEAK_HBM)
+    del sets
+    return {"name": f"swiglu_{'i8' if int8 else 'f32'}_m{m}_h{H}_i{I}", "ms": ms,
+            "value": ops / ms / 1e9, "unit": "TOP/s" if int8 else "TFLOP/s", "gbps": byts / ms / 1e6,
+            "frac": ops / (ms * 1e-3) / attain,
+            "bound": ("mfma_i8" if int8 else "mfma_f32") if attain == peak else "hbm", "weight_sets": ncopy}
+
+
 def run_components(lib, torch, only):
-    want = set(filter(None, only.split(","))) or {"sgemm", "qlinear", "gemv", "sdpa", "decode"}
+    want = set(filter(None, only.split(","))) or {"sgemm", "qlinear", "gemv", "sdpa", "decode", "swiglu"}
     out = []
 
     def add(fn, *a, **kw):
@@ -436,6 +492,11 @@ def run_components(lib, torch, only):
             add(comp_linear_decode, m)
         add(comp_kv_attention)
         add(comp_mha_decode)
+    if "swiglu" in want:
+        for m in (1, 16, 256, 4096):
+            add(comp_swiglu, m, True)
+        for m in (1, 16, 4096):
+            add(comp_swiglu, m, False)
     return out
 
 

@@ -116,3 +116,21 @@ __device__ __forceinline__ float half_wave_sum(float v) {
     const float hi = readlane_f(v, 32) + readlane_f(v, 48);
     return (threadIdx.x & 32) ? hi : lo;
 }
+
+// silu(g) * up as the reference computes it (activation.rs:117-122 and
+// arithmetic.rs:39-45): negate, expf, add, IEEE division, multiply -- each
+// a separate f32 rounding.
+__device__ __forceinline__ float silu_mul1(float g, float u) {
+#pragma clang fp contract(off)
+    const float s = g / (1.0f + expf(-g));
+    return s * u;
+}
+
+// (min, max) over the 64 lanes, NaN-ignoring like f32::min / f32::max.
+__device__ __forceinline__ void wave_minmax(float &mn, float &mx) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        mn = fminf(mn, __shfl_xor(mn, off));
+        mx = fmaxf(mx, __shfl_xor(mx, off));
+    }
+}

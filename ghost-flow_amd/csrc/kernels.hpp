@@ -33,6 +33,8 @@ int launch_quantize_per_channel(const float *x, int64_t rows, int64_t cols, bool
 size_t quantize_per_tensor_workspace(int64_t n);
 int launch_quantize_per_tensor(const float *x, int64_t n, bool symmetric, int8_t *q, float *scale, int8_t *zp,
                                void *ws, hipStream_t s);
+int launch_quantize_per_tensor_partials(const float *x, int64_t n, bool symmetric, const float2 *partials,
+                                       int npartials, int8_t *q, float *scale, int8_t *zp, hipStream_t s);
 int launch_dequantize(const int8_t *q, int64_t rows, int64_t cols, const float *scales, const int8_t *zps,
                       int64_t nscales, float *out, hipStream_t s);
 int launch_rowsum_i8(const int8_t *q, int64_t n, int64_t k, int32_t *rowsum, hipStream_t s);
@@ -52,6 +54,23 @@ struct QLinearDesc {
     int64_t m = 0, n = 0, k = 0;
 };
 int launch_qlinear_i8(const QLinearDesc &d, hipStream_t s);
+// SwiGLU gate/up in one launch: h = silu(x.Wg^T + bg) * (x.Wu^T + bu) with x
+// quantized per tensor (g.zx per tensor, g.x_per_row false); g carries x,
+// the gate weight and h (as y), the up_* fields the up weight.  Writes one
+// (min, max) of h per workgroup into hpart and their count into *npart.
+struct QSwigluDesc {
+    QLinearDesc g;
+    const int8_t *qw_up = nullptr;
+    const float *sw_up = nullptr;
+    const int32_t *rowsum_up = nullptr;
+    const float *bias_up = nullptr;
+    float2 *hpart = nullptr;
+};
+// Whether the fused launch serves this shape (else: two INT8 linears and
+// launch_silu_mul), and the hpart capacity it needs.
+bool qlinear_swiglu_fits(int64_t m, int64_t n, int64_t k);
+int64_t qlinear_swiglu_partials(int64_t m, int64_t n);
+int launch_qlinear_swiglu_i8(const QSwigluDesc &d, int *npart, hipStream_t s);
 
 // gemv.hip
 int launch_gemv_f32(const float *x, const float *w, float *y, int64_t b, int64_t k, int64_t n, hipStream_t s);

@@ -54,6 +54,13 @@ struct QParams {
     int64_t m, n, k;
     int x_per_row;
     int tiles_m, tiles_n;
+    // SwiGLU gate/up mode (the `*2` operand is up_proj, the first gate_proj):
+    // y = silu(gate) * up, and per-workgroup (min, max) of y into hpart.
+    const int8_t *qw2;
+    const float *sw2;
+    const int32_t *rowsum2;
+    const float *bias2;
+    float2 *hpart;
 };
 
 // One 128 x BK byte stage of a K-contiguous int8 operand: 1024 16-byte
@@ -295,11 +302,16 @@ struct Tile {
     static_assert(kLds <= 160 * 1024, "LDS per workgroup");
 };
 
-template <int BM, int BN, int BK, int SA, int SB, int NWM, int NWN, bool X_PER_ROW, bool WANT_ACC>
+// DUAL (SwiGLU gate/up): the B tile's 32-row blocks alternate between
+// gate_proj and up_proj rows of the same BN / 2 output columns, so a wave's
+// accumulator blocks j = 0 / 1 hold gate / up of one 32-column group and the
+// epilogue writes silu(gate) * up straight from registers.
+template <int BM, int BN, int BK, int SA, int SB, int NWM, int NWN, bool X_PER_ROW, bool WANT_ACC, bool DUAL = false>
 __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
                              ((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kLds > 80 * 1024) ? 1 : 2)) void qlinear_tile_kernel(
     QParams p) {
     using T = Tile<BM, BN, BK, SA, SB, NWM, NWN>;
+    static_assert(!DUAL || (!X_PER_ROW && !WANT_ACC && NWN * 64 == BN), "dual mode: wave = 2 column blocks");
     constexpr int NW = T::kNW;
     constexpr int FM = T::kFM, FN = T::kFN, WM = T::kWM, WN = T::kWN;
     constexpr int RPL = T::kRowsPerLoad, CPR = T::kChunks;
@@ -320,7 +332,8 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
     const int gm = min(p.tiles_m - first_m, kGroupM);
     const int in_group = bid - group * group_size;
     const int64_t m0 = (int64_t)(first_m + in_group % gm) * BM;
-    const int64_t n0 = (int64_t)(in_group / gm) * BN;
+    // first output column (in dual mode BN / 2 columns of gate and of up)
+    const int64_t n0 = (int64_t)(in_group / gm) * (DUAL ? BN / 2 : BN);
 
     // Byte offsets, relative to the tile's first row, of this wave's load
     // instructions: A instruction j covers tile rows wave*(BM/NW) + j*RPL ..
@@ -328,7 +341,7 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
     // chunk l % CPR) from logical chunk (l % CPR) ^ swz(row).  The host
     // guarantees BM * K < 2^32.
     const int8_t *a_base = p.qx + m0 * p.k;
-    const int8_t *b_base = p.qw + n0 * p.k;
+    const int8_t *b_src[T::kLB];  // per load instruction: its matrix at row n0 (uniform)
     uint32_t a_off[T::kLA], b_off[T::kLB];
 #pragma unroll
     for (int j = 0; j < T::kLA; ++j) {
@@ -337,8 +350,11 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
     }
 #pragma unroll
     for (int j = 0; j < T::kLB; ++j) {
-        const int r = wave * (BN / NW) + j * RPL + lane / CPR;
-        b_off[j] = (uint32_t)((min(n0 + r, p.n - 1) - n0) * p.k) + (uint32_t)(((lane % CPR) ^ swz<BK>(r)) * 16);
+        const int r0 = wave * (BN / NW) + j * RPL;  // multiple of RPL: one 32-row block per instruction
+        const int r = r0 + lane / CPR;
+        const int rl = DUAL ? ((r >> 6) << 5) + (r & 31) : r;  // row of its matrix, from n0
+        b_src[j] = (DUAL && ((r0 >> 5) & 1) ? p.qw2 : p.qw) + n0 * p.k;
+        b_off[j] = (uint32_t)((min(n0 + rl, p.n - 1) - n0) * p.k) + (uint32_t)(((lane % CPR) ^ swz<BK>(r)) * 16);
     }
     const int nk = (int)(p.k / BK);
 
@@ -355,11 +371,10 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
     };
     auto issue_b = [&](int t, int slot) {
         int8_t *lb = ring_b + slot * T::kBBytes;
-        const int8_t *gb = b_base + (int64_t)t * BK;
 #pragma unroll
         for (int j = 0; j < T::kLB; ++j)
-            __builtin_amdgcn_global_load_lds((glb_ptr)(gb + b_off[j]), (lds_ptr)(lb + (wave * (BN / NW) + j * RPL) * BK),
-                                             16, 0, 0);
+            __builtin_amdgcn_global_load_lds((glb_ptr)(b_src[j] + (int64_t)t * BK + b_off[j]),
+                                             (lds_ptr)(lb + (wave * (BN / NW) + j * RPL) * BK), 16, 0, 0);
     };
 
     // Fragment address inside a stage: lane l reads row l%32 of a 32-row
@@ -440,6 +455,51 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
     mfmas((T::kSteps - 1) & 1);
     // No load may still be writing the ring when the workgroup moves on.
     wait_vmcnt<0>();
+
+    if constexpr (DUAL) {
+        // Lane l, register r of block (i, j): row 8*(r/4) + 4*(l/32) + r%4,
+        // column l%32 of the wave's 32-column group; j = 0 gate, j = 1 up.
+        const int64_t col = n0 + wn0 / 2 + (lane & 31);
+        const int64_t cc = min(col, p.n - 1);
+        const int32_t zx0 = p.zx ? (int32_t)p.zx[0] : 0;
+        const float sx0 = p.sx[0];
+        const int32_t rs_g = p.zx ? p.rowsum[cc] : 0, rs_u = p.zx ? p.rowsum2[cc] : 0;
+        const float sc_g = sx0 * p.sw[cc], sc_u = sx0 * p.sw2[cc];
+        const float b_g = p.bias ? p.bias[cc] : 0.f, b_u = p.bias2 ? p.bias2[cc] : 0.f;
+        float mn = INFINITY, mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                const int32_t ag = (int32_t)((uint32_t)acc[i][0][r] - (uint32_t)(zx0 * rs_g));
+                const int32_t au = (int32_t)((uint32_t)acc[i][1][r] - (uint32_t)(zx0 * rs_u));
+                float g = (float)ag * sc_g;
+                float u = (float)au * sc_u;
+                if (p.bias) g = g + b_g;
+                if (p.bias2) u = u + b_u;
+                const float h = silu_mul1(g, u);
+                if (row < p.m && col < p.n) {
+                    p.y[row * p.n + col] = h;
+                    mn = fminf(mn, h);
+                    mx = fmaxf(mx, h);
+                }
+            }
+        wave_minmax(mn, mx);
+        // Cross-wave fold through the (now idle) operand ring.
+        wait_lgkm0();
+        __builtin_amdgcn_s_barrier();
+        float2 *red = reinterpret_cast<float2 *>(lds);
+        if (lane == 0) red[wave] = make_float2(mn, mx);
+        __syncthreads();
+        if (tid == 0) {
+            float2 t = red[0];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) t = make_float2(fminf(t.x, red[w].x), fmaxf(t.y, red[w].y));
+            p.hpart[blockIdx.x] = t;
+        }
+        return;
+    }
 
     // Epilogue: lane l, register r of block (i, j) holds
     // row 8*(r/4) + 4*(l/32) + r%4, column l%32 of that 32 x 32 block.
@@ -557,6 +617,18 @@ int launch_tiles(QParams p, hipStream_t s) {
     return check_launch("qlinear_i8");
 }
 
+// Dual (SwiGLU gate/up) launch: p.n logical columns of each matrix, BN / 2
+// per tile; one hpart entry per workgroup.
+template <int BM, int BN, int BK, int SA, int SB, int NWM, int NWN>
+int launch_tiles_dual(QParams p, hipStream_t s, int *npart) {
+    p.tiles_m = (int)((p.m + BM - 1) / BM);
+    p.tiles_n = (int)((p.n + BN / 2 - 1) / (BN / 2));
+    *npart = p.tiles_m * p.tiles_n;
+    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n)), block(Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT);
+    hipLaunchKernelGGL((qlinear_tile_kernel<BM, BN, BK, SA, SB, NWM, NWN, false, false, true>), grid, block, 0, s, p);
+    return check_launch("qlinear_swiglu_i8");
+}
+
 }  // namespace big
 
 
@@ -581,19 +653,23 @@ namespace skinny {
 
 constexpr int kCols = 16;  // output columns per workgroup
 constexpr int kWaves = kThreads / 64;
-constexpr int kU = 8;
 
 struct SkParams {
     QParams q;
     int64_t kslice, slices, nblk;
-    int32_t *part;  // [slices][m][n] partial accumulators (slices > 1)
+    int32_t *part;  // [slices][D][m][n] partial accumulators (slices > 1)
     int *counters;  // one per column block, zero at rest (slices > 1)
 };
 
-template <int MB>
+// DUAL (SwiGLU gate/up): each wave multiplies the same x fragments with the
+// gate rows and the up rows of its 16 columns (D = 2 accumulator sets), and
+// the epilogue writes silu(gate) * up plus the workgroup's (min, max) of it.
+template <int MB, bool DUAL>
 __global__ __launch_bounds__(kThreads) void qlinear_skinny_kernel(SkParams sp) {
+    constexpr int D = DUAL ? 2 : 1;
+    constexpr int kU = (DUAL && MB > 2) ? 4 : 8;  // k-steps in flight per lane
     const QParams &p = sp.q;
-    __shared__ i32x4 red[kWaves - 1][MB][64];
+    __shared__ i32x4 red[kWaves - 1][D * MB][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t blk = blockIdx.x % sp.nblk, slice = blockIdx.x / sp.nblk;
     const int64_t n0 = blk * kCols;
@@ -608,19 +684,26 @@ __global__ __launch_bounds__(kThreads) void qlinear_skinny_kernel(SkParams sp) {
     // columns are never stored) / x row l % 16 + 16 mb, bytes 16 * (l / 16)
     // of each 64-byte k-step.
     const int kb = 16 * (lane >> 4);
-    const int8_t *wsrc = p.qw + min(n0 + (lane & 15), p.n - 1) * p.k + k_lo + kb;
+    const int64_t wrow = min(n0 + (lane & 15), p.n - 1) * p.k + k_lo + kb;
+    const int8_t *wsrc[D];
+    wsrc[0] = p.qw + wrow;
+    if (DUAL) wsrc[D - 1] = p.qw2 + wrow;
     const int8_t *xsrc = p.qx + k_lo + kb;
 
-    i32x4 acc[MB];
+    i32x4 acc[D][MB];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) acc[mb] = i32x4{0, 0, 0, 0};
+    for (int d = 0; d < D; ++d)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[d][mb] = i32x4{0, 0, 0, 0};
     for (int s0 = st0; s0 < st1; s0 += kU) {
-        i32x4 w[kU], xf[kU][MB];
+        i32x4 w[kU][D], xf[kU][MB];
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
             const int off = (s0 + u) * 64;
             const bool ok = s0 + u < st1 && off + kb < kl;
-            w[u] = ok ? *reinterpret_cast<const i32x4 *>(wsrc + off) : i32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int d = 0; d < D; ++d)
+                w[u][d] = ok ? *reinterpret_cast<const i32x4 *>(wsrc[d] + off) : i32x4{0, 0, 0, 0};
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
                 const int64_t row = mb * 16 + (lane & 15);
@@ -631,49 +714,83 @@ __global__ __launch_bounds__(kThreads) void qlinear_skinny_kernel(SkParams sp) {
 #pragma unroll
         for (int u = 0; u < kU; ++u)
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb)
-                acc[mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xf[u][mb], w[u], acc[mb], 0, 0, 0);
+            for (int d = 0; d < D; ++d)
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb)
+                    acc[d][mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xf[u][mb], w[u][d], acc[d][mb], 0, 0, 0);
     }
 
     // Add the four waves' accumulators (exact int32) in wave 0.
     if (wave > 0) {
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) red[wave - 1][mb][lane] = acc[mb];
+        for (int d = 0; d < D; ++d)
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) red[wave - 1][d * MB + mb][lane] = acc[d][mb];
     }
     __syncthreads();
     if (wave > 0) return;
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+    for (int d = 0; d < D; ++d)
 #pragma unroll
-        for (int w2 = 0; w2 < kWaves - 1; ++w2) acc[mb] += red[w2][mb][lane];
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int w2 = 0; w2 < kWaves - 1; ++w2) acc[d][mb] += red[w2][d * MB + mb][lane];
 
     // 16x16 accumulator layout: lane l, register r -> row 4 * (l / 16) + r,
     // column l % 16 of the block.
     const int64_t col = n0 + (lane & 15);
     const bool col_ok = col < p.n;
     auto row_of = [&](int mb, int r) -> int64_t { return (int64_t)mb * 16 + 4 * (lane >> 4) + r; };
-    auto epilogue = [&](int64_t row, int32_t raw) {
-        const int64_t g = p.x_per_row ? row : 0;
-        int32_t a = raw;
-        if (p.zx) a = (int32_t)((uint32_t)a - (uint32_t)((int32_t)p.zx[g] * p.rowsum[col]));
-        if (p.acc) p.acc[row * p.n + col] = a;
-        if (p.y) {
-            const float sc = p.sx[g] * p.sw[col];
-            float v = (float)a * sc;
-            if (p.bias) v = v + p.bias[col];
-            p.y[row * p.n + col] = v;
+    // Zero-point-corrected accumulator of matrix d (0 = qw, 1 = qw2), and its
+    // dequantized value plus bias.
+    auto corrected = [&](int d, int64_t row, int32_t raw) -> int32_t {
+        if (!p.zx) return raw;
+        const int32_t *rs = d ? p.rowsum2 : p.rowsum;
+        return (int32_t)((uint32_t)raw - (uint32_t)((int32_t)p.zx[p.x_per_row ? row : 0] * rs[col]));
+    };
+    auto dequant = [&](int d, int64_t row, int32_t a) -> float {
+        const float *sw = d ? p.sw2 : p.sw;
+        const float *bias = d ? p.bias2 : p.bias;
+        const float sc = p.sx[p.x_per_row ? row : 0] * sw[col];
+        float v = (float)a * sc;
+        if (bias) v = v + bias[col];
+        return v;
+    };
+    float mn = INFINITY, mx = -INFINITY;
+    auto epilogue = [&](int64_t row, const int32_t *raw) {
+        if (DUAL) {
+            const float g = dequant(0, row, corrected(0, row, raw[0]));
+            const float u = dequant(1, row, corrected(1, row, raw[D - 1]));
+            const float h = silu_mul1(g, u);
+            p.y[row * p.n + col] = h;
+            mn = fminf(mn, h);
+            mx = fmaxf(mx, h);
+            return;
         }
+        const int32_t a = corrected(0, row, raw[0]);
+        if (p.acc) p.acc[row * p.n + col] = a;
+        if (p.y) p.y[row * p.n + col] = dequant(0, row, a);
+    };
+    auto publish_minmax = [&]() {
+        if (!DUAL) return;
+        wave_minmax(mn, mx);
+        if (lane == 0) p.hpart[blk] = make_float2(mn, mx);
     };
 
     if (sp.slices == 1) {
-        if (!col_ok) return;
+        if (col_ok) {
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
+            for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t row = row_of(mb, r);
-                if (row < p.m) epilogue(row, acc[mb][r]);
-            }
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t row = row_of(mb, r);
+                    int32_t raw[D];
+#pragma unroll
+                    for (int d = 0; d < D; ++d) raw[d] = acc[d][mb][r];
+                    if (row < p.m) epilogue(row, raw);
+                }
+        }
+        publish_minmax();
         return;
     }
 
@@ -682,14 +799,16 @@ __global__ __launch_bounds__(kThreads) void qlinear_skinny_kernel(SkParams sp) {
     // them to complete, then count this workgroup's arrival (wave 0 only).
     if (col_ok) {
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
+        for (int d = 0; d < D; ++d)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t row = row_of(mb, r);
-                if (row < p.m)
-                    __hip_atomic_store(sp.part + (slice * p.m + row) * p.n + col, acc[mb][r], __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-            }
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t row = row_of(mb, r);
+                    if (row < p.m)
+                        __hip_atomic_store(sp.part + ((slice * D + d) * p.m + row) * p.n + col, acc[d][mb][r],
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
     }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
@@ -707,14 +826,21 @@ __global__ __launch_bounds__(kThreads) void qlinear_skinny_kernel(SkParams sp) {
             for (int r = 0; r < 4; ++r) {
                 const int64_t row = row_of(mb, r);
                 if (row >= p.m) continue;
-                const int32_t *src = sp.part + row * p.n + col;
-                // integer sum: exact whatever the order; wrapping as int32
-                uint32_t a = 0;
-                for (int64_t j = 0; j < sp.slices; ++j)
-                    a += (uint32_t)__hip_atomic_load(src + j * p.m * p.n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                epilogue(row, (int32_t)a);
+                int32_t raw[D];
+#pragma unroll
+                for (int d = 0; d < D; ++d) {
+                    const int32_t *src = sp.part + (d * p.m + row) * p.n + col;
+                    // integer sum: exact whatever the order; wrapping as int32
+                    uint32_t a = 0;
+                    for (int64_t j = 0; j < sp.slices; ++j)
+                        a += (uint32_t)__hip_atomic_load(src + j * D * p.m * p.n, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+                    raw[d] = (int32_t)a;
+                }
+                epilogue(row, raw);
             }
     }
+    publish_minmax();
     if (lane == 0) __hip_atomic_store(sp.counters + blk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -728,26 +854,29 @@ int64_t choose_kslice(int64_t nblk, int64_t k) {
     return (ks + 63) & ~(int64_t)63;
 }
 
-int launch(const QParams &p, hipStream_t s) {
+template <bool DUAL>
+int launch(const QParams &p, hipStream_t s, int *npart = nullptr) {
+    constexpr int D = DUAL ? 2 : 1;
     SkParams sp{};
     sp.q = p;
     sp.nblk = (p.n + kCols - 1) / kCols;
     sp.kslice = choose_kslice(sp.nblk, p.k);
     sp.slices = (p.k + sp.kslice - 1) / sp.kslice;
+    if (npart) *npart = (int)sp.nblk;
     if (sp.slices > 1) {
         void *ws = nullptr;
-        GFH_TRY(stream_workspace(s, sizeof(int32_t) * (size_t)(sp.slices * p.m * p.n), &ws));
+        GFH_TRY(stream_workspace(s, sizeof(int32_t) * (size_t)(sp.slices * D * p.m * p.n), &ws));
         sp.part = static_cast<int32_t *>(ws);
         GFH_TRY(stream_counters(s, (size_t)sp.nblk, &sp.counters));
     }
     const dim3 grid((unsigned)(sp.nblk * sp.slices)), block(kThreads);
     if (p.m <= 16)
-        hipLaunchKernelGGL(qlinear_skinny_kernel<1>, grid, block, 0, s, sp);
+        hipLaunchKernelGGL((qlinear_skinny_kernel<1, DUAL>), grid, block, 0, s, sp);
     else if (p.m <= 32)
-        hipLaunchKernelGGL(qlinear_skinny_kernel<2>, grid, block, 0, s, sp);
+        hipLaunchKernelGGL((qlinear_skinny_kernel<2, DUAL>), grid, block, 0, s, sp);
     else
-        hipLaunchKernelGGL(qlinear_skinny_kernel<4>, grid, block, 0, s, sp);
-    return check_launch("qlinear_i8 (skinny)");
+        hipLaunchKernelGGL((qlinear_skinny_kernel<4, DUAL>), grid, block, 0, s, sp);
+    return check_launch(DUAL ? "qlinear_swiglu_i8 (skinny)" : "qlinear_i8 (skinny)");
 }
 
 }  // namespace skinny
@@ -769,7 +898,7 @@ int launch_qlinear_i8(const QLinearDesc &d, hipStream_t s) {
     p.n = d.n;
     p.k = d.k;
     p.x_per_row = d.x_per_row ? 1 : 0;
-    if (d.m <= 64 && d.k % 16 == 0 && d.k > 0 && aligned16(d.qx) && aligned16(d.qw)) return skinny::launch(p, s);
+    if (d.m <= 64 && d.k % 16 == 0 && d.k > 0 && aligned16(d.qx) && aligned16(d.qw)) return skinny::launch<false>(p, s);
     // Direct-to-LDS tiles need 16-byte aligned rows (K % 64 == 0) and 32-bit
     // row offsets inside a tile (256 * K < 2^32).
     const bool ring_ok = d.k > 0 && d.k % 64 == 0 && d.k <= (int64_t(1) << 24) && aligned16(d.qx) && aligned16(d.qw);
@@ -798,6 +927,57 @@ int launch_qlinear_i8(const QLinearDesc &d, hipStream_t s) {
     else
         hipLaunchKernelGGL(qlinear_mfma_kernel<false>, grid, dim3(kThreads), 0, s, p);
     return check_launch("qlinear_i8");
+}
+
+// ---- SwiGLU gate/up ------------------------------------------------------------
+//
+// Decode sizes (m <= 64) use the skinny kernel with two weight streams;
+// larger m the direct-to-LDS tiles with gate and up rows interleaved in
+// 32-row blocks (256 x (128 + 128) above m = 512, 128 x (64 + 64) below, the
+// latter as a 4 x 2 wave grid so that every wave holds both halves of its
+// columns).
+
+bool qlinear_swiglu_fits(int64_t m, int64_t n, int64_t k) {
+    if (m <= 0 || n <= 0 || k <= 0 || k % 16 != 0) return false;
+    if (m <= 64) return true;
+    return k % 64 == 0 && k <= (int64_t(1) << 24);
+}
+
+int64_t qlinear_swiglu_partials(int64_t m, int64_t n) {
+    if (m <= 64) return (n + skinny::kCols - 1) / skinny::kCols;
+    if (m > 512) return ((m + 255) / 256) * ((n + 127) / 128);
+    return ((m + 127) / 128) * ((n + 63) / 64);
+}
+
+int launch_qlinear_swiglu_i8(const QSwigluDesc &d, int *npart, hipStream_t s) {
+    const QLinearDesc &g = d.g;
+    if (!qlinear_swiglu_fits(g.m, g.n, g.k) || g.x_per_row || !aligned16(g.qx) || !aligned16(g.qw) ||
+        !aligned16(d.qw_up))
+        return set_error(GFH_INVALID_DATA, "qlinear_swiglu_i8: shape or alignment not served by the fused kernel");
+    QParams p{};
+    p.qx = g.qx;
+    p.sx = g.sx;
+    p.zx = g.zx;
+    p.qw = g.qw;
+    p.sw = g.sw;
+    p.rowsum = g.w_rowsum;
+    p.bias = g.bias;
+    p.y = g.y;
+    p.m = g.m;
+    p.n = g.n;
+    p.k = g.k;
+    p.qw2 = d.qw_up;
+    p.sw2 = d.sw_up;
+    p.rowsum2 = d.rowsum_up;
+    p.bias2 = d.bias_up;
+    p.hpart = d.hpart;
+    if (g.m <= 64) return skinny::launch<true>(p, s, npart);
+    const bool bk128 = g.k % 128 == 0;
+    if (g.m > 512)
+        return bk128 ? big::launch_tiles_dual<256, 256, 128, 3, 2, 2, 4>(p, s, npart)
+                     : big::launch_tiles_dual<256, 256, 64, 4, 4, 2, 4>(p, s, npart);
+    return bk128 ? big::launch_tiles_dual<128, 128, 128, 3, 3, 4, 2>(p, s, npart)
+                 : big::launch_tiles_dual<128, 128, 64, 4, 4, 4, 2>(p, s, npart);
 }
 
 }  // namespace gfh

@@ -285,6 +285,21 @@ int launch_quantize_per_tensor(const float *x, int64_t n, bool symmetric, int8_t
     return check_launch("quantize_per_tensor/quantize");
 }
 
+// The quantize pass alone, on (min, max) partials a producer kernel already
+// wrote (the fused SwiGLU gate/up kernel does, one per workgroup).
+int launch_quantize_per_tensor_partials(const float *x, int64_t n, bool symmetric, const float2 *partials,
+                                       int npartials, int8_t *q, float *scale, int8_t *zp, hipStream_t s) {
+    const int nb = per_tensor_blocks(n);
+    const bool vec = aligned16(x) && ((reinterpret_cast<uintptr_t>(q) & 3u) == 0);
+    if (vec)
+        hipLaunchKernelGGL(quant_per_tensor_kernel<true>, dim3(nb), dim3(kBlock), 0, s, x, n, symmetric, partials,
+                           npartials, q, scale, zp);
+    else
+        hipLaunchKernelGGL(quant_per_tensor_kernel<false>, dim3(nb), dim3(kBlock), 0, s, x, n, symmetric, partials,
+                           npartials, q, scale, zp);
+    return check_launch("quantize_per_tensor/quantize");
+}
+
 int launch_dequantize(const int8_t *q, int64_t rows, int64_t cols, const float *scales, const int8_t *zps,
                       int64_t nscales, float *out, hipStream_t s) {
     const bool per_row = nscales != 1;

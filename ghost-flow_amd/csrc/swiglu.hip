@@ -23,12 +23,6 @@
 namespace gfh {
 namespace {
 
-__device__ __forceinline__ float silu_mul1(float g, float u) {
-    // negate, expf, add, true division (IEEE, correctly rounded), multiply
-    const float s = g / (1.0f + expf(-g));
-    return s * u;
-}
-
 // out[i] = silu(gate[i]) * up[i]; 16-byte vectors when every pointer allows.
 template <bool VEC>
 __global__ __launch_bounds__(256) void silu_mul_kernel(const float *__restrict__ g, const float *__restrict__ u,
@@ -100,16 +94,31 @@ int launch_swiglu_f32(const SwigluDesc &d, void *workspace, hipStream_t s) {
 
 // Workspace of the int8 block, each region 256-byte aligned:
 //   qx [m*hidden] i8 | sx, zx | x min/max partials |
-//   gate [m*inter] f32 | up [m*inter] f32 | qh [m*inter] i8 | sh, zh |
-//   h min/max partials
+//   gate (= h) [m*inter] f32 | up [m*inter] f32, unfused path only |
+//   qh [m*inter] i8 | sh, zh | h min/max partials
+namespace {
+// (min, max) partials of h: the fused launch's or the full quantize pass's.
+size_t h_partials_bytes(int64_t m, int64_t inter) {
+    return std::max(sizeof(float2) * (size_t)qlinear_swiglu_partials(m, inter),
+                    quantize_per_tensor_workspace(m * inter));
+}
+}  // namespace
+
 size_t swiglu_i8_workspace_bytes(int64_t m, int64_t hidden, int64_t inter) {
     const size_t mh = (size_t)m * (size_t)hidden, mi = (size_t)m * (size_t)inter;
-    return round_up(mh) + kAlign + round_up(quantize_per_tensor_workspace((int64_t)mh)) + 2 * round_up(mi * 4) +
-           round_up(mi) + kAlign + round_up(quantize_per_tensor_workspace((int64_t)mi));
+    const bool fused = qlinear_swiglu_fits(m, inter, hidden);
+    return round_up(mh) + kAlign + round_up(quantize_per_tensor_workspace((int64_t)mh)) +
+           (fused ? 1 : 2) * round_up(mi * 4) + round_up(mi) + kAlign + round_up(h_partials_bytes(m, inter));
 }
 
+// x -> quantize (per tensor, asymmetric: quantize_activation,
+// quantization.rs:280-287) -> gate/up with silu * up in one launch, its
+// (min, max) partials feeding the quantize pass of h directly -> down.
+// Shapes the fused launch does not serve run gate and up as two INT8
+// linears, the silu * up kernel and the full per-tensor quantize of h.
 int launch_swiglu_i8(const SwigluDesc &d, void *workspace, hipStream_t s) {
     const size_t mh = (size_t)d.m * (size_t)d.hidden, mi = (size_t)d.m * (size_t)d.inter;
+    const bool fused = qlinear_swiglu_fits(d.m, d.inter, d.hidden);
     char *p = static_cast<char *>(workspace);
     auto take = [&](size_t bytes) {
         char *r = p;
@@ -122,15 +131,14 @@ int launch_swiglu_i8(const SwigluDesc &d, void *workspace, hipStream_t s) {
     int8_t *zx = reinterpret_cast<int8_t *>(xs + 4);
     void *xpart = take(quantize_per_tensor_workspace((int64_t)mh));
     float *gate = reinterpret_cast<float *>(take(mi * 4));
-    float *up = reinterpret_cast<float *>(take(mi * 4));
+    float *up = fused ? nullptr : reinterpret_cast<float *>(take(mi * 4));
     int8_t *qh = reinterpret_cast<int8_t *>(take(mi));
     char *hs = take(kAlign);
     float *sh = reinterpret_cast<float *>(hs);
     int8_t *zh = reinterpret_cast<int8_t *>(hs + 4);
-    void *hpart = take(quantize_per_tensor_workspace((int64_t)mi));
+    void *hpart = take(h_partials_bytes(d.m, d.inter));
     float *h = d.h ? d.h : gate;
 
-    // quantize_activation (quantization.rs:280-287): per tensor, asymmetric
     GFH_TRY(launch_quantize_per_tensor(d.x, (int64_t)mh, false, qx, sx, zx, xpart, s));
     QLinearDesc q;
     q.qx = qx;
@@ -143,16 +151,30 @@ int launch_swiglu_i8(const SwigluDesc &d, void *workspace, hipStream_t s) {
     q.sw = d.swg;
     q.w_rowsum = d.rsg;
     q.bias = d.bg;
-    q.y = gate;
-    GFH_TRY(launch_qlinear_i8(q, s));
-    q.qw = d.qwu;
-    q.sw = d.swu;
-    q.w_rowsum = d.rsu;
-    q.bias = d.bu;
-    q.y = up;
-    GFH_TRY(launch_qlinear_i8(q, s));
-    GFH_TRY(launch_silu_mul(gate, up, h, (int64_t)mi, s));
-    GFH_TRY(launch_quantize_per_tensor(h, (int64_t)mi, false, qh, sh, zh, hpart, s));
+    if (fused) {
+        QSwigluDesc f;
+        f.g = q;
+        f.g.y = h;
+        f.qw_up = d.qwu;
+        f.sw_up = d.swu;
+        f.rowsum_up = d.rsu;
+        f.bias_up = d.bu;
+        f.hpart = static_cast<float2 *>(hpart);
+        int npart = 0;
+        GFH_TRY(launch_qlinear_swiglu_i8(f, &npart, s));
+        GFH_TRY(launch_quantize_per_tensor_partials(h, (int64_t)mi, false, f.hpart, npart, qh, sh, zh, s));
+    } else {
+        q.y = gate;
+        GFH_TRY(launch_qlinear_i8(q, s));
+        q.qw = d.qwu;
+        q.sw = d.swu;
+        q.w_rowsum = d.rsu;
+        q.bias = d.bu;
+        q.y = up;
+        GFH_TRY(launch_qlinear_i8(q, s));
+        GFH_TRY(launch_silu_mul(gate, up, h, (int64_t)mi, s));
+        GFH_TRY(launch_quantize_per_tensor(h, (int64_t)mi, false, qh, sh, zh, hpart, s));
+    }
     q.qx = qh;
     q.sx = sh;
     q.zx = zh;

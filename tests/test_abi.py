@@ -162,6 +162,8 @@ def test_swiglu_rejects_bad_shapes():
 def test_swiglu_workspace_sizes():
     lib = _lib()
     assert lib.gfh_swiglu_f32_workspace_size(4, 100) >= 2 * 4 * 100 * 4
-    n = lib.gfh_swiglu_i8_workspace_size(4, 64, 96)
-    assert n >= 4 * 64 + 2 * 4 * 96 * 4 + 4 * 96
+    # fused gate/up (hidden % 64 == 0): x codes, h, h codes
+    assert lib.gfh_swiglu_i8_workspace_size(4, 64, 96) >= 4 * 64 + 4 * 96 * 4 + 4 * 96
+    # unfused (hidden = 80): gate and up in fp32 as well
+    assert lib.gfh_swiglu_i8_workspace_size(70, 80, 96) >= 70 * 80 + 2 * 70 * 96 * 4 + 70 * 96
     assert lib.gfh_swiglu_i8_workspace_size(-1, -1, -1) >= 0

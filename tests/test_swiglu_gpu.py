@@ -117,8 +117,13 @@ def _int8_layer(rng, hidden, inter, bias):
     return q
 
 
-@pytest.mark.parametrize("m,hidden,inter", [(1, 64, 96), (7, 128, 352), (16, 4096, 11008), (64, 256, 512),
-                                            (70, 80, 208), (300, 256, 512), (1024, 512, 768)])
+# m <= 64: the skinny gate/up kernel (5 x 4096 x 256 splits K over workgroups);
+# 100..512: 128 x (64 + 64) tiles (hidden % 128 == 64 -> 64-byte stages);
+# above 512: 256 x (128 + 128) tiles; hidden = 80 (not a multiple of 64)
+# takes the unfused path.
+@pytest.mark.parametrize("m,hidden,inter", [(1, 64, 96), (7, 128, 352), (5, 4096, 256), (16, 4096, 11008),
+                                            (64, 256, 512), (70, 80, 208), (100, 256, 208), (200, 192, 320),
+                                            (300, 256, 512), (600, 320, 256), (1024, 512, 768)])
 @pytest.mark.parametrize("bias", [True, False])
 def test_swiglu_i8_stages(torch_dev, m, hidden, inter, bias):
     if not bias and hidden > 512:
