@@ -307,8 +307,9 @@ def comp_sdpa(lib, torch, S):
 
 def comp_linear_decode(lib, torch, m):
     """Linear::forward at decode batch sizes: x [m, 4096] . W^T + b with W
-    [4096, 4096] (gfh_sgemm NT -> the row-dot GEMV).  HBM-bound: bytes =
-    4*N*K + 4*m*K + 4*N (bias) + 4*m*N."""
+    [4096, 4096] (gfh_sgemm NT -> the row-dot GEMV up to 4 rows, the skinny
+    f32-MFMA kernel up to 64).  HBM-bound below m ~ 40: bytes = 4*N*K +
+    4*m*K + 4*N (bias) + 4*m*N; the roofline is min(f32 MFMA, AI * HBM)."""
     dev = torch.device("cuda:0")
     N = K = 4096
     wbytes = 4 * N * K
@@ -327,9 +328,12 @@ def comp_linear_decode(lib, torch, m):
     ms = event_time_ms(torch, f, 300)
     byts = wbytes + 4 * m * K + 4 * N + 4 * m * N
     gbs = byts / ms / 1e6
+    fl = 2.0 * m * N * K
+    attain = min(PEAK_F32, fl / byts * PEAK_HBM)
     del ws
     return {"name": f"linear_decode_m{m}_4096", "ms": ms, "value": gbs, "unit": "GB/s",
-            "frac": gbs * 1e9 / PEAK_HBM, "bound": "hbm", "weight_copies": ncopy}
+            "tflops": fl / ms / 1e9, "frac": fl / (ms * 1e-3) / attain,
+            "bound": "mfma_f32" if attain == PEAK_F32 else "hbm", "weight_copies": ncopy}
 
 
 def _kv_sets(torch, dev, B, C, E, n):
@@ -488,7 +492,7 @@ def run_components(lib, torch, only):
         for S in (512, 2048):
             add(comp_sdpa, S)
     if "decode" in want:
-        for m in (1, 4, 8):
+        for m in (1, 4, 8, 16, 64):
             add(comp_linear_decode, m)
         add(comp_kv_attention)
         add(comp_mha_decode)

@@ -305,7 +305,7 @@ int launch_mb(const NtParams &p, int64_t batch, hipStream_t s) {
 }  // namespace
 
 bool gemv_nt_fits(const SgemmDesc &d) {
-    return !d.trans_a && d.trans_b && d.m >= 1 && d.m <= 8 && d.k > 0 && d.n > 0 && d.k % 4 == 0 &&
+    return !d.trans_a && d.trans_b && d.m >= 1 && d.m <= kNtSkinnyMinM && d.k > 0 && d.n > 0 && d.k % 4 == 0 &&
            d.lda % 4 == 0 && d.ldb % 4 == 0 && aligned16(d.a) && aligned16(d.b) &&
            (d.batch_a <= 1 || d.stride_a % 4 == 0) && (d.batch_b <= 1 || d.stride_b % 4 == 0) && d.batch <= 65535;
 }

@@ -26,6 +26,12 @@ int launch_sgemm(const SgemmDesc &d, hipStream_t s);
 // uses it when gemv_nt_fits.
 bool gemv_nt_fits(const SgemmDesc &d);
 int launch_gemv_nt(const SgemmDesc &d, hipStream_t s);
+// gemm_nt_skinny.hip: the NT form at kNtSkinnyMinM < m <= 64 on f32 MFMA
+// with the weight streamed into registers; launch_sgemm uses it when
+// gemm_nt_skinny_fits.
+constexpr int64_t kNtSkinnyMinM = 4;
+bool gemm_nt_skinny_fits(const SgemmDesc &d);
+int launch_gemm_nt_skinny(const SgemmDesc &d, hipStream_t s);
 
 // quant.hip
 int launch_quantize_per_channel(const float *x, int64_t rows, int64_t cols, bool symmetric, int8_t *q,

@@ -277,6 +277,8 @@ int launch_sgemm(const SgemmDesc &d, hipStream_t s) {
     // x . W^T with at most 8 rows of x: a tile of this kernel would leave
     // most of its MFMA rows empty and its grid far too small to stream W.
     if (gemv_nt_fits(d)) return launch_gemv_nt(d, s);
+    // up to 64 rows: the weight streamed straight into f32 MFMA operands
+    if (gemm_nt_skinny_fits(d)) return launch_gemm_nt_skinny(d, s);
     SgemmParams p{};
     p.a = d.a;
     p.b = d.b;

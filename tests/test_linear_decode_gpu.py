@@ -1,5 +1,6 @@
-"""Linear::forward at decode sizes (x [m <= 8, k] . W^T, W [out, in]) on the
-GPU: gfh_sgemm sends these NT calls to the row-dot GEMV kernel.  Against
+"""Linear::forward at decode sizes (x [m <= 64, k] . W^T, W [out, in]) on the
+GPU: gfh_sgemm sends these NT calls to the row-dot GEMV kernel (m <= 4) or
+to the skinny f32-MFMA kernel (4 < m <= 64).  Against
 the oracle's Linear::forward / matmul (ghostflow-nn/src/linear.rs:56-69,
 ghostflow-core/src/ops/matmul.rs:91-170).  Bars: bit-exact on
 integer-valued inputs (every partial sum exact in any order), otherwise the
@@ -22,11 +23,16 @@ def _O():
     return oracle
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 5, 8])
-@pytest.mark.parametrize("k,n", [(4, 1), (256, 17), (260, 300), (1000, 4100), (4096, 16385)])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 9, 16, 17, 33, 48, 64])
+@pytest.mark.parametrize("k,n", [(4, 1), (256, 17), (260, 300), (1000, 4100), (4100, 300), (4096, 16385)])
 def test_nt_gemv_integer_exact(torch_dev, m, k, n):
-    """k = 260 / 1000: a partial last 256-element step; n = 4100 / 16385:
-    the 2- and 4-row-per-wave tilings with a ragged last wave."""
+    """GEMV (m <= 4): k = 260 / 1000 end in a partial 256-element step; n =
+    4100 / 16385 give the 2- and 4-row tilings a ragged last wave.  Skinny
+    MFMA (m > 4): ragged m inside a 16-row block, ragged n inside a 16-column
+    block, k % 16 != 0, and 4100 x 300 splits K over 4 workgroups (the last
+    slice shorter)."""
+    if m > 8 and n * k > 4096 * 4100:
+        pytest.skip("oracle time; the large n is covered at m <= 8 and by test_decode_linear_4096")
     gh, O = _gh(), _O()
     rng = np.random.default_rng(m * 7919 + k * 31 + n)
     x = rng.integers(-8, 9, size=(m, k)).astype(np.float32)
@@ -36,10 +42,10 @@ def test_nt_gemv_integer_exact(torch_dev, m, k, n):
     np.testing.assert_array_equal(got, O.linear_forward(x, w, bias))
 
 
-def test_nt_gemv_alpha_beta(torch_dev):
+@pytest.mark.parametrize("m,k,n", [(3, 520, 777), (6, 520, 777), (20, 4100, 100)])
+def test_nt_gemv_alpha_beta(torch_dev, m, k, n):
     gh, O = _gh(), _O()
     rng = np.random.default_rng(21)
-    m, k, n = 6, 520, 777
     x = rng.integers(-4, 5, size=(m, k)).astype(np.float32)
     w = rng.integers(-4, 5, size=(n, k)).astype(np.float32)
     c0 = rng.integers(-4, 5, size=(m, n)).astype(np.float32)
@@ -51,13 +57,14 @@ def test_nt_gemv_alpha_beta(torch_dev):
     np.testing.assert_array_equal(to_np(dc), ref.astype(np.float32))
 
 
-def test_nt_gemv_strided_rows(torch_dev):
+@pytest.mark.parametrize("m", [4, 24])
+def test_nt_gemv_strided_rows(torch_dev, m):
     """lda > k and ldc > n (rows of a larger buffer, as when a projection
     writes into a KV cache); the bytes between rows stay untouched."""
     import torch
     gh, O = _gh(), _O()
     rng = np.random.default_rng(22)
-    m, k, n, lda, ldc = 4, 512, 300, 520, 1000
+    k, n, lda, ldc = 512, 300, 520, 1000
     xa = rng.integers(-8, 9, size=(m, lda)).astype(np.float32)
     w = rng.integers(-8, 9, size=(n, k)).astype(np.float32)
     dx, dw = to_dev(xa, torch_dev), to_dev(w, torch_dev)
@@ -70,13 +77,14 @@ def test_nt_gemv_strided_rows(torch_dev):
     assert (got[:, n:] == 7.0).all()
 
 
-def test_nt_gemv_batched_modulo(torch_dev):
+@pytest.mark.parametrize("m", [2, 12])
+def test_nt_gemv_batched_modulo(torch_dev, m):
     """Batched NT with one shared weight (batch_b = 1): every batch slice
     uses W, as the reference's modulo indexing gives (matmul.rs:148-149)."""
     import torch
     gh, O = _gh(), _O()
     rng = np.random.default_rng(23)
-    batch, m, k, n = 3, 2, 256, 129
+    batch, k, n = 3, 256, 129
     x = rng.integers(-8, 9, size=(batch, m, k)).astype(np.float32)
     w = rng.integers(-8, 9, size=(n, k)).astype(np.float32)
     dx, dw = to_dev(x, torch_dev), to_dev(w, torch_dev)
@@ -89,7 +97,7 @@ def test_nt_gemv_batched_modulo(torch_dev):
     np.testing.assert_array_equal(to_np(out), ref)
 
 
-@pytest.mark.parametrize("m", [1, 4, 8])
+@pytest.mark.parametrize("m", [1, 4, 8, 16, 64])
 
 def test_decode_linear_4096(torch_dev, m):
     """x [m, 4096] ~ N(0,1), W [4096, 4096] and b ~ U(-1/64, 1/64) (the
