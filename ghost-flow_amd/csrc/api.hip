@@ -6,6 +6,7 @@
 // the access), then lazy device init, then the launch on the caller's
 // stream.  No C++ exception crosses the boundary.  Status codes follow
 // GhostFlowError (ghostflow-ffi/src/lib.rs:27-35).
+#include <algorithm>
 #include <climits>
 #include <cmath>
 #include <new>
@@ -153,6 +154,26 @@ GFH_API int gfh_sgemm_strided_batched(int trans_a, int trans_b, int64_t m, int64
     return guarded([&]() -> int {
         return sgemm_common(trans_a, trans_b, m, n, k, alpha, a, lda, stride_a, batch_a, b, ldb, stride_b, batch_b,
                             beta, c, ldc, stride_c, batch, bias, stream);
+    });
+}
+
+// grad_a = grad . b^T (NT, K = n) and grad_b = a^T . grad (TN, K = m): the
+// two products of matmul_backward (ghostflow-autograd/src/backward.rs:131-160)
+// as two validated sgemm launches.
+GFH_API int gfh_matmul_backward_f32(const float *grad, const float *a, const float *b, int64_t m, int64_t k,
+                                    int64_t n, float *grad_a, float *grad_b, gfh_stream_t stream) {
+    return guarded([&]() -> int {
+        if (m < 0 || k < 0 || n < 0)
+            return set_error(GFH_INVALID_SHAPE, "matmul_backward: dims m=%lld k=%lld n=%lld must be >= 0",
+                             (long long)m, (long long)k, (long long)n);
+        const int64_t ln = std::max<int64_t>(n, 1), lk = std::max<int64_t>(k, 1);
+        if (grad_a)
+            GFH_TRY(sgemm_common(0, 1, m, k, n, 1.f, grad, ln, 0, 1, b, ln, 0, 1, 0.f, grad_a, lk, 0, 1, nullptr,
+                                 stream));
+        if (grad_b)
+            GFH_TRY(sgemm_common(1, 0, k, n, m, 1.f, a, lk, 0, 1, grad, ln, 0, 1, 0.f, grad_b, ln, 0, 1, nullptr,
+                                 stream));
+        return GFH_SUCCESS;
     });
 }
 

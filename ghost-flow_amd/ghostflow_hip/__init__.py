@@ -17,6 +17,7 @@ from .ops import (  # noqa: F401
     lib,
     linear,
     matmul,
+    matmul_backward,
     mha_forward_cached,
     mha_forward_with_cache,
     mha_workspace_size,

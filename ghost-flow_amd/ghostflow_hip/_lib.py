@@ -46,6 +46,7 @@ SIGNATURES = {
     "gfh_sgemm": (_i, [_i, _i, _i64, _i64, _i64, _f, _p, _i64, _p, _i64, _f, _p, _i64, _p, _p]),
     "gfh_sgemm_strided_batched": (_i, [_i, _i, _i64, _i64, _i64, _f, _p, _i64, _i64, _i64, _p, _i64,
                                        _i64, _i64, _f, _p, _i64, _i64, _i64, _p, _p]),
+    "gfh_matmul_backward_f32": (_i, [_p, _p, _p, _i64, _i64, _i64, _p, _p, _p]),
     "gfh_quantize_i8_per_channel": (_i, [_p, _i64, _i64, _i, _p, _p, _p, _p]),
     "gfh_quantize_i8_per_tensor": (_i, [_p, _i64, _i, _p, _p, _p, _p, _sz, _p]),
     "gfh_quantize_i8_per_tensor_workspace_size": (_sz, [_i64]),

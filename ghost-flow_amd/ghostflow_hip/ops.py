@@ -115,6 +115,23 @@ def linear(x, weight, bias=None):
 
 # ---- int8 quantization ---------------------------------------------------------
 
+def matmul_backward(grad, a, b, *, need_a=True, need_b=True):
+    """matmul_backward (ghostflow-autograd/src/backward.rs:131-160) for
+    C = a @ b: returns (grad @ b^T, a^T @ grad); a part not needed is None."""
+    for t, n in ((grad, "grad"), (a, "a"), (b, "b")):
+        _need(t, torch.float32, n)
+    m, k = a.shape
+    n = b.shape[1]
+    if b.shape[0] != k or tuple(grad.shape) != (m, n):
+        raise GhostFlowError(_lib.INVALID_SHAPE, f"ShapeMismatch a {list(a.shape)} b {list(b.shape)} "
+                             f"grad {list(grad.shape)}")
+    ga = torch.empty((m, k), dtype=torch.float32, device=a.device) if need_a else None
+    gb = torch.empty((k, n), dtype=torch.float32, device=a.device) if need_b else None
+    _check(lib().gfh_matmul_backward_f32(grad.data_ptr(), a.data_ptr(), b.data_ptr(), m, k, n, _ptr(ga), _ptr(gb),
+                                         _stream(a.device)))
+    return ga, gb
+
+
 def quantize_per_channel(x, symmetric=True):
     _need(x, torch.float32, "x")
     rows = x.shape[0]

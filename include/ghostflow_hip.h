@@ -102,6 +102,17 @@ GFH_API int gfh_sgemm_strided_batched(int trans_a, int trans_b, int64_t m,
                                       int64_t batch, const float *bias,
                                       gfh_stream_t stream);
 
+/* ---- matmul gradient ----------------------------------------------------- */
+
+/* matmul_backward (ghostflow-autograd/src/backward.rs:131-160) for
+ * C = A . B with grad = dL/dC [m, n], a [m, k], b [k, n], all row-major:
+ *   grad_a [m, k] = grad . b^T      grad_b [k, n] = a^T . grad
+ * Either output may be NULL (not computed).  Two gfh_sgemm launches (NT and
+ * TN) on the stream. */
+GFH_API int gfh_matmul_backward_f32(const float *grad, const float *a, const float *b,
+                                    int64_t m, int64_t k, int64_t n, float *grad_a,
+                                    float *grad_b, gfh_stream_t stream);
+
 /* ---- int8 quantization (ghostflow-nn/src/quantization.rs) ---------------- */
 
 /* quantize_per_channel_int8 (quantization.rs:110-153): channel = dim 0, one

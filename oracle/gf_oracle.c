@@ -24,6 +24,10 @@
  *       (exact in any order) against an int64 brute force; fp64 brute force
  *       error bound on random inputs; identity / permutation matrices.
  *   gfo_transpose_last2 : explicit index check against numpy transpose.
+ *   gfo_matmul_backward : integer-valued inputs against int64 brute force
+ *       (grad . b^T and a^T . grad); the sequential-order tie 2^24 + 1 + 1;
+ *       fp64 brute force bound; finite-difference-free identity
+ *       <grad, A.B> consistency with the forward.
  *   gfo_linear_forward  : integer-valued inputs against int64 brute force
  *       with bias; equals matmul(x, W^T) + b computed by the pinned parts.
  *   gfo_softmax_lastdim : rows sum to 1 (activation.rs:266-272,
@@ -169,6 +173,34 @@ GFO_API void gfo_add_row_bias(float *y, const float *bias, size_t rows,
 /* arithmetic.rs:69-72 `mul_scalar`: x * s. */
 GFO_API void gfo_mul_scalar(float *x, size_t n, float s) {
     for (size_t i = 0; i < n; ++i) x[i] = x[i] * s;
+}
+
+/* ------------------------------------------------------------------------ */
+/* ghostflow-autograd/src/backward.rs                                        */
+/* ------------------------------------------------------------------------ */
+
+/* backward.rs:131-160 `matmul_backward`: grad [m,n], a [m,k], b [k,n];
+ * grad_a[i,j] = sum_l grad[i,l] * b[j,l]  (grad . b^T, l ascending),
+ * grad_b[i,j] = sum_l a[l,i] * grad[l,j]  (a^T . grad, l ascending);
+ * each sum starts from 0.0f and adds separately rounded products.  Either
+ * output may be NULL. */
+GFO_API void gfo_matmul_backward(const float *grad, const float *a, const float *b,
+                                 size_t m, size_t k, size_t n, float *grad_a,
+                                 float *grad_b) {
+    if (grad_a)
+        for (size_t i = 0; i < m; ++i)
+            for (size_t j = 0; j < k; ++j) {
+                float sum = 0.0f;
+                for (size_t l = 0; l < n; ++l) sum = sum + grad[i * n + l] * b[j * n + l];
+                grad_a[i * k + j] = sum;
+            }
+    if (grad_b)
+        for (size_t i = 0; i < k; ++i)
+            for (size_t j = 0; j < n; ++j) {
+                float sum = 0.0f;
+                for (size_t l = 0; l < m; ++l) sum = sum + a[l * k + i] * grad[l * n + j];
+                grad_b[i * n + j] = sum;
+            }
 }
 
 /* ------------------------------------------------------------------------ */

@@ -37,6 +37,7 @@ def lib():
         L.gfo_matmul_blocked.argtypes = [_f32p, _f32p, _f32p, _sz, _sz, _sz]
         L.gfo_batched_matmul.argtypes = [_f32p, _sz, _f32p, _sz, _f32p, _sz, _sz, _sz, _sz]
         L.gfo_transpose_last2.argtypes = [_f32p, _f32p, _sz, _sz, _sz]
+        L.gfo_matmul_backward.argtypes = [_f32p, _f32p, _f32p, _sz, _sz, _sz, C.c_void_p, C.c_void_p]
         L.gfo_add_row_bias.argtypes = [_f32p, _f32p, _sz, _sz]
         L.gfo_mul_scalar.argtypes = [_f32p, _sz, C.c_float]
         L.gfo_linear_forward.argtypes = [_f32p, _f32p, C.c_void_p, _f32p, _sz, _sz, _sz]
@@ -107,6 +108,20 @@ def transpose_last2(x):
     out = np.empty(x.shape[:-2] + (c, r), np.float32)
     lib().gfo_transpose_last2(x, out, batch, r, c)
     return out
+
+
+def matmul_backward(grad, a, b):
+    """matmul_backward (ghostflow-autograd/src/backward.rs:131-160):
+    (grad . b^T, a^T . grad) for grad [m,n], a [m,k], b [k,n]."""
+    grad, a, b = _f32(grad), _f32(a), _f32(b)
+    m, k = a.shape
+    n = b.shape[1]
+    if b.shape[0] != k or grad.shape != (m, n):
+        raise ValueError("matmul_backward: shape mismatch")
+    ga = np.empty((m, k), np.float32)
+    gb = np.empty((k, n), np.float32)
+    lib().gfo_matmul_backward(grad, a, b, m, k, n, _ptr(ga), _ptr(gb))
+    return ga, gb
 
 
 def linear_forward(x, w, bias=None):

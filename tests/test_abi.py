@@ -167,3 +167,11 @@ def test_swiglu_workspace_sizes():
     # unfused (hidden = 80): gate and up in fp32 as well
     assert lib.gfh_swiglu_i8_workspace_size(70, 80, 96) >= 70 * 80 + 2 * 70 * 96 * 4 + 70 * 96
     assert lib.gfh_swiglu_i8_workspace_size(-1, -1, -1) >= 0
+
+
+def test_matmul_backward_rejects_bad_dims():
+    lib = _lib()
+    assert lib.gfh_matmul_backward_f32(None, None, None, -1, 2, 2, None, None, None) == 1
+    assert b"matmul_backward" in lib.gfh_last_error()
+    # nothing requested: no work, no pointer needed
+    assert lib.gfh_matmul_backward_f32(None, None, None, 2, 2, 2, None, None, None) == 0

@@ -418,3 +418,60 @@ def test_qlinear_matches_reference_composite():
     comp = O.matmul(O.dequantize(qx, np.array([sx]), np.array([zx])), O.dequantize(qw, sw, zw).T.copy())
     bound = 1e-4 * np.sqrt(k) * np.abs(x).max() * np.abs(w).max() * 4
     assert np.abs(y - comp).max() <= bound
+
+
+# ---------------------------------------------------------------------------
+# matmul_backward (ghostflow-autograd/src/backward.rs:131-160)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (3, 5, 7), (33, 17, 29), (64, 48, 80)])
+def test_matmul_backward_integer_exact(m, k, n):
+    rng = np.random.default_rng(m * 101 + k * 7 + n)
+    g = rng.integers(-8, 9, size=(m, n))
+    a = rng.integers(-8, 9, size=(m, k))
+    b = rng.integers(-8, 9, size=(k, n))
+    ga, gb = O.matmul_backward(g.astype(np.float32), a.astype(np.float32), b.astype(np.float32))
+    np.testing.assert_array_equal(ga, (g @ b.T).astype(np.float32))
+    np.testing.assert_array_equal(gb, (a.T @ g).astype(np.float32))
+
+
+def test_matmul_backward_sums_sequentially():
+    """grad_a sums over l = 0..n-1 and grad_b over l = 0..m-1, ascending,
+    each add rounded: 2^24 + 1 + 1 -> 2^24, while 1 + 1 + 2^24 -> 2^24 + 2.
+    A transposed operand or a swapped loop order changes the result."""
+    g = np.array([[2.0 ** 24, 1.0, 1.0]], np.float32)        # [1, 3]
+    b = np.ones((1, 3), np.float32)                            # [k=1, n=3]
+    a = np.ones((1, 1), np.float32)
+    ga, _ = O.matmul_backward(g, a, b)
+    assert ga.item() == 2.0 ** 24
+    g2 = np.array([[1.0, 1.0, 2.0 ** 24]], np.float32)
+    assert O.matmul_backward(g2, a, b)[0].item() == 2.0 ** 24 + 2
+    # grad_b: the sum runs over the rows of a and grad
+    a = np.array([[2.0 ** 24], [1.0], [1.0]], np.float32)     # [m=3, k=1]
+    g = np.ones((3, 1), np.float32)
+    b = np.ones((1, 1), np.float32)
+    assert O.matmul_backward(g, a, b)[1].item() == 2.0 ** 24
+    a = np.array([[1.0], [1.0], [2.0 ** 24]], np.float32)
+    assert O.matmul_backward(g, a, b)[1].item() == 2.0 ** 24 + 2
+
+
+def test_matmul_backward_fp64_and_adjoint():
+    """fp64 brute force within the fp32 GEMM rounding bound, and the adjoint
+    identity <grad, A.dB + dA.B> = <grad_a, dA> + <grad_b, dB> that defines
+    the gradient of C = A.B."""
+    rng = np.random.default_rng(5)
+    m, k, n = 40, 30, 50
+    g, a, b = (rng.standard_normal(s).astype(np.float32) for s in ((m, n), (m, k), (k, n)))
+    ga, gb = O.matmul_backward(g, a, b)
+    g64, a64, b64 = g.astype(np.float64), a.astype(np.float64), b.astype(np.float64)
+    assert np.abs(ga - g64 @ b64.T).max() <= n * EPS * (np.abs(g64) @ np.abs(b64).T).max()
+    assert np.abs(gb - a64.T @ g64).max() <= m * EPS * (np.abs(a64).T @ np.abs(g64)).max()
+    da, db = rng.standard_normal((m, k)), rng.standard_normal((k, n))
+    lhs = np.sum(g64 * (a64 @ db + da @ b64))
+    rhs = np.sum(ga * da) + np.sum(gb * db)
+    assert abs(lhs - rhs) <= 1e-4 * (abs(lhs) + 1)
+
+
+def test_matmul_backward_shape_check():
+    with pytest.raises(ValueError):
+        O.matmul_backward(np.zeros((2, 3), np.float32), np.zeros((2, 4), np.float32), np.zeros((5, 3), np.float32))
