@@ -61,7 +61,7 @@ def parse_args():
     ap.add_argument("--cpu-rows", type=int, default=768,
                     help="rows of x in the CPU-baseline sample (of 4096)")
     ap.add_argument("--only", default="",
-                    help="comma list of components to run (sgemm,qlinear,gemv,sdpa,decode,swiglu); "
+                    help="comma list of components to run (sgemm,qlinear,gemv,sdpa,decode,swiglu,io); "
                          "used for focused profiling")
     ap.add_argument("--detail", default="", help="also write the full result JSON to this file")
     ap.add_argument("--calib-copy", action="store_true",
@@ -464,8 +464,63 @@ def comp_swiglu(lib, torch, m, int8, H=4096, I=11008):
             "bound": ("mfma_i8" if int8 else "mfma_f32") if attain == peak else "hbm", "weight_sets": ncopy}
 
 
+def comp_state_dict_load(lib, torch, int8):
+    """Weight load, file -> HBM: the three LLaMA-7B MLP weights (4096 x 11008
+    each) as a GHOSTFLW state dict (fp32, 541 MB) or a GHOSTFLQ file of their
+    int8 codes + scales (135 MB), read from the page cache through
+    gfh_state_dict_read_* (mapped file, pinned double-buffered H2D copies).
+    Bound: the host link (PCIe 5 x16, ~64 GB/s per direction)."""
+    import tempfile
+    dev = torch.device("cuda:0")
+    gh = lib.gh
+    H, I = 4096, 11008
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    state = {}
+    for name, shape in (("mlp.gate_proj.weight", (I, H)), ("mlp.up_proj.weight", (I, H)),
+                        ("mlp.down_proj.weight", (H, I))):
+        w = torch.randn(shape, device=dev, generator=g) * 0.02
+        state[name] = gh.quantize_per_channel(w, symmetric=True) if int8 else w
+    fd, path = tempfile.mkstemp(suffix=".gfq" if int8 else ".gf", dir=os.environ.get("TMPDIR", "/tmp"))
+    os.close(fd)
+    try:
+        gh.save_state_dict(path, state, quantized_format=int8)
+        nbytes = os.path.getsize(path)
+        with gh.StateDict(path) as sd:
+            keys = sd.keys()
+            outs = {k: (tuple(torch.empty_like(t) for t in state[k]) if int8 else torch.empty_like(state[k]))
+                    for k in keys}
+
+            def load_all():
+                for k in keys:
+                    i = sd._info[k][0]
+                    o = outs[k]
+                    if int8:
+                        lib.check(lib.L.gfh_state_dict_read_q8(sd._h, i, o[0].data_ptr(), o[1].data_ptr(),
+                                                               o[2].data_ptr(), None), "read_q8")
+                    else:
+                        lib.check(lib.L.gfh_state_dict_read_f32(sd._h, i, o.data_ptr(), None), "read_f32")
+            load_all()  # warm the page cache and the staging buffers
+            torch.cuda.synchronize()
+            reps = 5
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                load_all()
+            torch.cuda.synchronize()
+            sec = (time.perf_counter() - t0) / reps
+        for k in keys:
+            a, b = (state[k], outs[k]) if not int8 else (state[k][0], outs[k][0])
+            if not torch.equal(a, b):
+                raise RuntimeError(f"state dict reload mismatch in {k}")
+    finally:
+        os.unlink(path)
+    gbs = nbytes / sec / 1e9
+    return {"name": f"state_dict_load_{'ghostflq_i8' if int8 else 'ghostflw_f32'}_llama7b_mlp", "ms": sec * 1e3,
+            "value": gbs, "unit": "GB/s", "bytes": nbytes, "frac": gbs / 64.0, "bound": "pcie5_x16"}
+
+
 def run_components(lib, torch, only):
-    want = set(filter(None, only.split(","))) or {"sgemm", "qlinear", "gemv", "sdpa", "decode", "swiglu"}
+    want = set(filter(None, only.split(","))) or {"sgemm", "qlinear", "gemv", "sdpa", "decode", "swiglu", "io"}
     out = []
 
     def add(fn, *a, **kw):
@@ -501,6 +556,9 @@ def run_components(lib, torch, only):
             add(comp_swiglu, m, True)
         for m in (1, 16, 4096):
             add(comp_swiglu, m, False)
+    if "io" in want:
+        for int8 in (False, True):
+            add(comp_state_dict_load, int8)
     return out
 
 

@@ -9,6 +9,7 @@ All compute goes through the C ABI of libghostflow_hip.so
 from . import _lib  # noqa: F401
 from .ops import (  # noqa: F401
     GhostFlowError,
+    StateDict,
     dequantize,
     gemv_f32,
     gemv_w8,
@@ -16,6 +17,7 @@ from .ops import (  # noqa: F401
     kv_attention,
     lib,
     linear,
+    load_state_dict,
     matmul,
     matmul_backward,
     mha_forward_cached,
@@ -27,6 +29,7 @@ from .ops import (  # noqa: F401
     quantize_per_tensor,
     quantize_per_tensor_workspace_size,
     qweight_rowsum,
+    save_state_dict,
     sdpa,
     set_pointer_checks,
     silu_mul,

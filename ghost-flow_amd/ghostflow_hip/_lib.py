@@ -63,6 +63,15 @@ SIGNATURES = {
     "gfh_mha_forward_with_cache_f32": (_i, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _p,
                                             _i64, _i, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _sz, _p]),
     "gfh_silu_mul_f32": (_i, [_p, _p, _p, _i64, _p]),
+    "gfh_state_dict_open": (_i, [C.c_char_p, C.POINTER(C.c_void_p)]),
+    "gfh_state_dict_close": (None, [_p]),
+    "gfh_state_dict_count": (_i64, [_p]),
+    "gfh_state_dict_entry": (_i, [_p, _i64, C.POINTER(C.c_char_p), C.POINTER(_i), C.POINTER(_i), C.POINTER(_i),
+                                  C.POINTER(_i64), _i, C.POINTER(_i64)]),
+    "gfh_state_dict_find": (_i64, [_p, C.c_char_p]),
+    "gfh_state_dict_read_f32": (_i, [_p, _i64, _p, _p]),
+    "gfh_state_dict_read_q8": (_i, [_p, _i64, _p, _p, _p, _p]),
+    "gfh_state_dict_save": (_i, [C.c_char_p, _i, _p, _i64, _p]),
     "gfh_swiglu_f32_workspace_size": (_sz, [_i64, _i64]),
     "gfh_swiglu_f32": (_i, [_p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p]),
     "gfh_swiglu_i8_workspace_size": (_sz, [_i64, _i64, _i64]),
@@ -71,6 +80,13 @@ SIGNATURES = {
 }
 
 _lib = None
+
+
+class TensorEntry(C.Structure):
+    """gfh_tensor_entry (include/ghostflow_hip.h)."""
+    _fields_ = [("name", C.c_char_p), ("kind", C.c_int), ("dtype", C.c_int), ("ndim", C.c_int),
+                ("dims", C.POINTER(C.c_int64)), ("data", C.c_void_p), ("scales", C.c_void_p),
+                ("zero_points", C.c_void_p), ("nscales", C.c_int64)]
 
 
 def load():

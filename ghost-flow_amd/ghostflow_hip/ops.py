@@ -419,3 +419,115 @@ def qswiglu(x, gate, up, down, *, want_h=False):
     _check(lib().gfh_swiglu_i8(x.data_ptr(), m, hidden, inter, *args, y.data_ptr(), _ptr(h), None, 0,
                                _stream(x.device)))
     return (y, h) if want_h else y
+
+
+# ---- state dict files (ghostflow-core/src/serialize.rs) -------------------------
+
+class StateDict:
+    """An opened GHOSTFLW / GHOSTFLQ file (gfh_state_dict_open): names,
+    shapes and kinds from the mapped header; tensors copied to the device on
+    request.  Use as a context manager or call close()."""
+
+    def __init__(self, path: str):
+        import ctypes as C
+        h = C.c_void_p()
+        _check(lib().gfh_state_dict_open(str(path).encode(), C.byref(h)))
+        self._h = h
+        self._keys = []
+        self._info = {}
+        for i in range(int(lib().gfh_state_dict_count(h))):
+            name, kind, dtype, ndim, nsc = C.c_char_p(), C.c_int(), C.c_int(), C.c_int(), C.c_int64()
+            _check(lib().gfh_state_dict_entry(h, i, C.byref(name), C.byref(kind), C.byref(dtype), C.byref(ndim),
+                                              None, 0, C.byref(nsc)))
+            dims = (C.c_int64 * max(ndim.value, 1))()
+            _check(lib().gfh_state_dict_entry(h, i, None, None, None, None, dims, ndim.value, None))
+            key = name.value.decode("utf-8")
+            self._keys.append(key)
+            self._info[key] = (i, kind.value, dtype.value, tuple(dims[d] for d in range(ndim.value)), nsc.value)
+
+    def close(self):
+        if self._h:
+            lib().gfh_state_dict_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def keys(self):
+        return list(self._keys)
+
+    def __contains__(self, key):
+        return key in self._info
+
+    def info(self, key):
+        """(kind, dtype byte or scheme, shape, nscales)."""
+        return self._info[key][1:]
+
+    def tensor(self, key, device="cuda"):
+        """A kind-0 entry as a float32 device tensor of its stored shape, or a
+        kind-1 entry as (codes int8, scales f32, zero points int8)."""
+        idx, kind, _dtype, shape, nsc = self._info[key]
+        if kind == 0:
+            out = torch.empty(shape, dtype=torch.float32, device=device)
+            _check(lib().gfh_state_dict_read_f32(self._h, idx, out.data_ptr(), _stream(out.device)))
+            return out
+        codes = torch.empty(shape, dtype=torch.int8, device=device)
+        scales = torch.empty(nsc, dtype=torch.float32, device=device)
+        zps = torch.empty(nsc, dtype=torch.int8, device=device)
+        _check(lib().gfh_state_dict_read_q8(self._h, idx, codes.data_ptr(), scales.data_ptr(), zps.data_ptr(),
+                                            _stream(codes.device)))
+        return codes, scales, zps
+
+
+def load_state_dict(path, device="cuda"):
+    """load_state_dict (serialize.rs:48-88) straight into device memory:
+    name -> float32 tensor (GHOSTFLW), or name -> (codes, scales, zero
+    points) for the quantized entries of a GHOSTFLQ file."""
+    with StateDict(path) as sd:
+        return {k: sd.tensor(k, device) for k in sd.keys()}
+
+
+def save_state_dict(path, state, *, quantized_format=False, dtypes=None):
+    """save_state_dict (serialize.rs:20-45) from device tensors, in the
+    dict's order.  Values are float32 device tensors, or -- in a GHOSTFLQ
+    file -- (codes, scales, zero points) tuples of a QuantizedTensor.
+    dtypes optionally maps a name to the dtype byte (or scheme) recorded."""
+    import ctypes as C
+    entries = (_lib.TensorEntry * max(len(state), 1))()
+    keep = []
+    dev = None
+    for i, (name, v) in enumerate(state.items()):
+        e = entries[i]
+        nb = str(name).encode("utf-8")
+        keep.append(nb)
+        e.name = nb
+        quant = isinstance(v, (tuple, list))
+        t = v[0] if quant else v
+        if quant and not quantized_format:
+            raise GhostFlowError(_lib.INVALID_DATA, f"{name}: quantized entries need quantized_format=True")
+        _need(t, torch.int8 if quant else torch.float32, str(name))
+        dev = t.device
+        dims = (C.c_int64 * max(t.dim(), 1))(*t.shape)
+        keep.append(dims)
+        e.kind = 1 if quant else 0
+        e.dtype = (dtypes or {}).get(name, 0 if quant else 2)
+        e.ndim = t.dim()
+        e.dims = C.cast(dims, C.POINTER(C.c_int64))
+        e.data = t.data_ptr()
+        if quant:
+            _need(v[1], torch.float32, f"{name} scales")
+            _need(v[2], torch.int8, f"{name} zero points")
+            e.scales = v[1].data_ptr()
+            e.zero_points = v[2].data_ptr()
+            e.nscales = v[1].numel()
+    _check(lib().gfh_state_dict_save(str(path).encode(), int(bool(quantized_format)), C.addressof(entries),
+                                     len(state), _stream(dev) if dev is not None else None))

@@ -310,6 +310,77 @@ GFH_API int gfh_swiglu_i8(const float *x, int64_t m, int64_t hidden, int64_t int
                           float *h, void *workspace, size_t workspace_bytes,
                           gfh_stream_t stream);
 
+/* ---- state dict files (ghostflow-core/src/serialize.rs) ------------------ */
+
+/* An opened weight file, mapped into host memory.  Two formats:
+ *
+ * GHOSTFLW -- the reference's state dict (serialize.rs:11-186):
+ *   "GHOSTFLW" | u32 version (1) | u32 count | count x entry, where an entry
+ *   is u32 name length | UTF-8 name | u8 dtype (serialize.rs:188-215:
+ *   0 F16 .. 2 F32 .. 9 Bool) | u32 ndim | ndim x u64 dims | numel x f32;
+ *   every integer and float little-endian, the data always f32 whatever the
+ *   dtype byte says (write_tensor uses data_f32).
+ *
+ * GHOSTFLQ -- this library's file for QuantizedTensor
+ *   (ghostflow-nn/src/quantization.rs:40-51), which the reference cannot
+ *   write; payloads start at 64-byte file offsets:
+ *   "GHOSTFLQ" | u32 version (1) | u32 count | count x entry, an entry being
+ *   u32 name length | UTF-8 name | u8 kind, then
+ *     kind 0 (f32 tensor): u8 dtype | u32 ndim | u64 dims | pad | numel x f32
+ *     kind 1 (QuantizedTensor): u8 scheme (QuantizationScheme order: 0 INT8,
+ *       1 FP16, 2 Dynamic) | u32 ndim | u64 dims | u64 nscales (1: per
+ *       tensor, dims[0]: per channel over dim 0) | pad | nscales x f32
+ *       scales | nscales x i8 zero points | pad | numel x i8 codes
+ *
+ * Opening validates the file the way load_state_dict does (serialize.rs:
+ * 47-88, 122-167): magic, version <= 1, dtype byte 0-9, UTF-8 names, every
+ * size inside the file; errors are GFH_INVALID_DATA with the reason in
+ * gfh_last_error().  A name stored twice keeps its last entry, as the
+ * reference's HashMap insert does.  The handle owns the mapping and the
+ * pinned staging buffers; it is not thread-safe. */
+typedef struct gfh_state_dict gfh_state_dict;
+GFH_API int gfh_state_dict_open(const char *path, gfh_state_dict **out);
+GFH_API void gfh_state_dict_close(gfh_state_dict *sd);
+/* Number of distinct names. */
+GFH_API int64_t gfh_state_dict_count(const gfh_state_dict *sd);
+/* Entry `index` (0 .. count-1, in order of first appearance): name (valid
+ * until close), kind (0 f32, 1 quantized), dtype byte (kind 0) or scheme
+ * (kind 1), ndim, the first max_dims dims, nscales (kind 1; 0 otherwise).
+ * Any output pointer may be NULL. */
+GFH_API int gfh_state_dict_entry(const gfh_state_dict *sd, int64_t index, const char **name,
+                                 int *kind, int *dtype, int *ndim, int64_t *dims, int max_dims,
+                                 int64_t *nscales);
+/* Index of `name`, or -1. */
+GFH_API int64_t gfh_state_dict_find(const gfh_state_dict *sd, const char *name);
+/* Copy an entry into device memory: a kind-0 entry's numel floats into dst;
+ * a kind-1 entry's codes, scales and zero points.  The copies run on
+ * `stream` through pinned staging buffers; the call returns once the data
+ * is in device memory. */
+GFH_API int gfh_state_dict_read_f32(gfh_state_dict *sd, int64_t index, float *dst,
+                                    gfh_stream_t stream);
+GFH_API int gfh_state_dict_read_q8(gfh_state_dict *sd, int64_t index, int8_t *codes,
+                                   float *scales, int8_t *zero_points, gfh_stream_t stream);
+
+/* One tensor to write; pointers marked device are device memory. */
+typedef struct gfh_tensor_entry {
+    const char *name;
+    int kind;                   /* 0 f32 tensor, 1 QuantizedTensor (GHOSTFLQ only) */
+    int dtype;                  /* kind 0: dtype byte to record (2 = F32); kind 1: scheme */
+    int ndim;
+    const int64_t *dims;        /* host, ndim entries */
+    const void *data;           /* device: numel f32 (kind 0) or numel int8 codes (kind 1) */
+    const float *scales;        /* device, kind 1: nscales */
+    const int8_t *zero_points;  /* device, kind 1: nscales */
+    int64_t nscales;            /* kind 1: 1 or dims[0] */
+} gfh_tensor_entry;
+/* save_state_dict (serialize.rs:20-45) from device memory: a GHOSTFLW file
+ * (quantized_format == 0; kind-0 entries only, in the given order, byte for
+ * byte what write_tensor writes) or a GHOSTFLQ file.  Waits for `stream`
+ * before reading the tensors. */
+GFH_API int gfh_state_dict_save(const char *path, int quantized_format,
+                                const gfh_tensor_entry *entries, int64_t count,
+                                gfh_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
