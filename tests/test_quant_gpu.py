@@ -286,3 +286,28 @@ def test_qlinear_large_tile_y_variants_bit_exact(torch_dev, m, n, k, x_per_row, 
                         want_acc=False)
     assert acc is None
     assert _same_f32(to_np(y), ry)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1, 16), (1, 17, 80), (2, 100, 1040), (3, 33, 4096), (4, 1000, 4112),
+                                   (1, 11008, 4096), (4, 4100, 11008)])
+@pytest.mark.parametrize("x_per_row,with_zp", [(False, True), (True, False), (True, True)])
+def test_qlinear_decode_rows_bit_exact(torch_dev, m, n, k, x_per_row, with_zp):
+    """M <= 4 on the skinny kernel: k down to one 16-byte group, k % 64 != 0,
+    ragged n inside a 16-column block, the config-3 weight at M = 1 and the
+    SwiGLU down projection's K = 11008, every activation-scale variant,
+    bit-exact to the oracle."""
+    _qlinear_case(torch_dev, m, n, k, x_per_row, with_zp, with_bias=(n % 2 == 0))
+
+
+def test_qlinear_decode_acc_only(torch_dev):
+    """Accumulators without the fp32 output (sx / sw unused, NULL)."""
+    gh, O = _gh(), _O()
+    rng = np.random.default_rng(4)
+    qx = rng.integers(-128, 128, size=(3, 2064), dtype=np.int8)
+    qw = rng.integers(-127, 128, size=(70, 2064), dtype=np.int8)
+    zx = np.array([-5], np.int8)
+    _, racc = O.qlinear_i8(qx, np.ones(1, np.float32), zx, False, qw, np.ones(70, np.float32))
+    y, acc = gh.qlinear(to_dev(qx, torch_dev), None, to_dev(zx, torch_dev), to_dev(qw, torch_dev), None,
+                        want_y=False, want_acc=True)
+    assert y is None
+    np.testing.assert_array_equal(to_np(acc), racc)
