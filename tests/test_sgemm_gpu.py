@@ -38,13 +38,15 @@ def test_reference_known_answers(torch_dev):
 
 
 @pytest.mark.parametrize("m,k,n", [(1, 1, 1), (7, 3, 5), (33, 29, 17), (64, 64, 64), (128, 200, 96),
-                                   (257, 300, 131), (1024, 1024, 1024), (1500, 300, 1300), (2048, 96, 2048)])
+                                   (257, 300, 131), (1024, 1024, 1024), (1500, 300, 1300), (2048, 96, 2048),
+                                   (300, 4100, 200), (130, 600, 70)])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 def test_integer_inputs_bit_exact(torch_dev, m, k, n, ta, tb):
     """|a|,|b| <= 8 integers: every partial sum < 2^24 is exact, so the GPU
     must equal the oracle bit for bit whatever the summation order.  The
     shapes cover all three tilings (64x64 below 128 tiles of 128x128,
-    128x64 up to 512 of them, 128x128 beyond) with ragged edges."""
+    128x64 up to 512 of them, 128x128 beyond) with ragged edges, and long K
+    on few tiles (300 x 4100 x 200)."""
     gh, O = _gh(), _oracle()
     rng = np.random.default_rng(m * 1000003 + k * 1009 + n)
     a = rng.integers(-8, 9, size=(m, k)).astype(np.float32)
@@ -78,10 +80,11 @@ def test_unaligned_leading_dims(torch_dev, m, k, n):
     assert np.abs(got - O.matmul(a, b)).max() <= gemm_tol(k, a, b)
 
 
-def test_alpha_beta_bias(torch_dev):
+@pytest.mark.parametrize("m,k,n", [(70, 96, 150), (70, 2048, 150)])
+def test_alpha_beta_bias(torch_dev, m, k, n):
+    """alpha, beta and bias: each a separate rounding after the sum."""
     gh, O = _gh(), _oracle()
     rng = np.random.default_rng(11)
-    m, k, n = 70, 96, 150
     a = rng.integers(-4, 5, size=(m, k)).astype(np.float32)
     b = rng.integers(-4, 5, size=(k, n)).astype(np.float32)
     c0 = rng.integers(-4, 5, size=(m, n)).astype(np.float32)
