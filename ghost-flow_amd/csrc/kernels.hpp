@@ -32,6 +32,10 @@ int launch_gemv_nt(const SgemmDesc &d, hipStream_t s);
 constexpr int64_t kNtSkinnyMinM = 4;
 bool gemm_nt_skinny_fits(const SgemmDesc &d);
 int launch_gemm_nt_skinny(const SgemmDesc &d, hipStream_t s);
+// sgemm_big.hip: NT with both operands K-contiguous on 256 x 256 tiles when
+// they fill the GPU (K % 32 == 0, batch 1).
+bool sgemm_big_fits(const SgemmDesc &d);
+int launch_sgemm_big(const SgemmDesc &d, hipStream_t s);
 
 // quant.hip
 int launch_quantize_per_channel(const float *x, int64_t rows, int64_t cols, bool symmetric, int8_t *q,

@@ -1,0 +1,299 @@
+// sgemm_big.hip -- fp32 GEMM on 256 x 256 tiles fed by direct-to-LDS loads,
+// for the NT form with both operands K-contiguous: C = alpha * A . B^T
+// (+ beta C) (+ bias), A [m, k] and B [n, k] row-major -- Linear::forward's
+// x . W^T with the reference's [out, in] weight (ghostflow-nn/src/linear.rs:
+// 56-69).  gfh_sgemm sends NT calls here when the problem fills the GPU with
+// such tiles; the general tile kernel (sgemm.hip) serves everything else.
+//
+// Design (one 512-thread workgroup = 8 wave64s, 2 x 4, per 256 x 256 tile):
+//  * Each wave holds a 128 x 64 sub-tile as 4 x 2 v_mfma_f32_32x32x2_f32
+//    accumulators (128 registers): 8 independent MFMA chains, and two waves
+//    per SIMD so that one issues MFMAs while the other waits on LDS.
+//  * K advances in stages of 32 floats (128 bytes per row).  Both operands
+//    stream into a 2-stage LDS ring with global_load_lds_dwordx4 (global ->
+//    LDS, no VGPR staging): one load instruction fills 1 KB = 8 rows x 128
+//    bytes, whole cache lines.  Chunk c (16 bytes) of row r sits at
+//    c ^ ((r >> 1) & 7), which puts the 16-byte fragment reads of 16 lanes
+//    on 16 distinct 4-bank groups.
+//  * Fragments: lane l reads row l % 32, chunk 2 kg + l / 32 of k-group kg
+//    (8 floats): lanes 0-31 hold k 8kg .. 8kg+3, lanes 32-63 8kg+4 .. +7, and
+//    element e of both operands feeds MFMA e of the group, so every product
+//    pairs matching k.  The next group's fragments are read while the
+//    current group's MFMAs run.
+//  * The loop body is branch-free: past the end of K the ring reloads the
+//    last stage into the slot just freed, so every s_waitcnt is a constant.
+//  * Epilogue: alpha * acc (+ beta C) (+ bias), separate f32 roundings as in
+//    the reference; the tile goes through LDS so each wave stores whole
+//    row runs with 16-byte stores.
+//  * Workgroups are renumbered XCD-contiguous and walked in 4-tile bands so
+//    tiles running together share A / B panels in one L2.
+#include <algorithm>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+#pragma clang fp contract(off)
+
+namespace gfh {
+namespace {
+
+constexpr int BM = 256, BN = 256;
+constexpr int BKB = 128;                 // K bytes per stage (32 floats)
+constexpr int NWM = 2, NWN = 4, NW = 8;  // wave grid
+constexpr int NT = 64 * NW;
+constexpr int WM = BM / NWM, WN = BN / NWN;  // 128 x 64 per wave
+constexpr int FM = WM / 32, FN = WN / 32;    // 4 x 2 accumulators
+constexpr int STAGES = 2;
+constexpr int kRowsPerLoad = 1024 / BKB;                  // rows per load instruction
+constexpr int kLA = BM * BKB / (1024 * NW), kLB = BN * BKB / (1024 * NW);  // load instructions per wave per stage
+constexpr int kLPS = kLA + kLB;
+constexpr int kABytes = BM * BKB, kBBytes = BN * BKB;
+constexpr int kStageBytes = kABytes + kBBytes;
+constexpr int kRing = STAGES * kStageBytes;
+constexpr int kOutStride = WN + 8;  // floats per staged output row (two row groups on disjoint banks)
+constexpr int kOut = NW * (WM / 2) * kOutStride * 4;
+constexpr int kLds = kRing > kOut ? kRing : kOut;
+static_assert(kLds <= 160 * 1024, "LDS per workgroup");
+constexpr int kGroupM = 4;
+constexpr int kKGroups = BKB / 32;  // 8-float k-groups per stage
+
+typedef __attribute__((address_space(3))) void *lds_ptr;
+typedef __attribute__((address_space(1))) void *glb_ptr;
+
+struct BigParams {
+    const float *a, *b;
+    float *c;
+    const float *bias;
+    int64_t m, n, k, lda, ldb, ldc;
+    float alpha, beta;
+    int tiles_m, tiles_n;
+};
+
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// NM MFMAs with ND LDS reads and NV global loads spread between them.
+template <int NV, int ND, int NM, int G = 0>
+__device__ __forceinline__ void interleave() {
+    if constexpr (G < NM) {
+        constexpr int v = (G + 1) * NV / NM - G * NV / NM;
+        constexpr int d = (G + 1) * ND / NM - G * ND / NM;
+        if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x010, v, 0);  // VMEM
+        if constexpr (d > 0) __builtin_amdgcn_sched_group_barrier(0x100, d, 0);  // DS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                       // MFMA
+        interleave<NV, ND, NM, G + 1>();
+    }
+}
+
+__global__ __launch_bounds__(NT, 1) void sgemm_big_kernel(BigParams p) {
+    __shared__ __attribute__((aligned(1024))) char lds[kLds];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm0 = (wave / NWN) * WM;
+    const int wn0 = (wave % NWN) * WN;
+
+    const int nblk = p.tiles_m * p.tiles_n;
+    int bid = blockIdx.x;
+    if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+    const int group_size = kGroupM * p.tiles_n;
+    const int group = bid / group_size;
+    const int first_m = group * kGroupM;
+    const int gm = min(p.tiles_m - first_m, kGroupM);
+    const int in_group = bid - group * group_size;
+    const int64_t m0 = (int64_t)(first_m + in_group % gm) * BM;
+    const int64_t n0 = (int64_t)(in_group / gm) * BN;
+
+    // Byte offsets, from the tile's first row, of this wave's load
+    // instructions: instruction j covers tile rows wave * (BM / NW) + j * 8
+    // .. + 7; lane l fills LDS slot l of that 1 KB run (row l / 8, chunk
+    // l % 8) from logical chunk (l % 8) ^ swz(row).  Rows past m / n read
+    // the last row (their products are never stored).
+    const char *a_base = reinterpret_cast<const char *>(p.a + m0 * p.lda);
+    const char *b_base = reinterpret_cast<const char *>(p.b + n0 * p.ldb);
+    int64_t a_off[kLA], b_off[kLB];
+#pragma unroll
+    for (int j = 0; j < kLA; ++j) {
+        const int r = wave * (BM / NW) + j * kRowsPerLoad + lane / 8;
+        a_off[j] = (min(m0 + r, p.m - 1) - m0) * p.lda * 4 + ((lane % 8) ^ swz(r)) * 16;
+    }
+#pragma unroll
+    for (int j = 0; j < kLB; ++j) {
+        const int r = wave * (BN / NW) + j * kRowsPerLoad + lane / 8;
+        b_off[j] = (min(n0 + r, p.n - 1) - n0) * p.ldb * 4 + ((lane % 8) ^ swz(r)) * 16;
+    }
+    const int nk = (int)(p.k / 32);
+
+    auto issue = [&](int t, int slot) {
+        char *la = lds + slot * kStageBytes;
+        char *lb = la + kABytes;
+        const int64_t kb = (int64_t)t * BKB;
+#pragma unroll
+        for (int j = 0; j < kLA; ++j)
+            __builtin_amdgcn_global_load_lds((glb_ptr)(a_base + kb + a_off[j]),
+                                             (lds_ptr)(la + (wave * (BM / NW) + j * kRowsPerLoad) * BKB), 16, 0, 0);
+#pragma unroll
+        for (int j = 0; j < kLB; ++j)
+            __builtin_amdgcn_global_load_lds((glb_ptr)(b_base + kb + b_off[j]),
+                                             (lds_ptr)(lb + (wave * (BN / NW) + j * kRowsPerLoad) * BKB), 16, 0, 0);
+    };
+
+    // Fragment of k-group kg: lane l reads row l % 32 of a 32-row block,
+    // logical chunk 2 kg + l / 32; blocks start at multiples of 32 rows, so
+    // the swizzle depends on the lane only.
+    const int frow = lane & 31;
+    const int foff0 = frow * BKB + (((lane >> 5) ^ swz(frow)) * 16);
+    f32x4 af[2][FM], bf[2][FN];
+    auto load_frags = [&](int buf, int t, int kg) {
+        const char *la = lds + (t % STAGES) * kStageBytes;
+        const char *lb = la + kABytes;
+        const int fo = foff0 ^ (kg << 5);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) af[buf][i] = *reinterpret_cast<const f32x4 *>(la + (wm0 + i * 32) * BKB + fo);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) bf[buf][j] = *reinterpret_cast<const f32x4 *>(lb + (wn0 + j * 32) * BKB + fo);
+    };
+
+    f32x16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    auto mfmas = [&](int buf) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[buf][i][e], bf[buf][j][e], acc[i][j], 0, 0, 0);
+    };
+
+    constexpr int NR = FM + FN, NM = 4 * FM * FN;
+    for (int t = 0; t < STAGES; ++t) issue(min(t, nk - 1), t);
+    wait_vmcnt<(STAGES - 1) * kLPS>();
+    __builtin_amdgcn_s_barrier();
+    load_frags(0, 0, 0);
+    auto k_groups = [&](int t) {
+#pragma unroll
+        for (int kg = 0; kg + 1 < kKGroups; ++kg) {
+            load_frags((kg + 1) & 1, t, kg + 1);
+            mfmas(kg & 1);
+            interleave<0, NR, NM>();
+        }
+    };
+    for (int t = 0; t + 1 < nk; ++t) {
+        k_groups(t);
+        __builtin_amdgcn_sched_barrier(0);
+        wait_lgkm0();  // this wave's reads of stage t are done
+        wait_vmcnt<(STAGES - 2) * kLPS>();  // stage t + 1 landed
+        __builtin_amdgcn_s_barrier();
+        issue(min(t + STAGES, nk - 1), t % STAGES);
+        load_frags(0, t + 1, 0);
+        mfmas((kKGroups - 1) & 1);
+        interleave<kLPS, NR, NM>();
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    k_groups(nk - 1);
+    mfmas((kKGroups - 1) & 1);
+    wait_vmcnt<0>();  // no load may still be writing the ring
+
+    // Epilogue.  Lane l, register r of block (i, j): row 8 (r / 4) +
+    // 4 (l / 32) + r % 4, column l % 32.  Each wave converts half of its
+    // sub-tile at a time into its own LDS region, then writes whole row
+    // runs of WN floats with 16-byte stores.
+    constexpr int LPR = WN / 4;    // lanes per output row
+    constexpr int RPI = 64 / LPR;  // rows per store instruction
+    constexpr int HALF = WM / 2;
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();  // every wave is done with the operand ring
+    float *lt = reinterpret_cast<float *>(lds) + wave * (HALF * kOutStride);
+    const bool vec_out = (p.ldc % 4) == 0 && (reinterpret_cast<uintptr_t>(p.c) & 15) == 0;
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+        for (int ii = 0; ii < FM / 2; ++ii)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int lr = ii * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    lt[lr * kOutStride + j * 32 + (lane & 31)] = p.alpha * acc[hf * (FM / 2) + ii][j][r];
+                }
+        const int64_t col = n0 + wn0 + 4 * (lane % LPR);
+#pragma unroll
+        for (int q = 0; q < HALF / RPI; ++q) {
+            const int lr = RPI * q + lane / LPR;
+            f32x4 v = *reinterpret_cast<const f32x4 *>(lt + lr * kOutStride + 4 * (lane % LPR));
+            const int64_t row = m0 + wm0 + hf * HALF + lr;
+            if (row >= p.m) continue;
+            float *dst = p.c + row * p.ldc + col;
+            if (vec_out && col + 3 < p.n) {
+                if (p.beta != 0.f) {
+                    const f32x4 c0 = *reinterpret_cast<const f32x4 *>(dst);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = v[e] + p.beta * c0[e];
+                }
+                if (p.bias) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = v[e] + p.bias[col + e];
+                }
+                *reinterpret_cast<f32x4 *>(dst) = v;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (col + e >= p.n) continue;
+                    float x = v[e];
+                    if (p.beta != 0.f) x = x + p.beta * dst[e];
+                    if (p.bias) x = x + p.bias[col + e];
+                    dst[e] = x;
+                }
+            }
+        }
+        __builtin_amdgcn_s_barrier();  // the region is refilled by the next half
+    }
+}
+
+}  // namespace
+
+bool sgemm_big_fits(const SgemmDesc &d) {
+    if (d.trans_a || !d.trans_b || d.batch > 1 || d.batch_a > 1 || d.batch_b > 1) return false;
+    if (d.k <= 0 || d.k % 32 != 0 || d.lda % 4 != 0 || d.ldb % 4 != 0) return false;
+    if (!aligned16(d.a) || !aligned16(d.b)) return false;
+    // 256 x 256 tiles must fill the GPU; 32-bit tile-relative offsets are
+    // not needed (offsets are 64-bit), but rows must exist.
+    const int64_t tiles = ((d.m + BM - 1) / BM) * ((d.n + BN - 1) / BN);
+    return d.m >= BM && d.n >= BN && tiles >= 256;
+}
+
+int launch_sgemm_big(const SgemmDesc &d, hipStream_t s) {
+    BigParams p{};
+    p.a = d.a;
+    p.b = d.b;
+    p.c = d.c;
+    p.bias = d.bias;
+    p.m = d.m;
+    p.n = d.n;
+    p.k = d.k;
+    p.lda = d.lda;
+    p.ldb = d.ldb;
+    p.ldc = d.ldc;
+    p.alpha = d.alpha;
+    p.beta = d.beta;
+    p.tiles_m = (int)((d.m + BM - 1) / BM);
+    p.tiles_n = (int)((d.n + BN - 1) / BN);
+    hipLaunchKernelGGL(sgemm_big_kernel, dim3((unsigned)(p.tiles_m * p.tiles_n)), dim3(NT), 0, s, p);
+    return check_launch("sgemm (256x256 tiles)");
+}
+
+}  // namespace gfh

@@ -165,3 +165,40 @@ def test_k_zero_gives_bias(torch_dev):
     bias = torch.arange(6, dtype=torch.float32, device=torch_dev)
     out = gh.sgemm(a, b, bias=bias)
     assert to_np(out).tolist() == [list(range(6))] * 4
+
+
+@pytest.mark.parametrize("m,n,k", [(4096, 4096, 64), (4100, 4000, 96), (4352, 3900, 32)])
+def test_nt_big_tiles_integer_exact(torch_dev, m, n, k):
+    """NT (Linear's x . W^T) shapes that fill the GPU with 256 x 256 tiles
+    take the direct-to-LDS kernel: ragged m and n inside the last tiles,
+    alpha, beta and bias, on integer data (exact in any summation order)."""
+    gh, O = _gh(), _oracle()
+    rng = np.random.default_rng(m + n + k)
+    a = rng.integers(-4, 5, size=(m, k)).astype(np.float32)
+    w = rng.integers(-4, 5, size=(n, k)).astype(np.float32)
+    c0 = rng.integers(-4, 5, size=(m, n)).astype(np.float32)
+    bias = rng.integers(-4, 5, size=(n,)).astype(np.float32)
+    dc = to_dev(c0, torch_dev)
+    gh.sgemm(to_dev(a, torch_dev), to_dev(w, torch_dev), trans_b=True, alpha=2.0, beta=-1.0,
+             bias=to_dev(bias, torch_dev), out=dc)
+    ref = (2.0 * O.linear_forward(a, w) - c0 + bias).astype(np.float32)
+    np.testing.assert_array_equal(to_np(dc), ref)
+
+
+def test_nt_big_tiles_strided(torch_dev):
+    """lda > k and ldc > n on the 256 x 256 kernel; bytes between rows of C
+    stay untouched."""
+    import torch
+    gh, O = _gh(), _oracle()
+    rng = np.random.default_rng(31)
+    m, n, k, lda, ldc = 4096, 4096, 96, 100, 4100
+    xa = rng.integers(-4, 5, size=(m, lda)).astype(np.float32)
+    w = rng.integers(-4, 5, size=(n, k)).astype(np.float32)
+    dx, dw = to_dev(xa, torch_dev), to_dev(w, torch_dev)
+    out = torch.full((m, ldc), 7.0, device=torch_dev)
+    rc = gh.lib().gfh_sgemm(0, 1, m, n, k, 1.0, dx.data_ptr(), lda, dw.data_ptr(), k, 0.0, out.data_ptr(), ldc,
+                            None, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    got = to_np(out)
+    np.testing.assert_array_equal(got[:, :n], O.linear_forward(np.ascontiguousarray(xa[:, :k]), w))
+    assert (got[:, n:] == 7.0).all()
