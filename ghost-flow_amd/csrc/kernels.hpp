@@ -32,8 +32,8 @@ int launch_gemv_nt(const SgemmDesc &d, hipStream_t s);
 constexpr int64_t kNtSkinnyMinM = 4;
 bool gemm_nt_skinny_fits(const SgemmDesc &d);
 int launch_gemm_nt_skinny(const SgemmDesc &d, hipStream_t s);
-// sgemm_big.hip: NT with both operands K-contiguous on 256 x 256 tiles when
-// they fill the GPU (K % 32 == 0, batch 1).
+// sgemm_big.hip: NT and NN (A [m, k]) on 256 x 256 tiles when they fill the
+// GPU (K % 32 == 0, batch 1; NN with n % 4 == 0).
 bool sgemm_big_fits(const SgemmDesc &d);
 int launch_sgemm_big(const SgemmDesc &d, hipStream_t s);
 

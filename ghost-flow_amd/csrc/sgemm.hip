@@ -279,7 +279,7 @@ int launch_sgemm(const SgemmDesc &d, hipStream_t s) {
     if (gemv_nt_fits(d)) return launch_gemv_nt(d, s);
     // up to 64 rows: the weight streamed straight into f32 MFMA operands
     if (gemm_nt_skinny_fits(d)) return launch_gemm_nt_skinny(d, s);
-    // NT on 256 x 256 tiles fed by direct-to-LDS loads, when they fill the GPU
+    // NT / NN on 256 x 256 tiles fed by direct-to-LDS loads, when they fill the GPU
     if (sgemm_big_fits(d)) return launch_sgemm_big(d, s);
     SgemmParams p{};
     p.a = d.a;

@@ -1,9 +1,10 @@
-// sgemm_big.hip -- fp32 GEMM on 256 x 256 tiles fed by direct-to-LDS loads,
-// for the NT form with both operands K-contiguous: C = alpha * A . B^T
-// (+ beta C) (+ bias), A [m, k] and B [n, k] row-major -- Linear::forward's
-// x . W^T with the reference's [out, in] weight (ghostflow-nn/src/linear.rs:
-// 56-69).  gfh_sgemm sends NT calls here when the problem fills the GPU with
-// such tiles; the general tile kernel (sgemm.hip) serves everything else.
+// sgemm_big.hip -- fp32 GEMM on 256 x 256 tiles fed by direct-to-LDS loads:
+// C = alpha * A . op(B) (+ beta C) (+ bias) with A [m, k] row-major and B
+// either [n, k] (NT: Linear::forward's x . W^T with the reference's
+// [out, in] weight, ghostflow-nn/src/linear.rs:56-69) or [k, n] (NN:
+// Tensor::matmul, ghostflow-core/src/ops/matmul.rs:91-119).  gfh_sgemm
+// sends those calls here when the problem fills the GPU with such tiles;
+// the general tile kernel (sgemm.hip) serves everything else.
 //
 // Design (one 512-thread workgroup = 8 wave64s, 2 x 4, per 256 x 256 tile):
 //  * Each wave holds a 128 x 64 sub-tile as 4 x 2 v_mfma_f32_32x32x2_f32
@@ -20,6 +21,10 @@
 //    element e of both operands feeds MFMA e of the group, so every product
 //    pairs matching k.  The next group's fragments are read while the
 //    current group's MFMAs run.
+//  * NN: the B stage is 32 k-rows of 256 columns; one load instruction
+//    fills one k-row (1 KB).  Rows sit 264 floats apart, so the B fragment
+//    -- 4 scalar reads of 4 consecutive k for column l % 32 -- puts lanes
+//    0-31 and 32-63 (4 rows apart) on disjoint halves of the 64 banks.
 //  * The loop body is branch-free: past the end of K the ring reloads the
 //    last stage into the slot just freed, so every s_waitcnt is a constant.
 //  * Epilogue: alpha * acc (+ beta C) (+ bias), separate f32 roundings as in
@@ -47,13 +52,17 @@ constexpr int STAGES = 2;
 constexpr int kRowsPerLoad = 1024 / BKB;                  // rows per load instruction
 constexpr int kLA = BM * BKB / (1024 * NW), kLB = BN * BKB / (1024 * NW);  // load instructions per wave per stage
 constexpr int kLPS = kLA + kLB;
-constexpr int kABytes = BM * BKB, kBBytes = BN * BKB;
-constexpr int kStageBytes = kABytes + kBBytes;
-constexpr int kRing = STAGES * kStageBytes;
+constexpr int kABytes = BM * BKB;
+constexpr int kBRowNN = BN + 8;  // floats per B k-row in LDS (NN)
+template <bool NN>
+constexpr int b_bytes() { return NN ? 32 * kBRowNN * 4 : BN * BKB; }
+template <bool NN>
+constexpr int stage_bytes() { return kABytes + b_bytes<NN>(); }
 constexpr int kOutStride = WN + 8;  // floats per staged output row (two row groups on disjoint banks)
 constexpr int kOut = NW * (WM / 2) * kOutStride * 4;
-constexpr int kLds = kRing > kOut ? kRing : kOut;
-static_assert(kLds <= 160 * 1024, "LDS per workgroup");
+template <bool NN>
+constexpr int lds_bytes() { return STAGES * stage_bytes<NN>() > kOut ? STAGES * stage_bytes<NN>() : kOut; }
+static_assert(lds_bytes<false>() <= 160 * 1024 && lds_bytes<true>() <= 160 * 1024, "LDS per workgroup");
 constexpr int kGroupM = 4;
 constexpr int kKGroups = BKB / 32;  // 8-float k-groups per stage
 
@@ -92,8 +101,10 @@ __device__ __forceinline__ void interleave() {
     }
 }
 
+template <bool NN>
 __global__ __launch_bounds__(NT, 1) void sgemm_big_kernel(BigParams p) {
-    __shared__ __attribute__((aligned(1024))) char lds[kLds];
+    constexpr int kStageBytes = stage_bytes<NN>();
+    __shared__ __attribute__((aligned(1024))) char lds[lds_bytes<NN>()];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -117,7 +128,7 @@ __global__ __launch_bounds__(NT, 1) void sgemm_big_kernel(BigParams p) {
     // l % 8) from logical chunk (l % 8) ^ swz(row).  Rows past m / n read
     // the last row (their products are never stored).
     const char *a_base = reinterpret_cast<const char *>(p.a + m0 * p.lda);
-    const char *b_base = reinterpret_cast<const char *>(p.b + n0 * p.ldb);
+    const char *b_base = reinterpret_cast<const char *>(NN ? p.b + n0 : p.b + n0 * p.ldb);
     int64_t a_off[kLA], b_off[kLB];
 #pragma unroll
     for (int j = 0; j < kLA; ++j) {
@@ -126,12 +137,21 @@ __global__ __launch_bounds__(NT, 1) void sgemm_big_kernel(BigParams p) {
     }
 #pragma unroll
     for (int j = 0; j < kLB; ++j) {
-        const int r = wave * (BN / NW) + j * kRowsPerLoad + lane / 8;
-        b_off[j] = (min(n0 + r, p.n - 1) - n0) * p.ldb * 4 + ((lane % 8) ^ swz(r)) * 16;
+        if (NN) {
+            // k-row wave * 4 + j of the stage, columns n0 + 4 l .. + 3
+            // (clamped below n; n % 4 == 0, so a lane's 4 are all valid)
+            const int kr = wave * (32 / NW) + j;
+            b_off[j] = (int64_t)kr * p.ldb * 4 + (min(n0 + 4 * lane, p.n - 4) - n0) * 4;
+        } else {
+            const int r = wave * (BN / NW) + j * kRowsPerLoad + lane / 8;
+            b_off[j] = (min(n0 + r, p.n - 1) - n0) * p.ldb * 4 + ((lane % 8) ^ swz(r)) * 16;
+        }
     }
+    // bytes between consecutive stages of B in global memory
+    const int64_t b_stage = NN ? (int64_t)32 * p.ldb * 4 : BKB;
     const int nk = (int)(p.k / 32);
 
-    auto issue = [&](int t, int slot) {
+    auto issue = [&](int t, int slot) __attribute__((always_inline)) {
         char *la = lds + slot * kStageBytes;
         char *lb = la + kABytes;
         const int64_t kb = (int64_t)t * BKB;
@@ -140,9 +160,11 @@ __global__ __launch_bounds__(NT, 1) void sgemm_big_kernel(BigParams p) {
             __builtin_amdgcn_global_load_lds((glb_ptr)(a_base + kb + a_off[j]),
                                              (lds_ptr)(la + (wave * (BM / NW) + j * kRowsPerLoad) * BKB), 16, 0, 0);
 #pragma unroll
-        for (int j = 0; j < kLB; ++j)
-            __builtin_amdgcn_global_load_lds((glb_ptr)(b_base + kb + b_off[j]),
-                                             (lds_ptr)(lb + (wave * (BN / NW) + j * kRowsPerLoad) * BKB), 16, 0, 0);
+        for (int j = 0; j < kLB; ++j) {
+            char *dst = NN ? lb + (wave * (32 / NW) + j) * kBRowNN * 4 : lb + (wave * (BN / NW) + j * kRowsPerLoad) * BKB;
+            __builtin_amdgcn_global_load_lds((glb_ptr)(b_base + (int64_t)t * b_stage + b_off[j]), (lds_ptr)dst, 16, 0,
+                                             0);
+        }
     };
 
     // Fragment of k-group kg: lane l reads row l % 32 of a 32-row block,
@@ -151,14 +173,22 @@ __global__ __launch_bounds__(NT, 1) void sgemm_big_kernel(BigParams p) {
     const int frow = lane & 31;
     const int foff0 = frow * BKB + (((lane >> 5) ^ swz(frow)) * 16);
     f32x4 af[2][FM], bf[2][FN];
-    auto load_frags = [&](int buf, int t, int kg) {
+    auto load_frags = [&](int buf, int t, int kg) __attribute__((always_inline)) {
         const char *la = lds + (t % STAGES) * kStageBytes;
         const char *lb = la + kABytes;
         const int fo = foff0 ^ (kg << 5);
 #pragma unroll
         for (int i = 0; i < FM; ++i) af[buf][i] = *reinterpret_cast<const f32x4 *>(la + (wm0 + i * 32) * BKB + fo);
+        if (NN) {
+            const float *fb = reinterpret_cast<const float *>(lb) + (8 * kg + 4 * (lane >> 5)) * kBRowNN + (lane & 31);
 #pragma unroll
-        for (int j = 0; j < FN; ++j) bf[buf][j] = *reinterpret_cast<const f32x4 *>(lb + (wn0 + j * 32) * BKB + fo);
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) bf[buf][j][e] = fb[e * kBRowNN + wn0 + j * 32];
+        } else {
+#pragma unroll
+            for (int j = 0; j < FN; ++j) bf[buf][j] = *reinterpret_cast<const f32x4 *>(lb + (wn0 + j * 32) * BKB + fo);
+        }
     };
 
     f32x16 acc[FM][FN];
@@ -169,7 +199,7 @@ __global__ __launch_bounds__(NT, 1) void sgemm_big_kernel(BigParams p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    auto mfmas = [&](int buf) {
+    auto mfmas = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
 #pragma unroll
@@ -179,12 +209,13 @@ __global__ __launch_bounds__(NT, 1) void sgemm_big_kernel(BigParams p) {
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[buf][i][e], bf[buf][j][e], acc[i][j], 0, 0, 0);
     };
 
-    constexpr int NR = FM + FN, NM = 4 * FM * FN;
+    constexpr int NR = FM + (NN ? 4 : 1) * FN, NM = 4 * FM * FN;
     for (int t = 0; t < STAGES; ++t) issue(min(t, nk - 1), t);
     wait_vmcnt<(STAGES - 1) * kLPS>();
     __builtin_amdgcn_s_barrier();
     load_frags(0, 0, 0);
-    auto k_groups = [&](int t) {
+    // (inlined: a call would pass the accumulators through scratch memory)
+    auto k_groups = [&](int t) __attribute__((always_inline)) {
 #pragma unroll
         for (int kg = 0; kg + 1 < kKGroups; ++kg) {
             load_frags((kg + 1) & 1, t, kg + 1);
@@ -267,8 +298,9 @@ __global__ __launch_bounds__(NT, 1) void sgemm_big_kernel(BigParams p) {
 }  // namespace
 
 bool sgemm_big_fits(const SgemmDesc &d) {
-    if (d.trans_a || !d.trans_b || d.batch > 1 || d.batch_a > 1 || d.batch_b > 1) return false;
+    if (d.trans_a || d.batch > 1 || d.batch_a > 1 || d.batch_b > 1) return false;
     if (d.k <= 0 || d.k % 32 != 0 || d.lda % 4 != 0 || d.ldb % 4 != 0) return false;
+    if (!d.trans_b && d.n % 4 != 0) return false;  // NN: whole 16-byte column groups
     if (!aligned16(d.a) || !aligned16(d.b)) return false;
     // 256 x 256 tiles must fill the GPU; 32-bit tile-relative offsets are
     // not needed (offsets are 64-bit), but rows must exist.
@@ -292,7 +324,11 @@ int launch_sgemm_big(const SgemmDesc &d, hipStream_t s) {
     p.beta = d.beta;
     p.tiles_m = (int)((d.m + BM - 1) / BM);
     p.tiles_n = (int)((d.n + BN - 1) / BN);
-    hipLaunchKernelGGL(sgemm_big_kernel, dim3((unsigned)(p.tiles_m * p.tiles_n)), dim3(NT), 0, s, p);
+    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n));
+    if (d.trans_b)
+        hipLaunchKernelGGL(sgemm_big_kernel<false>, grid, dim3(NT), 0, s, p);
+    else
+        hipLaunchKernelGGL(sgemm_big_kernel<true>, grid, dim3(NT), 0, s, p);
     return check_launch("sgemm (256x256 tiles)");
 }
 

@@ -168,10 +168,12 @@ def test_k_zero_gives_bias(torch_dev):
 
 
 @pytest.mark.parametrize("m,n,k", [(4096, 4096, 64), (4100, 4000, 96), (4352, 3900, 32)])
-def test_nt_big_tiles_integer_exact(torch_dev, m, n, k):
-    """NT (Linear's x . W^T) shapes that fill the GPU with 256 x 256 tiles
-    take the direct-to-LDS kernel: ragged m and n inside the last tiles,
-    alpha, beta and bias, on integer data (exact in any summation order)."""
+@pytest.mark.parametrize("tb", [True, False])
+def test_big_tiles_integer_exact(torch_dev, m, n, k, tb):
+    """NT (Linear's x . W^T) and NN (Tensor::matmul) shapes that fill the GPU
+    with 256 x 256 tiles take the direct-to-LDS kernel: ragged m and n
+    inside the last tiles, alpha, beta and bias, on integer data (exact in
+    any summation order)."""
     gh, O = _gh(), _oracle()
     rng = np.random.default_rng(m + n + k)
     a = rng.integers(-4, 5, size=(m, k)).astype(np.float32)
@@ -179,10 +181,23 @@ def test_nt_big_tiles_integer_exact(torch_dev, m, n, k):
     c0 = rng.integers(-4, 5, size=(m, n)).astype(np.float32)
     bias = rng.integers(-4, 5, size=(n,)).astype(np.float32)
     dc = to_dev(c0, torch_dev)
-    gh.sgemm(to_dev(a, torch_dev), to_dev(w, torch_dev), trans_b=True, alpha=2.0, beta=-1.0,
-             bias=to_dev(bias, torch_dev), out=dc)
+    b_dev = to_dev(w if tb else np.ascontiguousarray(w.T), torch_dev)
+    gh.sgemm(to_dev(a, torch_dev), b_dev, trans_b=tb, alpha=2.0, beta=-1.0, bias=to_dev(bias, torch_dev), out=dc)
     ref = (2.0 * O.linear_forward(a, w) - c0 + bias).astype(np.float32)
     np.testing.assert_array_equal(to_np(dc), ref)
+
+
+def test_big_tiles_nn_random(torch_dev):
+    """NN at 4096^3 on N(0,1) data (the sweep's shape) against the oracle on
+    sampled rows, within the GEMM bound."""
+    gh, O = _gh(), _oracle()
+    rng = np.random.default_rng(8)
+    a = rng.standard_normal((4096, 4096)).astype(np.float32)
+    b = rng.standard_normal((4096, 4096)).astype(np.float32)
+    got = to_np(gh.sgemm(to_dev(a, torch_dev), to_dev(b, torch_dev)))
+    rows = rng.choice(4096, size=48, replace=False)
+    ref = O.matmul(a[rows], b)
+    assert np.abs(got[rows] - ref).max() <= gemm_tol(4096, a, b)
 
 
 def test_nt_big_tiles_strided(torch_dev):
