@@ -42,29 +42,37 @@
 namespace gfh {
 namespace {
 
-constexpr int BM = 256, BN = 256;
 constexpr int BKB = 128;                 // K bytes per stage (32 floats)
 constexpr int NWM = 2, NWN = 4, NW = 8;  // wave grid
 constexpr int NT = 64 * NW;
-constexpr int WM = BM / NWM, WN = BN / NWN;  // 128 x 64 per wave
-constexpr int FM = WM / 32, FN = WN / 32;    // 4 x 2 accumulators
 constexpr int STAGES = 2;
-constexpr int kRowsPerLoad = 1024 / BKB;                  // rows per load instruction
-constexpr int kLA = BM * BKB / (1024 * NW), kLB = BN * BKB / (1024 * NW);  // load instructions per wave per stage
-constexpr int kLPS = kLA + kLB;
-constexpr int kABytes = BM * BKB;
-constexpr int kBRowNN = BN + 8;  // floats per B k-row in LDS (NN)
-template <bool NN>
-constexpr int b_bytes() { return NN ? 32 * kBRowNN * 4 : BN * BKB; }
-template <bool NN>
-constexpr int stage_bytes() { return kABytes + b_bytes<NN>(); }
-constexpr int kOutStride = WN + 8;  // floats per staged output row (two row groups on disjoint banks)
-constexpr int kOut = NW * (WM / 2) * kOutStride * 4;
-template <bool NN>
-constexpr int lds_bytes() { return STAGES * stage_bytes<NN>() > kOut ? STAGES * stage_bytes<NN>() : kOut; }
-static_assert(lds_bytes<false>() <= 160 * 1024 && lds_bytes<true>() <= 160 * 1024, "LDS per workgroup");
+constexpr int kRowsPerLoad = 1024 / BKB;  // K-contiguous rows per load instruction
 constexpr int kGroupM = 4;
 constexpr int kKGroups = BKB / 32;  // 8-float k-groups per stage
+
+// Geometry of a BM x BN tile (256 x 256 or 128 x 128).
+template <int BM, int BN, bool NN>
+struct Geo {
+    static constexpr int WM = BM / NWM, WN = BN / NWN;  // wave sub-tile
+    static constexpr int FM = WM / 32, FN = WN / 32;    // accumulators per wave
+    static constexpr int kLA = BM / 64, kLB = BN / 64;  // load instructions per wave per stage
+    static constexpr int kLPS = kLA + kLB;
+    static constexpr int kABytes = BM * BKB;
+    // NN: a load instruction fills RPL k-rows of BN floats (1 KB); groups
+    // of RPL rows sit 1024 + 32 RPL bytes apart, which puts rows 4 apart
+    // 32 banks apart.
+    static constexpr int RPL = 1024 / (BN * 4);
+    static constexpr int kGroupStride = 1024 + 32 * RPL;
+    static constexpr int kBBytes = NN ? (32 / RPL) * kGroupStride : BN * BKB;
+    static constexpr int kStageBytes = kABytes + kBBytes;
+    static constexpr int kOutStride = WN + 8;  // floats per staged output row
+    static constexpr int kOut = NW * (WM / 2) * kOutStride * 4;
+    static constexpr int kLds = STAGES * kStageBytes > kOut ? STAGES * kStageBytes : kOut;
+    static_assert(kLds <= 160 * 1024, "LDS per workgroup");
+    static_assert(FM >= 2 && FN >= 1, "wave sub-tile");
+    // byte offset of k-row r inside an NN B stage
+    static __device__ __forceinline__ int brow(int r) { return (r / RPL) * kGroupStride + (r % RPL) * BN * 4; }
+};
 
 typedef __attribute__((address_space(3))) void *lds_ptr;
 typedef __attribute__((address_space(1))) void *glb_ptr;
@@ -101,10 +109,13 @@ __device__ __forceinline__ void interleave() {
     }
 }
 
-template <bool NN>
-__global__ __launch_bounds__(NT, 1) void sgemm_big_kernel(BigParams p) {
-    constexpr int kStageBytes = stage_bytes<NN>();
-    __shared__ __attribute__((aligned(1024))) char lds[lds_bytes<NN>()];
+template <int BM, int BN, bool NN>
+__global__ __launch_bounds__(NT, (BM * BN <= 128 * 128) ? 2 : 1) void sgemm_big_kernel(BigParams p) {
+    using G = Geo<BM, BN, NN>;
+    constexpr int WM = G::WM, WN = G::WN, FM = G::FM, FN = G::FN;
+    constexpr int kLA = G::kLA, kLB = G::kLB, kLPS = G::kLPS;
+    constexpr int kABytes = G::kABytes, kStageBytes = G::kStageBytes, kOutStride = G::kOutStride;
+    __shared__ __attribute__((aligned(1024))) char lds[G::kLds];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -138,10 +149,12 @@ __global__ __launch_bounds__(NT, 1) void sgemm_big_kernel(BigParams p) {
 #pragma unroll
     for (int j = 0; j < kLB; ++j) {
         if (NN) {
-            // k-row wave * 4 + j of the stage, columns n0 + 4 l .. + 3
-            // (clamped below n; n % 4 == 0, so a lane's 4 are all valid)
-            const int kr = wave * (32 / NW) + j;
-            b_off[j] = (int64_t)kr * p.ldb * 4 + (min(n0 + 4 * lane, p.n - 4) - n0) * 4;
+            // row group wave * kLB + j: k-row RPL g + l / (64 / RPL), columns
+            // n0 + 4 (l % (64 / RPL)) .. + 3 (clamped below n; n % 4 == 0, so a
+            // lane's 4 are all valid)
+            constexpr int LPR = 64 / G::RPL;
+            const int kr = (wave * kLB + j) * G::RPL + lane / LPR;
+            b_off[j] = (int64_t)kr * p.ldb * 4 + (min(n0 + 4 * (lane % LPR), p.n - 4) - n0) * 4;
         } else {
             const int r = wave * (BN / NW) + j * kRowsPerLoad + lane / 8;
             b_off[j] = (min(n0 + r, p.n - 1) - n0) * p.ldb * 4 + ((lane % 8) ^ swz(r)) * 16;
@@ -161,7 +174,7 @@ __global__ __launch_bounds__(NT, 1) void sgemm_big_kernel(BigParams p) {
                                              (lds_ptr)(la + (wave * (BM / NW) + j * kRowsPerLoad) * BKB), 16, 0, 0);
 #pragma unroll
         for (int j = 0; j < kLB; ++j) {
-            char *dst = NN ? lb + (wave * (32 / NW) + j) * kBRowNN * 4 : lb + (wave * (BN / NW) + j * kRowsPerLoad) * BKB;
+            char *dst = NN ? lb + (wave * kLB + j) * G::kGroupStride : lb + (wave * (BN / NW) + j * kRowsPerLoad) * BKB;
             __builtin_amdgcn_global_load_lds((glb_ptr)(b_base + (int64_t)t * b_stage + b_off[j]), (lds_ptr)dst, 16, 0,
                                              0);
         }
@@ -180,11 +193,13 @@ __global__ __launch_bounds__(NT, 1) void sgemm_big_kernel(BigParams p) {
 #pragma unroll
         for (int i = 0; i < FM; ++i) af[buf][i] = *reinterpret_cast<const f32x4 *>(la + (wm0 + i * 32) * BKB + fo);
         if (NN) {
-            const float *fb = reinterpret_cast<const float *>(lb) + (8 * kg + 4 * (lane >> 5)) * kBRowNN + (lane & 31);
+            const int r0 = 8 * kg + 4 * (lane >> 5);
 #pragma unroll
-            for (int j = 0; j < FN; ++j)
+            for (int e = 0; e < 4; ++e) {
+                const float *fb = reinterpret_cast<const float *>(lb + G::brow(r0 + e)) + (lane & 31);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) bf[buf][j][e] = fb[e * kBRowNN + wn0 + j * 32];
+                for (int j = 0; j < FN; ++j) bf[buf][j][e] = fb[wn0 + j * 32];
+            }
         } else {
 #pragma unroll
             for (int j = 0; j < FN; ++j) bf[buf][j] = *reinterpret_cast<const f32x4 *>(lb + (wn0 + j * 32) * BKB + fo);
@@ -297,15 +312,18 @@ __global__ __launch_bounds__(NT, 1) void sgemm_big_kernel(BigParams p) {
 
 }  // namespace
 
+namespace {
+int64_t tiles_of(const SgemmDesc &d, int64_t t) { return ((d.m + t - 1) / t) * ((d.n + t - 1) / t); }
+}  // namespace
+
+// 256 x 256 tiles when there are at least 256 of them (one per CU), else
+// 128 x 128 tiles (two workgroups per CU fit) when those number 256.
 bool sgemm_big_fits(const SgemmDesc &d) {
     if (d.trans_a || d.batch > 1 || d.batch_a > 1 || d.batch_b > 1) return false;
     if (d.k <= 0 || d.k % 32 != 0 || d.lda % 4 != 0 || d.ldb % 4 != 0) return false;
     if (!d.trans_b && d.n % 4 != 0) return false;  // NN: whole 16-byte column groups
     if (!aligned16(d.a) || !aligned16(d.b)) return false;
-    // 256 x 256 tiles must fill the GPU; 32-bit tile-relative offsets are
-    // not needed (offsets are 64-bit), but rows must exist.
-    const int64_t tiles = ((d.m + BM - 1) / BM) * ((d.n + BN - 1) / BN);
-    return d.m >= BM && d.n >= BN && tiles >= 256;
+    return d.m >= 128 && d.n >= 128 && tiles_of(d, 128) >= 256;
 }
 
 int launch_sgemm_big(const SgemmDesc &d, hipStream_t s) {
@@ -322,14 +340,22 @@ int launch_sgemm_big(const SgemmDesc &d, hipStream_t s) {
     p.ldc = d.ldc;
     p.alpha = d.alpha;
     p.beta = d.beta;
-    p.tiles_m = (int)((d.m + BM - 1) / BM);
-    p.tiles_n = (int)((d.n + BN - 1) / BN);
+    const int t = (d.m >= 256 && d.n >= 256 && tiles_of(d, 256) >= 256) ? 256 : 128;
+    p.tiles_m = (int)((d.m + t - 1) / t);
+    p.tiles_n = (int)((d.n + t - 1) / t);
     const dim3 grid((unsigned)(p.tiles_m * p.tiles_n));
-    if (d.trans_b)
-        hipLaunchKernelGGL(sgemm_big_kernel<false>, grid, dim3(NT), 0, s, p);
-    else
-        hipLaunchKernelGGL(sgemm_big_kernel<true>, grid, dim3(NT), 0, s, p);
-    return check_launch("sgemm (256x256 tiles)");
+    if (t == 256) {
+        if (d.trans_b)
+            hipLaunchKernelGGL((sgemm_big_kernel<256, 256, false>), grid, dim3(NT), 0, s, p);
+        else
+            hipLaunchKernelGGL((sgemm_big_kernel<256, 256, true>), grid, dim3(NT), 0, s, p);
+    } else {
+        if (d.trans_b)
+            hipLaunchKernelGGL((sgemm_big_kernel<128, 128, false>), grid, dim3(NT), 0, s, p);
+        else
+            hipLaunchKernelGGL((sgemm_big_kernel<128, 128, true>), grid, dim3(NT), 0, s, p);
+    }
+    return check_launch("sgemm (direct-to-LDS tiles)");
 }
 
 }  // namespace gfh

@@ -167,13 +167,14 @@ def test_k_zero_gives_bias(torch_dev):
     assert to_np(out).tolist() == [list(range(6))] * 4
 
 
-@pytest.mark.parametrize("m,n,k", [(4096, 4096, 64), (4100, 4000, 96), (4352, 3900, 32)])
+@pytest.mark.parametrize("m,n,k", [(4096, 4096, 64), (4100, 4000, 96), (4352, 3900, 32), (2048, 2048, 64),
+                                   (2100, 2000, 96), (1024, 4096, 32)])
 @pytest.mark.parametrize("tb", [True, False])
 def test_big_tiles_integer_exact(torch_dev, m, n, k, tb):
     """NT (Linear's x . W^T) and NN (Tensor::matmul) shapes that fill the GPU
-    with 256 x 256 tiles take the direct-to-LDS kernel: ragged m and n
-    inside the last tiles, alpha, beta and bias, on integer data (exact in
-    any summation order)."""
+    take the direct-to-LDS kernel, on 256 x 256 tiles (the first three) or
+    128 x 128 tiles (the rest): ragged m and n inside the last tiles, alpha,
+    beta and bias, on integer data (exact in any summation order)."""
     gh, O = _gh(), _oracle()
     rng = np.random.default_rng(m + n + k)
     a = rng.integers(-4, 5, size=(m, k)).astype(np.float32)
@@ -187,17 +188,19 @@ def test_big_tiles_integer_exact(torch_dev, m, n, k, tb):
     np.testing.assert_array_equal(to_np(dc), ref)
 
 
-def test_big_tiles_nn_random(torch_dev):
-    """NN at 4096^3 on N(0,1) data (the sweep's shape) against the oracle on
-    sampled rows, within the GEMM bound."""
+@pytest.mark.parametrize("n", [2048, 4096])
+def test_big_tiles_nn_random(torch_dev, n):
+    """NN at n^3 on N(0,1) data (the sweep's shapes: 128 x 128 tiles at 2048,
+    256 x 256 at 4096) against the oracle on sampled rows, within the GEMM
+    bound."""
     gh, O = _gh(), _oracle()
     rng = np.random.default_rng(8)
-    a = rng.standard_normal((4096, 4096)).astype(np.float32)
-    b = rng.standard_normal((4096, 4096)).astype(np.float32)
+    a = rng.standard_normal((n, n)).astype(np.float32)
+    b = rng.standard_normal((n, n)).astype(np.float32)
     got = to_np(gh.sgemm(to_dev(a, torch_dev), to_dev(b, torch_dev)))
-    rows = rng.choice(4096, size=48, replace=False)
+    rows = rng.choice(n, size=48, replace=False)
     ref = O.matmul(a[rows], b)
-    assert np.abs(got[rows] - ref).max() <= gemm_tol(4096, a, b)
+    assert np.abs(got[rows] - ref).max() <= gemm_tol(n, a, b)
 
 
 def test_nt_big_tiles_strided(torch_dev):
