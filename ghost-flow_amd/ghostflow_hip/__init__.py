@@ -38,4 +38,11 @@ from .ops import (  # noqa: F401
     swiglu,
 )
 from .nn import KVCache, MultiHeadAttention, QuantizedSwiGLU, SwiGLU  # noqa: F401
+from .quantization import (  # noqa: F401
+    DynamicQuantization,
+    QuantizationAwareTraining,
+    QuantizationConfig,
+    QuantizationScheme,
+    QuantizedTensor,
+)
 from .synth import normal, uniform  # noqa: F401
