@@ -6,27 +6,36 @@
 // At these sizes the layer is HBM-bound up to m ~ 40 (every weight byte is
 // used m times) and no tile GEMM fills the GPU: a 64-row tile wastes most
 // of its MFMA rows and a grid of n / 64 workgroups cannot stream W.  So the
-// weight is streamed from HBM straight into v_mfma_f32_16x16x4_f32 operands,
-// as the skinny int8 linear does:
-//  * a workgroup owns NB blocks of 16 output columns (weight rows); lane l
-//    reads 16 bytes of row l % 16 of each block at float offset 4 * (l / 16)
-//    of each 16-float k-step, and the same bytes of x row l % 16 (+ 16 per
+// weight is streamed from HBM straight into v_mfma_f32_16x16x4_f32
+// operands:
+//  * a workgroup owns 64 weight rows (output columns) over one K-slice;
+//    wave w owns rows 16 w .. 16 w + 15 and computes all m rows of x for
+//    them, so no sums cross waves;
+//  * K advances in chunks of 64 elements (256 bytes of every row).  Lane l
+//    holds 16 bytes of weight row l % 16 at element 16 s + 4 (l / 16) of
+//    step s of the chunk, and the same elements of x row l % 16 (+ 16 per
 //    row block); element e of those vectors feeds MFMA e, so the four MFMAs
-//    of a step pair every (row, k) of x with the same k of W.  NB = 1: at
-//    [4096, 4096] two or four blocks per workgroup (x re-read half or a
-//    quarter as often) measured slower, 30.9 against 27.4 us at m = 16 and
-//    93 against 67 us at m = 64, as the grid shrinks by the same factor;
-//  * the 4 waves take contiguous quarters of the workgroup's k-steps and
-//    their accumulators are added in LDS in a fixed order;
-//  * with fewer than ~512 column blocks K is also split over workgroups:
-//    each publishes its partial tile with agent-scope stores and counts its
-//    arrival, and the last one adds the slices in slice order and runs the
-//    epilogue (alpha, + beta y, + bias: separate f32 roundings, as in the
-//    tile GEMM).
+//    of a step pair every (row, k) of x with the same k of W;
+//  * the chunk of x is staged once per workgroup and read by all four
+//    waves: a 3-stage LDS ring filled by global_load_lds_dwordx4 (1 KB per
+//    instruction: 4 rows x 256 bytes), 16-byte slots swizzled by row so the
+//    fragment reads are conflict-free.  Read per wave straight from L2 (as
+//    the weight is), x made every workgroup move m / 16 times the weight
+//    bytes again: a read-only probe of the weight stream at [4096, 4096]
+//    took 12.8 us alone and 18.2 us with the x reads of m = 16;
+//  * the weight chunks go to registers two chunks ahead of the MFMAs (three
+//    register sets), so 8 KB per wave stay in flight while it computes (at
+//    [4096, 4096], m = 8-64: three or four chunks ahead were 1-2 us slower);
+//  * with fewer than ~512 workgroups K is also split over workgroups: each
+//    wave publishes its partial block with agent-scope stores and counts
+//    its arrival on its 16-column block, and the last one adds the slices
+//    in slice order and runs the epilogue (alpha, + beta y, + bias:
+//    separate f32 roundings, as in the tile GEMM).
 // The sums are regrouped against the reference's sequential k order, so the
 // result is within the fp32 GEMM bound (bit-exact when every partial sum is
 // exact, e.g. on small-integer inputs).
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -36,7 +45,13 @@
 namespace gfh {
 namespace {
 
+typedef __attribute__((address_space(3))) void *lds_ptr;
+typedef __attribute__((address_space(1))) void *glb_ptr;
+
 constexpr int kWaves = 4;
+constexpr int kGroupCols = 16 * kWaves;  // weight rows per workgroup
+constexpr int kKC = 64;                  // k elements per chunk
+constexpr int kRowBytes = kKC * 4;       // bytes of one row per chunk
 
 struct SkNtParams {
     const float *x;  // [batch_a][m][lda]
@@ -48,20 +63,30 @@ struct SkNtParams {
     int64_t batch_a, batch_b;
     int64_t m, n, k;
     float alpha, beta;
-    int64_t nblk, kslice, slices;
+    int64_t ngrp, kslice, slices;
     float *part;    // [slices][m][n] partial sums (slices > 1, batch 1)
-    int *counters;  // one per column block, zero at rest (slices > 1)
+    int *counters;  // one per 16-column block, zero at rest (slices > 1)
 };
 
-// MB: 16-row blocks of x (m <= 16 MB); NB: 16-column blocks per workgroup.
-template <int MB, int NB>
-__global__ __launch_bounds__(64 * kWaves) void gemm_nt_skinny_kernel(SkNtParams p) {
-    constexpr int kU = MB * NB > 2 ? 4 : 8;  // k-steps in flight per lane
-    __shared__ f32x4 red[kWaves - 1][MB * NB][64];
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// MB: 16-row blocks of x (m <= 16 MB); D: chunks in flight ahead of the
+// MFMAs (D + 1 ring stages and register sets).
+template <int MB, int D>
+__global__ __launch_bounds__(64 * kWaves, 2) void gemm_nt_skinny_kernel(SkNtParams p) {
+    constexpr int kXRows = 16 * MB;
+    constexpr int kStageBytes = kXRows * kRowBytes;
+    constexpr int kStages = D + 1;
+    constexpr int kOps = MB + 4;  // vector memory instructions per chunk and wave
+    __shared__ __attribute__((aligned(1024))) char xs[kStages * kStageBytes];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t blk = blockIdx.x % p.nblk, slice = blockIdx.x / p.nblk;
-    const int64_t n0 = blk * 16 * NB;
+    const int64_t grp = blockIdx.x % p.ngrp, slice = blockIdx.x / p.ngrp;
+    const int64_t n0 = grp * kGroupCols + 16 * wave;  // this wave's first weight row
     // batch slice blockIdx.y with the reference's modulo indexing
     // (matmul.rs:147-149)
     const uint32_t z = blockIdx.y;
@@ -70,114 +95,177 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_nt_skinny_kernel(SkNtParams 
     float *yb = p.y + (int64_t)z * p.stride_c;
 
     const int64_t k_lo = slice * p.kslice;
-    const int kl = (int)min(p.kslice, p.k - k_lo);  // a multiple of 4
-    const int nsteps = (kl + 15) / 16;
-    const int per = (nsteps + kWaves - 1) / kWaves;
-    const int st0 = min(wave * per, nsteps), st1 = min(st0 + per, nsteps);
+    const int kl = (int)min(p.kslice, p.k - k_lo);  // > 0, a multiple of 4
+    const int nch = (kl + kKC - 1) / kKC;
 
-    // Rows past n read row n - 1 and rows past m read row m - 1: their sums
-    // are never stored, and the loads need no condition.
-    const int kq = 4 * (lane >> 4);
-    const float *wsrc[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) wsrc[nb] = wb + min(n0 + nb * 16 + (lane & 15), p.n - 1) * p.ldb + k_lo + kq;
+    // x: instruction j of wave w fills stage rows 4 (w MB + j) .. + 3; lane l
+    // fills slot l % 16 of row l / 16 of them from logical 16-byte chunk
+    // (l % 16) ^ (row % 16).  Rows past m read row m - 1 (never stored);
+    // elements past the slice read its last four (masked in the tail).
     const float *xsrc[MB];
+    int xcol[MB];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) xsrc[mb] = xb + min<int64_t>(mb * 16 + (lane & 15), p.m - 1) * p.lda + k_lo + kq;
+    for (int j = 0; j < MB; ++j) {
+        const int r = 4 * (wave * MB + j) + (lane >> 4);
+        xsrc[j] = xb + min<int64_t>(r, p.m - 1) * p.lda + k_lo;
+        xcol[j] = 4 * ((lane & 15) ^ (r & 15));
+    }
+    auto issue_x = [&](int i, int slot) __attribute__((always_inline)) {
+        char *stage = xs + slot * kStageBytes;
+#pragma unroll
+        for (int j = 0; j < MB; ++j)
+            __builtin_amdgcn_global_load_lds((glb_ptr)(xsrc[j] + min(i * kKC + xcol[j], kl - 4)),
+                                             (lds_ptr)(stage + 4 * (wave * MB + j) * kRowBytes), 16, 0, 0);
+    };
+    // W: rows past n read row n - 1 (never stored).
+    const float *wsrc = wb + min<int64_t>(n0 + (lane & 15), p.n - 1) * p.ldb + k_lo;
+    const int kq = 4 * (lane >> 4);
+    auto load_w = [&](int i, f32x4(&R)[4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+            R[s] = *reinterpret_cast<const f32x4 *>(wsrc + min(i * kKC + 16 * s + kq, kl - 4));
+    };
 
-    f32x4 acc[MB][NB];
+    f32x4 acc[MB];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // Fragment of x block mb, step s: row 16 mb + l % 16, logical chunk
+    // 4 s + l / 16 (block rows start at multiples of 16, so the swizzle is
+    // the lane's own l % 16).
+    const int xrd = (lane & 15) * kRowBytes;
+    auto compute = [&](int i, f32x4(&R)[4], auto tail) __attribute__((always_inline)) {
+        const char *stage = xs + (i % kStages) * kStageBytes;
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int s0 = st0; s0 < st1; s0 += kU) {
-        f32x4 wv[kU][NB], xv[kU][MB];
-#pragma unroll
-        for (int u = 0; u < kU; ++u) {
-            // k % 4 == 0: a lane's 4 floats are all inside the slice or all
-            // past it; past it both operands are zero (a zero x alone would
-            // turn an inf weight into NaN).
-            const int off = (s0 + u) * 16;
-            const bool ok = s0 + u < st1 && off + kq < kl;
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
-                wv[u][nb] = ok ? *reinterpret_cast<const f32x4 *>(wsrc[nb] + off) : f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < 4; ++s) {
+            f32x4 xv[MB];
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb)
-                xv[u][mb] = ok ? *reinterpret_cast<const f32x4 *>(xsrc[mb] + off) : f32x4{0.f, 0.f, 0.f, 0.f};
-        }
+                xv[mb] = *reinterpret_cast<const f32x4 *>(stage + mb * 16 * kRowBytes + xrd +
+                                                          (((4 * s + (lane >> 4)) ^ (lane & 15)) << 4));
+            f32x4 wv = R[s];
+            if constexpr (decltype(tail)::value) {
+                // k % 4 == 0: a lane's 4 elements are all inside the slice or
+                // all past it; past it both operands are zero (a zero x alone
+                // would turn an inf weight into NaN).
+                const bool ok = i * kKC + 16 * s + kq < kl;
 #pragma unroll
-        for (int u = 0; u < kU; ++u)
+                for (int e = 0; e < 4; ++e) {
+                    wv[e] = ok ? wv[e] : 0.f;
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb) xv[mb][e] = ok ? xv[mb][e] : 0.f;
+                }
+            }
 #pragma unroll
             for (int e = 0; e < 4; ++e)
 #pragma unroll
-                for (int mb = 0; mb < MB; ++mb) {
-                    const float xe = xv[u][mb][e];
-#pragma unroll
-                    for (int nb = 0; nb < NB; ++nb) {
-                        const float we = wv[u][nb][e];
-                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xe, we, acc[mb][nb], 0, 0, 0);
-                    }
-                }
-    }
+                for (int mb = 0; mb < MB; ++mb)
+                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(xv[mb][e], wv[e], acc[mb], 0, 0, 0);
+        }
+    };
 
-    // The four waves' partial sums, added in wave order in wave 0.
-    if (wave > 0) {
+    // Chunk i: wait for its x and W (the next D - 1 chunks' loads stay in
+    // flight), barrier (its x is visible, and every wave is done with chunk
+    // i - 1, whose ring stage and register set now refill), issue chunk
+    // i + D, compute chunk i.  The issue is unconditional -- past the last
+    // chunk it repeats the last one (an L2 hit) into the free stage and set
+    // -- so every chunk issues the same kOps instructions per wave, in the
+    // same order, and the register sets rotate without copies.  The
+    // compiler drops the register loads of repeats that no MFMA reads, so
+    // the last D - 1 chunks count only what is left behind their x: their
+    // own W, the x of the D - 1 chunks issued after them and the W of those
+    // that exist (a load the compiler keeps only makes the wait longer).
+    const bool ragged = (kl % kKC) != 0;
+    auto wait_chunk = [&](int i) __attribute__((always_inline)) {
+        static_assert(D >= 1 && D <= 4, "the tail waits below cover D <= 4");
+        const int rem = nch - 1 - i;  // chunks after chunk i
+        constexpr int kBase = 4 + (D - 1) * MB;
+        if (rem >= D - 1)
+            wait_vmcnt<(D - 1) * kOps>();
+        else if (rem == 0)
+            wait_vmcnt<kBase>();
+        else if (rem == 1)
+            wait_vmcnt<kBase + 4>();
+        else
+            wait_vmcnt<kBase + 8>();
+    };
+    auto step = [&](int i, f32x4(&Rc)[4], f32x4(&Rn)[4]) __attribute__((always_inline)) {
+        wait_chunk(i);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        const int nx = min(i + D, nch - 1);
+        issue_x(nx, (i + D) % kStages);
+        // x before W: the instructions after a chunk's x then always include
+        // its own W and the next chunks' x.
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(nx, Rn);
+        __builtin_amdgcn_sched_barrier(0);
+        if (ragged && i + 1 == nch)
+            compute(i, Rc, std::true_type{});
+        else
+            compute(i, Rc, std::false_type{});
+    };
+    f32x4 R[kStages][4];
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) red[wave - 1][mb * NB + nb][lane] = acc[mb][nb];
+    for (int c = 0; c < D; ++c) {
+        issue_x(min(c, nch - 1), c);
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(min(c, nch - 1), R[c]);
+        __builtin_amdgcn_sched_barrier(0);
     }
-    __syncthreads();
-    if (wave > 0) return;
+    // Whole rounds of kStages chunks in a loop without exits (an exit
+    // between steps gives the compiler a path on which a register set is
+    // still being loaded at the loop head, and it then waits for every load
+    // there), then the chunks left, in the same rotation.
+    int i = 0;
+    for (; i + kStages <= nch; i += kStages) {
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+        for (int u = 0; u < kStages; ++u) step(i + u, R[u], R[(u + D) % kStages]);
+    }
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-            for (int w2 = 0; w2 < kWaves - 1; ++w2) acc[mb][nb] = acc[mb][nb] + red[w2][mb * NB + nb][lane];
+    for (int u = 0; u + 1 < kStages; ++u)
+        if (i + u < nch) step(i + u, R[u], R[(u + D) % kStages]);
+    wait_vmcnt<0>();  // no load may still be writing the ring
+    if (n0 >= p.n) return;  // a wave past the last column (after every barrier)
 
-    // 16x16 accumulator layout: lane l, register r -> row 4 * (l / 16) + r,
-    // column l % 16 of the block.
-    auto col_of = [&](int nb) -> int64_t { return n0 + nb * 16 + (lane & 15); };
+    // 16x16 accumulator layout: lane l, register r -> row 4 (l / 16) + r of
+    // the block, column l % 16.
+    const int64_t col = n0 + (lane & 15);
     auto row_of = [&](int mb, int r) -> int64_t { return (int64_t)mb * 16 + 4 * (lane >> 4) + r; };
-    auto epilogue = [&](int64_t row, int64_t col, float sum) {
+    auto epilogue = [&](int64_t row, float sum) {
         float *dst = yb + row * p.ldc + col;
         float v = p.alpha * sum;
         if (p.beta != 0.f) v = v + p.beta * *dst;
         if (p.bias) v = v + p.bias[col];
         *dst = v;
     };
+    const bool col_ok = col < p.n;
 
     if (p.slices == 1) {
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-            for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int64_t row = row_of(mb, r), col = col_of(nb);
-                    if (row < p.m && col < p.n) epilogue(row, col, acc[mb][nb][r]);
-                }
-        return;
-    }
-
-    // Publish the partial tile with agent-scope stores (they reach the
-    // device coherence point, so no cache writeback is needed), wait for
-    // them, then count this workgroup's arrival.
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int64_t row = row_of(mb, r), col = col_of(nb);
-                if (row < p.m && col < p.n)
-                    __hip_atomic_store(p.part + (slice * p.m + row) * p.n + col, acc[mb][nb][r], __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+                const int64_t row = row_of(mb, r);
+                if (row < p.m && col_ok) epilogue(row, acc[mb][r]);
             }
+        return;
+    }
+
+    // Publish the partial block with agent-scope stores (they reach the
+    // device coherence point, so no cache writeback is needed), wait for
+    // them, then count this wave's arrival on its column block.
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t row = row_of(mb, r);
+            if (row < p.m && col_ok)
+                __hip_atomic_store(p.part + (slice * p.m + row) * p.n + col, acc[mb][r], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    wait_vmcnt<0>();
+    const int64_t blk = n0 / 16;
     int last = 0;
     if (lane == 0)
         last = __hip_atomic_fetch_add(p.counters + blk, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
@@ -185,32 +273,66 @@ __global__ __launch_bounds__(64 * kWaves) void gemm_nt_skinny_kernel(SkNtParams 
     last = __shfl(last, 0);
     if (!last) return;
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    // The lane requests the partials of all its outputs for kGroup slices
+    // at a time before adding any of them, so the loads overlap instead of
+    // paying one memory latency per output and slice; each output is still
+    // summed in slice order.
+    constexpr int kGroup = 32 / (4 * MB) > 0 ? 32 / (4 * MB) : 1;
+    const float *src[MB][4];
+    float sum[MB][4];
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
+    for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
+        for (int r = 0; r < 4; ++r) {
+            const int64_t row = row_of(mb, r);
+            src[mb][r] = (row < p.m && col_ok) ? p.part + row * p.n + col : nullptr;
+            sum[mb][r] = 0.f;
+        }
+    for (int64_t j0 = 0; j0 < p.slices; j0 += kGroup) {
+        float pv[kGroup][MB][4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t row = row_of(mb, r), col = col_of(nb);
-                if (row >= p.m || col >= p.n) continue;
-                const float *src = p.part + row * p.n + col;
-                float sum = 0.f;
-                for (int64_t j = 0; j < p.slices; ++j)
-                    sum = sum + __hip_atomic_load(src + j * p.m * p.n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                epilogue(row, col, sum);
-            }
+        for (int g = 0; g < kGroup; ++g)
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    pv[g][mb][r] = (src[mb][r] && j0 + g < p.slices)
+                                       ? __hip_atomic_load(src[mb][r] + (j0 + g) * p.m * p.n, __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT)
+                                       : 0.f;
+#pragma unroll
+        for (int g = 0; g < kGroup; ++g)
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (j0 + g < p.slices) sum[mb][r] = (j0 + g == 0) ? pv[g][mb][r] : sum[mb][r] + pv[g][mb][r];
+    }
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (src[mb][r]) epilogue(row_of(mb, r), sum[mb][r]);
     if (lane == 0) __hip_atomic_store(p.counters + blk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// K elements per workgroup: all of K with at least ~512 column blocks (or a
-// batched call), otherwise enough slices for ~512 workgroups, each at least
-// 1024 elements, a multiple of 16.
-int64_t choose_kslice(int64_t nblk, int64_t k, int64_t batch) {
-    if (batch > 1) return k;
-    int64_t s = (512 + nblk - 1) / nblk;
-    s = std::max<int64_t>(1, std::min<int64_t>(s, k / 1024));
+// K elements per workgroup: all of K with at least ~kTargetWgs workgroups
+// (or a batched call), otherwise enough slices for about that many, each at
+// least 4 chunks, a multiple of the chunk.  At [4096, 4096] (64 column
+// groups): 8 slices took 18.8 / 18.7 / 22.2 / 34.3 us at m = 8 / 16 / 32 /
+// 64, against 20.4-22.9 / 21.8-25.4 / 29-34 us with 4 and 21.3 / 27.2 /
+// 41.7 us (m = 8 / 32 / 64) with 16.  Of the 18.7 us at m = 16, about 2.7
+// us are the split-K tail (partial stores, arrival count, the last
+// arriver's reads: three memory round trips) and 1 us the x staging.
+constexpr int64_t kTargetWgs = 512;
+constexpr int kDepth = 2;
+int64_t choose_kslice(int64_t ngrp, int64_t k, int64_t batch) {
+    const int64_t kc = ((k + kKC - 1) / kKC) * kKC;
+    if (batch > 1) return kc;
+    int64_t s = (kTargetWgs + ngrp - 1) / ngrp;
+    s = std::max<int64_t>(1, std::min<int64_t>(s, k / (4 * kKC)));
     const int64_t ks = (k + s - 1) / s;
-    return (ks + 15) & ~(int64_t)15;
+    return (ks + kKC - 1) / kKC * kKC;
 }
 
 }  // namespace
@@ -241,25 +363,24 @@ int launch_gemm_nt_skinny(const SgemmDesc &d, hipStream_t s) {
     p.alpha = d.alpha;
     p.beta = d.beta;
     const int64_t batch = std::max<int64_t>(d.batch, 1);
-    constexpr int NB = 1;
-    p.nblk = (d.n + 16 * NB - 1) / (16 * NB);
-    p.kslice = choose_kslice(p.nblk, d.k, batch);
+    p.ngrp = (d.n + kGroupCols - 1) / kGroupCols;
+    p.kslice = choose_kslice(p.ngrp, d.k, batch);
     p.slices = (d.k + p.kslice - 1) / p.kslice;
     if (p.slices > 1) {
         void *ws = nullptr;
         GFH_TRY(stream_workspace(s, sizeof(float) * (size_t)(p.slices * d.m * d.n), &ws));
         p.part = static_cast<float *>(ws);
-        GFH_TRY(stream_counters(s, (size_t)p.nblk, &p.counters));
+        GFH_TRY(stream_counters(s, (size_t)(p.ngrp * kWaves), &p.counters));
     }
-    const dim3 grid((unsigned)(p.nblk * p.slices), (unsigned)batch), block(64 * kWaves);
+    const dim3 grid((unsigned)(p.ngrp * p.slices), (unsigned)batch), block(64 * kWaves);
     if (d.m <= 16)
-        hipLaunchKernelGGL((gemm_nt_skinny_kernel<1, NB>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((gemm_nt_skinny_kernel<1, kDepth>), grid, block, 0, s, p);
     else if (d.m <= 32)
-        hipLaunchKernelGGL((gemm_nt_skinny_kernel<2, NB>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((gemm_nt_skinny_kernel<2, kDepth>), grid, block, 0, s, p);
     else if (d.m <= 48)
-        hipLaunchKernelGGL((gemm_nt_skinny_kernel<3, NB>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((gemm_nt_skinny_kernel<3, kDepth>), grid, block, 0, s, p);
     else
-        hipLaunchKernelGGL((gemm_nt_skinny_kernel<4, NB>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((gemm_nt_skinny_kernel<4, kDepth>), grid, block, 0, s, p);
     return check_launch("sgemm (NT skinny MFMA)");
 }
 
