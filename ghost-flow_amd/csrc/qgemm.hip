@@ -294,10 +294,13 @@ struct Tile {
     // The same before the first stage, after the prologue's requests.
     static constexpr int kWaitFirst = (SB - 1) * (kLA + kLB) + (SA - SB) * kLA;
     // Output staging: each wave converts half of its sub-tile (kWM/2 rows x
-    // kWN columns) at a time; row stride kWN + 8 floats keeps the two row
-    // groups of one ds_write_b32 on disjoint banks.
+    // kWN columns) at a time -- all of it when it is a single 32-row block;
+    // row stride kWN + 8 floats keeps the two row groups of one ds_write_b32
+    // on disjoint banks.
+    static constexpr int kOutPasses = kFM >= 2 ? 2 : 1;
+    static constexpr int kOutRows = kWM / kOutPasses;
     static constexpr int kOutStride = kWN + 8;
-    static constexpr int kOut = kNW * (kWM / 2) * kOutStride * 4;
+    static constexpr int kOut = kNW * kOutRows * kOutStride * 4;
     static constexpr int kLds = kRing > kOut ? kRing : kOut;
     static_assert(kLds <= 160 * 1024, "LDS per workgroup");
 };
@@ -556,26 +559,29 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
         return;
     }
 
-    // Output tile through LDS: each wave converts half of its sub-tile at a
-    // time into its own region, then writes whole row runs (WN floats) with
-    // 16-byte stores.
-    constexpr int LPR = WN / 4;       // lanes per output row
-    constexpr int RPI = 64 / LPR;     // rows per read instruction
-    constexpr int HALF = WM / 2;      // rows per half
+    // Output tile through LDS: each wave converts half of its sub-tile (all
+    // of a single 32-row block) at a time into its own region, then writes
+    // whole row runs (WN floats) with 16-byte stores.
+    constexpr int LPR = WN / 4;                // lanes per output row
+    constexpr int RPI = 64 / LPR;              // rows per read instruction
+    constexpr int PASSES = T::kOutPasses;
+    constexpr int HALF = T::kOutRows;          // rows per pass
+    constexpr int BPP = FM / PASSES;           // 32-row blocks per pass
+    static_assert(BPP * PASSES == FM && BPP * 32 == HALF, "output passes cover the sub-tile");
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();  // every wave is done with the operand ring
     float *lt = reinterpret_cast<float *>(lds) + wave * (HALF * T::kOutStride);
     const bool vec_out = (p.n % 4) == 0;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < PASSES; ++h) {
 #pragma unroll
-        for (int ii = 0; ii < FM / 2; ++ii)
+        for (int ii = 0; ii < BPP; ++ii)
 #pragma unroll
             for (int j = 0; j < FN; ++j)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     int32_t a;
-                    const float v = finish(h * (FM / 2) + ii, j, r, a);
+                    const float v = finish(h * BPP + ii, j, r, a);
                     const int lr = ii * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                     lt[lr * T::kOutStride + j * 32 + (lane & 31)] = v;
                 }
@@ -913,10 +919,21 @@ int launch_qlinear_i8(const QLinearDesc &d, hipStream_t s) {
         if (d.m > 512)
             return bk128 ? big::launch_tiles<256, 256, 128, 3, 2, 2, 4>(p, s)
                          : big::launch_tiles<256, 256, 64, 4, 4, 2, 4>(p, s);
-        const int64_t tiles = ((d.m + 127) / 128) * ((d.n + 127) / 128);
         if (!bk128) return big::launch_tiles<128, 128, 64, 4, 4, 2, 4>(p, s);
-        return tiles <= 256 ? big::launch_tiles<128, 128, 128, 3, 3, 2, 4>(p, s)
-                            : big::launch_tiles<128, 128, 128, 2, 2, 2, 4>(p, s);
+        // 64 < M <= 512: the largest tile that still gives about 160
+        // workgroups (128 x 128, then 64 x 128, else 64 x 64 with 4 waves and
+        // a 4-deep ring, two or three workgroups per CU).  Measured (us,
+        // 128 x 128 / 64 x 128 / 64 x 64): M = 256, N = 4096, K = 11008 53.3 /
+        // 40.1 / 27.9; M = 512, N = 4096, K = 4096 19.4 / 11.6 / 13.9; M =
+        // 256, N = 4096, K = 4096 17.2 / 10.4 / 8.2; M = 256, N = 11008, K =
+        // 4096 26.0 / 31.7 / 29.8; M = 128, N = 11008 24.0 / 19.1 / 21.8.
+        auto tiles = [&](int64_t bm, int64_t bn) { return ((d.m + bm - 1) / bm) * ((d.n + bn - 1) / bn); };
+        constexpr int64_t kFill = 160;
+        if (tiles(128, 128) >= kFill)
+            return tiles(128, 128) <= 256 ? big::launch_tiles<128, 128, 128, 3, 3, 2, 4>(p, s)
+                                          : big::launch_tiles<128, 128, 128, 2, 2, 2, 4>(p, s);
+        if (tiles(64, 128) >= kFill) return big::launch_tiles<64, 128, 128, 4, 4, 2, 2>(p, s);
+        return big::launch_tiles<64, 64, 128, 4, 4, 2, 2>(p, s);
     }
     p.tiles_m = (int)((d.m + kBM - 1) / kBM);
     p.tiles_n = (int)((d.n + kBN - 1) / kBN);
@@ -976,7 +993,9 @@ int launch_qlinear_swiglu_i8(const QSwigluDesc &d, int *npart, hipStream_t s) {
     if (g.m > 512)
         return bk128 ? big::launch_tiles_dual<256, 256, 128, 3, 2, 2, 4>(p, s, npart)
                      : big::launch_tiles_dual<256, 256, 64, 4, 4, 2, 4>(p, s, npart);
-    return bk128 ? big::launch_tiles_dual<128, 128, 128, 3, 3, 4, 2>(p, s, npart)
+    // (a 4-deep ring: M = 128 / 256 / 512 at N = 11008, K = 4096 28.6 / 51.4
+    // / 80.1 us against 29.2 / 54.1 / 85.2 with 3; 64-row tiles were slower)
+    return bk128 ? big::launch_tiles_dual<128, 128, 128, 4, 4, 4, 2>(p, s, npart)
                  : big::launch_tiles_dual<128, 128, 64, 4, 4, 4, 2>(p, s, npart);
 }
 

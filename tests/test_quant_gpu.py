@@ -251,6 +251,35 @@ def test_qlinear_large_tile_y_only(torch_dev, x_per_row):
     assert _same_f32(to_np(y), ry)
 
 
+@pytest.mark.parametrize("m,n,k", [(130, 257, 384), (192, 1100, 2048), (300, 4100, 1024), (500, 5000, 512)])
+@pytest.mark.parametrize("x_per_row,with_zp", [(False, True), (True, False), (True, True)])
+def test_qlinear_mid_m_tiles_bit_exact(torch_dev, m, n, k, x_per_row, with_zp):
+    """64 < M <= 512 with K % 128 == 0 takes the largest tile that still
+    gives ~160 workgroups: 64 x 64 (the first two shapes), 64 x 128 and
+    128 x 128 -- ragged M and N on each, every activation-scale variant,
+    int32 accumulators and fp32 outputs bit-exact to the oracle, through
+    both the accumulator variant and the output-only one (whose LDS-staged
+    stores take a single 32-row block per wave on the 64-row tiles)."""
+    _qlinear_case(torch_dev, m, n, k, x_per_row, with_zp, with_bias=(n % 2 == 1))
+    gh, O = _gh(), _O()
+    x = gh.normal((m, k), seed=m, tensor_id=3)
+    w = gh.normal((n, k), 0.0, 0.02, seed=m, tensor_id=4)
+    bias = gh.uniform((n,), -0.1, 0.1, seed=m, tensor_id=5)
+    qw, sw, _ = O.quantize_per_channel(w, True)
+    if x_per_row:
+        qx, sx, zx = O.quantize_per_channel(x, not with_zp)
+    else:
+        qx, sx, zx = O.quantize_per_tensor(x, not with_zp)
+    sx, zx = np.atleast_1d(sx), np.atleast_1d(zx)
+    zx_arg = zx if with_zp else None
+    ry, _ = O.qlinear_i8(qx, sx, zx_arg, x_per_row, qw, sw, bias, want_acc=False)
+    d = lambda a: None if a is None else to_dev(a, torch_dev)  # noqa: E731
+    y, acc = gh.qlinear(d(qx), d(sx), d(zx_arg), d(qw), d(sw), x_per_row=x_per_row, bias=d(bias),
+                        want_acc=False)
+    assert acc is None
+    assert _same_f32(to_np(y), ry)
+
+
 @pytest.mark.parametrize("m,n,k", [(1, 1000, 4096), (7, 130, 1088), (16, 520, 2048), (17, 300, 4096),
                                    (33, 1000, 2048), (64, 130, 1088)])
 @pytest.mark.parametrize("x_per_row,with_zp", [(False, True), (True, False), (True, True)])
