@@ -21,6 +21,7 @@
 // stage t+1 issued before the MFMAs of stage t, one barrier per stage, and
 // the same XCD-contiguous / GROUP_M tile order as the fp32 GEMM.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -887,6 +888,379 @@ int launch(const QParams &p, hipStream_t s, int *npart = nullptr) {
 
 }  // namespace skinny
 
+// ---- skinny M, x shared through LDS (5 <= M <= 64) ------------------------------
+//
+// From 5 rows on, reading x per wave straight from L2 (as qlinear_skinny_kernel
+// does) moves m / 16 times the weight bytes again.  Here a workgroup owns 64
+// output columns -- wave w the 16 columns n0 + 16 w .. + 15, all m rows of x,
+// over the workgroup's K-slice, so no sums cross waves -- and the slice's x
+// goes through a 3-stage LDS ring shared by the four waves:
+//  * K advances in 256-byte chunks.  Lane l holds 16 bytes of weight row
+//    l % 16 at byte 64 s + 16 (l / 16) of step s of the chunk and the same
+//    bytes of x row l % 16 (+ 16 per row block): the operand layout of
+//    v_mfma_i32_16x16x64_i8;
+//  * x: global_load_lds_dwordx4 fills 4 rows x 256 bytes per instruction,
+//    16-byte slots swizzled by row (conflict-free fragment reads); the
+//    weight chunks (both matrices in DUAL mode) go to registers two chunks
+//    ahead of the MFMAs in three rotating register sets;
+//  * with fewer than ~512 workgroups K is also split over workgroups; each
+//    wave publishes its exact int32 partials, counts its arrival on its
+//    16-column block, and the last one adds the slices (exact in any order)
+//    and runs the dequantizing epilogue.
+// The layout, ring and wait accounting are those of the fp32 skinny NT GEMM
+// (gemm_nt_skinny.hip) on int8 operands.
+namespace skinny_lds {
+
+typedef __attribute__((address_space(3))) void *lds_ptr;
+typedef __attribute__((address_space(1))) void *glb_ptr;
+
+constexpr int kWaves = 4;
+constexpr int kGroupCols = 16 * kWaves;  // output columns per workgroup
+constexpr int kChunk = 256;              // k bytes per chunk
+constexpr int kStages = 3;               // x ring (two chunks in flight)
+
+struct Params {
+    QParams q;
+    int64_t ngrp, kslice, slices;
+    int32_t *part;  // [slices][D][m][n] partial accumulators (slices > 1)
+    int *counters;  // one per 16-column block, zero at rest (slices > 1)
+};
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
+template <int MB, bool DUAL>
+__global__ __launch_bounds__(64 * kWaves, 2) void qlinear_skinny_lds_kernel(Params sp) {
+    constexpr int D = DUAL ? 2 : 1;
+    constexpr int kStageBytes = 16 * MB * kChunk;
+    constexpr int kOps = MB + 4 * D;  // vector memory instructions per chunk and wave
+    __shared__ __attribute__((aligned(1024))) int8_t xs[kStages * kStageBytes];
+    const QParams &p = sp.q;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t grp = blockIdx.x % sp.ngrp, slice = blockIdx.x / sp.ngrp;
+    const int64_t n0 = grp * kGroupCols + 16 * wave;
+    const int64_t k_lo = slice * sp.kslice;
+    const int kl = (int)min(sp.kslice, p.k - k_lo);  // > 0, a multiple of 16
+    const int nch = (kl + kChunk - 1) / kChunk;
+
+    // x: instruction j of wave w fills stage rows 4 (w MB + j) .. + 3; lane l
+    // fills slot l % 16 of row l / 16 of them from logical 16-byte chunk
+    // (l % 16) ^ (row % 16).  Rows past m read row m - 1 (never stored);
+    // bytes past the slice read its last 16 (masked in the tail).
+    const int8_t *xsrc[MB];
+    int xcol[MB];
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+        const int r = 4 * (wave * MB + j) + (lane >> 4);
+        xsrc[j] = p.qx + min<int64_t>(r, p.m - 1) * p.k + k_lo;
+        xcol[j] = 16 * ((lane & 15) ^ (r & 15));
+    }
+    auto issue_x = [&](int i, int slot) __attribute__((always_inline)) {
+        int8_t *stage = xs + slot * kStageBytes;
+#pragma unroll
+        for (int j = 0; j < MB; ++j)
+            __builtin_amdgcn_global_load_lds((glb_ptr)(xsrc[j] + min(i * kChunk + xcol[j], kl - 16)),
+                                             (lds_ptr)(stage + 4 * (wave * MB + j) * kChunk), 16, 0, 0);
+    };
+    // W: rows past n read row n - 1 (never stored).
+    const int64_t wrow = min<int64_t>(n0 + (lane & 15), p.n - 1) * p.k + k_lo;
+    const int8_t *wsrc[D];
+    wsrc[0] = p.qw + wrow;
+    if (DUAL) wsrc[D - 1] = p.qw2 + wrow;
+    const int kq = 16 * (lane >> 4);
+    auto load_w = [&](int i, i32x4(&R)[D][4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+                R[d][s] = *reinterpret_cast<const i32x4 *>(wsrc[d] + min(i * kChunk + 64 * s + kq, kl - 16));
+    };
+
+    i32x4 acc[D][MB];
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[d][mb] = i32x4{0, 0, 0, 0};
+    // Fragment of x block mb, step s: row 16 mb + l % 16, logical chunk
+    // 4 s + l / 16.
+    const int xrd = (lane & 15) * kChunk;
+    auto compute = [&](int i, i32x4(&R)[D][4], auto tail) __attribute__((always_inline)) {
+        const int8_t *stage = xs + (i % kStages) * kStageBytes;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            i32x4 xv[MB], wv[D];
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+                xv[mb] = *reinterpret_cast<const i32x4 *>(stage + mb * 16 * kChunk + xrd +
+                                                          (((4 * s + (lane >> 4)) ^ (lane & 15)) << 4));
+#pragma unroll
+            for (int d = 0; d < D; ++d) wv[d] = R[d][s];
+            if constexpr (decltype(tail)::value) {
+                // K % 16 == 0: a lane's 16 bytes are all inside the slice or
+                // all past it; past it both operands are zero.
+                const bool ok = i * kChunk + 64 * s + kq < kl;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+#pragma unroll
+                    for (int d = 0; d < D; ++d) wv[d][e] = ok ? wv[d][e] : 0;
+#pragma unroll
+                    for (int mb = 0; mb < MB; ++mb) xv[mb][e] = ok ? xv[mb][e] : 0;
+                }
+            }
+#pragma unroll
+            for (int d = 0; d < D; ++d)
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb)
+                    acc[d][mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xv[mb], wv[d], acc[d][mb], 0, 0, 0);
+        }
+    };
+
+    // Chunk i: wait for its x and W (the next chunk's loads stay in flight),
+    // barrier (its x is visible, and every wave is done with chunk i - 1,
+    // whose ring stage and register set now refill), issue chunk i + 2
+    // (unconditionally: past the last chunk it repeats the last one into the
+    // free stage and set, so the counts stay constant and the register sets
+    // rotate without copies), compute chunk i.  The compiler drops the
+    // register loads of repeats that no MFMA reads, so the last chunk counts
+    // only its own W and the repeated x behind its x.
+    const bool ragged = (kl % kChunk) != 0;
+    auto step = [&](int i, i32x4(&Rc)[D][4], i32x4(&Rn)[D][4]) __attribute__((always_inline)) {
+        if (i + 1 < nch)
+            wait_vmcnt<kOps>();
+        else
+            wait_vmcnt<4 * D + MB>();
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        const int nx = min(i + 2, nch - 1);
+        issue_x(nx, (i + 2) % kStages);
+        __builtin_amdgcn_sched_barrier(0);  // x before W
+        load_w(nx, Rn);
+        __builtin_amdgcn_sched_barrier(0);
+        if (ragged && i + 1 == nch)
+            compute(i, Rc, std::true_type{});
+        else
+            compute(i, Rc, std::false_type{});
+    };
+    i32x4 R[kStages][D][4];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        issue_x(min(c, nch - 1), c);
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(min(c, nch - 1), R[c]);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // Whole rounds of three chunks in a loop without exits, then the one or
+    // two left, in the same rotation.
+    int i = 0;
+    for (; i + kStages <= nch; i += kStages) {
+#pragma unroll
+        for (int u = 0; u < kStages; ++u) step(i + u, R[u], R[(u + 2) % kStages]);
+    }
+#pragma unroll
+    for (int u = 0; u + 1 < kStages; ++u)
+        if (i + u < nch) step(i + u, R[u], R[(u + 2) % kStages]);
+    wait_vmcnt<0>();          // no load may still be writing the ring
+    if (n0 >= p.n) return;  // a wave past the last column (after every barrier)
+
+    // 16x16 accumulator layout: lane l, register r -> row 4 (l / 16) + r of
+    // the block, column l % 16.
+    const int64_t col = n0 + (lane & 15);
+    const bool col_ok = col < p.n;
+    const int64_t blk = n0 / 16;
+    auto row_of = [&](int mb, int r) -> int64_t { return (int64_t)mb * 16 + 4 * (lane >> 4) + r; };
+    auto corrected = [&](int d, int64_t row, int32_t raw) -> int32_t {
+        if (!p.zx) return raw;
+        const int32_t *rs = d ? p.rowsum2 : p.rowsum;
+        return (int32_t)((uint32_t)raw - (uint32_t)((int32_t)p.zx[p.x_per_row ? row : 0] * rs[col]));
+    };
+    auto dequant = [&](int d, int64_t row, int32_t a) -> float {
+        const float *sw = d ? p.sw2 : p.sw;
+        const float *bias = d ? p.bias2 : p.bias;
+        const float sc = p.sx[p.x_per_row ? row : 0] * sw[col];
+        float v = (float)a * sc;
+        if (bias) v = v + bias[col];
+        return v;
+    };
+    float mn = INFINITY, mx = -INFINITY;
+    auto epilogue = [&](int64_t row, const int32_t *raw) {
+        if (DUAL) {
+            const float g = dequant(0, row, corrected(0, row, raw[0]));
+            const float u = dequant(1, row, corrected(1, row, raw[D - 1]));
+            const float h = silu_mul1(g, u);
+            p.y[row * p.n + col] = h;
+            mn = fminf(mn, h);
+            mx = fmaxf(mx, h);
+            return;
+        }
+        const int32_t a = corrected(0, row, raw[0]);
+        if (p.acc) p.acc[row * p.n + col] = a;
+        if (p.y) p.y[row * p.n + col] = dequant(0, row, a);
+    };
+    auto publish_minmax = [&]() {
+        if (!DUAL) return;
+        wave_minmax(mn, mx);
+        if (lane == 0) p.hpart[blk] = make_float2(mn, mx);
+    };
+
+    if (sp.slices == 1) {
+        if (col_ok) {
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t row = row_of(mb, r);
+                    int32_t raw[D];
+#pragma unroll
+                    for (int d = 0; d < D; ++d) raw[d] = acc[d][mb][r];
+                    if (row < p.m) epilogue(row, raw);
+                }
+        }
+        publish_minmax();
+        return;
+    }
+
+    // Publish the partial block with agent-scope stores (they go to the
+    // device coherence point, so no cache writeback is needed), wait for
+    // them, then count this wave's arrival on its column block.
+    if (col_ok) {
+#pragma unroll
+        for (int d = 0; d < D; ++d)
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t row = row_of(mb, r);
+                    if (row < p.m)
+                        __hip_atomic_store(sp.part + ((slice * D + d) * p.m + row) * p.n + col, acc[d][mb][r],
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    wait_vmcnt<0>();
+    int last = 0;
+    if (lane == 0)
+        last = __hip_atomic_fetch_add(sp.counters + blk, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               (int)sp.slices - 1;
+    last = __shfl(last, 0);
+    if (!last) return;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    // The partials of all the lane's outputs for kGroup slices at a time are
+    // requested before any is added, so the loads overlap; integer sums are
+    // exact (wrapping as int32) in any order.
+    constexpr int kGroup = 32 / (4 * MB * D) > 0 ? 32 / (4 * MB * D) : 1;
+    uint32_t sum[D][MB][4];
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sum[d][mb][r] = 0;
+    for (int64_t j0 = 0; j0 < sp.slices; j0 += kGroup) {
+        int32_t pv[kGroup][D][MB][4];
+#pragma unroll
+        for (int g = 0; g < kGroup; ++g)
+#pragma unroll
+            for (int d = 0; d < D; ++d)
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int64_t row = row_of(mb, r);
+                        const bool ok = col_ok && row < p.m && j0 + g < sp.slices;
+                        pv[g][d][mb][r] = ok ? __hip_atomic_load(sp.part + (((j0 + g) * D + d) * p.m + row) * p.n + col,
+                                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                             : 0;
+                    }
+#pragma unroll
+        for (int g = 0; g < kGroup; ++g)
+#pragma unroll
+            for (int d = 0; d < D; ++d)
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) sum[d][mb][r] += (uint32_t)pv[g][d][mb][r];
+    }
+    if (col_ok) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t row = row_of(mb, r);
+                if (row >= p.m) continue;
+                int32_t raw[D];
+#pragma unroll
+                for (int d = 0; d < D; ++d) raw[d] = (int32_t)sum[d][mb][r];
+                epilogue(row, raw);
+            }
+    }
+    publish_minmax();
+    if (lane == 0) __hip_atomic_store(sp.counters + blk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// K bytes per workgroup: all of K with at least ~512 workgroups, otherwise
+// enough slices for about that many, each at least 4 chunks, a multiple of
+// the chunk.
+int64_t choose_kslice(int64_t ngrp, int64_t k) {
+    const int64_t kc = (k + kChunk - 1) / kChunk * kChunk;
+    int64_t s = (512 + ngrp - 1) / ngrp;
+    s = std::max<int64_t>(1, std::min<int64_t>(s, k / (4 * kChunk)));
+    if (s == 1) return kc;
+    const int64_t ks = (k + s - 1) / s;
+    return (ks + kChunk - 1) / kChunk * kChunk;
+}
+
+template <bool DUAL>
+int launch(const QParams &p, hipStream_t s, int *npart = nullptr) {
+    constexpr int D = DUAL ? 2 : 1;
+    Params sp{};
+    sp.q = p;
+    sp.ngrp = (p.n + kGroupCols - 1) / kGroupCols;
+    sp.kslice = choose_kslice(sp.ngrp, p.k);
+    sp.slices = (p.k + sp.kslice - 1) / sp.kslice;
+    if (npart) *npart = (int)((p.n + 15) / 16);
+    if (sp.slices > 1) {
+        void *ws = nullptr;
+        GFH_TRY(stream_workspace(s, sizeof(int32_t) * (size_t)(sp.slices * D * p.m * p.n), &ws));
+        sp.part = static_cast<int32_t *>(ws);
+        GFH_TRY(stream_counters(s, (size_t)(sp.ngrp * kWaves), &sp.counters));
+    }
+    const dim3 grid((unsigned)(sp.ngrp * sp.slices)), block(64 * kWaves);
+    if (p.m <= 16)
+        hipLaunchKernelGGL((qlinear_skinny_lds_kernel<1, DUAL>), grid, block, 0, s, sp);
+    else if (p.m <= 32)
+        hipLaunchKernelGGL((qlinear_skinny_lds_kernel<2, DUAL>), grid, block, 0, s, sp);
+    else if constexpr (!DUAL) {  // (two weight streams at 3-4 row blocks would spill)
+        if (p.m <= 48)
+            hipLaunchKernelGGL((qlinear_skinny_lds_kernel<3, DUAL>), grid, block, 0, s, sp);
+        else
+            hipLaunchKernelGGL((qlinear_skinny_lds_kernel<4, DUAL>), grid, block, 0, s, sp);
+    } else {
+        return set_error(GFH_INVALID_SHAPE, "qlinear_swiglu_i8: shared-x skinny kernel serves M <= 32");
+    }
+    return check_launch(DUAL ? "qlinear_swiglu_i8 (skinny, shared x)" : "qlinear_i8 (skinny, shared x)");
+}
+
+}  // namespace skinny_lds
+
+// Which skinny kernel serves 1 <= M <= 64.  The 16-column kernel re-reads x
+// per wave (m / 16 times the weight bytes again) but needs no K split when
+// N / 16 gives ~512 workgroups; the shared-x kernel's 64-column groups
+// split K sooner, and its tail costs ~2-3 us.  Measured (us, 16-column /
+// shared x): N = 11008, K = 4096: M = 8 14.2 / 17.9, 16 16.3 / 18.5, 32
+// 22.9 / 21.9, 64 37.0 / 29.8; N = 4096, K = 11008: M = 16 19.6 / 16.9, 32
+// 28.7 / 19.7; N = 4096, K = 4096, M = 16 11.2 / 9.2; the two-weight (gate /
+// up) forms follow the same pattern, and the shared-x one would spill
+// registers above 32 rows.
+bool use_skinny_lds(int64_t m, int64_t n, int64_t k, bool dual) {
+    if (m <= 4 || (dual && m > 32)) return false;
+    const bool narrow_splits = skinny::choose_kslice((n + skinny::kCols - 1) / skinny::kCols, k) < k;
+    return narrow_splits || m > 32;
+}
+
 }  // namespace
 
 int launch_qlinear_i8(const QLinearDesc &d, hipStream_t s) {
@@ -904,7 +1278,8 @@ int launch_qlinear_i8(const QLinearDesc &d, hipStream_t s) {
     p.n = d.n;
     p.k = d.k;
     p.x_per_row = d.x_per_row ? 1 : 0;
-    if (d.m <= 64 && d.k % 16 == 0 && d.k > 0 && aligned16(d.qx) && aligned16(d.qw)) return skinny::launch<false>(p, s);
+    if (d.m <= 64 && d.k % 16 == 0 && d.k > 0 && aligned16(d.qx) && aligned16(d.qw))
+        return use_skinny_lds(d.m, d.n, d.k, false) ? skinny_lds::launch<false>(p, s) : skinny::launch<false>(p, s);
     // Direct-to-LDS tiles need 16-byte aligned rows (K % 64 == 0) and 32-bit
     // row offsets inside a tile (256 * K < 2^32).
     const bool ring_ok = d.k > 0 && d.k % 64 == 0 && d.k <= (int64_t(1) << 24) && aligned16(d.qx) && aligned16(d.qw);
@@ -988,7 +1363,9 @@ int launch_qlinear_swiglu_i8(const QSwigluDesc &d, int *npart, hipStream_t s) {
     p.rowsum2 = d.rowsum_up;
     p.bias2 = d.bias_up;
     p.hpart = d.hpart;
-    if (g.m <= 64) return skinny::launch<true>(p, s, npart);
+    if (g.m <= 64)
+        return use_skinny_lds(g.m, g.n, g.k, true) ? skinny_lds::launch<true>(p, s, npart)
+                                                    : skinny::launch<true>(p, s, npart);
     const bool bk128 = g.k % 128 == 0;
     if (g.m > 512)
         return bk128 ? big::launch_tiles_dual<256, 256, 128, 3, 2, 2, 4>(p, s, npart)
