@@ -127,8 +127,12 @@ __device__ __forceinline__ void tile_scores(const SdpaParams &p, const float *ks
     }
 }
 
+// Two workgroups per CU (at most 256 registers per lane): with one, every
+// softmax, LDS and barrier stall of a wave left its SIMD's MFMA idle --
+// B=4, H=32, D=128 causal at S=2048: 1487 us with 243 VGPRs + 64 AGPRs, one
+// wave per SIMD; 1287 us with 249 VGPRs, two.
 template <int DMAX, bool CAUSAL, bool MASK, bool WEIGHTS>
-__global__ __launch_bounds__(kThreads) void sdpa_fwd_kernel(SdpaParams p) {
+__global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(SdpaParams p) {
     constexpr int NG = DMAX / 8, ND = DMAX / 32;
     constexpr int kStride = DMAX + 4;
     constexpr int kTile = kBKV * kStride;
