@@ -63,6 +63,7 @@ struct SdpaParams {
     int64_t causal_off;  // causal keeps key j for query i when j <= i + causal_off
     float scale;
     int nqb;
+    int fold;  // causal issue order for a grid that is resident all at once (below)
 };
 
 __device__ __forceinline__ int key_of(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
@@ -144,7 +145,17 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(SdpaParams p) {
     const int lane = tid & 63, wave = tid >> 6;
     const int c = lane & 31, h = lane >> 5;
     const int64_t bh = blockIdx.x;
-    const int qb = CAUSAL ? (p.nqb - 1 - (int)blockIdx.y) : (int)blockIdx.y;
+    // Causal issue order.  Query block qb walks qb + 1 key blocks, so the
+    // heaviest go first; when the whole grid is resident at once (two
+    // workgroups per CU), workgroups j and j + #CUs share a CU, and the
+    // second half of the y range then runs the light blocks in ascending
+    // order, pairing the heaviest with the lightest (B=4, H=32, S=512: CU
+    // loads 16 + 4 and 12 + 8 key blocks instead of 16 + 8 and 12 + 4).
+    int qb = (int)blockIdx.y;
+    if (CAUSAL) {
+        const int y = (int)blockIdx.y, half = (p.nqb + 1) / 2;
+        qb = (p.fold && y >= half) ? y - half : p.nqb - 1 - y;
+    }
     const int64_t q0 = (int64_t)qb * kBQ;
     const int64_t wq0 = q0 + wave * 32;
     const int64_t my_q = wq0 + c;
@@ -365,6 +376,7 @@ int launch_sdpa(const SdpaDesc &d, hipStream_t s) {
     p.causal_off = d.causal ? d.skv - d.sq : 0;
     p.scale = d.scale;
     p.nqb = (int)((d.sq + kBQ - 1) / kBQ);
+    p.fold = d.causal && p.bh * p.nqb <= 2 * (int64_t)device_cu_count();
     dim3 grid((unsigned)p.bh, (unsigned)p.nqb);
     const bool mask = d.mask != nullptr, weights = d.weights != nullptr;
     if (d.d <= 32)

@@ -192,6 +192,18 @@ int stream_counters(hipStream_t s, size_t count, int **out) {
     return GFH_SUCCESS;
 }
 
+int device_cu_count() {
+    constexpr int kMaxDevices = 64;
+    static std::atomic<int> cache[kMaxDevices];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+    int n = cache[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
+
 int stream_workspace(hipStream_t s, size_t bytes, void **out) {
     std::lock_guard<std::mutex> lock(g_state_mu);
     StreamState *st = nullptr;

@@ -67,6 +67,9 @@ int stream_counters(hipStream_t s, size_t count, int **out);
 int stream_workspace(hipStream_t s, size_t bytes, void **out);
 void release_stream_state();
 
+// Compute units of the current device (queried once per device).
+int device_cu_count();
+
 }  // namespace gfh
 
 // Propagate a non-zero status.
