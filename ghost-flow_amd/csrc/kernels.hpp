@@ -32,8 +32,9 @@ int launch_gemv_nt(const SgemmDesc &d, hipStream_t s);
 constexpr int64_t kNtSkinnyMinM = 4;
 bool gemm_nt_skinny_fits(const SgemmDesc &d);
 int launch_gemm_nt_skinny(const SgemmDesc &d, hipStream_t s);
-// sgemm_big.hip: NT and NN (A [m, k]) on 256 x 256 tiles when they fill the
-// GPU (K % 32 == 0, batch 1; NN with n % 4 == 0).
+// sgemm_big.hip: NT and NN (A [m, k]) on direct-to-LDS tiles -- 256 x 256 or
+// 128 x 128 when they fill the GPU, else 64 x 64 (K % 32 == 0, batch 1; NN
+// with n % 4 == 0).
 bool sgemm_big_fits(const SgemmDesc &d);
 int launch_sgemm_big(const SgemmDesc &d, hipStream_t s);
 

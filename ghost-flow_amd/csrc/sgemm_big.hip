@@ -1,4 +1,5 @@
-// sgemm_big.hip -- fp32 GEMM on 256 x 256 tiles fed by direct-to-LDS loads:
+// sgemm_big.hip -- fp32 GEMM on 256 x 256, 128 x 128 or 64 x 64 tiles fed by
+// direct-to-LDS loads:
 // C = alpha * A . op(B) (+ beta C) (+ bias) with A [m, k] row-major and B
 // either [n, k] (NT: Linear::forward's x . W^T with the reference's
 // [out, in] weight, ghostflow-nn/src/linear.rs:56-69) or [k, n] (NN:
@@ -42,20 +43,23 @@
 namespace gfh {
 namespace {
 
-constexpr int BKB = 128;                 // K bytes per stage (32 floats)
-constexpr int NWM = 2, NWN = 4, NW = 8;  // wave grid
-constexpr int NT = 64 * NW;
-constexpr int STAGES = 2;
+constexpr int BKB = 128;                  // K bytes per stage (32 floats)
 constexpr int kRowsPerLoad = 1024 / BKB;  // K-contiguous rows per load instruction
 constexpr int kGroupM = 4;
 constexpr int kKGroups = BKB / 32;  // 8-float k-groups per stage
 
-// Geometry of a BM x BN tile (256 x 256 or 128 x 128).
-template <int BM, int BN, bool NN>
+// Geometry of a BM x BN tile on an NWM_ x NWN_ wave grid with an
+// STAGES_-deep ring: 256 x 256 and 128 x 128 on 2 x 4 waves and 2 stages,
+// 64 x 64 on 2 x 2 waves and 4 stages.
+template <int BM, int BN, bool NN, int NWM_ = 2, int NWN_ = 4, int STAGES_ = 2>
 struct Geo {
+    static constexpr int NWM = NWM_, NWN = NWN_, NW = NWM * NWN, NT = 64 * NW;  // wave grid, threads
+    static constexpr int STAGES = STAGES_;
     static constexpr int WM = BM / NWM, WN = BN / NWN;  // wave sub-tile
     static constexpr int FM = WM / 32, FN = WN / 32;    // accumulators per wave
-    static constexpr int kLA = BM / 64, kLB = BN / 64;  // load instructions per wave per stage
+    // load instructions (1 KB each) per wave per stage
+    static constexpr int kLA = BM * BKB / (1024 * NW), kLB = BN * BKB / (1024 * NW);
+    static_assert(kLA * 1024 * NW == BM * BKB && kLB * 1024 * NW == BN * BKB, "whole load instructions per wave");
     static constexpr int kLPS = kLA + kLB;
     static constexpr int kABytes = BM * BKB;
     // NN: a load instruction fills RPL k-rows of BN floats (1 KB); groups
@@ -66,10 +70,15 @@ struct Geo {
     static constexpr int kBBytes = NN ? (32 / RPL) * kGroupStride : BN * BKB;
     static constexpr int kStageBytes = kABytes + kBBytes;
     static constexpr int kOutStride = WN + 8;  // floats per staged output row
-    static constexpr int kOut = NW * (WM / 2) * kOutStride * 4;
+    // The output goes through LDS half a wave sub-tile at a time, all of it
+    // when the sub-tile is a single 32-row block.
+    static constexpr int kOutPasses = FM >= 2 ? 2 : 1;
+    static constexpr int kOutRows = WM / kOutPasses;
+    static constexpr int kOut = NW * kOutRows * kOutStride * 4;
     static constexpr int kLds = STAGES * kStageBytes > kOut ? STAGES * kStageBytes : kOut;
     static_assert(kLds <= 160 * 1024, "LDS per workgroup");
-    static_assert(FM >= 2 && FN >= 1, "wave sub-tile");
+    static_assert(FM >= 1 && FN >= 1 && (FM == 1 || FM % 2 == 0), "wave sub-tile");
+    static_assert((STAGES - 1) * kLPS < 64, "vmcnt is 6 bits");
     // byte offset of k-row r inside an NN B stage
     static __device__ __forceinline__ int brow(int r) { return (r / RPL) * kGroupStride + (r % RPL) * BN * 4; }
 };
@@ -109,9 +118,11 @@ __device__ __forceinline__ void interleave() {
     }
 }
 
-template <int BM, int BN, bool NN>
-__global__ __launch_bounds__(NT, (BM * BN <= 128 * 128) ? 2 : 1) void sgemm_big_kernel(BigParams p) {
-    using G = Geo<BM, BN, NN>;
+template <int BM, int BN, bool NN, int NWM_ = 2, int NWN_ = 4, int STAGES_ = 2>
+__global__ __launch_bounds__((Geo<BM, BN, NN, NWM_, NWN_, STAGES_>::NT),
+                             (BM * BN <= 128 * 128) ? 2 : 1) void sgemm_big_kernel(BigParams p) {
+    using G = Geo<BM, BN, NN, NWM_, NWN_, STAGES_>;
+    constexpr int NWN = G::NWN, NW = G::NW, STAGES = G::STAGES;
     constexpr int WM = G::WM, WN = G::WN, FM = G::FM, FN = G::FN;
     constexpr int kLA = G::kLA, kLB = G::kLB, kLPS = G::kLPS;
     constexpr int kABytes = G::kABytes, kStageBytes = G::kStageBytes, kOutStride = G::kOutStride;
@@ -260,21 +271,23 @@ __global__ __launch_bounds__(NT, (BM * BN <= 128 * 128) ? 2 : 1) void sgemm_big_
     // runs of WN floats with 16-byte stores.
     constexpr int LPR = WN / 4;    // lanes per output row
     constexpr int RPI = 64 / LPR;  // rows per store instruction
-    constexpr int HALF = WM / 2;
+    constexpr int PASSES = G::kOutPasses;
+    constexpr int HALF = G::kOutRows;  // rows per pass
+    constexpr int BPP = FM / PASSES;   // 32-row blocks per pass
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();  // every wave is done with the operand ring
     float *lt = reinterpret_cast<float *>(lds) + wave * (HALF * kOutStride);
     const bool vec_out = (p.ldc % 4) == 0 && (reinterpret_cast<uintptr_t>(p.c) & 15) == 0;
 #pragma unroll
-    for (int hf = 0; hf < 2; ++hf) {
+    for (int hf = 0; hf < PASSES; ++hf) {
 #pragma unroll
-        for (int ii = 0; ii < FM / 2; ++ii)
+        for (int ii = 0; ii < BPP; ++ii)
 #pragma unroll
             for (int j = 0; j < FN; ++j)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
                     const int lr = ii * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    lt[lr * kOutStride + j * 32 + (lane & 31)] = p.alpha * acc[hf * (FM / 2) + ii][j][r];
+                    lt[lr * kOutStride + j * 32 + (lane & 31)] = p.alpha * acc[hf * BPP + ii][j][r];
                 }
         const int64_t col = n0 + wn0 + 4 * (lane % LPR);
 #pragma unroll
@@ -317,13 +330,17 @@ int64_t tiles_of(const SgemmDesc &d, int64_t t) { return ((d.m + t - 1) / t) * (
 }  // namespace
 
 // 256 x 256 tiles when there are at least 256 of them (one per CU), else
-// 128 x 128 tiles (two workgroups per CU fit) when those number 256.
+// 128 x 128 tiles when those number 256, else 64 x 64 tiles on 2 x 2 waves
+// (at least 32 of them).  Measured against the register-staged tile kernel
+// (us): 1024^3 NN 31.3 -> 25.8, NT 29.5 -> 20.9; 1536^3 NN 120.5 -> 84.4;
+// 1024 x 1024 x 4096 NN 107.2 -> 86.6; 512 x 2048 x 1024 NT 29.5 -> 20.7.
 bool sgemm_big_fits(const SgemmDesc &d) {
     if (d.trans_a || d.batch > 1 || d.batch_a > 1 || d.batch_b > 1) return false;
     if (d.k <= 0 || d.k % 32 != 0 || d.lda % 4 != 0 || d.ldb % 4 != 0) return false;
     if (!d.trans_b && d.n % 4 != 0) return false;  // NN: whole 16-byte column groups
     if (!aligned16(d.a) || !aligned16(d.b)) return false;
-    return d.m >= 128 && d.n >= 128 && tiles_of(d, 128) >= 256;
+    if (d.m >= 128 && d.n >= 128 && tiles_of(d, 128) >= 256) return true;
+    return d.m >= 64 && d.n >= 64 && tiles_of(d, 64) >= 32;
 }
 
 int launch_sgemm_big(const SgemmDesc &d, hipStream_t s) {
@@ -340,20 +357,40 @@ int launch_sgemm_big(const SgemmDesc &d, hipStream_t s) {
     p.ldc = d.ldc;
     p.alpha = d.alpha;
     p.beta = d.beta;
-    const int t = (d.m >= 256 && d.n >= 256 && tiles_of(d, 256) >= 256) ? 256 : 128;
+    const int64_t t128 = tiles_of(d, 128);
+    const int t = (d.m >= 256 && d.n >= 256 && tiles_of(d, 256) >= 256) ? 256
+                  : (d.m >= 128 && d.n >= 128 && t128 >= 256)           ? 128
+                                                                         : 64;
     p.tiles_m = (int)((d.m + t - 1) / t);
     p.tiles_n = (int)((d.n + t - 1) / t);
     const dim3 grid((unsigned)(p.tiles_m * p.tiles_n));
+    constexpr int kNT = Geo<128, 128, false>::NT;
+    constexpr int kNT64 = Geo<64, 64, false, 2, 2>::NT;
     if (t == 256) {
         if (d.trans_b)
-            hipLaunchKernelGGL((sgemm_big_kernel<256, 256, false>), grid, dim3(NT), 0, s, p);
+            hipLaunchKernelGGL((sgemm_big_kernel<256, 256, false>), grid, dim3(kNT), 0, s, p);
         else
-            hipLaunchKernelGGL((sgemm_big_kernel<256, 256, true>), grid, dim3(NT), 0, s, p);
+            hipLaunchKernelGGL((sgemm_big_kernel<256, 256, true>), grid, dim3(kNT), 0, s, p);
+    } else if (t == 128) {
+        // One round of tiles (one workgroup per CU): a 3-deep ring (2048^3 NN
+        // 143.7 -> 133.7 us); more tiles: 2 stages, two workgroups per CU.
+        if (t128 <= 256) {
+            if (d.trans_b)
+                hipLaunchKernelGGL((sgemm_big_kernel<128, 128, false, 2, 4, 3>), grid, dim3(kNT), 0, s, p);
+            else
+                hipLaunchKernelGGL((sgemm_big_kernel<128, 128, true, 2, 4, 3>), grid, dim3(kNT), 0, s, p);
+        } else {
+            if (d.trans_b)
+                hipLaunchKernelGGL((sgemm_big_kernel<128, 128, false>), grid, dim3(kNT), 0, s, p);
+            else
+                hipLaunchKernelGGL((sgemm_big_kernel<128, 128, true>), grid, dim3(kNT), 0, s, p);
+        }
     } else {
+        // (NT 4 stages, NN 3: the better of 3 / 4 / 6 at 1024^3)
         if (d.trans_b)
-            hipLaunchKernelGGL((sgemm_big_kernel<128, 128, false>), grid, dim3(NT), 0, s, p);
+            hipLaunchKernelGGL((sgemm_big_kernel<64, 64, false, 2, 2, 4>), grid, dim3(kNT64), 0, s, p);
         else
-            hipLaunchKernelGGL((sgemm_big_kernel<128, 128, true>), grid, dim3(NT), 0, s, p);
+            hipLaunchKernelGGL((sgemm_big_kernel<64, 64, true, 2, 2, 3>), grid, dim3(kNT64), 0, s, p);
     }
     return check_launch("sgemm (direct-to-LDS tiles)");
 }

@@ -168,13 +168,16 @@ def test_k_zero_gives_bias(torch_dev):
 
 
 @pytest.mark.parametrize("m,n,k", [(4096, 4096, 64), (4100, 4000, 96), (4352, 3900, 32), (2048, 2048, 64),
-                                   (2100, 2000, 96), (1024, 4096, 32)])
+                                   (2100, 2000, 96), (1024, 4096, 32), (330, 700, 96), (1000, 520, 1024),
+                                   (1024, 1024, 1024)])
 @pytest.mark.parametrize("tb", [True, False])
 def test_big_tiles_integer_exact(torch_dev, m, n, k, tb):
-    """NT (Linear's x . W^T) and NN (Tensor::matmul) shapes that fill the GPU
-    take the direct-to-LDS kernel, on 256 x 256 tiles (the first three) or
-    128 x 128 tiles (the rest): ragged m and n inside the last tiles, alpha,
-    beta and bias, on integer data (exact in any summation order)."""
+    """NT (Linear's x . W^T) and NN (Tensor::matmul) shapes with K % 32 == 0
+    take the direct-to-LDS kernel: 256 x 256 tiles (the first three), 128 x
+    128 tiles with a 3-deep ring (one round of tiles: 2048^2, 1024 x 4096)
+    or 2 stages (2100 x 2000), and 64 x 64 tiles on 2 x 2 waves (the last
+    three) -- ragged m and n inside the last tiles, alpha, beta and bias, on
+    integer data (exact in any summation order)."""
     gh, O = _gh(), _oracle()
     rng = np.random.default_rng(m + n + k)
     a = rng.integers(-4, 5, size=(m, k)).astype(np.float32)
@@ -203,13 +206,14 @@ def test_big_tiles_nn_random(torch_dev, n):
     assert np.abs(got[rows] - ref).max() <= gemm_tol(n, a, b)
 
 
-def test_nt_big_tiles_strided(torch_dev):
-    """lda > k and ldc > n on the 256 x 256 kernel; bytes between rows of C
-    stay untouched."""
+@pytest.mark.parametrize("m,n", [(4096, 4096), (1000, 900)])
+def test_nt_big_tiles_strided(torch_dev, m, n):
+    """lda > k and ldc > n on the 256 x 256 and the 64 x 64 kernels; bytes
+    between rows of C stay untouched."""
     import torch
     gh, O = _gh(), _oracle()
     rng = np.random.default_rng(31)
-    m, n, k, lda, ldc = 4096, 4096, 96, 100, 4100
+    k, lda, ldc = 96, 100, n + 4
     xa = rng.integers(-4, 5, size=(m, lda)).astype(np.float32)
     w = rng.integers(-4, 5, size=(n, k)).astype(np.float32)
     dx, dw = to_dev(xa, torch_dev), to_dev(w, torch_dev)
