@@ -144,14 +144,15 @@ __device__ __forceinline__ void store_strip(const GemvParams &p, int64_t strip, 
 }
 
 // NW waves per workgroup: 8 when the grid has at most one workgroup per CU,
-// so that twice the weight bytes are in flight per CU.
-template <int MAXB, int U, bool VEC, int NW = kWaves>
+// so that twice the weight bytes are in flight per CU.  ROWS: the longest
+// slice the LDS staging of x holds.
+template <int MAXB, int U, bool VEC, int NW = kWaves, int ROWS = f32_max_rows<MAXB>()>
 __global__ __launch_bounds__(64 * NW) void gemv_f32_kernel(GemvParams p) {
     constexpr int NT = 64 * NW;               // threads
     constexpr int EPL = 4;                    // floats per lane per load
     constexpr int SCOLS = kStripBytes / 4;    // strip columns
     constexpr int kStep = 4 * U;              // rows per wave step
-    constexpr int kMaxRows = f32_max_rows<MAXB>();
+    constexpr int kMaxRows = ROWS;
     __shared__ __attribute__((aligned(16))) float xs[kMaxRows * MAXB];  // this slice's x, [row][batch]
     __shared__ float red[NW][MAXB][SCOLS];
     __shared__ int last_flag;
@@ -576,10 +577,20 @@ void launch(const GemvParams &q, bool vec, hipStream_t s) {
 
 }  // namespace w8mf
 
+// 8 batch rows in one slice of up to 4096 rows, one 8-wave workgroup per CU:
+// x takes 128 KB of LDS, the wave partials 16 KB.
+constexpr int kWideRows8 = 4096;
+
 template <int MAXB>
 void launch_f32(const GemvParams &p, bool vec, hipStream_t s) {
     constexpr int U = 8;
     const unsigned nwg = (unsigned)(p.nstrips * p.slices);
+    if constexpr (MAXB == 8) {
+        if (vec && nwg <= 256 && p.kslice > f32_max_rows<8>()) {
+            hipLaunchKernelGGL((gemv_f32_kernel<8, U, true, 8, kWideRows8>), dim3(nwg), dim3(512), 0, s, p);
+            return;
+        }
+    }
     if (vec && nwg <= 256)
         hipLaunchKernelGGL((gemv_f32_kernel<MAXB, U, true, 8>), dim3(nwg), dim3(512), 0, s, p);
     else if (vec)
@@ -661,10 +672,15 @@ int launch_gemv_f32(const float *x, const float *w, float *y, int64_t b, int64_t
     const bool vec = n % 4 == 0 && aligned16(w);
     return for_batch_groups(p, x, y, b, [&](GemvParams &q) {
         const int maxb = q.b == 1 ? 1 : q.b == 2 ? 2 : q.b <= 4 ? 4 : 8;
-        const int64_t max_rows = maxb == 1   ? f32_max_rows<1>()
-                                 : maxb == 2 ? f32_max_rows<2>()
-                                 : maxb == 4 ? f32_max_rows<4>()
-                                             : f32_max_rows<8>();
+        int64_t max_rows = maxb == 1   ? f32_max_rows<1>()
+                           : maxb == 2 ? f32_max_rows<2>()
+                           : maxb == 4 ? f32_max_rows<4>()
+                                       : f32_max_rows<8>();
+        // 8 batch rows: all of K <= 4096 in one slice when the strips alone
+        // fill the GPU with one 8-wave workgroup per CU (W [4096, 14336]:
+        // see kWideRows8), instead of 4 slices of 1024 rows.
+        if (maxb == 8 && vec && k > 0 && k <= kWideRows8 && q.nstrips >= 192 && q.nstrips <= 256)
+            max_rows = kWideRows8;
         GFH_TRY(set_slices(q, k > 0 ? choose_kslice_f32(q.nstrips, k, q.b, max_rows) : 32, s));
         if (maxb == 1)
             launch_f32<1>(q, vec, s);
