@@ -324,12 +324,16 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_nt_skinny_kernel(SkNtPara
 // 41.7 us (m = 8 / 32 / 64) with 16.  Of the 18.7 us at m = 16, about 2.7
 // us are the split-K tail (partial stores, arrival count, the last
 // arriver's reads: three memory round trips) and 1 us the x staging.
+// Above 48 rows (four row blocks, a 16 KB x stage per chunk) half as many
+// workgroups: m = 64 took 29.1 / 33.8 us at 4 slices against 32.0 / 34.4 us
+// at 8 in two sweeps, while m <= 32 prefers 8.
 constexpr int64_t kTargetWgs = 512;
 constexpr int kDepth = 2;
-int64_t choose_kslice(int64_t ngrp, int64_t k, int64_t batch) {
+int64_t choose_kslice(int64_t ngrp, int64_t k, int64_t batch, int64_t m) {
     const int64_t kc = ((k + kKC - 1) / kKC) * kKC;
     if (batch > 1) return kc;
-    int64_t s = (kTargetWgs + ngrp - 1) / ngrp;
+    const int64_t target = m > 48 ? kTargetWgs / 2 : kTargetWgs;
+    int64_t s = (target + ngrp - 1) / ngrp;
     s = std::max<int64_t>(1, std::min<int64_t>(s, k / (4 * kKC)));
     const int64_t ks = (k + s - 1) / s;
     return (ks + kKC - 1) / kKC * kKC;
@@ -364,7 +368,7 @@ int launch_gemm_nt_skinny(const SgemmDesc &d, hipStream_t s) {
     p.beta = d.beta;
     const int64_t batch = std::max<int64_t>(d.batch, 1);
     p.ngrp = (d.n + kGroupCols - 1) / kGroupCols;
-    p.kslice = choose_kslice(p.ngrp, d.k, batch);
+    p.kslice = choose_kslice(p.ngrp, d.k, batch, d.m);
     p.slices = (d.k + p.kslice - 1) / p.kslice;
     if (p.slices > 1) {
         void *ws = nullptr;
