@@ -16,7 +16,7 @@
  * the Rust build on the same host.
  *
  * Pinning (what checks each function; tests/test_oracle.py, and the
- * committed fixtures tests/golden/*.npz that tests/test_golden.py
+ * committed .npz fixtures under tests/golden/ that tests/test_golden.py
  * regenerates bit for bit):
  *   gfo_matmul_blocked / gfo_batched_matmul : reference known answers
  *       [[22,28],[49,64]] (matmul.rs:331-352) and [19,22,43,50]
