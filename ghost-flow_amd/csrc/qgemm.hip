@@ -1201,11 +1201,16 @@ __global__ __launch_bounds__(64 * kWaves, 2) void qlinear_skinny_lds_kernel(Para
     if (lane == 0) __hip_atomic_store(sp.counters + blk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// K bytes per workgroup: all of K with at least ~512 workgroups, otherwise
-// enough slices for about that many, each at least 4 chunks, a multiple of
-// the chunk.
+// K bytes per workgroup: all of K with at least 128 column groups (half
+// the CUs), otherwise enough slices for about 512 workgroups, each at least
+// 4 chunks, a multiple of the chunk.  At N = 11008 (172 groups), K = 4096,
+// no split beat 2 / 3 / 4 slices at every M measured: M = 8 / 16 / 32 14.1 /
+// 14.0 / 15.5 us against 14.9-17.6 / 15.2-18.2 / 18.1-21.5 (the gate/up form
+// 22.4 / 22.5 / 24.9 against 25.0-27.8 / 25.7-27.7 / 29.4-33.8): the split
+// tail costs more than half the CUs idle.
 int64_t choose_kslice(int64_t ngrp, int64_t k) {
     const int64_t kc = (k + kChunk - 1) / kChunk * kChunk;
+    if (ngrp >= 128) return kc;
     int64_t s = (512 + ngrp - 1) / ngrp;
     s = std::max<int64_t>(1, std::min<int64_t>(s, k / (4 * kChunk)));
     if (s == 1) return kc;
@@ -1247,18 +1252,17 @@ int launch(const QParams &p, hipStream_t s, int *npart = nullptr) {
 }  // namespace skinny_lds
 
 // Which skinny kernel serves 1 <= M <= 64.  The 16-column kernel re-reads x
-// per wave (m / 16 times the weight bytes again) but needs no K split when
-// N / 16 gives ~512 workgroups; the shared-x kernel's 64-column groups
-// split K sooner, and its tail costs ~2-3 us.  Measured (us, 16-column /
-// shared x): N = 11008, K = 4096: M = 8 14.2 / 17.9, 16 16.3 / 18.5, 32
-// 22.9 / 21.9, 64 37.0 / 29.8; N = 4096, K = 11008: M = 16 19.6 / 16.9, 32
-// 28.7 / 19.7; N = 4096, K = 4096, M = 16 11.2 / 9.2; the two-weight (gate /
-// up) forms follow the same pattern, and the shared-x one would spill
-// registers above 32 rows.
+// per wave (m / 16 times the weight bytes again); the shared-x kernel reads
+// it once per workgroup.  Measured (us, 16-column / shared x): N = 11008,
+// K = 4096: M = 8 14.2 / 14.1, 16 16.3 / 14.0, 32 22.9 / 15.5, gate/up M =
+// 16 25.8 / 22.5, 32 33.2 / 24.9; N = 4096, K = 11008: M = 16 19.6 / 16.9,
+// 32 28.7 / 19.7; N = 4096, K = 4096, M = 16 11.2 / 9.2.  Up to 4 rows x is
+// cheap to re-read; the two-weight (gate / up) form of the shared-x kernel
+// would spill registers above 32 rows.
 bool use_skinny_lds(int64_t m, int64_t n, int64_t k, bool dual) {
-    if (m <= 4 || (dual && m > 32)) return false;
-    const bool narrow_splits = skinny::choose_kslice((n + skinny::kCols - 1) / skinny::kCols, k) < k;
-    return narrow_splits || m > 32;
+    (void)n;
+    (void)k;
+    return m > 4 && !(dual && m > 32);
 }
 
 }  // namespace
