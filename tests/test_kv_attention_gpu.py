@@ -127,7 +127,7 @@ def test_split_counters_deterministic_across_calls(torch_dev):
 
 def test_decode_step_llama_shape(torch_dev):
     """One decode step at B=4, H=32, D=128 over 2048 cached positions (the
-    attention shape of the survey's config 5), every (b, h) checked."""
+    benchmark's SDPA head shape), every (b, h) checked."""
     gh = _gh()
     b, h, d, kv_len = 4, 32, 128, 2048
     q = gh.normal((b, 1, h * d), seed=5, tensor_id=0)

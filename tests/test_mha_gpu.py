@@ -129,7 +129,7 @@ def test_incremental_decoding_matches_full_causal_forward(torch_dev):
 
 def test_decode_step_llama_shape(torch_dev):
     """One decode step of a 4096-wide, 32-head layer at B=4 over 2047 cached
-    positions (LLaMA-7B attention at the survey's config-5 head shape)."""
+    positions (LLaMA-7B attention: 32 heads of 128, as in the benchmark's SDPA shape)."""
     import torch
     gh, O = _gh(), _O()
     b, e, h, p = 4, 4096, 32, 2047
