@@ -106,6 +106,25 @@ def test_beta_zero_ignores_nan_output(torch_dev):
     assert (to_np(out) == 8.0).all()
 
 
+@pytest.mark.parametrize("m,n,k,tb", [(4096, 4096, 32, True), (2048, 2048, 32, False), (2100, 2000, 32, True),
+                                      (512, 512, 64, False), (16, 4096, 256, True), (2, 1000, 512, True)])
+def test_beta_zero_ignores_nan_output_every_path(torch_dev, m, n, k, tb):
+    """The same contract on every kernel gfh_sgemm routes to: 256 x 256,
+    128 x 128 with 3 and 2 ring stages, 64 x 64 (direct-to-LDS tiles), the
+    skinny MFMA kernel (16 rows) and the row-dot GEMV (2 rows), with a bias;
+    integer data, so the result is exact."""
+    import torch
+    gh, O = _gh(), _oracle()
+    rng = np.random.default_rng(m + n + k)
+    a = rng.integers(-4, 5, size=(m, k)).astype(np.float32)
+    w = rng.integers(-4, 5, size=(n, k)).astype(np.float32)
+    bias = rng.integers(-4, 5, size=(n,)).astype(np.float32)
+    out = torch.full((m, n), float("nan"), device=torch_dev)
+    b_dev = to_dev(w if tb else np.ascontiguousarray(w.T), torch_dev)
+    gh.sgemm(to_dev(a, torch_dev), b_dev, trans_b=tb, bias=to_dev(bias, torch_dev), out=out)
+    np.testing.assert_array_equal(to_np(out), (O.linear_forward(a, w) + bias).astype(np.float32))
+
+
 def test_linear_known_small(torch_dev):
     """Linear::forward restated: x W^T + b, integer data -> exact."""
     gh, O = _gh(), _oracle()
