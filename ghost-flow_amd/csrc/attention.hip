@@ -33,10 +33,15 @@
 //     wave), and workgroups are issued heaviest query block first.  The
 //     (b,h) index is the fastest grid dimension, so all query blocks of one
 //     (b,h) land on the same XCD and share its K/V in that L2.
+#include <algorithm>
 #include <cmath>
 
 #include "common.hpp"
 #include "kernels.hpp"
+
+// Every f32 product and sum is its own rounding, as in the reference CPU
+// path (no FMA contraction).
+#pragma clang fp contract(off)
 
 namespace gfh {
 namespace {
@@ -287,35 +292,93 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(SdpaParams p) {
 }
 
 // ---- row softmax (Tensor::softmax(-1)) ---------------------------------------
-// One workgroup per row: max fold, sum of exp, then exp(x - max) / sum with a
-// true division, as activation.rs:188-212.  expf is ROCm's full-precision
-// device expf.
+// Per row, as activation.rs:188-212: a max fold from -inf (NaN-ignoring, like
+// f32::max), the sum of exp(x - max), then exp(x - max) / sum with a true
+// division.  expf is ROCm's full-precision device expf.  The sum is taken in
+// a different order than the reference's ascending one (within its rounding
+// bound); the max is exact in any order.
+//
+// Rows of up to 4096 columns (cols % 4 == 0, 16-byte aligned): one wave per
+// row, the row held in registers between the passes, so x is read once and y
+// written once (8 bytes per element); 16-byte loads, NV per lane.
+// Longer rows: one workgroup per row, x read twice.
+// Both walk the rows with a grid stride, so any row count fits one launch.
+constexpr int kSoftmaxGrid = 8 * 1024;  // workgroups: 32 per CU
+
+template <int NV>
+__global__ __launch_bounds__(kThreads) void softmax_rows_wave_kernel(const float *__restrict__ x,
+                                                                     float *__restrict__ y, int64_t rows,
+                                                                     int64_t cols) {
+    const int lane = threadIdx.x & 63;
+    const int64_t nwaves = (int64_t)gridDim.x * (kThreads / 64);
+    for (int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6); row < rows; row += nwaves) {
+        const float *xr = x + row * cols;
+        float *yr = y + row * cols;
+        f32x4 v[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int64_t c = 4 * (lane + 64 * i);
+            v[i] = c < cols ? *reinterpret_cast<const f32x4 *>(xr + c)
+                            : f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) mx = fmaxf(mx, v[i][e]);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        // exp, then a pairwise sum inside the lane (log2(4 NV) levels) and
+        // across the wave: the rounding error grows with the tree depth,
+        // not with the row length.
+        float part[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[i][e] = expf(v[i][e] - mx);
+            part[i] = 4 * (lane + 64 * i) < cols ? (v[i][0] + v[i][1]) + (v[i][2] + v[i][3]) : 0.f;
+        }
+#pragma unroll
+        for (int w = 1; w < NV; w *= 2)
+#pragma unroll
+            for (int i = 0; i + w < NV; i += 2 * w) part[i] += part[i + w];
+        const float sum = wave_sum(part[0]);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int64_t c = 4 * (lane + 64 * i);
+            if (c < cols) *reinterpret_cast<f32x4 *>(yr + c) = v[i] / sum;
+        }
+    }
+}
+
 __global__ __launch_bounds__(kThreads) void softmax_rows_kernel(const float *__restrict__ x, float *__restrict__ y,
-                                                               int64_t cols) {
+                                                               int64_t rows, int64_t cols) {
     __shared__ float red[kThreads / 64];
-    const int64_t row = blockIdx.x;
-    const float *xr = x + row * cols;
-    float *yr = y + row * cols;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+        const float *xr = x + row * cols;
+        float *yr = y + row * cols;
 
-    float mx = -INFINITY;
-    for (int64_t i = threadIdx.x; i < cols; i += kThreads) mx = fmaxf(mx, xr[i]);
+        float mx = -INFINITY;
+        for (int64_t i = threadIdx.x; i < cols; i += kThreads) mx = fmaxf(mx, xr[i]);
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+        if (lane == 0) red[wave] = mx;
+        __syncthreads();
+        mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        __syncthreads();
 
-    float sum = 0.f;
-    for (int64_t i = threadIdx.x; i < cols; i += kThreads) sum += expf(xr[i] - mx);
+        float sum = 0.f;
+        for (int64_t i = threadIdx.x; i < cols; i += kThreads) sum += expf(xr[i] - mx);
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
-    if (lane == 0) red[wave] = sum;
-    __syncthreads();
-    sum = (red[0] + red[1]) + (red[2] + red[3]);
+        for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+        if (lane == 0) red[wave] = sum;
+        __syncthreads();
+        sum = (red[0] + red[1]) + (red[2] + red[3]);
+        __syncthreads();  // red is rewritten by the next row
 
-    for (int64_t i = threadIdx.x; i < cols; i += kThreads) yr[i] = expf(xr[i] - mx) / sum;
+        for (int64_t i = threadIdx.x; i < cols; i += kThreads) yr[i] = expf(xr[i] - mx) / sum;
+    }
 }
 
 template <int DMAX, bool CAUSAL, bool MASK>
@@ -344,7 +407,25 @@ void launch_sdpa_d(const SdpaParams &p, dim3 grid, bool causal, bool mask, bool 
 }  // namespace
 
 int launch_softmax_lastdim(const float *x, float *y, int64_t rows, int64_t cols, hipStream_t s) {
-    hipLaunchKernelGGL(softmax_rows_kernel, dim3((unsigned)rows), dim3(kThreads), 0, s, x, y, cols);
+    if (rows <= 0 || cols <= 0) return GFH_SUCCESS;
+    if (cols % 4 == 0 && cols <= 4096 && aligned16(x) && aligned16(y)) {
+        const int64_t wgs = std::min<int64_t>((rows + kThreads / 64 - 1) / (kThreads / 64), kSoftmaxGrid);
+        const dim3 grid((unsigned)wgs), block(kThreads);
+        const int nv = (int)((cols / 4 + 63) / 64);  // f32x4 per lane
+        if (nv <= 1)
+            hipLaunchKernelGGL(softmax_rows_wave_kernel<1>, grid, block, 0, s, x, y, rows, cols);
+        else if (nv <= 2)
+            hipLaunchKernelGGL(softmax_rows_wave_kernel<2>, grid, block, 0, s, x, y, rows, cols);
+        else if (nv <= 4)
+            hipLaunchKernelGGL(softmax_rows_wave_kernel<4>, grid, block, 0, s, x, y, rows, cols);
+        else if (nv <= 8)
+            hipLaunchKernelGGL(softmax_rows_wave_kernel<8>, grid, block, 0, s, x, y, rows, cols);
+        else
+            hipLaunchKernelGGL(softmax_rows_wave_kernel<16>, grid, block, 0, s, x, y, rows, cols);
+    } else {
+        const dim3 grid((unsigned)std::min<int64_t>(rows, kSoftmaxGrid));
+        hipLaunchKernelGGL(softmax_rows_kernel, grid, dim3(kThreads), 0, s, x, y, rows, cols);
+    }
     return check_launch("softmax_lastdim");
 }
 

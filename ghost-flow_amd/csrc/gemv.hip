@@ -34,6 +34,10 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+// Every f32 product and sum is its own rounding, as in the reference CPU
+// path (no FMA contraction).
+#pragma clang fp contract(off)
+
 namespace gfh {
 namespace {
 
@@ -243,7 +247,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_f32_kernel(GemvParams p) {
 #pragma unroll
         for (int bi = 0; bi < MAXB; ++bi)
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) acc[bi][e] += x[bi] * wf[e];
+            for (int e = 0; e < EPL; ++e) acc[bi][e] = fmaf(x[bi], wf[e], acc[bi][e]);  // explicit FMA
     };
     // The next step is requested before the current one is used.  Every
     // branch is wave-uniform and every block issues its loads
@@ -452,11 +456,16 @@ __global__ __launch_bounds__(64 * NW, (VEC && NW == 4) ? 2 : 1) void gemv_w8_mfm
     // (zero past the slice), and the zero-point pairs.  Split columns of
     // batch rows past MAXB are never written: an MFMA output column depends
     // only on its own B column, and those are not stored.
+    // The prescale comes from the largest FINITE |x s| of the slice, so that
+    // every finite value lands at most at 2^15 (no f16 overflow); an
+    // infinite or NaN x s becomes hi = itself, lo = 0 below, and its products
+    // give inf / NaN as x * dequantize(W) does in the reference.
     float amax = 0.f;
 #pragma unroll
     for (int i = 0; i < kRowsPerThread; ++i)
 #pragma unroll
-        for (int bi = 0; bi < MAXB; ++bi) amax = fmaxf(amax, fabsf(xv[i][bi]));
+        for (int bi = 0; bi < MAXB; ++bi)
+            amax = fmaxf(amax, __builtin_isfinite(xv[i][bi]) ? fabsf(xv[i][bi]) : 0.f);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
     if (lane == 0) amax_red[wave] = amax;
@@ -473,7 +482,7 @@ __global__ __launch_bounds__(64 * NW, (VEC && NW == 4) ? 2 : 1) void gemv_w8_mfm
 #pragma unroll
     for (int w2 = 1; w2 < NW; ++w2) amax = fmaxf(amax, amax_red[w2]);
     int ex = 0;
-    if (amax > 0.f && amax <= 3.4e38f) {
+    if (amax > 0.f) {
         (void)frexpf(amax, &ex);  // amax = f 2^ex, f in [0.5, 1)
         ex = 15 - ex;
     }
@@ -485,8 +494,9 @@ __global__ __launch_bounds__(64 * NW, (VEC && NW == 4) ? 2 : 1) void gemv_w8_mfm
         for (int bi = 0; bi < MAXB; ++bi) {
             const float X = ldexpf(xv[i][bi], ex);
             const _Float16 hi = (_Float16)X;
+            const bool fin = __builtin_isfinite(X);
             xsh[bi * kXStride + r] = hi;
-            xsh[(8 + bi) * kXStride + r] = (_Float16)(X - (float)hi);
+            xsh[(8 + bi) * kXStride + r] = fin ? (_Float16)(X - (float)hi) : (_Float16)0.f;
         }
     }
     __syncthreads();

@@ -24,6 +24,10 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+// Every f32 product and sum is its own rounding, as in the reference CPU
+// path (no FMA contraction).
+#pragma clang fp contract(off)
+
 namespace gfh {
 namespace {
 

@@ -41,6 +41,10 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
+// Every f32 product and sum is its own rounding, as in the reference CPU
+// path (no FMA contraction).
+#pragma clang fp contract(off)
+
 namespace gfh {
 namespace {
 
@@ -135,8 +139,10 @@ __global__ __launch_bounds__(kKvThreads, 2) void kv_attention_kernel(KvParams p)
                 if (m_new == -INFINITY) continue;  // every key so far masked (uniform over the half-wave)
                 const float corr = __expf(m[i] - m_new);
                 const float pj = __expf(s - m_new);
-                l[i] = l[i] * corr + pj;
-                acc[i] = acc[i] * corr + pj * vr[u];
+                // explicit FMAs: this file does not contract a * b + c
+                l[i] = fmaf(l[i], corr, pj);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[i][e] = fmaf(acc[i][e], corr, pj * vr[u][e]);
                 m[i] = m_new;
             }
         }

@@ -16,6 +16,9 @@ use that to check sampled rows of full-size outputs).
 """
 from __future__ import annotations
 
+import os
+from concurrent.futures import ThreadPoolExecutor
+
 import numpy as np
 
 _GOLDEN = np.uint64(0x9E3779B97F4A7C15)
@@ -37,31 +40,53 @@ def _hashes(seed, tensor_id, start, count, j):
         return _mix64((c * np.uint64(2) + np.uint64(j + 1)) * _GOLDEN)
 
 
+def _fill(n, chunk_fn):
+    """Fills a float32 vector of n elements chunk by chunk; chunks are
+    independent (counter-based), so large tensors are filled by a few
+    threads (numpy releases the GIL in these element-wise passes) with the
+    same values as a sequential fill."""
+    out = np.empty(n, np.float32)
+    starts = range(0, n, _CHUNK)
+
+    def one(s):
+        cnt = min(_CHUNK, n - s)
+        out[s:s + cnt] = chunk_fn(s, cnt)
+
+    workers = min(8, os.cpu_count() or 1, len(starts))
+    if workers <= 1:
+        for s in starts:
+            one(s)
+    else:
+        with ThreadPoolExecutor(workers) as pool:
+            list(pool.map(one, starts))
+    return out
+
+
 def uniform(shape, low, high, *, seed=0, tensor_id=0, start=0):
     """U(low, high) as float32, element i drawn from counter start + i."""
     n = int(np.prod(shape)) if len(shape) else 1
-    out = np.empty(n, np.float32)
-    for s in range(0, n, _CHUNK):
-        cnt = min(_CHUNK, n - s)
+
+    def chunk(s, cnt):
         h0 = _hashes(seed, tensor_id, start + s, cnt, 0)
         u = (h0 >> np.uint64(40)).astype(np.float64) * (2.0 ** -24)
-        out[s:s + cnt] = (low + (high - low) * u).astype(np.float32)
-    return out.reshape(shape)
+        return (low + (high - low) * u).astype(np.float32)
+
+    return _fill(n, chunk).reshape(shape)
 
 
 def normal(shape, mean=0.0, std=1.0, *, seed=0, tensor_id=0, start=0):
     """N(mean, std) as float32 via fp64 Box-Muller, element i from counter start + i."""
     n = int(np.prod(shape)) if len(shape) else 1
-    out = np.empty(n, np.float32)
-    for s in range(0, n, _CHUNK):
-        cnt = min(_CHUNK, n - s)
+
+    def chunk(s, cnt):
         h0 = _hashes(seed, tensor_id, start + s, cnt, 0)
         h1 = _hashes(seed, tensor_id, start + s, cnt, 1)
         u1 = ((h0 >> np.uint64(11)).astype(np.float64) + 1.0) * (2.0 ** -53)
         u2 = (h1 >> np.uint64(11)).astype(np.float64) * (2.0 ** -53)
         z = np.sqrt(-2.0 * np.log(u1)) * np.cos(2.0 * np.pi * u2)
-        out[s:s + cnt] = (mean + std * z).astype(np.float32)
-    return out.reshape(shape)
+        return (mean + std * z).astype(np.float32)
+
+    return _fill(n, chunk).reshape(shape)
 
 
 def rows(shape, r0, r1, dist, *, seed=0, tensor_id=0, **kw):

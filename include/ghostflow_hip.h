@@ -178,7 +178,15 @@ GFH_API int gfh_gemv_f32(const float *x, const float *w, float *y, int64_t b,
  * row k has scale s[k] and zero point zp[k] (zp nullable = 0):
  *   y[b, n] = sum_k x[b, k] * ((q[k, n] - zp[k]) * s[k])
  * i.e. DynamicQuantization::get_weights (dequantize_int8, :173-204) followed
- * by Tensor::matmul, without materializing the fp32 weight. b <= 64. */
+ * by Tensor::matmul, without materializing the fp32 weight. b <= 64.
+ * Precision: the products are regrouped as (x[b, k] * s[k]) * (q - zp).  Per
+ * K-slice of up to 1024 rows, x * s is scaled by a power of two so that its
+ * largest finite magnitude lies in [2^14, 2^15), then carried as two f16
+ * (hi + lo: 22 significant bits near the slice maximum; values far below it
+ * keep an absolute error under 2^-39 times that maximum).  The multiply-adds
+ * are exact in fp32 and summed in fp32, so y stays within the fp32 GEMM
+ * bound of the reference but is not bit-identical to it.  An infinite or
+ * NaN x * s is carried unchanged and gives inf / NaN as the reference does. */
 GFH_API int gfh_gemv_w8(const float *x, const int8_t *qw, const float *scales,
                         const int8_t *zero_points, float *y, int64_t b,
                         int64_t k, int64_t n, gfh_stream_t stream);

@@ -28,3 +28,23 @@ def assert_rel(got, ref, tol=1e-4):
     bound = tol * (np.abs(ref) + np.abs(ref).mean())
     bad = err > bound
     assert not bad.any(), (int(bad.sum()), float(err[bad].max()))
+
+
+def rows_parallel(fn, a_rows, *args, workers=None, chunk=32):
+    """fn(a_rows[i:j], *args) over row chunks on a few threads, stacked.
+
+    For oracle functions whose output rows depend only on the same input rows
+    (matmul_blocked, Linear::forward, the INT8 linear): each chunk gives the
+    same bits as one call on all rows.  ctypes releases the GIL during the C
+    call, so the chunks run in parallel."""
+    import os
+    from concurrent.futures import ThreadPoolExecutor
+    a_rows = np.ascontiguousarray(a_rows)
+    n = a_rows.shape[0]
+    if n == 0:
+        return fn(a_rows, *args)
+    workers = workers or min(16, os.cpu_count() or 1)
+    parts = [a_rows[i:i + chunk] for i in range(0, n, chunk)]
+    with ThreadPoolExecutor(workers) as pool:
+        outs = list(pool.map(lambda p: fn(p, *args), parts))
+    return np.concatenate(outs, axis=0)

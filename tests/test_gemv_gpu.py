@@ -141,3 +141,49 @@ def test_split_k_counters_reset_across_calls_and_streams(torch_dev):
             y2 = gh.gemv_w8(dx, dq, ds, dz)
     side.synchronize()
     np.testing.assert_array_equal(to_np(y2), first)
+
+
+def test_gemv_w8_wide_dynamic_range(torch_dev):
+    """One K-slice whose |x s| spans more than 2^30 (log-uniform magnitudes
+    from 2^-16 to 2^15, random signs): the f16 hi + lo carry of x s loses
+    relative precision only far below the slice maximum, so the result must
+    stay within the GEMM bound of the reference's dequantize + matmul."""
+    gh, O = _gh(), _O()
+    rng = np.random.default_rng(21)
+    b, k, n = 3, 1024, 768
+    mag = 2.0 ** rng.uniform(-16, 15, size=(b, k))
+    x = (mag * rng.choice([-1.0, 1.0], size=(b, k))).astype(np.float32)
+    x[0, 5], x[1, 7] = np.float32(2.0 ** 15), np.float32(2.0 ** -16)
+    q = rng.integers(-128, 128, size=(k, n)).astype(np.int8)
+    s = rng.uniform(0.5, 2.0, size=k).astype(np.float32)
+    z = rng.integers(-5, 6, size=k).astype(np.int8)
+    got = to_np(gh.gemv_w8(to_dev(x, torch_dev), to_dev(q, torch_dev), to_dev(s, torch_dev), to_dev(z, torch_dev)))
+    dw = O.dequantize(q, s, z)
+    ref = O.matmul(x, dw)
+    assert np.abs(got - ref).max() <= gemm_tol(k, x, dw)
+
+
+def test_gemv_w8_non_finite_activations(torch_dev):
+    """An inf or NaN activation gives the reference's inf / NaN in its own
+    batch row (x * dequantize(W): +-inf where the weight is non-zero, NaN
+    where it is zero) and leaves the other batch rows of the same strip
+    untouched -- the prescale of the slice ignores non-finite values."""
+    gh, O = _gh(), _O()
+    rng = np.random.default_rng(22)
+    b, k, n = 4, 512, 320
+    x = rng.standard_normal((b, k)).astype(np.float32)
+    x[0, 10] = np.inf
+    x[1, 20] = -np.inf
+    x[2, 30] = np.nan
+    q = rng.integers(-128, 128, size=(k, n)).astype(np.int8)
+    q[10, :5] = 0  # zero weights under the inf: inf * 0 = NaN in the reference
+    s = (2.0 ** rng.integers(-3, 2, size=k)).astype(np.float32)
+    got = to_np(gh.gemv_w8(to_dev(x, torch_dev), to_dev(q, torch_dev), to_dev(s, torch_dev)))
+    dw = O.dequantize(q, s, np.zeros(k, np.int8))
+    ref = O.matmul(x, dw)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+    np.testing.assert_array_equal(np.isinf(got), np.isinf(ref))
+    fin = np.isfinite(ref)
+    np.testing.assert_array_equal(got[np.isinf(ref)], ref[np.isinf(ref)])
+    assert np.abs(got[fin] - ref[fin]).max() <= gemm_tol(k, x[3], dw)
+    assert np.isfinite(ref[3]).all()

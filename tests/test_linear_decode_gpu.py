@@ -109,3 +109,32 @@ def test_decode_linear_4096(torch_dev, m):
     got = to_np(gh.linear(to_dev(x, torch_dev), to_dev(w, torch_dev), to_dev(bias, torch_dev)))
     ref = O.linear_forward(x, w, bias)
     assert np.abs(got - ref).max() <= gemm_tol(4096, x, w)
+
+
+@pytest.mark.parametrize("m,k,n,tb", [(1, 300, 200, True), (3, 1000, 130, True), (4, 4096, 512, True),
+                                      (16, 520, 300, True), (64, 1024, 260, True), (300, 256, 520, True),
+                                      (2, 300, 200, False), (300, 256, 520, False)])
+def test_epilogue_rounding_non_integer(torch_dev, m, k, n, tb):
+    """alpha, beta and bias with non-integer values (0.7, -1.3, random
+    bias): the epilogue is alpha * acc, then + beta * C, then + bias, each a
+    separately rounded f32 operation -- no FMA -- on every route (row-dot
+    GEMV at m <= 4, skinny MFMA, tiles).  Checked bit for bit against the
+    same route run with alpha = 1, beta = 0 and no bias, rounded on the host
+    in that order."""
+    import torch
+    gh = _gh()
+    rng = np.random.default_rng(m * 13 + k + n)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    c0 = rng.standard_normal((m, n)).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32)
+    dx = to_dev(x, torch_dev)
+    dw = to_dev(w if tb else np.ascontiguousarray(w.T), torch_dev)
+    acc = to_np(gh.sgemm(dx, dw, trans_b=tb))
+    out = to_dev(c0, torch_dev)
+    gh.sgemm(dx, dw, trans_b=tb, alpha=0.7, beta=-1.3, bias=to_dev(bias, torch_dev), out=out)
+    a32, b32 = np.float32(0.7), np.float32(-1.3)
+    ref = ((a32 * acc).astype(np.float32) + (b32 * c0).astype(np.float32)).astype(np.float32)
+    ref = (ref + bias).astype(np.float32)
+    np.testing.assert_array_equal(to_np(out).view(np.uint32), ref.view(np.uint32))
+    torch.cuda.synchronize()

@@ -6,7 +6,7 @@ reference's executable composite (dequantize both operands, fp32 matmul)."""
 import numpy as np
 import pytest
 
-from _util import gemm_tol, to_dev, to_np
+from _util import gemm_tol, rows_parallel, to_dev, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -199,6 +199,41 @@ def test_qlinear_config3_w11008_sampled(torch_dev):
         rows = np.arange(m) if m <= 16 else np.random.default_rng(m).choice(m, 16, replace=False)
         ry, _ = O.qlinear_i8(rqx[rows], rsx, np.atleast_1d(rzx), False, rqw, rsw)
         assert _same_f32(to_np(y)[rows], ry)
+
+
+def test_qlinear_config3_m4096_w11008(torch_dev):
+    """Config 3 at M = 4096, as the bench runs it: W [11008, 4096] ~
+    N(0, 0.02) quantized per channel (symmetric), x [4096, 4096] ~ N(0, 1)
+    quantized per tensor (asymmetric, DynamicQuantization::
+    quantize_activation), the 256 x 256 tile kernel.  Every int32
+    accumulator against the exact integer product (fp64 holds it exactly:
+    |acc| < 2^31), and the output-only call (the bench's variant, no
+    accumulator buffer) bit-exact to the oracle on 256 sampled rows plus the
+    first and last."""
+    gh, O = _gh(), _O()
+    m, n, k = 4096, 11008, 4096
+    w = gh.normal((n, k), 0.0, 0.02, seed=0, tensor_id=1)
+    x = gh.normal((m, k), seed=0, tensor_id=0)
+    qw, sw, _ = gh.quantize_per_channel(to_dev(w, torch_dev), True)
+    qx, sx, zx = gh.quantize_per_tensor(to_dev(x, torch_dev), False)
+    rqw, rsw, _ = O.quantize_per_channel(w, True)
+    rqx, rsx, rzx = O.quantize_per_tensor(x, False)
+    del w, x
+    np.testing.assert_array_equal(to_np(qw), rqw)
+    np.testing.assert_array_equal(to_np(qx), rqx)
+    assert _same_f32(to_np(sx), np.atleast_1d(rsx)) and int(to_np(zx)[0]) == int(rzx)
+    rowsum = gh.qweight_rowsum(qw)
+    y_only, none = gh.qlinear(qx, sx, zx, qw, sw, w_rowsum=rowsum, want_acc=False)
+    assert none is None
+    _, acc = gh.qlinear(qx, sx, zx, qw, sw, w_rowsum=rowsum, want_y=False, want_acc=True)
+    exact = (rqx.astype(np.float64) - float(rzx)) @ rqw.astype(np.float64).T
+    np.testing.assert_array_equal(to_np(acc), exact.astype(np.int32))
+    del exact, acc
+    rows = np.random.default_rng(3).choice(np.arange(1, m - 1), 256, replace=False)
+    rows = np.concatenate([[0, m - 1], rows])
+    zxa = np.atleast_1d(rzx)
+    ry = rows_parallel(lambda r: O.qlinear_i8(r, rsx, zxa, False, rqw, rsw, want_acc=False)[0], rqx[rows])
+    assert _same_f32(to_np(y_only)[rows], ry)
 
 
 def test_qlinear_4096_cube_sampled(torch_dev):

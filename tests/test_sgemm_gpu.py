@@ -8,7 +8,7 @@ max|err| <= 1e-4 * sqrt(K) * max|a| * max|b| (the north-star GEMM bound).
 import numpy as np
 import pytest
 
-from _util import gemm_tol, to_dev, to_np
+from _util import gemm_tol, rows_parallel, to_dev, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -138,16 +138,16 @@ def test_linear_known_small(torch_dev):
 
 def test_config2_linear_4096_sampled_rows(torch_dev):
     """Config 2 at full size: x [4096,4096] ~ N(0,1), W, b ~ U(-1/64,1/64).
-    Output rows are independent, so 48 sampled rows are checked exactly
-    against the oracle's Linear::forward on those rows."""
+    Output rows are independent, so 256 sampled rows (plus the first and
+    last) are checked against the oracle's Linear::forward on those rows."""
     gh, O = _gh(), _oracle()
     x = gh.normal((4096, 4096), seed=0, tensor_id=0)
     w = gh.uniform((4096, 4096), -1 / 64, 1 / 64, seed=0, tensor_id=1)
     bias = gh.uniform((4096,), -1 / 64, 1 / 64, seed=0, tensor_id=2)
     y = to_np(gh.linear(to_dev(x, torch_dev), to_dev(w, torch_dev), to_dev(bias, torch_dev)))
-    rows = np.random.default_rng(0).choice(4096, 48, replace=False)
+    rows = np.random.default_rng(0).choice(np.arange(1, 4095), 256, replace=False)
     rows = np.concatenate([[0, 4095], rows])
-    ref = O.linear_forward(x[rows], w, bias)
+    ref = rows_parallel(O.linear_forward, x[rows], w, bias)
     err = np.abs(y[rows] - ref).max()
     assert err <= gemm_tol(4096, x, w), err
 
@@ -165,15 +165,21 @@ def test_batched_modulo_semantics(torch_dev):
     np.testing.assert_array_equal(got, ref)
 
 
-@pytest.mark.parametrize("n", [2048])
+@pytest.mark.parametrize("n", [2048, 4096, 8192])
 def test_square_sweep_sampled_rows(torch_dev, n):
+    """The config-2 square sweep, A, B [n, n] ~ N(0,1) from seed 0 through
+    Tensor::matmul (NN): 256 sampled rows of C (plus the first and last)
+    against the oracle's matmul_blocked, within the GEMM bound.  Rows of C
+    are independent, so a row subset is checked exactly as the full C."""
     gh, O = _gh(), _oracle()
     a = gh.normal((n, n), seed=0, tensor_id=0)
     b = gh.normal((n, n), seed=0, tensor_id=1)
     c = to_np(gh.matmul(to_dev(a, torch_dev), to_dev(b, torch_dev)))
-    rows = np.random.default_rng(1).choice(n, 32, replace=False)
-    ref = O.matmul(a[rows], b)
-    assert np.abs(c[rows] - ref).max() <= gemm_tol(n, a, b)
+    rows = np.random.default_rng(1).choice(np.arange(1, n - 1), 256, replace=False)
+    rows = np.concatenate([[0, n - 1], rows])
+    ref = rows_parallel(O.matmul, a[rows], b)
+    err = np.abs(c[rows] - ref).max()
+    assert err <= gemm_tol(n, a, b), err
 
 
 def test_k_zero_gives_bias(torch_dev):
@@ -220,8 +226,8 @@ def test_big_tiles_nn_random(torch_dev, n):
     a = rng.standard_normal((n, n)).astype(np.float32)
     b = rng.standard_normal((n, n)).astype(np.float32)
     got = to_np(gh.sgemm(to_dev(a, torch_dev), to_dev(b, torch_dev)))
-    rows = rng.choice(n, size=48, replace=False)
-    ref = O.matmul(a[rows], b)
+    rows = rng.choice(n, size=256, replace=False)
+    ref = rows_parallel(O.matmul, a[rows], b)
     assert np.abs(got[rows] - ref).max() <= gemm_tol(n, a, b)
 
 
