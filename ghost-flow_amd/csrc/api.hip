@@ -330,6 +330,23 @@ GFH_API int gfh_gemv_w8(const float *x, const int8_t *qw, const float *scales, c
     });
 }
 
+GFH_API int gfh_gemv_w8_noalloc(const float *x, const int8_t *qw, const float *scales, const int8_t *zero_points,
+                                float *y, int64_t b, int64_t k, int64_t n, gfh_stream_t stream) {
+    return guarded([&]() -> int {
+        if (b < 0 || k < 0 || n < 0 || b > 64 || k > kMaxDim || n > kMaxDim)
+            return set_error(GFH_INVALID_SHAPE, "gemv_w8_noalloc: b=%lld (<= 64) k=%lld n=%lld out of range",
+                             (long long)b, (long long)k, (long long)n);
+        if (b == 0 || n == 0) return GFH_SUCCESS;
+        GFH_TRY(require_range(x, (size_t)b * (size_t)k * 4, "x"));
+        GFH_TRY(require_range(qw, (size_t)k * (size_t)n, "qw"));
+        GFH_TRY(require_range(scales, (size_t)k * 4, "scales"));
+        GFH_TRY(optional_range(zero_points, (size_t)k, "zero_points"));
+        GFH_TRY(require_range(y, (size_t)b * (size_t)n * 4, "y"));
+        GFH_TRY(ensure_init());
+        return launch_gemv_w8_noalloc(x, qw, scales, zero_points, y, b, k, n, as_stream(stream));
+    });
+}
+
 GFH_API int gfh_softmax_lastdim_f32(const float *x, float *y, int64_t rows, int64_t cols, gfh_stream_t stream) {
     return guarded([&]() -> int {
         if (rows < 0 || cols < 0 || rows > kMaxDim || cols > kMaxDim)

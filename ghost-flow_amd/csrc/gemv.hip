@@ -29,6 +29,7 @@
 //    partials in slice order and writes y -- deterministic, one launch.  The
 //    counter is returned to 0 by that last workgroup.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "common.hpp"
@@ -641,17 +642,38 @@ int64_t choose_kslice_f32(int64_t nstrips, int64_t k, int64_t nb, int64_t max_ro
     return std::min<int64_t>(ks, max_rows);
 }
 
+// Where the split-K partial strips and arrival counters of a call live:
+// either the per-stream buffers the library allocates on demand (fixed ==
+// false), or a fixed region that the allocation-free entry point owns.
+struct SplitScratch {
+    bool fixed = false;
+    float *part = nullptr;
+    size_t part_bytes = 0;
+    int *counters = nullptr;
+    size_t ncounters = 0;
+};
+
 // Sets the slicing of one batch group and, for more than one slice, its
-// per-stream partial workspace and arrival counters.  Groups of a call run
-// one after another on the stream, so they share the workspace.
-int set_slices(GemvParams &q, int64_t kslice, hipStream_t s) {
+// partial workspace and arrival counters.  Groups of a call run one after
+// another on the stream, so they share the workspace.
+int set_slices(GemvParams &q, int64_t kslice, hipStream_t s, const SplitScratch &sc) {
     q.kslice = kslice;
     q.slices = q.k > 0 ? (q.k + kslice - 1) / kslice : 1;
     q.part = nullptr;
     q.counters = nullptr;
     if (q.slices > 1) {
+        const size_t part_bytes = sizeof(float) * (size_t)(q.slices * q.b * q.n);
+        if (sc.fixed) {
+            if (part_bytes > sc.part_bytes || (size_t)q.nstrips > sc.ncounters)
+                return set_error(GFH_INVALID_SHAPE, "gemv_w8: %zu bytes of partials and %lld counters exceed the "
+                                 "fixed scratch (%zu bytes, %zu counters)", part_bytes, (long long)q.nstrips,
+                                 sc.part_bytes, sc.ncounters);
+            q.part = sc.part;
+            q.counters = sc.counters;
+            return GFH_SUCCESS;
+        }
         void *ws = nullptr;
-        GFH_TRY(stream_workspace(s, sizeof(float) * (size_t)(q.slices * q.b * q.n), &ws));
+        GFH_TRY(stream_workspace(s, part_bytes, &ws));
         q.part = static_cast<float *>(ws);
         GFH_TRY(stream_counters(s, (size_t)q.nstrips, &q.counters));
     }
@@ -691,7 +713,7 @@ int launch_gemv_f32(const float *x, const float *w, float *y, int64_t b, int64_t
         // see kWideRows8), instead of 4 slices of 1024 rows.
         if (maxb == 8 && vec && k > 0 && k <= kWideRows8 && q.nstrips >= 192 && q.nstrips <= 256)
             max_rows = kWideRows8;
-        GFH_TRY(set_slices(q, k > 0 ? choose_kslice_f32(q.nstrips, k, q.b, max_rows) : 32, s));
+        GFH_TRY(set_slices(q, k > 0 ? choose_kslice_f32(q.nstrips, k, q.b, max_rows) : 32, s, SplitScratch{}));
         if (maxb == 1)
             launch_f32<1>(q, vec, s);
         else if (maxb == 2)
@@ -704,8 +726,10 @@ int launch_gemv_f32(const float *x, const float *w, float *y, int64_t b, int64_t
     });
 }
 
-int launch_gemv_w8(const float *x, const int8_t *qw, const float *scales, const int8_t *zps, float *y, int64_t b,
-                   int64_t k, int64_t n, hipStream_t s) {
+namespace {
+
+int gemv_w8_common(const float *x, const int8_t *qw, const float *scales, const int8_t *zps, float *y, int64_t b,
+                   int64_t k, int64_t n, hipStream_t s, const SplitScratch &sc) {
     GemvParams p{};
     p.w = qw;
     p.scales = scales;
@@ -715,7 +739,7 @@ int launch_gemv_w8(const float *x, const int8_t *qw, const float *scales, const 
     p.nstrips = (n + kStripBytes - 1) / kStripBytes;
     const bool vec = n % 16 == 0 && aligned16(qw);
     return for_batch_groups(p, x, y, b, [&](GemvParams &q) {
-        GFH_TRY(set_slices(q, k > 0 ? choose_kslice_w8(q.nstrips, k) : 128, s));
+        GFH_TRY(set_slices(q, k > 0 ? choose_kslice_w8(q.nstrips, k) : 128, s, sc));
         // At most one workgroup per CU: 8 waves each, so that twice the weight
         // blocks are in flight while the activations are staged (at
         // [4096, 14336] and 1024-row slices, 1-8 batch rows: 16.6-18.2 us
@@ -740,6 +764,97 @@ int launch_gemv_w8(const float *x, const int8_t *qw, const float *scales, const 
             go(std::integral_constant<int, 8>{});
         return check_launch("gemv_w8");
     });
+}
+
+// ---- the allocation-free variant ---------------------------------------------
+//
+// Its split-K partials and arrival counters live in `scratch`, a static
+// device array (each GPU the library runs on holds its own copy, at its own
+// address, until the process ends).  Host code never uses the array's name
+// as an address: it keeps the device address hipGetSymbolAddress returns,
+// per device, taken on the entry point's first call on that device.
+constexpr size_t kNoAllocCounters = 16384;           // arrival counters (int32)
+constexpr size_t kNoAllocPartBytes = (size_t)8 << 20;  // split-K partial strips
+constexpr size_t kNoAllocBytes = kNoAllocCounters * sizeof(int) + kNoAllocPartBytes;
+constexpr int kMaxDevices = 64;
+
+std::mutex g_noalloc_mu;
+void *g_noalloc_ptr[kMaxDevices] = {};
+
+__global__ void zero_ints_kernel(int *p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0;
+}
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+namespace {
+
+// Device address of this device's copy of `scratch`.
+int noalloc_scratch(void **out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return set_error(GFH_COMPUTATION_FAILED, "hipGetDevice failed");
+    }
+    if (dev < 0 || dev >= kMaxDevices) return set_error(GFH_COMPUTATION_FAILED, "device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_noalloc_mu);
+    if (!g_noalloc_ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            (void)hipGetLastError();
+            return set_error(GFH_COMPUTATION_FAILED, "hipGetSymbolAddress(scratch) failed: %s",
+                             hipGetErrorString(e));
+        }
+        g_noalloc_ptr[dev] = p;
+    }
+    *out = g_noalloc_ptr[dev];
+    return GFH_SUCCESS;
+}
+
+}  // namespace
+
+int launch_gemv_w8(const float *x, const int8_t *qw, const float *scales, const int8_t *zps, float *y, int64_t b,
+                   int64_t k, int64_t n, hipStream_t s) {
+    return gemv_w8_common(x, qw, scales, zps, y, b, k, n, s, SplitScratch{});
+}
+
+int launch_gemv_w8_noalloc(const float *x, const int8_t *qw, const float *scales, const int8_t *zps, float *y,
+                           int64_t b, int64_t k, int64_t n, hipStream_t s) {
+    // Sizes first: the first batch group (the largest) needs the most, and
+    // nothing is launched when it does not fit.
+    const int64_t nstrips = (n + kStripBytes - 1) / kStripBytes;
+    const int64_t kslice = k > 0 ? choose_kslice_w8(nstrips, k) : 128;
+    const int64_t slices = k > 0 ? (k + kslice - 1) / kslice : 1;
+    const int64_t b0 = b < 8 ? b : 8;
+    if (slices > 1 && ((size_t)nstrips > kNoAllocCounters ||
+                       sizeof(float) * (size_t)slices * (size_t)b0 * (size_t)n > kNoAllocPartBytes))
+        return set_error(GFH_INVALID_SHAPE,
+                         "gemv_w8_noalloc: k=%lld n=%lld needs %lld slices x %lld rows x %lld columns of partials "
+                         "and %lld counters; the fixed scratch holds %zu bytes of partials and %zu counters",
+                         (long long)k, (long long)n, (long long)slices, (long long)b0, (long long)n,
+                         (long long)nstrips, kNoAllocPartBytes, kNoAllocCounters);
+    void *base = nullptr;
+    GFH_TRY(noalloc_scratch(&base));
+    SplitScratch sc;
+    sc.fixed = true;
+    sc.counters = static_cast<int *>(base);
+    sc.ncounters = kNoAllocCounters;
+    sc.part = reinterpret_cast<float *>(static_cast<unsigned char *>(base) + kNoAllocCounters * sizeof(int));
+    sc.part_bytes = kNoAllocPartBytes;
+    if (slices > 1) {
+        // The counters must start at zero.  A completed call leaves them at
+        // zero, but the array keeps whatever the last call on this GPU left,
+        // so they are cleared here, by a kernel (no memset node, so a caller
+        // may capture the call in a graph).
+        const unsigned grid = (unsigned)std::min<int64_t>((nstrips + 255) / 256, 64);
+        hipLaunchKernelGGL(zero_ints_kernel, dim3(grid), dim3(256), 0, s, sc.counters, nstrips);
+        GFH_TRY(check_launch("gemv_w8_noalloc (counter clear)"));
+    }
+    return gemv_w8_common(x, qw, scales, zps, y, b, k, n, s, sc);
 }
 
 }  // namespace gfh

@@ -87,6 +87,10 @@ int launch_qlinear_swiglu_i8(const QSwigluDesc &d, int *npart, hipStream_t s);
 int launch_gemv_f32(const float *x, const float *w, float *y, int64_t b, int64_t k, int64_t n, hipStream_t s);
 int launch_gemv_w8(const float *x, const int8_t *qw, const float *scales, const int8_t *zps, float *y, int64_t b,
                    int64_t k, int64_t n, hipStream_t s);
+// Same computation with its split-K scratch in a static device array: no
+// allocation.  Sizes beyond that array are rejected before any launch.
+int launch_gemv_w8_noalloc(const float *x, const int8_t *qw, const float *scales, const int8_t *zps, float *y,
+                           int64_t b, int64_t k, int64_t n, hipStream_t s);
 
 // attention.hip
 int launch_softmax_lastdim(const float *x, float *y, int64_t rows, int64_t cols, hipStream_t s);

@@ -55,6 +55,7 @@ SIGNATURES = {
     "gfh_qlinear_i8": (_i, [_p, _p, _p, _i, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "gfh_gemv_f32": (_i, [_p, _p, _p, _i64, _i64, _i64, _p]),
     "gfh_gemv_w8": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
+    "gfh_gemv_w8_noalloc": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "gfh_softmax_lastdim_f32": (_i, [_p, _p, _i64, _i64, _p]),
     "gfh_sdpa_f32": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f, _i, _p, _i64, _p]),
     "gfh_kv_attention_f32": (_i, [_p, _i64, _p, _p, _i64, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _f,

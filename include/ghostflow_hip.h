@@ -191,6 +191,24 @@ GFH_API int gfh_gemv_w8(const float *x, const int8_t *qw, const float *scales,
                         const int8_t *zero_points, float *y, int64_t b,
                         int64_t k, int64_t n, gfh_stream_t stream);
 
+/* Allocation-free gfh_gemv_w8.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory -- code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  Same
+ * arguments, kernels and results as gfh_gemv_w8 (bit for bit); it calls no
+ * hipMalloc / hipFree / allocating library routine.  Its split-K partials
+ * and arrival counters live in a static device array of 8 MiB + 64 KiB that
+ * each GPU holds until the process ends.  Limit: a call whose K is split
+ * needs 4 * slices * min(b, 8) * n bytes of partials (at most 8 MiB) and
+ * ceil(n / 256) counters (at most 16384); larger calls return
+ * GFH_INVALID_SHAPE before launching anything.  (W [4096, 14336] at b = 8
+ * needs 1.8 MiB; W [11008, 4096]-shaped [4096, 11008] at b = 8, 2.8 MiB.)
+ * Every call on one GPU shares that array: calls that overlap on one GPU
+ * (other streams, other threads) race and must be serialized by the caller. */
+GFH_API int gfh_gemv_w8_noalloc(const float *x, const int8_t *qw,
+                                const float *scales, const int8_t *zero_points,
+                                float *y, int64_t b, int64_t k, int64_t n,
+                                gfh_stream_t stream);
+
 /* ---- attention ----------------------------------------------------------- */
 
 /* Row softmax over the last dimension (Tensor::softmax(-1),
