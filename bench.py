@@ -61,7 +61,8 @@ def parse_args():
     ap.add_argument("--cpu-rows", type=int, default=768,
                     help="rows of x in the CPU-baseline sample (of 4096)")
     ap.add_argument("--only", default="",
-                    help="comma list of components to run (sgemm,qlinear,gemv,sdpa,decode,swiglu,io); "
+                    help="comma list of components to run (sgemm,qlinear,gemv,sdpa,flash,softmax,quantize,"
+                         "decode,swiglu,io); "
                          "used for focused profiling")
     ap.add_argument("--detail", default="", help="also write the full result JSON to this file")
     ap.add_argument("--calib-copy", action="store_true",
@@ -83,12 +84,35 @@ class Lib:
             raise RuntimeError(f"{what}: status {rc}: {self.L.gfh_last_error().decode()}")
 
 
+# After any idle gap the GPU's clock needs ~25 ms of sustained work to reach
+# its steady state (measured on this MI355X with back-to-back 4096^3 fp32
+# GEMMs: 1140 us per launch right after 0.5 s idle, falling to 930 us after
+# ~25 launches).  Every timing below therefore starts after at least
+# SETTLE_S of back-to-back work.
+SETTLE_S = 0.06
+
+
+def settle(torch, fn, seconds=SETTLE_S):
+    """Back-to-back calls of fn until `seconds` of wall time have passed."""
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    i = 0
+    while True:
+        for _ in range(4):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= seconds:
+            return
+
+
 def event_time_ms(torch, fn, reps, warmup=3):
     """Average ms per call of fn() over `reps` back-to-back calls, timed
-    with events on torch's current stream (the stream every call uses)."""
+    with events on torch's current stream (the stream every call uses),
+    after the clock has settled."""
     for _ in range(warmup):
         fn(0)
-    torch.cuda.synchronize()
+    settle(torch, fn)
     s = torch.cuda.Event(enable_timing=True)
     e = torch.cuda.Event(enable_timing=True)
     s.record()
@@ -120,6 +144,14 @@ def bench_linear(lib, torch, args):
         if rc:
             lib.check(rc, "gfh_sgemm")
 
+    # Clock settle: ~60 ms of a separate 4096^3 GEMM on other buffers (the
+    # GPU idled while the inputs were generated on the host), then the W
+    # warmup steps and the K timed steps of the headline itself.
+    sa = torch.randn((M, K), device=dev)
+    sb = torch.randn((K, N), device=dev)
+    sc = torch.empty((M, N), device=dev)
+    settle(torch, lambda _: L.gfh_sgemm(0, 0, M, N, K, 1.0, sa.data_ptr(), K, sb.data_ptr(), N, 0.0,
+                                        sc.data_ptr(), N, None, stream))
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -187,6 +219,350 @@ def cpu_baseline_linear(rows):
                    f"extrapolated to 4096 rows: {t_full:.1f}s per forward"),
         "seconds_measured": t_gather + t_mm + t_bias,
     }
+
+
+# ---------------------------------------------------------------------------
+# the reference CPU path of each component (oracle restatement, this host)
+# ---------------------------------------------------------------------------
+
+class CpuRef:
+    """Times the oracle's restatement of the reference CPU path (oracle/
+    gf_oracle.c) for one component, threaded as the reference is: matmul,
+    batched matmul, the view gather, quantize / dequantize and the mask on
+    one thread (matmul.rs:101,147; quantization.rs:93,119; attention.rs:
+    51-64), softmax and mul_scalar on a pool of nproc threads over rows
+    (rayon's default pool: activation.rs:180-213, arithmetic.rs:69-72).
+
+    Large workloads are timed on a bounded sample of independent rows or
+    (b,h) slices -- identical work per row -- and scaled to the full shape
+    ("extrapolated" in the sample text).  Tensor copies the reference makes
+    (data_f32 of each operand, from_slice of the output) are memcpy's of the
+    full tensors and are timed in full."""
+
+    RATE = 14e9        # rough single-thread matmul_blocked FLOP/s, only to size samples
+    TARGET_S = 0.4     # seconds of matmul per sample
+
+    def __init__(self):
+        import numpy as np
+        from oracle import oracle as O
+        self.np = np
+        self.O = O
+        self.L = O.lib()
+        self.nproc = os.cpu_count() or 1
+        self.rng = np.random.default_rng(0)
+        self._warm()
+
+    def _warm(self):
+        """One small call of every primitive, so no sample pays first-use costs."""
+        np, L = self.np, self.L
+        self._copy_s(1 << 20)
+        a = self._randn((8, 64))
+        b = self._randn((64, 64))
+        c = np.empty((8, 64), np.float32)
+        L.gfo_matmul_blocked(a, b, c, 8, 64, 64)
+        L.gfo_transpose_last2(b, np.empty((64, 64), np.float32), 1, 64, 64)
+        q = np.empty(512, np.int8)
+        s_, z_ = C.c_float(), C.c_int8()
+        L.gfo_quantize_per_tensor(a.reshape(-1), 512, 0, q, C.byref(s_), C.byref(z_))
+        d = np.empty(512, np.float32)
+        L.gfo_dequantize(q, 8, 64, np.ones(8, np.float32), np.zeros(8, np.int8), 8, d)
+        y = np.empty_like(a)
+        self._par_rows(8, lambda r0, r1: L.gfo_softmax_lastdim(a.reshape(-1)[r0 * 64:r1 * 64],
+                                                                y.reshape(-1)[r0 * 64:r1 * 64], r1 - r0, 64))
+
+    # -- helpers ------------------------------------------------------------
+    @staticmethod
+    def _t(fn):
+        t0 = time.perf_counter()
+        fn()
+        return time.perf_counter() - t0
+
+    def _randn(self, shape):
+        """N(0,1)-distributed f32 data: a 1 Mi-element random block repeated
+        (the timed loops are data-independent; this only keeps the set-up of
+        large operands fast)."""
+        np = self.np
+        n = int(np.prod(shape))
+        if not hasattr(self, "_block"):
+            self._block = self.rng.standard_normal(1 << 20, dtype=np.float32)
+        reps = -(-n // self._block.size)
+        return np.tile(self._block, reps)[:n].reshape(shape).copy() if reps > 1 else \
+            self._block[:n].reshape(shape).copy()
+
+    def _copy_s(self, nbytes):
+        """One memcpy of nbytes (data_f32 / from_slice of a contiguous tensor)."""
+        np = self.np
+        src = np.ones(nbytes // 4, np.float32)
+        dst = np.empty_like(src)
+        dst[:1] = 0  # touch
+        return self._t(lambda: np.copyto(dst, src))
+
+    def _par_rows(self, rows, fn):
+        """fn(r0, r1) over row chunks on nproc threads (rayon's pool)."""
+        from concurrent.futures import ThreadPoolExecutor
+        n = self.nproc
+        step = max(1, -(-rows // (4 * n)))
+        chunks = [(r, min(r + step, rows)) for r in range(0, rows, step)]
+        with ThreadPoolExecutor(n) as pool:
+            list(pool.map(lambda c: fn(*c), chunks))
+
+    def _sample_rows(self, m, k, n):
+        return int(max(1, min(m, round(self.TARGET_S * self.RATE / (2.0 * k * n)))))
+
+    def matmul_s(self, m, k, n, b_transposed=False):
+        """Tensor::matmul [m,k] x [k,n] (a W^T view when b_transposed, as
+        Linear::forward): data_f32 of both operands (the W^T view is the
+        gather), matmul_blocked, from_slice of the output.  Returns (seconds
+        for the full shape, rows timed, seconds measured)."""
+        np, L = self.np, self.L
+        rows = self._sample_rows(m, k, n)
+        a = self._randn((rows, k))
+        t_copy = self._copy_s(4 * m * k) + self._copy_s(4 * m * n)
+        if b_transposed:
+            w = self._randn((n, k))
+            bt = np.empty((k, n), np.float32)
+            t_b = self._t(lambda: L.gfo_transpose_last2(w, bt, 1, n, k))
+        else:
+            bt = self._randn((k, n))
+            t_b = self._copy_s(4 * k * n)
+        c = np.empty((rows, n), np.float32)
+        t_mm = self._t(lambda: L.gfo_matmul_blocked(a, bt, c, rows, k, n))
+        full = t_copy + t_b + t_mm * (m / rows)
+        return full, rows, t_copy + t_b + t_mm
+
+    def result(self, value, unit, seconds_full, sample, cores=1, **extra):
+        r = {"value": value, "unit": unit, "cores": cores, "kind": "port", "sample": sample,
+             "seconds_full": seconds_full}
+        r.update(extra)
+        return r
+
+    # -- components ---------------------------------------------------------
+    def sgemm(self, n):
+        full, rows, meas = self.matmul_s(n, n, n)
+        fl = 2.0 * n ** 3
+        ext = "extrapolated" if rows < n else "full"
+        return self.result(fl / full / 1e12, "TFLOP/s", full,
+                           f"oracle Tensor::matmul {n}^3 (2 operand copies + matmul_blocked + output copy); "
+                           f"matmul_blocked on {rows}/{n} rows, {ext}: {full:.2f} s per call ({meas:.2f} s measured)")
+
+    def qlinear(self, m, n, k, per_tensor=True):
+        """The reference's executable INT8 path: DynamicQuantization::
+        quantize_activation (per tensor, asymmetric) of x, dequantize of x
+        and get_weights (dequantize of W, per channel), then the fp32 layer
+        x . W^T (gather + matmul_blocked).  Quantization is reported on its
+        own (quantize_s) beside the dequantize and matmul parts."""
+        np, L = self.np, self.L
+        x = self._randn((m, k))
+        qx = np.empty((m, k), np.int8)
+        sx, zx = C.c_float(), C.c_int8()
+        if per_tensor:
+            t_q = self._t(lambda: L.gfo_quantize_per_tensor(x.reshape(-1), m * k, 0, qx.reshape(-1),
+                                                             C.byref(sx), C.byref(zx)))
+            sxa, zxa = np.array([sx.value], np.float32), np.array([zx.value], np.int8)
+        else:
+            sxa, zxa = np.empty(m, np.float32), np.empty(m, np.int8)
+            t_q = self._t(lambda: L.gfo_quantize_per_channel(x.reshape(-1), m, k, 1, qx.reshape(-1), sxa, zxa))
+        dx = np.empty((m, k), np.float32)
+        t_dqx = self._t(lambda: L.gfo_dequantize(qx.reshape(-1), m, k, sxa, zxa, sxa.size, dx.reshape(-1)))
+        qw = (self._randn((n, k)) * 40).astype(np.int8)
+        sw = (self.rng.random(n, dtype=np.float32) * 1e-3).astype(np.float32)
+        zw = np.zeros(n, np.int8)
+        dw = np.empty((n, k), np.float32)
+        t_dqw = self._t(lambda: L.gfo_dequantize(qw.reshape(-1), n, k, sw, zw, n, dw.reshape(-1)))
+        del dw, qw
+        t_lin, rows, _ = self.matmul_s(m, k, n, b_transposed=True)
+        full = t_q + t_dqx + t_dqw + t_lin
+        ops = 2.0 * m * n * k
+        ext = "extrapolated" if rows < m else "full"
+        return self.result(ops / full / 1e12, "TOP/s", full,
+                           f"oracle quantize_activation + dequantize(x) + get_weights (dequantize W [{n},{k}]) + "
+                           f"Linear x.W^T (gather + matmul_blocked on {rows}/{m} rows, {ext}); "
+                           f"{full:.3f} s per call",
+                           quantize_s=t_q, dequantize_s=t_dqx + t_dqw, matmul_s=t_lin)
+
+    def gemv(self, bsz, int8, k=4096, n=14336):
+        """Tensor::matmul x [B,K] . W [K,N] (int8: get_weights, i.e. dequantize
+        of the [K,N] codes per K row, first), timed in full."""
+        np, L = self.np, self.L
+        t_deq = 0.0
+        if int8:
+            qw = (self._randn((k, n)) * 40).astype(np.int8)
+            sw = (self.rng.random(k, dtype=np.float32) * 1e-3).astype(np.float32)
+            zw = np.zeros(k, np.int8)
+            w = np.empty((k, n), np.float32)
+            t_deq = self._t(lambda: L.gfo_dequantize(qw.reshape(-1), k, n, sw, zw, k, w.reshape(-1)))
+            del qw
+        else:
+            w = self._randn((k, n))
+        x = self._randn((bsz, k))
+        y = np.empty((bsz, n), np.float32)
+        t_copy = self._copy_s(4 * k * n) + self._copy_s(4 * bsz * k) + self._copy_s(4 * bsz * n)
+        t_mm = self._t(lambda: L.gfo_matmul_blocked(x, w, y, bsz, k, n))
+        full = t_deq + t_copy + t_mm
+        byts = k * n * (1 if int8 else 4) + 4 * bsz * k + 4 * bsz * n + (4 * k if int8 else 0)
+        return self.result(byts / full / 1e9, "GB/s", full,
+                           f"oracle {'get_weights (dequantize) + ' if int8 else ''}Tensor::matmul at M={bsz} "
+                           f"(W copy + matmul_blocked + copies), full: {full * 1e3:.1f} ms per call",
+                           matmul_s=t_mm, copy_s=t_copy, dequantize_s=t_deq)
+
+    def sdpa(self, S, B=4, H=32, D=128, nslices=None):
+        """scaled_dot_product_attention (attention.rs:11-49) with a causal
+        [S,S] mask: K^T gather, batched QK^T, mul_scalar, the cycled mask,
+        softmax, batched PV -- on a sample of (b,h) slices, extrapolated to
+        B*H."""
+        np, L = self.np, self.L
+        bh = B * H
+        ns = nslices or max(1, min(bh, int(round(self.TARGET_S * 3 * self.RATE / (4.0 * S * S * D)))))
+        q, k, v = (self._randn((ns, S, D)) for _ in range(3))
+        kt = np.empty((ns, D, S), np.float32)
+        sc = np.empty((ns, S, S), np.float32)
+        w = np.empty((ns, S, S), np.float32)
+        o = np.empty((ns, S, D), np.float32)
+        mask = np.tril(np.ones((S, S), np.float32)).reshape(-1)
+        scale = np.float32(1.0) / np.sqrt(np.float32(D))
+        t = {}
+        t["gather"] = self._t(lambda: L.gfo_transpose_last2(k.reshape(-1), kt.reshape(-1), ns, S, D))
+        t["qk"] = self._t(lambda: L.gfo_batched_matmul(q.reshape(-1), ns, kt.reshape(-1), ns, sc.reshape(-1),
+                                                       ns, S, D, S))
+        scf = sc.reshape(-1)
+        rows = ns * S
+
+        def scale_rows(r0, r1):
+            seg = scf[r0 * S:r1 * S]
+            L.gfo_mul_scalar(seg, seg.size, float(scale))
+        t["mul_scalar"] = self._t(lambda: self._par_rows(rows, scale_rows))
+        t["mask"] = self._t(lambda: L.gfo_apply_mask_cycled(scf, scf.size, mask, mask.size))
+        wf = w.reshape(-1)
+
+        def softmax_rows(r0, r1):
+            xs = scf[r0 * S:r1 * S]
+            ys = wf[r0 * S:r1 * S]
+            L.gfo_softmax_lastdim(xs, ys, r1 - r0, S)
+        t["softmax"] = self._t(lambda: self._par_rows(rows, softmax_rows))
+        t["pv"] = self._t(lambda: L.gfo_batched_matmul(w.reshape(-1), ns, v.reshape(-1), ns, o.reshape(-1),
+                                                       ns, S, S, D))
+        meas = sum(t.values())
+        full = meas * bh / ns
+        fl = 4.0 * B * H * S * S * D * 0.5
+        return self.result(fl / full / 1e12, "TFLOP/s", full,
+                           f"oracle scaled_dot_product_attention with a causal [S,S] mask on {ns}/{bh} (b,h) "
+                           f"slices ({meas:.2f} s), {'extrapolated' if ns < bh else 'full'}: {full:.1f} s per "
+                           f"call; softmax and mul_scalar on {self.nproc} threads, the rest on one",
+                           cores=self.nproc, stages_s={kk: round(vv * bh / ns, 4) for kk, vv in t.items()})
+
+    def flash_attention(self, S, B=128, D=128):
+        """FlashAttention::forward restated (the reference's loops, one
+        thread) on a sample of batch entries -- independent, identical work
+        -- extrapolated to B."""
+        O = self.O
+        nb = max(1, min(B, int(round(self.TARGET_S * self.RATE / (2.0 * S * S * D)))))
+        q, k, v = (self._randn((nb, S, D)) for _ in range(3))
+        scale = 1.0 / D ** 0.5
+        meas = self._t(lambda: O.flash_attention_blockwise(q, k, v, 64, 64, True, scale))
+        full = meas * B / nb
+        fl = 4.0 * B * S * S * D * 0.5
+        return self.result(fl / full / 1e12, "TFLOP/s", full,
+                           f"oracle FlashAttention::forward (causal, 64 x 64 blocks) on {nb}/{B} batch entries "
+                           f"({meas:.2f} s), {'extrapolated' if nb < B else 'full'}: {full:.1f} s per call")
+
+    def softmax(self, rows, cols):
+        np, L = self.np, self.L
+        rs = min(rows, max(1, int(2e7 // cols)))
+        x = self._randn((rs, cols))
+        y = np.empty_like(x)
+        xf, yf = x.reshape(-1), y.reshape(-1)
+
+        def part(r0, r1):
+            L.gfo_softmax_lastdim(xf[r0 * cols:r1 * cols], yf[r0 * cols:r1 * cols], r1 - r0, cols)
+        meas = self._t(lambda: self._par_rows(rs, part))
+        full = meas * rows / rs
+        byts = 8.0 * rows * cols
+        return self.result(byts / full / 1e9, "GB/s", full,
+                           f"oracle softmax(-1) on {rs}/{rows} rows on {self.nproc} threads (rayon), "
+                           f"{'extrapolated' if rs < rows else 'full'}: {full * 1e3:.1f} ms per call",
+                           cores=self.nproc)
+
+    def quantize(self, n):
+        np, L = self.np, self.L
+        x = self._randn((n,))
+        q = np.empty(n, np.int8)
+        s, z = C.c_float(), C.c_int8()
+        full = self._t(lambda: L.gfo_quantize_per_tensor(x, n, 0, q, C.byref(s), C.byref(z)))
+        return self.result(9.0 * n / full / 1e9, "GB/s", full,
+                           f"oracle quantize_activation (per tensor, asymmetric) of {n} elements, full: "
+                           f"{full * 1e3:.1f} ms per call")
+
+    def linear(self, m, n, k):
+        full, rows, meas = self.matmul_s(m, k, n, b_transposed=True)
+        t_bias = self._copy_s(4 * m * n)  # the broadcast add writes a new [m, n] tensor (same traffic)
+        full += t_bias
+        return full, rows
+
+    def swiglu(self, m, int8, H=4096, I=11008):
+        """SwiGLU::forward: gate, up, down Linear layers (int8: each through
+        the reference's quantize_activation + dequantize + get_weights +
+        fp32 Linear path) and silu(gate) * up."""
+        np, L = self.np, self.L
+        parts = []
+        for n_out, n_in in ((I, H), (I, H), (H, I)):
+            if int8:
+                parts.append(self.qlinear(m, n_out, n_in)["seconds_full"])
+            else:
+                parts.append(self.linear(m, n_out, n_in)[0])
+        g = self._randn((min(m, 256), I))
+        u = self._randn((min(m, 256), I))
+        h = np.empty_like(g)
+        t_silu = self._t(lambda: L.gfo_silu_mul(g.reshape(-1), u.reshape(-1), h.reshape(-1), g.size)) * m / g.shape[0]
+        full = sum(parts) + t_silu
+        ops = 6.0 * m * H * I
+        return self.result(ops / full / 1e12, "TOP/s" if int8 else "TFLOP/s", full,
+                           f"oracle SwiGLU::forward ({'int8 composite per Linear' if int8 else 'fp32 Linear'} "
+                           f"x3 + silu*up, matmuls on row samples, extrapolated): {full:.3f} s per call")
+
+
+def host_record(torch):
+    """The machine the bench ran on: host CPU, memory, ROCm / torch, GPU."""
+    rec = {"nproc": os.cpu_count()}
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for ln in fh:
+                if ln.startswith("model name"):
+                    rec["cpu_model"] = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        with open("/proc/meminfo") as fh:
+            for ln in fh:
+                if ln.startswith("MemTotal:"):
+                    rec["ram_gib"] = round(int(ln.split()[1]) / 2 ** 20, 1)
+                    break
+    except OSError:
+        pass
+    try:
+        with open("/opt/rocm/.info/version") as fh:
+            rec["rocm"] = fh.read().strip()
+    except OSError:
+        pass
+    rec["torch"] = torch.__version__
+    try:
+        p = torch.cuda.get_device_properties(0)
+        rec["gpu"] = f"{p.name} ({getattr(p, 'gcnArchName', '')}, {p.multi_processor_count} CUs, " \
+                     f"{p.total_memory / 2 ** 30:.0f} GiB)"
+    except Exception:  # noqa: BLE001
+        pass
+    import subprocess
+    for cmd in (["amd-smi", "metric", "--clock"], ["rocm-smi", "--showclocks"]):
+        try:
+            out = subprocess.run(cmd, capture_output=True, text=True, timeout=20)
+        except (OSError, subprocess.SubprocessError):
+            continue
+        if out.returncode == 0 and out.stdout.strip():
+            lines = [ln.strip() for ln in out.stdout.splitlines() if ln.strip() and "=" not in ln[:3]]
+            rec["clocks_after_run"] = " | ".join(lines[:24])[:1200]
+            rec["clocks_cmd"] = " ".join(cmd)
+            break
+    return rec
 
 
 # ---------------------------------------------------------------------------
@@ -303,6 +679,33 @@ def comp_sdpa(lib, torch, S):
     fl = 4.0 * B * H * S * S * D * 0.5
     return {"name": f"sdpa_causal_b4_h32_s{S}_d128", "ms": ms, "value": fl / ms / 1e9, "unit": "TFLOP/s",
             "frac": fl / ms / 1e9 / (PEAK_F32 / 1e12), "bound": "mfma_f32"}
+
+
+def comp_flash_attention(lib, torch, S, B=128, D=128):
+    """FlashAttention::forward (ghostflow-nn/src/flash_attention.rs:81-250)
+    on [B, S, D] with FlashAttentionConfig::causal(1/sqrt(D)) and the
+    default 64 x 64 blocks (gfh_flash_attention_f32: scores GEMM, blockwise
+    weights, weights . V GEMM) -- config 5's (b,h) slices as the layer's
+    batch.  Work: 4*B*S^2*D * 1/2 FLOP (causal, the FlashAttention
+    convention, as for SDPA); the bound is the f32 MFMA peak."""
+    dev = torch.device("cuda:0")
+    q = torch.randn((B, S, D), device=dev)
+    k = torch.randn((B, S, D), device=dev)
+    v = torch.randn((B, S, D), device=dev)
+    o = torch.empty_like(q)
+    L = lib.L
+    wsb = int(L.gfh_flash_attention_workspace_size(B, S, S))
+    ws = torch.empty((wsb + 3) // 4, device=dev)
+    s = torch.cuda.current_stream(dev).cuda_stream
+    scale = float(1.0 / (D ** 0.5))
+
+    def f(_):
+        L.gfh_flash_attention_f32(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), B, S, S, D, 64, 64, 1,
+                                  scale, ws.data_ptr(), wsb, s)
+    ms = event_time_ms(torch, f, 50 if S <= 512 else 10)
+    fl = 4.0 * B * S * S * D * 0.5
+    return {"name": f"flash_attention_causal_b{B}_s{S}_d{D}_blocks64", "ms": ms, "value": fl / ms / 1e9,
+            "unit": "TFLOP/s", "frac": fl / ms / 1e9 / (PEAK_F32 / 1e12), "bound": "mfma_f32"}
 
 
 def comp_linear_decode(lib, torch, m):
@@ -519,47 +922,129 @@ def comp_state_dict_load(lib, torch, int8):
             "value": gbs, "unit": "GB/s", "bytes": nbytes, "frac": gbs / 64.0, "bound": "pcie5_x16"}
 
 
-def run_components(lib, torch, only):
-    want = set(filter(None, only.split(","))) or {"sgemm", "qlinear", "gemv", "sdpa", "decode", "swiglu", "io"}
+def comp_quantize(lib, torch, m, k=4096):
+    """DynamicQuantization::quantize_activation on the device
+    (gfh_quantize_i8_per_tensor, asymmetric) of x [m, k] ~ N(0, 1): a min/max
+    pass, then the codes.  Algorithmic bytes = 9 per element (two reads of
+    the f32 input -- the codes need the global min/max first -- and one
+    int8 write).  HBM-bound."""
+    dev = torch.device("cuda:0")
+    n = m * k
+    ncopy = max(1, -(-2 * MALL_BYTES // (4 * n)) + 1)
+    xs = [torch.randn((n,), device=dev) for _ in range(ncopy)]
+    q = torch.empty((n,), dtype=torch.int8, device=dev)
+    sc = torch.empty((1,), device=dev)
+    zp = torch.empty((1,), dtype=torch.int8, device=dev)
+    L = lib.L
+    wsb = int(L.gfh_quantize_i8_per_tensor_workspace_size(n))
+    ws = torch.empty((wsb + 3) // 4, device=dev)
+    s = torch.cuda.current_stream(dev).cuda_stream
+    xp = [t.data_ptr() for t in xs]
+
+    def f(i):
+        L.gfh_quantize_i8_per_tensor(xp[i % ncopy], n, 0, q.data_ptr(), sc.data_ptr(), zp.data_ptr(),
+                                     ws.data_ptr(), wsb, s)
+    ms = event_time_ms(torch, f, 200)
+    byts = 9.0 * n
+    gbs = byts / ms / 1e6
+    del xs
+    return {"name": f"quantize_per_tensor_m{m}_k{k}", "ms": ms, "value": gbs, "unit": "GB/s",
+            "frac": gbs * 1e9 / PEAK_HBM, "bound": "hbm", "input_copies": ncopy}
+
+
+def comp_softmax(lib, torch, S, B=4, H=32):
+    """Tensor::softmax(-1) over the SDPA score shape [B*H*S, S]
+    (gfh_softmax_lastdim_f32).  Algorithmic bytes = 8 per element (read x,
+    write y).  HBM-bound."""
+    dev = torch.device("cuda:0")
+    rows = B * H * S
+    x = torch.randn((rows, S), device=dev) * 3
+    y = torch.empty_like(x)
+    s = torch.cuda.current_stream(dev).cuda_stream
+    L = lib.L
+
+    def f(_):
+        L.gfh_softmax_lastdim_f32(x.data_ptr(), y.data_ptr(), rows, S, s)
+    ms = event_time_ms(torch, f, 100 if S <= 512 else 20)
+    byts = 8.0 * rows * S
+    gbs = byts / ms / 1e6
+    return {"name": f"softmax_rows{rows}_cols{S}", "ms": ms, "value": gbs, "unit": "GB/s",
+            "frac": gbs * 1e9 / PEAK_HBM, "bound": "hbm"}
+
+
+def run_components(lib, torch, only, cpu=None):
+    """Every component's GPU figure, each with the reference CPU path's
+    figure for the same workload (`cpu_baseline`) when `cpu` is given.  The
+    square fp32 GEMMs run last, so the headline Linear (the same kernel)
+    starts on a settled clock right after them."""
+    want = set(filter(None, only.split(","))) or {"sgemm", "qlinear", "gemv", "sdpa", "flash", "softmax",
+                                                  "quantize", "decode", "swiglu", "io"}
     out = []
 
-    def add(fn, *a, **kw):
+    def add(fn, *a, cpu_fn=None, **kw):
         try:
             r = fn(lib, torch, *a, **kw)
         except Exception as e:  # report, keep going
             r = {"name": fn.__name__ + repr(a), "error": str(e)}
+        torch.cuda.empty_cache()
+        if cpu is not None and cpu_fn is not None and "error" not in r:
+            try:
+                r["cpu_baseline"] = cpu_fn()
+            except Exception as e:  # noqa: BLE001
+                r["cpu_baseline"] = {"error": str(e)}
         log("  " + json.dumps(r))
         out.append(r)
-        torch.cuda.empty_cache()
 
-    if "sgemm" in want:
-        for n in (1024, 2048, 4096, 8192):
-            add(comp_sgemm, n)
+    if "io" in want:
+        for int8 in (False, True):
+            add(comp_state_dict_load, int8)
     if "qlinear" in want:
-        add(comp_qlinear, 4096, 4096, 4096)
+        add(comp_qlinear, 4096, 4096, 4096, cpu_fn=lambda: cpu.qlinear(4096, 4096, 4096))
         for m in (1, 16, 256, 4096):
-            add(comp_qlinear, m, 11008, 4096)
+            add(comp_qlinear, m, 11008, 4096, cpu_fn=lambda m=m: cpu.qlinear(m, 11008, 4096))
+    if "quantize" in want:
+        for m in (256, 4096):
+            add(comp_quantize, m, cpu_fn=lambda m=m: cpu.quantize(m * 4096))
     if "gemv" in want:
         for int8 in (False, True):
             for bsz in (1, 4, 8):
-                add(comp_gemv, bsz, int8)
+                add(comp_gemv, bsz, int8, cpu_fn=lambda b=bsz, i=int8: cpu.gemv(b, i))
     if "sdpa" in want:
         for S in (512, 2048):
-            add(comp_sdpa, S)
+            add(comp_sdpa, S, cpu_fn=lambda S=S: cpu.sdpa(S))
+    if "flash" in want:
+        for S in (512, 2048):
+            add(comp_flash_attention, S, cpu_fn=lambda S=S: cpu.flash_attention(S))
+    if "softmax" in want:
+        for S in (512, 2048):
+            add(comp_softmax, S, cpu_fn=lambda S=S: cpu.softmax(4 * 32 * S, S))
     if "decode" in want:
         for m in (1, 4, 8, 16, 64):
-            add(comp_linear_decode, m)
+            add(comp_linear_decode, m, cpu_fn=lambda m=m: _cpu_linear_result(cpu, m, 4096, 4096))
         add(comp_kv_attention)
         add(comp_mha_decode)
     if "swiglu" in want:
         for m in (1, 16, 256, 4096):
-            add(comp_swiglu, m, True)
+            add(comp_swiglu, m, True, cpu_fn=lambda m=m: cpu.swiglu(m, True))
         for m in (1, 16, 4096):
-            add(comp_swiglu, m, False)
-    if "io" in want:
-        for int8 in (False, True):
-            add(comp_state_dict_load, int8)
+            add(comp_swiglu, m, False, cpu_fn=lambda m=m: cpu.swiglu(m, False))
+        # Mistral-7B's feed-forward width (ghostflow-ml/src/deep/architectures/transformer.rs:2021)
+        for m in (1, 16, 256, 4096):
+            add(comp_swiglu, m, True, I=14336, cpu_fn=lambda m=m: cpu.swiglu(m, True, I=14336))
+        for m in (1, 16):
+            add(comp_swiglu, m, False, I=14336, cpu_fn=lambda m=m: cpu.swiglu(m, False, I=14336))
+    if "sgemm" in want:
+        for n in (1024, 2048, 4096, 8192):
+            add(comp_sgemm, n, cpu_fn=lambda n=n: cpu.sgemm(n))
     return out
+
+
+def _cpu_linear_result(cpu, m, n, k):
+    full, rows = cpu.linear(m, n, k)
+    byts = 4.0 * n * k + 4 * m * k + 4 * n + 4 * m * n
+    return cpu.result(byts / full / 1e9, "GB/s", full,
+                      f"oracle Linear::forward at m={m} (W^T gather + matmul_blocked on {rows}/{m} rows + bias), "
+                      f"{'extrapolated' if rows < m else 'full'}: {full * 1e3:.1f} ms per call")
 
 
 def calib_copy(torch, steps):
@@ -597,15 +1082,15 @@ def main():
     # work that a serving loop with known-good buffers switches off.
     lib.L.gfh_set_pointer_checks(0)
 
+    components = []
+    if not args.no_components:
+        log("bench: components" + ("" if args.no_cpu else " (each with the reference CPU path timed on this host)"))
+        components = run_components(lib, torch, args.only, None if args.no_cpu else CpuRef())
+
     log(f"bench: fp32 Linear 4096^3, warmup {args.warmup}, steps {args.steps}")
     h = bench_linear(lib, torch, args)
     log(f"bench: {h['ms_per_step']:.3f} ms/step, {h['value']:.2f} TFLOP/s "
         f"(kernel {h['kernel_ms']:.3f} ms, {h['achieved']:.2f} TFLOP/s)")
-
-    components = []
-    if not args.no_components:
-        log("bench: components")
-        components = run_components(lib, torch, args.only)
 
     cpu = None
     if not args.no_cpu:
@@ -643,6 +1128,7 @@ def main():
                      "unit": "TFLOP/s", "frac": round(h["achieved"] / (PEAK_F32 / 1e12), 4),
                      "traffic": traffic},
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
+        "host": host_record(torch),
         "components": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in c.items()}
                        for c in components],
     }

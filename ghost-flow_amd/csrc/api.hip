@@ -362,6 +362,62 @@ GFH_API int gfh_softmax_lastdim_f32(const float *x, float *y, int64_t rows, int6
     });
 }
 
+GFH_API size_t gfh_flash_attention_workspace_size(int64_t batch, int64_t seq_len_q, int64_t seq_len_k) {
+    if (batch <= 0 || seq_len_q <= 0 || seq_len_k <= 0) return 0;
+    int64_t t, u;
+    if (!mul_ok(batch, seq_len_q, &t) || !mul_ok(t, seq_len_k, &u)) return 0;
+    return (size_t)u * sizeof(float);
+}
+
+GFH_API int gfh_flash_attention_f32(const float *q, const float *k, const float *v, float *out, int64_t batch,
+                                    int64_t seq_len_q, int64_t seq_len_k, int64_t d_model, int64_t block_size_m,
+                                    int64_t block_size_n, int causal, float scale, void *workspace,
+                                    size_t workspace_bytes, gfh_stream_t stream) {
+    return guarded([&]() -> int {
+        if (batch < 0 || seq_len_q < 0 || seq_len_k < 0 || d_model < 0 || batch > kMaxDim ||
+            seq_len_q > kMaxDim || seq_len_k > kMaxDim || d_model > kMaxDim)
+            return set_error(GFH_INVALID_SHAPE,
+                             "flash_attention: batch=%lld seq_len_q=%lld seq_len_k=%lld d_model=%lld out of range",
+                             (long long)batch, (long long)seq_len_q, (long long)seq_len_k, (long long)d_model);
+        if (block_size_m <= 0 || block_size_n <= 0)
+            return set_error(GFH_INVALID_SHAPE, "flash_attention: block sizes must be positive (m=%lld n=%lld)",
+                             (long long)block_size_m, (long long)block_size_n);
+        const int64_t nb = seq_len_k > 0 ? (seq_len_k + block_size_n - 1) / block_size_n : 0;
+        if (nb > flash_attention_max_blocks())
+            return set_error(GFH_INVALID_SHAPE,
+                             "flash_attention: seq_len_k / block_size_n = %lld key blocks; at most %lld are served",
+                             (long long)nb, (long long)flash_attention_max_blocks());
+        int64_t rows, qn, kn, sn;
+        if (!mul_ok(batch, seq_len_q, &rows) || rows > (int64_t)INT32_MAX || !mul_ok(rows, d_model, &qn) ||
+            !mul_ok(batch, seq_len_k, &kn) || !mul_ok(kn, d_model, &kn) || !mul_ok(rows, seq_len_k, &sn))
+            return set_error(GFH_INVALID_SHAPE, "flash_attention: size overflow");
+        if (qn == 0) return GFH_SUCCESS;
+        GFH_TRY(require_range(q, (size_t)qn * 4, "q"));
+        GFH_TRY(require_range(k, (size_t)kn * 4, "k"));
+        GFH_TRY(require_range(v, (size_t)kn * 4, "v"));
+        GFH_TRY(require_range(out, (size_t)qn * 4, "out"));
+        GFH_TRY(ensure_init());
+        hipStream_t s = as_stream(stream);
+        Scratch ws;
+        GFH_TRY(ws.acquire(workspace, workspace_bytes, (size_t)sn * 4, s));
+        FlashAttnDesc d;
+        d.q = q;
+        d.k = k;
+        d.v = v;
+        d.out = out;
+        d.ws = static_cast<float *>(ws.ptr());
+        d.batch = batch;
+        d.sq = seq_len_q;
+        d.sk = seq_len_k;
+        d.d = d_model;
+        d.block_m = block_size_m;
+        d.block_n = block_size_n;
+        d.causal = causal != 0;
+        d.scale = scale;
+        return launch_flash_attention_blockwise(d, s);
+    });
+}
+
 GFH_API int gfh_sdpa_f32(const float *q, const float *k, const float *v, float *out, float *weights, int64_t b,
                          int64_t h, int64_t sq, int64_t skv, int64_t d, float scale, int causal, const float *mask,
                          int64_t mask_numel, gfh_stream_t stream) {

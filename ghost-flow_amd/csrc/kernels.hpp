@@ -92,6 +92,20 @@ int launch_gemv_w8(const float *x, const int8_t *qw, const float *scales, const 
 int launch_gemv_w8_noalloc(const float *x, const int8_t *qw, const float *scales, const int8_t *zps, float *y,
                            int64_t b, int64_t k, int64_t n, hipStream_t s);
 
+// flash_attention.hip: FlashAttention::forward (blockwise recurrence) as
+// scores GEMM -> per-row weights kernel -> weights . V GEMM; ws holds
+// batch * sq * sk floats.
+struct FlashAttnDesc {
+    const float *q = nullptr, *k = nullptr, *v = nullptr;
+    float *out = nullptr;
+    float *ws = nullptr;
+    int64_t batch = 0, sq = 0, sk = 0, d = 0, block_m = 64, block_n = 64;
+    bool causal = false;
+    float scale = 1.f;
+};
+int64_t flash_attention_max_blocks();
+int launch_flash_attention_blockwise(const FlashAttnDesc &d, hipStream_t s);
+
 // attention.hip
 int launch_softmax_lastdim(const float *x, float *y, int64_t rows, int64_t cols, hipStream_t s);
 struct SdpaDesc {

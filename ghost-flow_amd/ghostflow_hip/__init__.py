@@ -11,6 +11,7 @@ from .ops import (  # noqa: F401
     GhostFlowError,
     StateDict,
     dequantize,
+    flash_attention_blockwise,
     gemv_f32,
     gemv_w8,
     init,
@@ -37,7 +38,14 @@ from .ops import (  # noqa: F401
     softmax_lastdim,
     swiglu,
 )
-from .nn import KVCache, MultiHeadAttention, QuantizedSwiGLU, SwiGLU  # noqa: F401
+from .nn import (  # noqa: F401
+    FlashAttention,
+    FlashAttentionConfig,
+    KVCache,
+    MultiHeadAttention,
+    QuantizedSwiGLU,
+    SwiGLU,
+)
 from .quantization import (  # noqa: F401
     DynamicQuantization,
     QuantizationAwareTraining,

@@ -57,6 +57,8 @@ SIGNATURES = {
     "gfh_gemv_w8": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "gfh_gemv_w8_noalloc": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "gfh_softmax_lastdim_f32": (_i, [_p, _p, _i64, _i64, _p]),
+    "gfh_flash_attention_workspace_size": (_sz, [_i64, _i64, _i64]),
+    "gfh_flash_attention_f32": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i, _f, _p, _sz, _p]),
     "gfh_sdpa_f32": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f, _i, _p, _i64, _p]),
     "gfh_kv_attention_f32": (_i, [_p, _i64, _p, _p, _i64, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _f,
                                   _i, _p, _i64, _p]),

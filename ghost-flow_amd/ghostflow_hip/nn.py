@@ -23,8 +23,56 @@ import math
 import torch
 
 from . import _lib
-from .ops import (GhostFlowError, mha_forward_cached, mha_forward_with_cache, qswiglu, quantize_per_channel,
-                  qweight_rowsum, swiglu)
+from .ops import (GhostFlowError, flash_attention_blockwise, mha_forward_cached, mha_forward_with_cache, qswiglu,
+                  quantize_per_channel, qweight_rowsum, swiglu)
+
+
+class FlashAttentionConfig:
+    """FlashAttentionConfig (ghostflow-nn/src/flash_attention.rs:14-68):
+    block sizes, causal flag, dropout (stored, never applied by the
+    reference's forward) and scale (default 1.0, not 1/sqrt(d))."""
+
+    def __init__(self, block_size_m=64, block_size_n=64, causal=False, dropout=0.0, scale=1.0):
+        self.block_size_m = block_size_m
+        self.block_size_n = block_size_n
+        self.causal = causal
+        self.dropout = dropout
+        self.scale = scale
+
+    @classmethod
+    def causal_config(cls, scale):
+        """FlashAttentionConfig::causal(scale) (:41-47)."""
+        return cls(causal=True, scale=scale)
+
+    @classmethod
+    def bidirectional(cls, scale):
+        """FlashAttentionConfig::bidirectional(scale) (:50-56)."""
+        return cls(causal=False, scale=scale)
+
+    @classmethod
+    def long_sequence(cls, scale):
+        """FlashAttentionConfig::long_sequence(scale) (:59-66): 128 x 128 blocks."""
+        return cls(block_size_m=128, block_size_n=128, scale=scale)
+
+
+class FlashAttention:
+    """FlashAttention (flash_attention.rs:70-296): forward(query, key, value)
+    on [batch, seq_len, d_model] device tensors, the reference's blockwise
+    recurrence on the GPU (gfh_flash_attention_f32)."""
+
+    def __init__(self, config: FlashAttentionConfig | None = None):
+        self.config = config or FlashAttentionConfig()
+
+    def forward(self, query, key, value):
+        c = self.config
+        return flash_attention_blockwise(query, key, value, block_size_m=c.block_size_m,
+                                         block_size_n=c.block_size_n, causal=c.causal, scale=c.scale)
+
+    __call__ = forward
+
+    def memory_usage_ratio(self, seq_len: int, _d_model: int) -> float:
+        """(block_m * block_n) / seq_len^2, as the reference reports (:285-295)."""
+        return float(self.config.block_size_m * self.config.block_size_n) / float(seq_len * seq_len)
 
 
 class KVCache:

@@ -261,6 +261,31 @@ def sdpa(q, k, v, *, scale=None, causal=False, mask=None, want_weights=False, ou
     return (o, w) if want_weights else o
 
 
+def flash_attention_blockwise(q, k, v, *, block_size_m=64, block_size_n=64, causal=False, scale=1.0,
+                              out=None, workspace=None):
+    """FlashAttention::forward (ghostflow-nn/src/flash_attention.rs:81-250)
+    on q [B, Sq, d], k / v [B, Sk, d]: the reference's blockwise recurrence
+    with its block sizes, causal flag (top-left j > i) and scale, including
+    its once-per-key correction (softmax attention only at block_size_n ==
+    1).  Errors as the reference: non-3-D inputs, a d_model mismatch."""
+    for t, nm in ((q, "q"), (k, "k"), (v, "v")):
+        _need(t, torch.float32, nm)
+    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3:
+        raise GhostFlowError(_lib.INVALID_SHAPE, "Expected 3D tensors [batch, seq_len, d_model]")
+    b, sq, d = q.shape
+    sk = k.shape[1]
+    if k.shape[2] != d or v.shape[2] != d:
+        raise GhostFlowError(_lib.INVALID_SHAPE, "Key and Value must have same d_model as Query")
+    if k.shape[0] != b or v.shape[0] != b or v.shape[1] != sk:
+        raise GhostFlowError(_lib.INVALID_SHAPE, "key / value must be [batch, seq_len_k, d_model] like query")
+    o = torch.empty_like(q) if out is None else out
+    _check(lib().gfh_flash_attention_f32(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), b, sq, sk, d,
+                                         int(block_size_m), int(block_size_n), int(bool(causal)), float(scale),
+                                         _ptr(workspace), 0 if workspace is None else workspace.numel() * 4,
+                                         _stream(q.device)))
+    return o
+
+
 def kv_attention(q, k_cache, v_cache, kv_len, num_heads, *, scale=None, causal=False, mask=None,
                  want_weights=False, out=None):
     """Attention of q [B, Sq, E] over the first kv_len rows of the caches

@@ -235,6 +235,34 @@ GFH_API int gfh_sdpa_f32(const float *q, const float *k, const float *v, float *
                          int64_t skv, int64_t d, float scale, int causal,
                          const float *mask, int64_t mask_numel, gfh_stream_t stream);
 
+/* FlashAttention::forward (ghostflow-nn/src/flash_attention.rs:81-250) with
+ * FlashAttentionConfig's block_size_m / block_size_n / causal / scale
+ * (:14-68; dropout is not applied by the reference's forward): q [batch,
+ * seq_len_q, d_model], k / v [batch, seq_len_k, d_model], out [batch,
+ * seq_len_q, d_model].  The reference's own blockwise recurrence, as it is:
+ *   - causal masks key j for query i when j > i (absolute indices, top-left
+ *     aligned also when seq_len_q != seq_len_k, :193-196), and skips key
+ *     blocks that start at or past the end of the query block (:150-152);
+ *   - the running-max correction exp(old_max - new_max) multiplies the
+ *     output once per KEY of each block (:233-241), so the result is not
+ *     softmax attention unless block_size_n == 1: the first key block keeps
+ *     only its last key, and a block whose max rises scales the earlier
+ *     output by the correction to the power of its key count;
+ *   - rows with row_sum == 0 are left undivided (:166-172); no keys gives 0.
+ * Within fp32 rounding of the reference (1e-4 relative) for finite inputs.
+ * Block sizes must be positive (the reference's step_by(0) panics) and
+ * ceil(seq_len_k / block_size_n) <= 8192.  Workspace: gfh_flash_attention_
+ * workspace_size(batch, seq_len_q, seq_len_k) bytes (nullable, see
+ * conventions).  For softmax attention use gfh_sdpa_f32. */
+GFH_API int gfh_flash_attention_f32(const float *q, const float *k, const float *v,
+                                    float *out, int64_t batch, int64_t seq_len_q,
+                                    int64_t seq_len_k, int64_t d_model,
+                                    int64_t block_size_m, int64_t block_size_n,
+                                    int causal, float scale, void *workspace,
+                                    size_t workspace_bytes, gfh_stream_t stream);
+GFH_API size_t gfh_flash_attention_workspace_size(int64_t batch, int64_t seq_len_q,
+                                                  int64_t seq_len_k);
+
 /* Attention of sq new queries over a key/value cache, in the reference's
  * [B, S, E] layout with head hh in columns hh*d .. hh*d+d-1 (the storage of
  * reshape_for_attention's [B, H, S, D] view, ghostflow-nn/src/attention.rs:

@@ -325,9 +325,9 @@ GFO_API int gfo_flash_attention(const float *q, const float *k, const float *v,
     return sdpa_body(q, k, v, out, NULL, bh, s, s, d, scale, NULL, 0, causal);
 }
 
-/* Rows [r0, r1) of one (b,h) slice of the causal flash path, used by bench.py
- * to time a bounded sample of the reference computation (rows are
- * independent: each needs Q row i and all of K, V). */
+/* Rows [r0, r1) of one (b,h) slice of the flash path (rows are
+ * independent: each needs Q row i and all of K, V), for checks of sampled
+ * rows of a large slice. */
 GFO_API int gfo_flash_attention_rows(const float *q, const float *k, const float *v,
                                      float *out, size_t s, size_t d, float scale,
                                      int causal, size_t r0, size_t r1) {
@@ -345,6 +345,112 @@ GFO_API int gfo_flash_attention_rows(const float *q, const float *k, const float
     gfo_softmax_lastdim(sc, w, rows, s);
     gfo_batched_matmul(w, 1, v, 1, out + r0 * d, 1, rows, s, d);
     free(kt); free(sc); free(w);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* ghostflow-nn/src/flash_attention.rs                                       */
+/* ------------------------------------------------------------------------ */
+
+/* flash_attention.rs:81-250 `FlashAttention::forward` on [batch, sq, d] query
+ * and [batch, sk, d] key / value, each batch independently (:106-116,
+ * extract_batch :253-264, concatenate_batches :266-282):
+ *   output = 0, row_max = -inf, row_sum = 0                       (:135-137)
+ *   for query blocks i0 (block_m), key blocks j0 (block_n)        (:143-163)
+ *     skip when causal && j0 >= end_i                             (:150-152)
+ *     process_block (:178-250), per row i of the query block:
+ *       score_j = (sum_d q*k, ascending, from 0.0) * scale, or -inf when
+ *                 causal && j > i (absolute indices: top-left)    (:193-206)
+ *       block_max = fold(-inf, f32::max) over unmasked scores     (:208)
+ *       new_max = max(old_max, block_max)                         (:212-214)
+ *       p_j = exp(score_j - new_max), 0 for masked; block_sum += p_j  (:217-226)
+ *       correction = exp(old_max - new_max)                       (:229)
+ *       row_sum = row_sum * correction + block_sum                (:230)
+ *       for every key j of the block (masked ones included):
+ *         output = output * correction + p_j * v_j                (:233-241)
+ *   output /= row_sum where row_sum > 0                           (:166-172)
+ * The correction multiplies the output once PER KEY of the block (:236-237),
+ * not once per block: the first block (correction = exp(-inf) = 0) keeps
+ * only its last key, and a later block whose max rises scales the earlier
+ * output by correction^(keys in the block).  With block_n == 1 this is the
+ * exact online softmax.  Returns 1 for a zero block size (Rust's step_by(0)
+ * panics), 4 on allocation failure. */
+GFO_API int gfo_flash_attention_blockwise(const float *q, const float *k, const float *v,
+                                          float *out, size_t batch, size_t sq, size_t sk,
+                                          size_t d, size_t block_m, size_t block_n,
+                                          int causal, float scale) {
+    if (block_m == 0 || block_n == 0) return 1;
+    float *row_max = (float *)malloc(sq * sizeof(float) + 1);
+    float *row_sum = (float *)malloc(sq * sizeof(float) + 1);
+    float *scores = (float *)malloc(block_n * sizeof(float) + 1);
+    if (!row_max || !row_sum || !scores) {
+        free(row_max); free(row_sum); free(scores);
+        return 4;
+    }
+    for (size_t b = 0; b < batch; ++b) {
+        const float *qb = q + b * sq * d, *kb = k + b * sk * d, *vb = v + b * sk * d;
+        float *ob = out + b * sq * d;
+        for (size_t i = 0; i < sq * d; ++i) ob[i] = 0.0f;
+        for (size_t i = 0; i < sq; ++i) {
+            row_max[i] = -INFINITY;
+            row_sum[i] = 0.0f;
+        }
+        for (size_t i0 = 0; i0 < sq; i0 += block_m) {
+            const size_t end_i = i0 + block_m < sq ? i0 + block_m : sq;
+            for (size_t j0 = 0; j0 < sk; j0 += block_n) {
+                const size_t end_j = j0 + block_n < sk ? j0 + block_n : sk;
+                if (causal && j0 >= end_i) continue;
+                for (size_t i = i0; i < end_i; ++i) {
+                    float block_max = -INFINITY;
+                    size_t ns = 0;
+                    for (size_t j = j0; j < end_j; ++j) {
+                        if (causal && j > i) {
+                            scores[ns++] = -INFINITY;
+                            continue;
+                        }
+                        float score = 0.0f;
+                        for (size_t t = 0; t < d; ++t) {
+                            float p = qb[i * d + t] * kb[j * d + t];
+                            score = score + p;
+                        }
+                        score = score * scale;
+                        scores[ns++] = score;
+                        block_max = fmaxf(block_max, score);
+                    }
+                    const float old_max = row_max[i];
+                    const float new_max = fmaxf(old_max, block_max);
+                    row_max[i] = new_max;
+                    float block_sum = 0.0f;
+                    for (size_t t = 0; t < ns; ++t) {
+                        if (scores[t] != -INFINITY) {
+                            scores[t] = expf(scores[t] - new_max);
+                            block_sum = block_sum + scores[t];
+                        } else {
+                            scores[t] = 0.0f;
+                        }
+                    }
+                    const float correction = expf(old_max - new_max);
+                    {
+                        float t1 = row_sum[i] * correction;
+                        row_sum[i] = t1 + block_sum;
+                    }
+                    for (size_t t = 0; t < ns; ++t) {
+                        const size_t j = j0 + t;
+                        if (j < sk)
+                            for (size_t e = 0; e < d; ++e) {
+                                float t1 = ob[i * d + e] * correction;
+                                float t2 = scores[t] * vb[j * d + e];
+                                ob[i * d + e] = t1 + t2;
+                            }
+                    }
+                }
+            }
+        }
+        for (size_t i = 0; i < sq; ++i)
+            if (row_sum[i] > 0.0f)
+                for (size_t e = 0; e < d; ++e) ob[i * d + e] = ob[i * d + e] / row_sum[i];
+    }
+    free(row_max); free(row_sum); free(scores);
     return 0;
 }
 

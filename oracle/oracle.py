@@ -55,6 +55,9 @@ def lib():
         L.gfo_flash_attention_rows.argtypes = [_f32p, _f32p, _f32p, _f32p, _sz, _sz,
                                                C.c_float, C.c_int, _sz, _sz]
         L.gfo_flash_attention_rows.restype = C.c_int
+        L.gfo_flash_attention_blockwise.argtypes = [_f32p, _f32p, _f32p, _f32p, _sz, _sz, _sz, _sz,
+                                                    _sz, _sz, C.c_int, C.c_float]
+        L.gfo_flash_attention_blockwise.restype = C.c_int
         L.gfo_quantize_per_tensor.argtypes = [_f32p, _sz, C.c_int, _i8p,
                                               C.POINTER(C.c_float), C.POINTER(C.c_int8)]
         L.gfo_quantize_per_channel.argtypes = [_f32p, _sz, _sz, C.c_int, _i8p, _f32p, _i8p]
@@ -248,6 +251,25 @@ def flash_attention_rows(q, k, v, scale, causal, r0, r1):
     if rc:
         raise MemoryError("oracle allocation failed")
     return out[r0:r1]
+
+
+def flash_attention_blockwise(q, k, v, block_m=64, block_n=64, causal=False, scale=1.0):
+    """FlashAttention::forward (ghostflow-nn/src/flash_attention.rs:81-250)
+    on q [B, Sq, d], k / v [B, Sk, d] with FlashAttentionConfig's block
+    sizes, causal flag and scale (the reference's own recurrence, including
+    its once-per-key correction)."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    bsz, sq, d = q.shape
+    sk = k.shape[1]
+    out = np.empty((bsz, sq, d), np.float32)
+    rc = lib().gfo_flash_attention_blockwise(q.reshape(-1), k.reshape(-1), v.reshape(-1), out.reshape(-1),
+                                             bsz, sq, sk, d, int(block_m), int(block_n), int(bool(causal)),
+                                             float(scale))
+    if rc == 1:
+        raise ValueError("block sizes must be positive")
+    if rc:
+        raise MemoryError("oracle allocation failed")
+    return out
 
 
 # -- ghostflow-nn quantization ----------------------------------------------

@@ -19,7 +19,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from _util import gemm_tol, to_dev, to_np
+from _util import gemm_tol, rows_parallel, to_dev, to_np
 
 pytestmark = pytest.mark.gpu
 F = np.float32
@@ -149,6 +149,61 @@ def test_swiglu_i8_stages(torch_dev, m, hidden, inter, bias):
     np.testing.assert_array_equal(y.view(np.uint32), y_ref.view(np.uint32))
     if np.array_equal(h.view(np.uint32), r["h"].view(np.uint32)):
         np.testing.assert_array_equal(y.view(np.uint32), r["y"].view(np.uint32))
+
+
+@pytest.mark.parametrize("m", [1, 16, 300])
+def test_swiglu_f32_mistral_ffn(torch_dev, m):
+    """The Mistral-7B feed-forward shape, hidden 4096, intermediate 14336
+    (Mistral::new(..., 14336), ghostflow-ml/src/deep/architectures/
+    transformer.rs:2021), fp32 with biases: the decode-size (1, 16) and tile
+    (300) routes, checked stage by stage as above."""
+    rng = np.random.default_rng(m + 14336)
+    hidden, inter = 4096, 14336
+    x = rng.normal(0, 1, (m, hidden)).astype(F)
+    wg, bg, wu, bu, wd, bd = _fp32_layer(rng, hidden, inter)
+    dev = lambda a: to_dev(a, torch_dev)  # noqa: E731
+    y, h = _gh().swiglu(dev(x), dev(wg), dev(bg), dev(wu), dev(bu), dev(wd), dev(bd), want_h=True)
+    y, h = to_np(y), to_np(h)
+    gate = rows_parallel(O.linear_forward, x, wg, bg)
+    up = rows_parallel(O.linear_forward, x, wu, bu)
+    h_ref = O.silu_mul(gate, up)
+    tg, tu = gemm_tol(hidden, x, wg), gemm_tol(hidden, x, wu)
+    sg = np.abs(h_ref / np.where(up == 0, 1, up))
+    bound = 1.1 * np.abs(up) * tg + (sg + 1.1 * tg) * tu + 4 * np.spacing(np.abs(h_ref))
+    assert (np.abs(h.astype(np.float64) - h_ref) <= bound).all(), float(np.abs(h - h_ref).max())
+    y_ref = rows_parallel(O.linear_forward, h, wd, bd)
+    assert np.abs(y - y_ref).max() <= gemm_tol(inter, h, wd), float(np.abs(y - y_ref).max())
+
+
+@pytest.mark.parametrize("m", [1, 16, 300, 600])
+def test_swiglu_i8_mistral_ffn(torch_dev, m):
+    """Mistral's 4096 x 14336 feed-forward block in int8 (DynamicQuantization
+    codes, biases): skinny gate/up at m <= 64, 128 x (64 + 64) tiles at 300,
+    256 x (128 + 128) at 600.  h within 4 ulp of the oracle's silu * up of its
+    bit-exact gate and up; y bit-exact against the oracle's quantize + INT8
+    linear of the GPU's own h."""
+    gh = _gh()
+    hidden, inter = 4096, 14336
+    rng = np.random.default_rng(m * 7 + inter)
+    x = rng.normal(0, 1, (m, hidden)).astype(F)
+    q = _int8_layer(rng, hidden, inter, True)
+    dev = {}
+    for k, (codes, scales, b) in q.items():
+        cd = to_dev(codes, torch_dev)
+        dev[k] = (cd, to_dev(scales, torch_dev), gh.qweight_rowsum(cd), to_dev(b, torch_dev))
+    y, h = gh.qswiglu(to_dev(x, torch_dev), dev["g"], dev["u"], dev["d"], want_h=True)
+    y, h = to_np(y), to_np(h)
+    qx, sx, zx = O.quantize_per_tensor(x, symmetric=False)
+    zxa = np.atleast_1d(zx)
+    lin = lambda r, w: O.qlinear_i8(r, sx, zxa, False, w[0], w[1], w[2], want_acc=False)[0]  # noqa: E731
+    gate = rows_parallel(lin, qx, q["g"])
+    up = rows_parallel(lin, qx, q["u"])
+    _ulp_close(h, O.silu_mul(gate, up))
+    qh, sh, zh = O.quantize_per_tensor(h, symmetric=False)
+    zha = np.atleast_1d(zh)
+    y_ref = rows_parallel(lambda r: O.qlinear_i8(r, sh, zha, False, q["d"][0], q["d"][1], q["d"][2],
+                                                 want_acc=False)[0], qh)
+    np.testing.assert_array_equal(y.view(np.uint32), y_ref.view(np.uint32))
 
 
 def test_swiglu_modules(torch_dev):
