@@ -151,6 +151,11 @@ def test_gemv_w8_wide_dynamic_range(torch_dev):
     gh, O = _gh(), _O()
     rng = np.random.default_rng(21)
     b, k, n = 3, 1024, 768
+    _wide_range_case(gh, O, torch_dev, rng, b, k, n)
+    _wide_range_case(gh, O, torch_dev, rng, b, k, 8192)
+
+
+def _wide_range_case(gh, O, torch_dev, rng, b, k, n):
     mag = 2.0 ** rng.uniform(-16, 15, size=(b, k))
     x = (mag * rng.choice([-1.0, 1.0], size=(b, k))).astype(np.float32)
     x[0, 5], x[1, 7] = np.float32(2.0 ** 15), np.float32(2.0 ** -16)
@@ -169,8 +174,11 @@ def test_gemv_w8_non_finite_activations(torch_dev):
     where it is zero) and leaves the other batch rows of the same strip
     untouched -- the prescale of the slice ignores non-finite values."""
     gh, O = _gh(), _O()
-    rng = np.random.default_rng(22)
-    b, k, n = 4, 512, 320
+    for n in (320, 8192):
+        _non_finite_case(gh, O, torch_dev, np.random.default_rng(22), 4, 512, n)
+
+
+def _non_finite_case(gh, O, torch_dev, rng, b, k, n):
     x = rng.standard_normal((b, k)).astype(np.float32)
     x[0, 10] = np.inf
     x[1, 20] = -np.inf
@@ -187,3 +195,20 @@ def test_gemv_w8_non_finite_activations(torch_dev):
     np.testing.assert_array_equal(got[np.isinf(ref)], ref[np.isinf(ref)])
     assert np.abs(got[fin] - ref[fin]).max() <= gemm_tol(k, x[3], dw)
     assert np.isfinite(ref[3]).all()
+
+
+@pytest.mark.parametrize("b,k,n", [(1, 4096, 8192), (3, 4100, 8208), (8, 5000, 14336), (13, 300, 10000),
+                                   (2, 64, 32768), (5, 1, 9008), (4, 2000, 16400)])
+def test_gemv_w8_wide_integer_exact(torch_dev, b, k, n):
+    """Wide W (N >= 8192): ragged last strips (8208, 9008, 10000, 16400),
+    K = 5000 in slices of unequal length, K = 1 and 64 (one short slice),
+    batch groups of 8 (13).  Power-of-two scales and small integers: exact,
+    so bit for bit against the oracle's dequantize + matmul."""
+    gh, O = _gh(), _O()
+    rng = np.random.default_rng(k * 5 + n + b)
+    q = rng.integers(-128, 128, size=(k, n)).astype(np.int8)
+    s = (2.0 ** rng.integers(-3, 2, size=k)).astype(np.float32)
+    z = rng.integers(-5, 6, size=k).astype(np.int8)
+    x = rng.integers(-4, 5, size=(b, k)).astype(np.float32)
+    got = to_np(gh.gemv_w8(to_dev(x, torch_dev), to_dev(q, torch_dev), to_dev(s, torch_dev), to_dev(z, torch_dev)))
+    np.testing.assert_array_equal(got, O.matmul(x, O.dequantize(q, s, z)))
