@@ -430,7 +430,9 @@ GFH_API int gfh_sdpa_f32(const float *q, const float *k, const float *v, float *
             return set_error(GFH_INVALID_SHAPE, "sdpa: head_dim %lld must be a multiple of 4 in [4, 128]",
                              (long long)d);
         if (causal && sq != skv)
-            return set_error(GFH_INVALID_SHAPE, "sdpa: causal attention needs sq == skv (got %lld, %lld)",
+            return set_error(GFH_INVALID_SHAPE,
+                             "sdpa: causal attention needs sq == skv (got %lld, %lld); the top-left causal rule of "
+                             "FlashAttention::forward for sq != skv is gfh_flash_attention_f32",
                              (long long)sq, (long long)skv);
         if (mask && mask_numel <= 0) return set_error(GFH_INVALID_SHAPE, "sdpa: mask_numel must be > 0");
         if (b == 0 || h == 0 || sq == 0) return GFH_SUCCESS;

@@ -70,6 +70,31 @@ void release_stream_state();
 // Compute units of the current device (queried once per device).
 int device_cu_count();
 
+// ---- split-K arrival protocol ------------------------------------------------
+// Kernels that split K over workgroups (the decode GEMVs, the skinny int8 and
+// fp32 linears, KV-cache attention) combine their partials in the same
+// launch:
+//   1. each workgroup (or wave) stores its partial with agent-scope relaxed
+//      atomic stores; these bypass the per-XCD L2 (which is not coherent
+//      across XCDs) and complete at the device coherence point;
+//   2. s_waitcnt vmcnt(0): the storing thread waits until its stores are
+//      acknowledged; an __atomic_signal_fence before it keeps the compiler
+//      from moving a store past the wait;
+//   3. after a barrier (when several threads stored), one thread counts the
+//      arrival with an agent-scope relaxed fetch_add; the one that reads
+//      slices - 1 is the last to arrive;
+//   4. the last arriver loads the other partials with agent-scope relaxed
+//      loads (also served by the coherence point), sums them in a fixed order
+//      and returns the counter to 0.
+// Ordering relied on: a partial store acknowledged before the arrival is
+// counted is visible to an agent-scope load that the last arriver issues
+// after reading the count.  This is the vmcnt form of release / acquire: the
+// HIP memory model's release / acquire fences order the same accesses but
+// compile to a whole-L2 writeback / invalidate on this target (measured: the
+// int8 GEMV fell to 1.8 TB/s).  It would break if a store were moved past
+// the wait (the signal fences prevent that in the compiler) or if hardware
+// acknowledged an agent-scope store before it reached the coherence point.
+
 }  // namespace gfh
 
 // Propagate a non-zero status.

@@ -263,6 +263,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_nt_skinny_kernel(SkNtPara
                 __hip_atomic_store(p.part + (slice * p.m + row) * p.n + col, acc[mb][r], __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
         }
+    // split-K arrival protocol (common.hpp): steps 2-4
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     wait_vmcnt<0>();
     const int64_t blk = n0 / 16;

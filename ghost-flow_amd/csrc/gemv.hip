@@ -97,6 +97,7 @@ __device__ __forceinline__ void store_strip(const GemvParams &p, int64_t strip, 
         __hip_atomic_store(p.part + (slice * nb + bi) * p.n + col0 + c, value(bi, c), __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
     }
+    // split-K arrival protocol (common.hpp): steps 2-4
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's partial stores are complete
     __syncthreads();

@@ -166,6 +166,7 @@ __global__ __launch_bounds__(kKvThreads, 2) void kv_attention_kernel(KvParams p)
                 }
             }
         }
+        // split-K arrival protocol (common.hpp): steps 2-4
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this thread's stores (and raw scores) are complete
         __syncthreads();

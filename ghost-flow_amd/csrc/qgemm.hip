@@ -817,6 +817,7 @@ __global__ __launch_bounds__(kThreads) void qlinear_skinny_kernel(SkParams sp) {
                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
     }
+    // split-K arrival protocol (common.hpp): steps 2-4
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     int last = 0;
@@ -1139,6 +1140,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void qlinear_skinny_lds_kernel(Para
                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
     }
+    // split-K arrival protocol (common.hpp): steps 2-4
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     wait_vmcnt<0>();
     int last = 0;

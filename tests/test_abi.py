@@ -98,6 +98,22 @@ def test_gemv_batch_limit():
     assert lib.gfh_gemv_w8(None, None, None, None, None, 65, 16, 16, None) == 1
 
 
+def test_flash_attention_shape_rules():
+    """FlashAttention::forward's host checks: block sizes must be positive
+    (the reference's step_by(0) panics), at most 8192 key blocks; the
+    workspace size is batch * seq_len_q * seq_len_k floats."""
+    lib = _lib()
+    args = (None, None, None, None, 1, 4, 4, 8)
+    assert lib.gfh_flash_attention_f32(*args, 0, 64, 0, 1.0, None, 0, None) == 1
+    assert b"block sizes" in lib.gfh_last_error()
+    assert lib.gfh_flash_attention_f32(*args, 64, -1, 0, 1.0, None, 0, None) == 1
+    assert lib.gfh_flash_attention_f32(None, None, None, None, 1, 4, 8193, 8, 64, 1, 0, 1.0, None, 0, None) == 1
+    assert b"key blocks" in lib.gfh_last_error()
+    assert lib.gfh_flash_attention_f32(*args, 64, 64, 0, 1.0, None, 0, None) == 3  # NULL q
+    assert lib.gfh_flash_attention_workspace_size(3, 5, 7) == 3 * 5 * 7 * 4
+    assert lib.gfh_flash_attention_workspace_size(3, 5, 0) == 0
+
+
 def test_sdpa_shape_rules():
     lib = _lib()
     # head_dim must be a multiple of 4 in [4,128]
@@ -105,6 +121,7 @@ def test_sdpa_shape_rules():
     assert lib.gfh_sdpa_f32(None, None, None, None, None, 1, 1, 8, 8, 6, 1.0, 0, None, 0, None) == 1
     # causal needs sq == skv
     assert lib.gfh_sdpa_f32(None, None, None, None, None, 1, 1, 8, 9, 16, 1.0, 1, None, 0, None) == 1
+    assert b"gfh_flash_attention_f32" in lib.gfh_last_error()  # the documented route for top-left causal
     # missing tensors
     assert lib.gfh_sdpa_f32(None, None, None, None, None, 1, 1, 8, 8, 16, 1.0, 1, None, 0, None) == 3
 
