@@ -7,7 +7,9 @@
 // sends those calls here when the problem fills the GPU with such tiles;
 // the general tile kernel (sgemm.hip) serves everything else.
 //
-// Design (one 512-thread workgroup = 8 wave64s, 2 x 4, per 256 x 256 tile):
+// Design (one 512-thread workgroup = 8 wave64s, 2 x 4, per 256 x 256 tile;
+// 64 x 64 tiles run 2 x 2 waves twice over, as two wave sets that split
+// every stage's k-groups and add their accumulators through LDS at the end):
 //  * Each wave holds a 128 x 64 sub-tile as 4 x 2 v_mfma_f32_32x32x2_f32
 //    accumulators (128 registers): 8 independent MFMA chains, and two waves
 //    per SIMD so that one issues MFMAs while the other waits on LDS.
@@ -51,15 +53,22 @@ constexpr int kKGroups = BKB / 32;  // 8-float k-groups per stage
 // Geometry of a BM x BN tile on an NWM_ x NWN_ wave grid with an
 // STAGES_-deep ring: 256 x 256 and 128 x 128 on 2 x 4 waves and 2 stages,
 // 64 x 64 on 2 x 2 waves and 4 stages.
-template <int BM, int BN, bool NN, int NWM_ = 2, int NWN_ = 4, int STAGES_ = 2>
+template <int BM, int BN, bool NN, int NWM_ = 2, int NWN_ = 4, int STAGES_ = 2, int KS_ = 1>
 struct Geo {
-    static constexpr int NWM = NWM_, NWN = NWN_, NW = NWM * NWN, NT = 64 * NW;  // wave grid, threads
+    // KS wave sets share the tile: set s computes k-groups [s kKGroups / KS,
+    // (s + 1) kKGroups / KS) of every stage into its own accumulators, which
+    // are added through LDS at the end -- KS waves per SIMD on a tile that
+    // has one wave per SIMD otherwise.
+    static constexpr int KS = KS_;
+    static_assert(KS == 1 || KS == 2, "wave sets");
+    static constexpr int NWM = NWM_, NWN = NWN_, NW = NWM * NWN;  // tile wave grid
+    static constexpr int NWT = NW * KS, NT = 64 * NWT;            // waves, threads
     static constexpr int STAGES = STAGES_;
     static constexpr int WM = BM / NWM, WN = BN / NWN;  // wave sub-tile
     static constexpr int FM = WM / 32, FN = WN / 32;    // accumulators per wave
-    // load instructions (1 KB each) per wave per stage
-    static constexpr int kLA = BM * BKB / (1024 * NW), kLB = BN * BKB / (1024 * NW);
-    static_assert(kLA * 1024 * NW == BM * BKB && kLB * 1024 * NW == BN * BKB, "whole load instructions per wave");
+    // load instructions (1 KB each) per wave per stage, over all NWT waves
+    static constexpr int kLA = BM * BKB / (1024 * NWT), kLB = BN * BKB / (1024 * NWT);
+    static_assert(kLA * 1024 * NWT == BM * BKB && kLB * 1024 * NWT == BN * BKB, "whole load instructions per wave");
     static constexpr int kLPS = kLA + kLB;
     static constexpr int kABytes = BM * BKB;
     // NN: a load instruction fills RPL k-rows of BN floats (1 KB); groups
@@ -77,6 +86,7 @@ struct Geo {
     static constexpr int kOut = NW * kOutRows * kOutStride * 4;
     static constexpr int kLds = STAGES * kStageBytes > kOut ? STAGES * kStageBytes : kOut;
     static_assert(kLds <= 160 * 1024, "LDS per workgroup");
+    static_assert(KS == 1 || NW * FM * FN * 16 * 64 * 4 <= kLds, "accumulator exchange fits the ring");
     static_assert(FM >= 1 && FN >= 1 && (FM == 1 || FM % 2 == 0), "wave sub-tile");
     static_assert((STAGES - 1) * kLPS < 64, "vmcnt is 6 bits");
     // byte offset of k-row r inside an NN B stage
@@ -118,20 +128,24 @@ __device__ __forceinline__ void interleave() {
     }
 }
 
-template <int BM, int BN, bool NN, int NWM_ = 2, int NWN_ = 4, int STAGES_ = 2>
-__global__ __launch_bounds__((Geo<BM, BN, NN, NWM_, NWN_, STAGES_>::NT),
+template <int BM, int BN, bool NN, int NWM_ = 2, int NWN_ = 4, int STAGES_ = 2, int KS_ = 1>
+__global__ __launch_bounds__((Geo<BM, BN, NN, NWM_, NWN_, STAGES_, KS_>::NT),
                              (BM * BN <= 128 * 128) ? 2 : 1) void sgemm_big_kernel(BigParams p) {
-    using G = Geo<BM, BN, NN, NWM_, NWN_, STAGES_>;
-    constexpr int NWN = G::NWN, NW = G::NW, STAGES = G::STAGES;
+    using G = Geo<BM, BN, NN, NWM_, NWN_, STAGES_, KS_>;
+    constexpr int NWN = G::NWN, NW = G::NW, NWT = G::NWT, STAGES = G::STAGES, KS = G::KS;
+    constexpr int KGP = kKGroups / KS;  // k-groups per stage of this wave's set
     constexpr int WM = G::WM, WN = G::WN, FM = G::FM, FN = G::FN;
     constexpr int kLA = G::kLA, kLB = G::kLB, kLPS = G::kLPS;
     constexpr int kABytes = G::kABytes, kStageBytes = G::kStageBytes, kOutStride = G::kOutStride;
     __shared__ __attribute__((aligned(1024))) char lds[G::kLds];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm0 = (wave / NWN) * WM;
-    const int wn0 = (wave % NWN) * WN;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // 0 .. NWT - 1: loads
+    const int wt = wave % NW;                                     // position in the tile
+    const int ks = wave / NW;                                     // wave set
+    const int kg0 = ks * KGP;                                     // its first k-group of a stage
+    const int wm0 = (wt / NWN) * WM;
+    const int wn0 = (wt % NWN) * WN;
 
     const int nblk = p.tiles_m * p.tiles_n;
     int bid = blockIdx.x;
@@ -154,7 +168,7 @@ __global__ __launch_bounds__((Geo<BM, BN, NN, NWM_, NWN_, STAGES_>::NT),
     int64_t a_off[kLA], b_off[kLB];
 #pragma unroll
     for (int j = 0; j < kLA; ++j) {
-        const int r = wave * (BM / NW) + j * kRowsPerLoad + lane / 8;
+        const int r = wave * (BM / NWT) + j * kRowsPerLoad + lane / 8;
         a_off[j] = (min(m0 + r, p.m - 1) - m0) * p.lda * 4 + ((lane % 8) ^ swz(r)) * 16;
     }
 #pragma unroll
@@ -167,7 +181,7 @@ __global__ __launch_bounds__((Geo<BM, BN, NN, NWM_, NWN_, STAGES_>::NT),
             const int kr = (wave * kLB + j) * G::RPL + lane / LPR;
             b_off[j] = (int64_t)kr * p.ldb * 4 + (min(n0 + 4 * (lane % LPR), p.n - 4) - n0) * 4;
         } else {
-            const int r = wave * (BN / NW) + j * kRowsPerLoad + lane / 8;
+            const int r = wave * (BN / NWT) + j * kRowsPerLoad + lane / 8;
             b_off[j] = (min(n0 + r, p.n - 1) - n0) * p.ldb * 4 + ((lane % 8) ^ swz(r)) * 16;
         }
     }
@@ -182,10 +196,10 @@ __global__ __launch_bounds__((Geo<BM, BN, NN, NWM_, NWN_, STAGES_>::NT),
 #pragma unroll
         for (int j = 0; j < kLA; ++j)
             __builtin_amdgcn_global_load_lds((glb_ptr)(a_base + kb + a_off[j]),
-                                             (lds_ptr)(la + (wave * (BM / NW) + j * kRowsPerLoad) * BKB), 16, 0, 0);
+                                             (lds_ptr)(la + (wave * (BM / NWT) + j * kRowsPerLoad) * BKB), 16, 0, 0);
 #pragma unroll
         for (int j = 0; j < kLB; ++j) {
-            char *dst = NN ? lb + (wave * kLB + j) * G::kGroupStride : lb + (wave * (BN / NW) + j * kRowsPerLoad) * BKB;
+            char *dst = NN ? lb + (wave * kLB + j) * G::kGroupStride : lb + (wave * (BN / NWT) + j * kRowsPerLoad) * BKB;
             __builtin_amdgcn_global_load_lds((glb_ptr)(b_base + (int64_t)t * b_stage + b_off[j]), (lds_ptr)dst, 16, 0,
                                              0);
         }
@@ -239,13 +253,13 @@ __global__ __launch_bounds__((Geo<BM, BN, NN, NWM_, NWN_, STAGES_>::NT),
     for (int t = 0; t < STAGES; ++t) issue(min(t, nk - 1), t);
     wait_vmcnt<(STAGES - 1) * kLPS>();
     __builtin_amdgcn_s_barrier();
-    load_frags(0, 0, 0);
+    load_frags(0, 0, kg0);
     // (inlined: a call would pass the accumulators through scratch memory)
     auto k_groups = [&](int t) __attribute__((always_inline)) {
 #pragma unroll
-        for (int kg = 0; kg + 1 < kKGroups; ++kg) {
-            load_frags((kg + 1) & 1, t, kg + 1);
-            mfmas(kg & 1);
+        for (int u = 0; u + 1 < KGP; ++u) {
+            load_frags((u + 1) & 1, t, kg0 + u + 1);
+            mfmas(u & 1);
             interleave<0, NR, NM>();
         }
     };
@@ -256,14 +270,38 @@ __global__ __launch_bounds__((Geo<BM, BN, NN, NWM_, NWN_, STAGES_>::NT),
         wait_vmcnt<(STAGES - 2) * kLPS>();  // stage t + 1 landed
         __builtin_amdgcn_s_barrier();
         issue(min(t + STAGES, nk - 1), t % STAGES);
-        load_frags(0, t + 1, 0);
-        mfmas((kKGroups - 1) & 1);
+        load_frags(0, t + 1, kg0);
+        mfmas((KGP - 1) & 1);
         interleave<kLPS, NR, NM>();
         __builtin_amdgcn_sched_barrier(0);
     }
     k_groups(nk - 1);
-    mfmas((kKGroups - 1) & 1);
+    mfmas((KGP - 1) & 1);
     wait_vmcnt<0>();  // no load may still be writing the ring
+
+    if constexpr (KS == 2) {
+        // set 1 hands its accumulators to set 0 through the idle ring; set 0
+        // adds them (set 0 + set 1, a fixed order) and writes the tile
+        __syncthreads();
+        float *xch = reinterpret_cast<float *>(lds) + wt * (FM * FN * 16 * 64) + lane;
+        if (ks == 1) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) xch[((i * FN + j) * 16 + r) * 64] = acc[i][j][r];
+        }
+        __syncthreads();
+        if (ks == 0) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] = acc[i][j][r] + xch[((i * FN + j) * 16 + r) * 64];
+        }
+    }
 
     // Epilogue.  Lane l, register r of block (i, j): row 8 (r / 4) +
     // 4 (l / 32) + r % 4, column l % 32.  Each wave converts half of its
@@ -276,46 +314,48 @@ __global__ __launch_bounds__((Geo<BM, BN, NN, NWM_, NWN_, STAGES_>::NT),
     constexpr int BPP = FM / PASSES;   // 32-row blocks per pass
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();  // every wave is done with the operand ring
-    float *lt = reinterpret_cast<float *>(lds) + wave * (HALF * kOutStride);
+    float *lt = reinterpret_cast<float *>(lds) + wt * (HALF * kOutStride);
     const bool vec_out = (p.ldc % 4) == 0 && (reinterpret_cast<uintptr_t>(p.c) & 15) == 0;
 #pragma unroll
     for (int hf = 0; hf < PASSES; ++hf) {
+        if (KS == 1 || ks == 0) {  // (set 1 only keeps the barriers)
 #pragma unroll
-        for (int ii = 0; ii < BPP; ++ii)
+            for (int ii = 0; ii < BPP; ++ii)
 #pragma unroll
-            for (int j = 0; j < FN; ++j)
+                for (int j = 0; j < FN; ++j)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int lr = ii * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    lt[lr * kOutStride + j * 32 + (lane & 31)] = p.alpha * acc[hf * BPP + ii][j][r];
-                }
-        const int64_t col = n0 + wn0 + 4 * (lane % LPR);
+                    for (int r = 0; r < 16; ++r) {
+                        const int lr = ii * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                        lt[lr * kOutStride + j * 32 + (lane & 31)] = p.alpha * acc[hf * BPP + ii][j][r];
+                    }
+            const int64_t col = n0 + wn0 + 4 * (lane % LPR);
 #pragma unroll
-        for (int q = 0; q < HALF / RPI; ++q) {
-            const int lr = RPI * q + lane / LPR;
-            f32x4 v = *reinterpret_cast<const f32x4 *>(lt + lr * kOutStride + 4 * (lane % LPR));
-            const int64_t row = m0 + wm0 + hf * HALF + lr;
-            if (row >= p.m) continue;
-            float *dst = p.c + row * p.ldc + col;
-            if (vec_out && col + 3 < p.n) {
-                if (p.beta != 0.f) {
-                    const f32x4 c0 = *reinterpret_cast<const f32x4 *>(dst);
+            for (int q = 0; q < HALF / RPI; ++q) {
+                const int lr = RPI * q + lane / LPR;
+                f32x4 v = *reinterpret_cast<const f32x4 *>(lt + lr * kOutStride + 4 * (lane % LPR));
+                const int64_t row = m0 + wm0 + hf * HALF + lr;
+                if (row >= p.m) continue;
+                float *dst = p.c + row * p.ldc + col;
+                if (vec_out && col + 3 < p.n) {
+                    if (p.beta != 0.f) {
+                        const f32x4 c0 = *reinterpret_cast<const f32x4 *>(dst);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) v[e] = v[e] + p.beta * c0[e];
-                }
-                if (p.bias) {
+                        for (int e = 0; e < 4; ++e) v[e] = v[e] + p.beta * c0[e];
+                    }
+                    if (p.bias) {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) v[e] = v[e] + p.bias[col + e];
-                }
-                *reinterpret_cast<f32x4 *>(dst) = v;
-            } else {
+                        for (int e = 0; e < 4; ++e) v[e] = v[e] + p.bias[col + e];
+                    }
+                    *reinterpret_cast<f32x4 *>(dst) = v;
+                } else {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    if (col + e >= p.n) continue;
-                    float x = v[e];
-                    if (p.beta != 0.f) x = x + p.beta * dst[e];
-                    if (p.bias) x = x + p.bias[col + e];
-                    dst[e] = x;
+                    for (int e = 0; e < 4; ++e) {
+                        if (col + e >= p.n) continue;
+                        float x = v[e];
+                        if (p.beta != 0.f) x = x + p.beta * dst[e];
+                        if (p.bias) x = x + p.bias[col + e];
+                        dst[e] = x;
+                    }
                 }
             }
         }
@@ -386,11 +426,14 @@ int launch_sgemm_big(const SgemmDesc &d, hipStream_t s) {
                 hipLaunchKernelGGL((sgemm_big_kernel<128, 128, true>), grid, dim3(kNT), 0, s, p);
         }
     } else {
-        // (NT 4 stages, NN 3: the better of 3 / 4 / 6 at 1024^3)
+        // Two wave sets splitting each stage's k-groups, so each SIMD runs
+        // two waves (1024^3 NN 24.1 -> 22.0 us, 1024 x 1024 x 4096 NN 86.3
+        // -> 77.5 us; NT unchanged).  Ring depth: NT 4 stages, NN 2 (of
+        // 2 / 3 / 4 / 6: NN 22.0 / 22.8 / 22.2 / 22.4 us at 1024^3).
         if (d.trans_b)
-            hipLaunchKernelGGL((sgemm_big_kernel<64, 64, false, 2, 2, 4>), grid, dim3(kNT64), 0, s, p);
+            hipLaunchKernelGGL((sgemm_big_kernel<64, 64, false, 2, 2, 4, 2>), grid, dim3(2 * kNT64), 0, s, p);
         else
-            hipLaunchKernelGGL((sgemm_big_kernel<64, 64, true, 2, 2, 3>), grid, dim3(kNT64), 0, s, p);
+            hipLaunchKernelGGL((sgemm_big_kernel<64, 64, true, 2, 2, 2, 2>), grid, dim3(2 * kNT64), 0, s, p);
     }
     return check_launch("sgemm (direct-to-LDS tiles)");
 }
