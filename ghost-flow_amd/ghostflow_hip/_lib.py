@@ -1,4 +1,5 @@
-"""ctypes declarations of the C ABI in include/ghostflow_hip.h.
+"""ctypes declarations of the C ABI in include/ghostflow_hip.h and of the
+Tensor-level API in include/ghostflow.h.
 
 The shared library is built in-tree (ghost-flow_amd/Makefile) and loaded from
 this directory.  There is no fallback: if the library is missing the import
@@ -82,6 +83,26 @@ SIGNATURES = {
                            _sz, _p]),
 }
 
+# The Tensor-level API of include/ghostflow.h (ghostflow-ffi/src/lib.rs).
+_up = C.POINTER(C.c_size_t)
+_tp = C.c_void_p
+TENSOR_SIGNATURES = {
+    "ghostflow_init": (_i, []),
+    "ghostflow_version": (_p, []),
+    "ghostflow_free_string": (None, [_p]),
+    "ghostflow_tensor_create": (_i, [C.POINTER(C.c_float), _sz, _up, _sz, C.POINTER(_tp)]),
+    "ghostflow_tensor_zeros": (_i, [_up, _sz, C.POINTER(_tp)]),
+    "ghostflow_tensor_ones": (_i, [_up, _sz, C.POINTER(_tp)]),
+    "ghostflow_tensor_free": (None, [_tp]),
+    "ghostflow_tensor_shape": (_i, [_tp, _up, C.POINTER(C.c_size_t)]),
+    "ghostflow_tensor_data": (_i, [_tp, C.POINTER(C.c_float), C.POINTER(C.c_size_t)]),
+    "ghostflow_tensor_add": (_i, [_tp, _tp, C.POINTER(_tp)]),
+    "ghostflow_tensor_mul": (_i, [_tp, _tp, C.POINTER(_tp)]),
+    "ghostflow_tensor_matmul": (_i, [_tp, _tp, C.POINTER(_tp)]),
+    "ghostflow_tensor_reshape": (_i, [_tp, _up, _sz, C.POINTER(_tp)]),
+    "ghostflow_get_last_error": (C.c_char_p, []),
+}
+
 _lib = None
 
 
@@ -101,7 +122,7 @@ def load():
                 f"{LIB_PATH} is not built; run __graft_entry__.build() "
                 "(or make -C ghost-flow_amd) first")
         lib = C.CDLL(LIB_PATH)
-        for name, (res, args) in SIGNATURES.items():
+        for name, (res, args) in list(SIGNATURES.items()) + list(TENSOR_SIGNATURES.items()):
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args

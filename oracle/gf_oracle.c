@@ -48,6 +48,10 @@
  *       exhaustive numpy restatement on random data.
  *   gfo_qlinear_i8 : int32 accumulator against an int64 brute force GEMM;
  *       epilogue against an fp64 evaluation of the same formula.
+ *   gfo_broadcast_binary : the reference's own add tests ([1,2,3] + [4,5,6]
+ *       = [5,7,9] and [3,1] + [1,2] -> [3,2], arithmetic.rs:257-271); numpy
+ *       broadcasting (a single IEEE add / mul per element, so bit-exact) on
+ *       stretched, prepended, scalar and zero-size shapes.
  */
 #include <math.h>
 #include <stddef.h>
@@ -136,6 +140,56 @@ GFO_API void gfo_batched_matmul(const float *a, size_t a_batch,
                 cs[i * n + j] = sum;
             }
     }
+}
+
+/* ------------------------------------------------------------------------ */
+/* ghostflow-core/src/ops/arithmetic.rs                                      */
+/* ------------------------------------------------------------------------ */
+
+/* arithmetic.rs:123-200 `broadcast_binary_op` for op 0 = add (x + y,
+ * :20-26) and op 1 = mul (x * y, :39-45).  The caller passes the result
+ * dims of Shape::broadcast_with (shape.rs:49-80).  Same shapes: element by
+ * element (:141-154).  Otherwise each operand gets the strides of
+ * compute_broadcast_strides (:180-201): walking its dims from the last,
+ * stride = running product where its dim equals the result's (aligned at
+ * the trailing dim), 0 where it is stretched; and flat index i of the
+ * result is split innermost-first by compute_broadcast_index (:204-215). */
+GFO_API void gfo_broadcast_binary(int op, const float *a, const size_t *a_dims, size_t a_nd,
+                                  const float *b, const size_t *b_dims, size_t b_nd,
+                                  float *c, const size_t *c_dims, size_t c_nd) {
+    size_t numel = 1;
+    for (size_t i = 0; i < c_nd; ++i) numel *= c_dims[i];
+    int same = a_nd == b_nd;
+    for (size_t i = 0; same && i < a_nd; ++i) same = a_dims[i] == b_dims[i];
+    if (same) {
+        for (size_t i = 0; i < numel; ++i) c[i] = op == 0 ? a[i] + b[i] : a[i] * b[i];
+        return;
+    }
+    size_t *sa = calloc(c_nd ? c_nd : 1, sizeof(size_t)), *sb = calloc(c_nd ? c_nd : 1, sizeof(size_t));
+    for (int w = 0; w < 2; ++w) {
+        const size_t *dims = w ? b_dims : a_dims, nd = w ? b_nd : a_nd, off = c_nd - nd;
+        size_t *st = w ? sb : sa, stride = 1;
+        for (size_t i = nd; i-- > 0;) {
+            if (dims[i] == c_dims[i + off]) {
+                st[i + off] = stride;
+                stride *= dims[i];
+            } else {
+                st[i + off] = 0;
+            }
+        }
+    }
+    for (size_t i = 0; i < numel; ++i) {
+        size_t ia = 0, ib = 0, rem = i;
+        for (size_t d = c_nd; d-- > 0;) {
+            size_t coord = rem % c_dims[d];
+            rem /= c_dims[d];
+            ia += coord * sa[d];
+            ib += coord * sb[d];
+        }
+        c[i] = op == 0 ? a[ia] + b[ib] : a[ia] * b[ib];
+    }
+    free(sa);
+    free(sb);
 }
 
 /* ------------------------------------------------------------------------ */

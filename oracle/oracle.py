@@ -36,6 +36,8 @@ def lib():
         L = C.CDLL(_LIB_PATH)
         L.gfo_matmul_blocked.argtypes = [_f32p, _f32p, _f32p, _sz, _sz, _sz]
         L.gfo_batched_matmul.argtypes = [_f32p, _sz, _f32p, _sz, _f32p, _sz, _sz, _sz, _sz]
+        _szp = np.ctypeslib.ndpointer(np.uintp, flags="C_CONTIGUOUS")
+        L.gfo_broadcast_binary.argtypes = [C.c_int, _f32p, _szp, _sz, _f32p, _szp, _sz, _f32p, _szp, _sz]
         L.gfo_transpose_last2.argtypes = [_f32p, _f32p, _sz, _sz, _sz]
         L.gfo_matmul_backward.argtypes = [_f32p, _f32p, _f32p, _sz, _sz, _sz, C.c_void_p, C.c_void_p]
         L.gfo_add_row_bias.argtypes = [_f32p, _f32p, _sz, _sz]
@@ -101,6 +103,32 @@ def batched_matmul(a, b):
     batch = int(np.prod(batch_shape)) if batch_shape else 1
     c = np.empty(tuple(batch_shape) + (m, n), np.float32)
     lib().gfo_batched_matmul(a, ab, b, bb, c, batch, m, k, n)
+    return c
+
+
+def broadcast_binary(a, b, op):
+    """Tensor::add / Tensor::mul (arithmetic.rs:19-45, broadcast_binary_op
+    :123-215); op is "add" or "mul".  Result dims by Shape::broadcast_with
+    (shape.rs:49-80); ValueError where the shapes do not broadcast."""
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    nd = max(a.ndim, b.ndim)
+    dims = []
+    for i in range(nd):
+        x = a.shape[a.ndim - 1 - i] if i < a.ndim else 1
+        y = b.shape[b.ndim - 1 - i] if i < b.ndim else 1
+        if x == y or y == 1:
+            dims.append(x)
+        elif x == 1:
+            dims.append(y)
+        else:
+            raise ValueError(f"BroadcastError a {list(a.shape)} b {list(b.shape)}")
+    dims = dims[::-1]
+    c = np.empty(dims, np.float32)
+    ad = np.array(a.shape or (1,), np.uintp)
+    bd = np.array(b.shape or (1,), np.uintp)
+    cd = np.array(dims or [1], np.uintp)
+    lib().gfo_broadcast_binary({"add": 0, "mul": 1}[op], np.ascontiguousarray(a).reshape(-1), ad, a.ndim,
+                               np.ascontiguousarray(b).reshape(-1), bd, b.ndim, c.reshape(-1), cd, len(dims))
     return c
 
 

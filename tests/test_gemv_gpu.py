@@ -21,10 +21,14 @@ def _O():
 
 
 @pytest.mark.parametrize("b,k,n", [(1, 1, 1), (3, 64, 80), (1, 300, 999), (8, 1024, 1024), (5, 77, 1030),
-                                   (13, 256, 512), (64, 128, 260), (8, 3000, 12300), (6, 4096, 16384)])
+                                   (13, 256, 512), (64, 128, 260), (8, 3000, 12300), (6, 4096, 16384),
+                                   (1, 2500, 12800), (2, 4096, 13000), (4, 1000, 16000), (3, 2000, 25600),
+                                   (9, 4096, 14336)])
 def test_gemv_f32_integer_exact(torch_dev, b, k, n):
-    """Integer data (exact in any order); the last two shapes take the
-    single-slice 8-row form with 4096 rows of x in LDS (192-256 strips)."""
+    """Integer data (exact in any order).  From (8, 3000, 12300) on, wide
+    N: 192-256 strips in one slice (4096 rows of x in LDS for 8-row groups),
+    2-4 slices with ragged K and a ragged last strip, and a second batch
+    group of 1 row at b = 9."""
     gh, O = _gh(), _O()
     rng = np.random.default_rng(b * 7 + k + n)
     x = rng.integers(-8, 9, size=(b, k)).astype(np.float32)

@@ -104,6 +104,37 @@ def test_batched_matmul_modulo_indexing():
         np.testing.assert_array_equal(got.reshape(6, 4, 5)[i], (af[i] @ b[i % 3]).astype(np.float32))
 
 
+def test_broadcast_binary_reference_known_answers():
+    """arithmetic.rs:257-271: [1,2,3] + [4,5,6] = [5,7,9]; [3,1] + [1,2] has
+    dims [3,2] (values fixed by the broadcast rule: a[i] + b[j])."""
+    assert O.broadcast_binary([1, 2, 3], [4, 5, 6], "add").tolist() == [5, 7, 9]
+    c = O.broadcast_binary(np.array([[1], [2], [3]], np.float32), np.array([[10, 20]], np.float32), "add")
+    assert c.shape == (3, 2)
+    assert c.tolist() == [[11, 21], [12, 22], [13, 23]]
+
+
+@pytest.mark.parametrize("sa,sb", [((4, 1, 3), (2, 3)), ((5,), ()), ((), (2, 2)), ((3, 1), (1, 4)),
+                                   ((2, 3, 4), (3, 1)), ((1, 1, 7), (6, 1, 1)), ((2, 0, 3), (1, 3)),
+                                   ((6, 5), (6, 5)), ((1,), (1, 1, 1))])
+@pytest.mark.parametrize("op", ["add", "mul"])
+def test_broadcast_binary_matches_numpy(sa, sb, op):
+    """Each element is one IEEE float32 add or multiply of the broadcast
+    operands, so numpy broadcasting gives the same bits; a dropped or
+    swapped stride would fetch the wrong element."""
+    rng = np.random.default_rng(len(sa) * 10 + len(sb))
+    a = rng.standard_normal(sa).astype(np.float32)
+    b = rng.standard_normal(sb).astype(np.float32)
+    want = (np.add if op == "add" else np.multiply)(a, b)
+    got = O.broadcast_binary(a, b, op)
+    assert got.shape == want.shape
+    np.testing.assert_array_equal(got, want)
+
+
+def test_broadcast_binary_rejects_incompatible():
+    with pytest.raises(ValueError):
+        O.broadcast_binary(np.zeros((2, 3), np.float32), np.zeros((4,), np.float32), "add")
+
+
 def test_transpose_last2_index_map():
     x = np.arange(2 * 3 * 5, dtype=np.float32).reshape(2, 3, 5)
     t = O.transpose_last2(x)
