@@ -398,14 +398,11 @@ GFH_API int gfh_flash_attention_f32(const float *q, const float *k, const float 
         GFH_TRY(require_range(out, (size_t)qn * 4, "out"));
         GFH_TRY(ensure_init());
         hipStream_t s = as_stream(stream);
-        Scratch ws;
-        GFH_TRY(ws.acquire(workspace, workspace_bytes, (size_t)sn * 4, s));
         FlashAttnDesc d;
         d.q = q;
         d.k = k;
         d.v = v;
         d.out = out;
-        d.ws = static_cast<float *>(ws.ptr());
         d.batch = batch;
         d.sq = seq_len_q;
         d.sk = seq_len_k;
@@ -414,6 +411,9 @@ GFH_API int gfh_flash_attention_f32(const float *q, const float *k, const float 
         d.block_n = block_size_n;
         d.causal = causal != 0;
         d.scale = scale;
+        Scratch ws;
+        GFH_TRY(ws.acquire(workspace, workspace_bytes, flash_attention_workspace_bytes(d), s));
+        d.ws = static_cast<float *>(ws.ptr());
         return launch_flash_attention_blockwise(d, s);
     });
 }

@@ -36,6 +36,7 @@
 #include <algorithm>
 #include <cmath>
 
+#include "attn_tiles.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -48,7 +49,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kBQ = 128;  // queries per workgroup (32 per wave)
-constexpr int kBKV = 32;  // keys per LDS tile
+constexpr int kBKV = attn::kBKV;  // keys per LDS tile
 
 // Element (b, h, i, d) of q is at q[b*q_bs + h*q_hs + i*q_rs + d] (K, V with
 // the kv_* strides, the output with o_*): [B, H, S, D] contiguous, or the
@@ -71,37 +72,9 @@ struct SdpaParams {
     int fold;  // causal issue order for a grid that is resident all at once (below)
 };
 
-__device__ __forceinline__ int key_of(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
-
-// One 32-key x DMAX tile of K or V: DMAX*8 float4 per tile, DMAX/32 per thread.
+using attn::key_of;
 template <int DMAX>
-struct KvStage {
-    static constexpr int kPer = kBKV * DMAX / 4 / kThreads;
-    static constexpr int kStride = DMAX + 4;
-    f32x4 r[kPer];
-
-    __device__ __forceinline__ void load(const float *__restrict__ base, int64_t key0, int64_t nkeys, int64_t d,
-                                         int64_t rs, int tid) {
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const int idx = tid + i * kThreads;
-            const int key = idx / (DMAX / 4);
-            const int dim = (idx % (DMAX / 4)) * 4;
-            f32x4 v = {0.f, 0.f, 0.f, 0.f};
-            if (key0 + key < nkeys && dim < d) v = *reinterpret_cast<const f32x4 *>(base + (key0 + key) * rs + dim);
-            r[i] = v;
-        }
-    }
-    __device__ __forceinline__ void store(float *lds, int tid) const {
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const int idx = tid + i * kThreads;
-            const int key = idx / (DMAX / 4);
-            const int dim = (idx % (DMAX / 4)) * 4;
-            *reinterpret_cast<f32x4 *>(lds + key * kStride + dim) = r[i];
-        }
-    }
-};
+using KvStage = attn::KvStage<DMAX, kThreads>;
 
 // Scaled, masked scores of one 32-key tile for this lane's query.
 template <int DMAX, bool CAUSAL, bool MASK>

@@ -33,6 +33,7 @@
 #include <algorithm>
 #include <cmath>
 
+#include "attn_tiles.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -167,6 +168,225 @@ __global__ __launch_bounds__(kFaThreads) void fa_weights_kernel(FaRow p) {
     }
 }
 
+// ---- fused two-pass form --------------------------------------------------
+//
+// With block_n a multiple of the 32-key tile, each tile lies in one key
+// block and the weights need, per row, only the running max M_t after each
+// block: for t >= 1
+//   W_j = exp((s_j - M_t) + (n_t - 1 - idx_j) (M_{t-1} - M_t) + E_t) / l,
+// block 0 keeping only its last key, and E_t = sum over later blocks t' <= V
+// of n_t' (M_{t'-1} - M_t') -- V the last block holding a visible key (later
+// processed blocks are fully masked: M stays, they add nothing).  Every block
+// before V is full (n = block_n), so the sum telescopes:
+//   E_t = block_n (M_t - M_{V-1}) + n_V (M_{V-1} - M_V),  E_V = 0.
+// One workgroup per 128 queries (4 waves x 32) of one batch element, laid
+// out as the SDPA kernel (S^T = K . Q^T on v_mfma_f32_32x32x2_f32, lane =
+// query, 32-key K / V tiles double-buffered through LDS):
+//   pass 1: scores tile by tile; the online max m and sum l (l = sum of
+//           exp(s_j - M_V) over the visible keys); m after a block's last
+//           tile is M_t, written to mblk[row][t];
+//   pass 2: the same scores again (same instructions, so the same bits),
+//           W_j (unnormalized) from mblk, and O += W . V on the MFMA with the
+//           weights straight from the score registers; O / l at the end.
+// Work: 1.5x the matmul FLOPs of plain attention, no score matrix in HBM.
+// Keys are processed up to the workgroup's last query (causal) or all of
+// them: the reference's skip of blocks past a query block (:150-152) only
+// skips fully masked blocks, which change neither M nor O.
+struct FaFused {
+    const float *q, *k, *v;
+    float *out;
+    float *mblk;  // [batch * sq][nbw]
+    int64_t sq, sk, d, bn, nbw;
+    float scale;
+    int nqb, fold;
+};
+
+constexpr int kFaBQ = 128;  // queries per workgroup
+
+template <int DMAX, bool CAUSAL>
+__device__ __forceinline__ void fa_tile_scores(const FaFused &p, const float *ks, const f32x4 (&qf)[DMAX / 8],
+                                               int64_t k0, int64_t my_q, int lane, float (&sv)[16]) {
+    constexpr int NG = DMAX / 8;
+    constexpr int kStride = DMAX + 4;
+    const int c = lane & 31, h = lane >> 5;
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        const f32x4 kf = *reinterpret_cast<const f32x4 *>(ks + c * kStride + 8 * g + 4 * h);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[s], qf[g][s], acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int64_t key = k0 + attn::key_of(r, h);
+        bool keep = key < p.sk;
+        if (CAUSAL) keep = keep && key <= my_q;
+        sv[r] = keep ? acc[r] * p.scale : -INFINITY;
+    }
+}
+
+template <int DMAX, bool CAUSAL>
+__global__ __launch_bounds__(kFaThreads, 2) void fa_fused_kernel(FaFused p) {
+    using KvStage = attn::KvStage<DMAX, kFaThreads>;
+    constexpr int NG = DMAX / 8, ND = DMAX / 32;
+    constexpr int kStride = DMAX + 4;
+    constexpr int kBKV = attn::kBKV;
+    constexpr int kTile = kBKV * kStride;
+    __shared__ __attribute__((aligned(16))) float lds[4 * kTile];  // K0 K1 V0 V1
+    float *const lk = lds;
+    float *const lv = lds + 2 * kTile;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int c = lane & 31, h = lane >> 5;
+    const int64_t b = blockIdx.x;
+    // Causal: heaviest query blocks first, and for a grid resident all at
+    // once the light half in ascending order (as the SDPA kernel).
+    int qb = (int)blockIdx.y;
+    if (CAUSAL) {
+        const int y = (int)blockIdx.y, half = (p.nqb + 1) / 2;
+        qb = (p.fold && y >= half) ? y - half : p.nqb - 1 - y;
+    }
+    const int64_t q0 = (int64_t)qb * kFaBQ;
+    const int64_t wq0 = q0 + wave * 32;
+    const int64_t my_q = wq0 + c;
+    const bool row_ok = my_q < p.sq;
+    const float *Q = p.q + b * p.sq * p.d;
+    const float *K = p.k + b * p.sk * p.d;
+    const float *V = p.v + b * p.sk * p.d;
+    float *mrow = p.mblk + (b * p.sq + (row_ok ? my_q : p.sq - 1)) * p.nbw;
+
+    f32x4 qf[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        const int dim = 8 * g + 4 * h;
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        if (row_ok && dim < p.d) v = *reinterpret_cast<const f32x4 *>(Q + my_q * p.d + dim);
+        qf[g] = v;
+    }
+
+    const int64_t kv_end = CAUSAL ? min(p.sk, q0 + kFaBQ) : p.sk;
+    const int64_t ntiles = (kv_end + kBKV - 1) / kBKV;
+
+    // ---- pass 1: running max after every key block, and l ----
+    KvStage gk, gv;
+    gk.load(K, 0, p.sk, p.d, p.d, tid);
+    gk.store(lk, tid);
+    __syncthreads();
+    float m = -INFINITY, l = 0.f;
+    for (int64_t t = 0; t < ntiles; ++t) {
+        const int cur = t & 1;
+        const bool more = t + 1 < ntiles;
+        if (more) gk.load(K, (t + 1) * kBKV, p.sk, p.d, p.d, tid);
+        const int64_t k0 = t * kBKV;
+        if (!CAUSAL || k0 <= wq0 + 31) {
+            float sv[16];
+            fa_tile_scores<DMAX, CAUSAL>(p, lk + cur * kTile, qf, k0, my_q, lane, sv);
+            float mt = sv[0];
+#pragma unroll
+            for (int r = 1; r < 16; ++r) mt = fmaxf(mt, sv[r]);
+            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            const float m_new = fmaxf(m, mt);
+            const bool dead = (m_new == -INFINITY);
+            const float alpha = dead ? 1.f : __expf(m - m_new);
+            float ps = 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) ps += dead ? 0.f : __expf(sv[r] - m_new);
+            ps += __shfl_xor(ps, 32);
+            l = l * alpha + ps;
+            m = m_new;
+        }
+        // After a block's last tile m is that block's M_t.  Both halves of
+        // the wave hold the same m and write it, so each lane later reads
+        // back its own store.
+        if ((k0 + kBKV) % p.bn == 0 || !more) {
+            if (row_ok) mrow[k0 / p.bn] = m;
+        }
+        if (more) gk.store(lk + (cur ^ 1) * kTile, tid);
+        __syncthreads();
+    }
+
+    // ---- pass 2: the weights from M, and O = W . V ----
+    const int64_t jv = CAUSAL ? min(p.sk, my_q + 1) : p.sk;  // visible keys of this row
+    const int64_t vb = (jv - 1) / p.bn;                         // last block with one
+    const float m_v = m;
+    const float m_v1 = vb >= 1 ? mrow[vb - 1] : 0.f;
+    const float e_tail = vb >= 1 ? (float)min(p.bn, p.sk - vb * p.bn) * (m_v1 - m_v) : 0.f;
+    f32x16 o[ND];
+#pragma unroll
+    for (int j = 0; j < ND; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[j][r] = 0.f;
+
+    gk.load(K, 0, p.sk, p.d, p.d, tid);
+    gv.load(V, 0, p.sk, p.d, p.d, tid);
+    gk.store(lk, tid);
+    gv.store(lv, tid);
+    __syncthreads();
+    for (int64_t t = 0; t < ntiles; ++t) {
+        const int cur = t & 1;
+        const bool more = t + 1 < ntiles;
+        if (more) {
+            gk.load(K, (t + 1) * kBKV, p.sk, p.d, p.d, tid);
+            gv.load(V, (t + 1) * kBKV, p.sk, p.d, p.d, tid);
+        }
+        const int64_t k0 = t * kBKV;
+        if (!CAUSAL || k0 <= wq0 + 31) {
+            const int64_t blk = k0 / p.bn;
+            const float mt = mrow[blk];
+            const float mp = blk >= 1 ? mrow[blk - 1] : 0.f;
+            float sv[16];
+            fa_tile_scores<DMAX, CAUSAL>(p, lk + cur * kTile, qf, k0, my_q, lane, sv);
+            const int64_t n = min(p.bn, p.sk - blk * p.bn);
+            const float e = blk < vb ? (float)p.bn * (mt - m_v1) + e_tail : 0.f;
+            const float delta = mp - mt;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t idx = k0 + attn::key_of(r, h) - blk * p.bn;
+                float w = 0.f;
+                if (sv[r] != -INFINITY) {
+                    if (blk == 0)
+                        w = idx == n - 1 ? __expf((sv[r] - mt) + e) : 0.f;
+                    else
+                        w = __expf(((sv[r] - mt) + (float)(n - 1 - idx) * delta) + e);
+                }
+                sv[r] = w;
+            }
+            const float *vt = lv + cur * kTile;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float *vrow = vt + attn::key_of(r, h) * kStride + c;
+#pragma unroll
+                for (int j = 0; j < ND; ++j)
+                    o[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(vrow[32 * j], sv[r], o[j], 0, 0, 0);
+            }
+        }
+        if (more) {
+            gk.store(lk + (cur ^ 1) * kTile, tid);
+            gv.store(lv + (cur ^ 1) * kTile, tid);
+        }
+        __syncthreads();
+    }
+
+    // O / l.  Lane (query c, half h), register r of block j holds head dim
+    // 32 j + 8 (r / 4) + 4 h + r % 4.
+    if (row_ok) {
+        float *orow = p.out + (b * p.sq + my_q) * p.d;
+#pragma unroll
+        for (int j = 0; j < ND; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int dim = 32 * j + 8 * i + 4 * h;
+                if (dim < p.d) {
+                    f32x4 v = {o[j][4 * i] / l, o[j][4 * i + 1] / l, o[j][4 * i + 2] / l, o[j][4 * i + 3] / l};
+                    *reinterpret_cast<f32x4 *>(orow + dim) = v;
+                }
+            }
+    }
+}
+
 __global__ void fa_zero_kernel(float *p, int64_t n) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
         p[i] = 0.f;
@@ -176,8 +396,50 @@ __global__ void fa_zero_kernel(float *p, int64_t n) {
 
 int64_t flash_attention_max_blocks() { return 8192; }
 
+// The fused form needs whole 32-key tiles per key block, head dims the
+// 16-byte staging covers (d % 4 == 0, at most 128) and aligned operands.
+bool flash_attention_fused_fits(const FlashAttnDesc &d) {
+    return d.block_n % attn::kBKV == 0 && d.d > 0 && d.d <= 128 && d.d % 4 == 0 && aligned16(d.q) &&
+           aligned16(d.k) && aligned16(d.v) && aligned16(d.out) && (d.sq + kFaBQ - 1) / kFaBQ <= 65535;
+}
+
+size_t flash_attention_workspace_bytes(const FlashAttnDesc &d) {
+    if (d.sk > 0 && flash_attention_fused_fits(d))
+        return sizeof(float) * (size_t)d.batch * (size_t)d.sq * (size_t)((d.sk + d.block_n - 1) / d.block_n);
+    return sizeof(float) * (size_t)d.batch * (size_t)d.sq * (size_t)d.sk;
+}
+
 int launch_flash_attention_blockwise(const FlashAttnDesc &d, hipStream_t s) {
     if (d.batch == 0 || d.sq == 0 || d.d == 0) return GFH_SUCCESS;
+    if (d.sk > 0 && flash_attention_fused_fits(d)) {
+        FaFused p;
+        p.q = d.q;
+        p.k = d.k;
+        p.v = d.v;
+        p.out = d.out;
+        p.mblk = d.ws;
+        p.sq = d.sq;
+        p.sk = d.sk;
+        p.d = d.d;
+        p.bn = d.block_n;
+        p.nbw = (d.sk + d.block_n - 1) / d.block_n;
+        p.scale = d.scale;
+        p.nqb = (int)((d.sq + kFaBQ - 1) / kFaBQ);
+        p.fold = d.causal && d.batch * p.nqb <= 2 * (int64_t)device_cu_count();
+        const dim3 grid((unsigned)d.batch, (unsigned)p.nqb), block(kFaThreads);
+        if (d.d <= 64) {
+            if (d.causal)
+                hipLaunchKernelGGL((fa_fused_kernel<64, true>), grid, block, 0, s, p);
+            else
+                hipLaunchKernelGGL((fa_fused_kernel<64, false>), grid, block, 0, s, p);
+        } else {
+            if (d.causal)
+                hipLaunchKernelGGL((fa_fused_kernel<128, true>), grid, block, 0, s, p);
+            else
+                hipLaunchKernelGGL((fa_fused_kernel<128, false>), grid, block, 0, s, p);
+        }
+        return check_launch("flash_attention (fused)");
+    }
     const bool big_batch = d.batch > 16;
     // 1. S = scale * Q . K^T  (per batch element when the single-GEMM tile
     //    kernels fit, else one strided-batched call)

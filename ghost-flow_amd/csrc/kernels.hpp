@@ -104,6 +104,9 @@ struct FlashAttnDesc {
     float scale = 1.f;
 };
 int64_t flash_attention_max_blocks();
+// Scratch the launch needs in d.ws: the per-row block maxima of the fused
+// form, or the [batch, sq, sk] scores of the three-step form.
+size_t flash_attention_workspace_bytes(const FlashAttnDesc &d);
 int launch_flash_attention_blockwise(const FlashAttnDesc &d, hipStream_t s);
 
 // attention.hip

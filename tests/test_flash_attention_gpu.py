@@ -53,6 +53,13 @@ CASES = [
     (1, 64, 700, 20, 16, 1, False, 0.22),       # block_n = 1: softmax attention, 700 blocks
     (20, 33, 65, 37, 64, 64, True, 0.16),       # d % 4 != 0, many batches (strided-batched GEMMs)
     (4, 512, 512, 128, 64, 64, True, 0.0883883476),
+    # the fused two-pass form (block_n a multiple of 32, d % 4 == 0, d <= 128)
+    (3, 130, 130, 128, 64, 32, True, 0.09),     # one 32-key tile per block
+    (2, 300, 290, 64, 48, 96, True, 0.12),      # three tiles per block, ragged last block
+    (2, 181, 250, 128, 64, 64, False, 0.09),    # non-causal, ragged key blocks
+    (2, 40, 20, 16, 64, 64, True, 0.3),         # every key in block 0 (sk < block_n)
+    (1, 2048, 2048, 128, 64, 64, True, 0.0883883476),  # the bench's sequence length
+    (2, 77, 333, 128, 128, 256, True, 0.09),    # block_n larger than a workgroup's queries
 ]
 
 
@@ -64,6 +71,25 @@ def test_flash_attention_vs_oracle(torch_dev, bsz, sq, sk, d, bm, bn, causal, sc
     got = to_np(gh.flash_attention_blockwise(to_dev(q, torch_dev), to_dev(k, torch_dev), to_dev(v, torch_dev),
                                              block_size_m=bm, block_size_n=bn, causal=causal, scale=scale))
     _check(got, ref)
+
+
+def test_fused_and_three_step_forms_agree(torch_dev):
+    """The same layer through both GPU forms: block_n = 64 takes the fused
+    two-pass kernel on aligned inputs and the scores / weights / weights.V
+    path when q starts 4 bytes into its buffer (not 16-byte aligned)."""
+    import torch
+    gh = _gh()
+    q, k, v = _inputs(2, 200, 260, 64, 77)
+    dq, dk, dv = (to_dev(a, torch_dev) for a in (q, k, v))
+    fused = to_np(gh.flash_attention_blockwise(dq, dk, dv, block_size_m=64, block_size_n=64, causal=True,
+                                               scale=0.125))
+    buf = torch.empty(dq.numel() + 1, device=torch_dev)
+    dq_off = buf[1:].view_as(dq)
+    dq_off.copy_(dq)
+    three = to_np(gh.flash_attention_blockwise(dq_off, dk, dv, block_size_m=64, block_size_n=64, causal=True,
+                                               scale=0.125))
+    np.testing.assert_array_equal(fused == 0.0, three == 0.0)
+    assert float(np.abs(fused - three).max()) <= 1e-4 * float(np.abs(three).max())
 
 
 def test_block_n_one_is_sdpa(torch_dev):
