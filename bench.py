@@ -684,10 +684,10 @@ def comp_sdpa(lib, torch, S):
 def comp_flash_attention(lib, torch, S, B=128, D=128):
     """FlashAttention::forward (ghostflow-nn/src/flash_attention.rs:81-250)
     on [B, S, D] with FlashAttentionConfig::causal(1/sqrt(D)) and the
-    default 64 x 64 blocks (gfh_flash_attention_f32, fused two-pass form)
-    -- config 5's (b,h) slices as the layer's batch.  Work: 4*B*S^2*D * 1/2
-    FLOP (causal, the FlashAttention convention, as for SDPA; the fused form
-    computes the scores twice); the bound is the f32 MFMA peak."""
+    default 64 x 64 blocks (gfh_flash_attention_f32, single-pass form) --
+    config 5's (b,h) slices as the layer's batch.  Work: 4*B*S^2*D * 1/2
+    FLOP (causal, the FlashAttention convention, as for SDPA); the bound is
+    the f32 MFMA peak."""
     dev = torch.device("cuda:0")
     q = torch.randn((B, S, D), device=dev)
     k = torch.randn((B, S, D), device=dev)

@@ -49,5 +49,73 @@ struct KvStage {
     }
 };
 
+// ---- direct-to-LDS tiles -------------------------------------------------------
+//
+// A 32-key x DMAX tile (DMAX = 64 or 128) requested straight into LDS with
+// global_load_lds_dwordx4: no staging registers, no LDS store instructions.
+// One load instruction fills 1 KB of LDS; which global 16-byte chunk lands
+// in which LDS slot is free per lane, so each operand gets the layout its
+// reads want:
+//  * K tiles are chunk-major: chunk q of key r at slot q * 32 + r.  A score
+//    fragment read (ds_read_b128; 16 lanes on keys 0..15 at one chunk) is
+//    256 contiguous bytes, and the address is a lane base plus a constant
+//    per chunk.  Instruction i loads chunks 2i, 2i + 1 of all 32 keys.
+//  * V tiles are key-major, chunk q of key r at chunk q ^ (8 * bit 2 of r):
+//    the two lane halves of a P.V operand read (ds_read_b32 of 32
+//    consecutive dims of keys k and k + 4) hit disjoint halves of the 64
+//    banks.  Instruction i loads 1024 / (4 DMAX) whole keys.
+// Keys past nkeys read the last key and chunks past d read chunk 0 of the
+// row: finite values that meet a -inf score (weight 0) or a zero query dim.
+typedef __attribute__((address_space(3))) void *lds_ptr_t;
+typedef __attribute__((address_space(1))) void *glb_ptr_t;
+
+template <int DMAX, int NT, bool IS_V>
+struct KvLds {
+    static_assert(DMAX == 64 || DMAX == 128, "direct-to-LDS tiles cover 64 or 128 dims");
+    static constexpr int kTileFloats = kBKV * DMAX;
+    static constexpr int kInstr = kTileFloats * 4 / 1024;  // load instructions per tile
+    static constexpr int kPerWave = kInstr / (NT / 64);
+    static_assert(kPerWave >= 1 && kPerWave * (NT / 64) == kInstr, "whole instructions per wave");
+    static constexpr int kChunks = DMAX / 4;  // 16-byte chunks per key
+
+    // This wave's share of the requests for keys key0 .. key0 + 31 (row
+    // stride rs floats, 16-byte aligned rows, d % 4 == 0, nkeys >= 1).
+    __device__ __forceinline__ static void issue(const float *__restrict__ base, int64_t key0, int64_t nkeys,
+                                                 int64_t d, int64_t rs, float *lds, int wave, int lane) {
+#pragma unroll
+        for (int i = 0; i < kPerWave; ++i) {
+            const int ins = wave * kPerWave + i;
+            int row, lc;
+            if (IS_V) {
+                row = ins * (64 / kChunks) + lane / kChunks;
+                lc = (lane % kChunks) ^ (8 * ((row >> 2) & 1));
+            } else {
+                row = lane & 31;
+                lc = 2 * ins + (lane >> 5);
+            }
+            if (4 * lc >= d) lc = 0;
+            const int64_t key = min(key0 + row, nkeys - 1);
+            __builtin_amdgcn_global_load_lds((glb_ptr_t)(base + key * rs + 4 * lc), (lds_ptr_t)(lds + ins * 256), 16,
+                                             0, 0);
+        }
+    }
+};
+
+// Score operand: dims 8 g + 4 h .. + 3 of key c of a K tile (chunk 2 g + h).
+template <int DMAX>
+__device__ __forceinline__ f32x4 k_frag(const float *ks, int c, int h, int g) {
+    return *reinterpret_cast<const f32x4 *>(ks + (2 * g + h) * (4 * kBKV) + 4 * c);
+}
+
+// P.V operand: dim 32 j + c of key row `key` of a V tile, for the lane half
+// h = bit 2 of key.
+template <int DMAX>
+__device__ __forceinline__ float v_elem(const float *vt, int key, int h, int c, int j) {
+    return vt[key * DMAX + 32 * (j ^ h) + c];
+}
+
+// s_waitcnt vmcnt(0): this wave's global loads (and LDS-bound requests) are done.
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 }  // namespace attn
 }  // namespace gfh

@@ -15,7 +15,12 @@
 // v:
 //   o = sum_t sum_{j in t} p_j c_t^(n_t - 1 - idx_j) prod_{t' > t} c_t'^n_t' v_j
 // where the first block has c_0 = exp(-inf) = 0 (only its last key survives),
-// and l = sum_j exp(s_j - m_last).  So the layer runs as
+// and l = sum_j exp(s_j - m_last).  Three forms compute it:
+//   * fa_onepass_kernel (block_n = 32 or 64): the recurrence per key block
+//     in closed form, one pass (below);
+//   * fa_fused_kernel (other multiples of 32): two passes, the block maxima
+//     first (below);
+//   * otherwise three steps:
 //   1. S = scale * Q . K^T                 (gfh_sgemm NT, alpha = scale: the
 //                                            scale rounds the finished sum,
 //                                            `score *= scale`, :203)
@@ -387,6 +392,219 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_fused_kernel(FaFused p) {
     }
 }
 
+// ---- single-pass form (block_n = 32 or 64) ----------------------------------
+//
+// Block by block, the recurrence itself in closed form per block: with M_t
+// the running max after block t and delta_t = M_{t-1} - M_t,
+//   O <- O * exp(n_t delta_t) + sum_{j in t} exp((s_j - M_t) + (n_t - 1 - idx_j) delta_t) v_j
+//   l <- l * exp(delta_t)     + sum_{j in t} exp(s_j - M_t)
+// (block 0: only its last key enters O), and O / l at the end -- the same
+// weights as the two-pass form, E_t now applied as the product of the later
+// blocks' factors.  A 64-key block spans two 32-key tiles: the first tile's
+// scores wait in registers until the second gives the block max.  K tiles
+// are double-buffered and V tiles triple-buffered through LDS (tile u in V
+// buffer u % 3), all requested straight into LDS one tile ahead; 80 KB per
+// workgroup at d <= 128, two workgroups per CU.
+template <int DMAX, bool CAUSAL>
+__device__ __forceinline__ void fa_scores_lds(const FaFused &p, const float *ks, const f32x4 (&qf)[DMAX / 8],
+                                              int64_t k0, int64_t my_q, int lane, float (&sv)[16]) {
+    constexpr int NG = DMAX / 8;
+    constexpr int kBKV = attn::kBKV;
+    const int c = lane & 31, h = lane >> 5;
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        const f32x4 kf = attn::k_frag<DMAX>(ks, c, h, g);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[s], qf[g][s], acc, 0, 0, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // MFMA
+    }
+    // keys k0 + i with i < lim are visible to this row
+    int64_t lim64 = p.sk - k0;
+    if (CAUSAL) lim64 = min(lim64, my_q - k0 + 1);
+    const int lim = (int)max<int64_t>(0, min<int64_t>(lim64, kBKV));
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sv[r] = attn::key_of(r, h) < lim ? acc[r] * p.scale : -INFINITY;
+}
+
+template <int DMAX, bool CAUSAL, int TPB>
+__global__ __launch_bounds__(kFaThreads, 2) void fa_onepass_kernel(FaFused p) {
+    static_assert(TPB == 1 || TPB == 2, "32- or 64-key blocks");
+    constexpr int NG = DMAX / 8, ND = DMAX / 32;
+    constexpr int kBKV = attn::kBKV;
+    constexpr int kTile = kBKV * DMAX;
+    constexpr int NVB = TPB + 1;  // V tile buffers
+    using KL = attn::KvLds<DMAX, kFaThreads, false>;
+    using VL = attn::KvLds<DMAX, kFaThreads, true>;
+    __shared__ __attribute__((aligned(1024))) float lds[(2 + NVB) * kTile];
+    float *const lk = lds;
+    float *const lv = lds + 2 * kTile;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int c = lane & 31, h = lane >> 5;
+    const int64_t b = blockIdx.x;
+    int qb = (int)blockIdx.y;
+    if (CAUSAL) {
+        const int y = (int)blockIdx.y, half = (p.nqb + 1) / 2;
+        qb = (p.fold && y >= half) ? y - half : p.nqb - 1 - y;
+    }
+    const int64_t q0 = (int64_t)qb * kFaBQ;
+    const int64_t wq0 = q0 + wave * 32;
+    const int64_t my_q = wq0 + c;
+    const bool row_ok = my_q < p.sq;
+    const float *Q = p.q + b * p.sq * p.d;
+    const float *K = p.k + b * p.sk * p.d;
+    const float *V = p.v + b * p.sk * p.d;
+
+    f32x4 qf[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+        const int dim = 8 * g + 4 * h;
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        if (row_ok && dim < p.d) v = *reinterpret_cast<const f32x4 *>(Q + my_q * p.d + dim);
+        qf[g] = v;
+    }
+    f32x16 o[ND];
+#pragma unroll
+    for (int j = 0; j < ND; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[j][r] = 0.f;
+    float m = -INFINITY, l = 0.f;
+    float sa[16];  // scores of a two-tile block's first tile
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sa[r] = -INFINITY;
+
+    const int64_t kv_end = CAUSAL ? min(p.sk, q0 + kFaBQ) : p.sk;
+    const int64_t ntiles = (kv_end + kBKV - 1) / kBKV;
+
+    // Requests tile u (K and V) into its buffers.
+    auto issue = [&](int64_t u) {
+        KL::issue(K, u * kBKV, p.sk, p.d, p.d, lk + (u & 1) * kTile, wave, lane);
+        VL::issue(V, u * kBKV, p.sk, p.d, p.d, lv + (u % NVB) * kTile, wave, lane);
+    };
+    auto scores = [&](int64_t u, float (&x)[16]) {
+        const int64_t k0 = u * kBKV;
+        if (!CAUSAL || k0 <= wq0 + 31) {
+            fa_scores_lds<DMAX, CAUSAL>(p, lk + (u & 1) * kTile, qf, k0, my_q, lane, x);
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) x[r] = -INFINITY;
+        }
+    };
+    // Weights of tile u of block blk in place (scores in x); adds
+    // exp(s - mt) of its visible keys to ps.
+    auto weights = [&](float (&x)[16], int64_t u, int64_t blk, int64_t n, float mt, float delta, float &ps) {
+        // key_of(r, h) = 4 h + kr, kr = 8 (r / 4) + r % 4; the key's
+        // position in its block is base + 4 h + kr, so n - 1 - idx =
+        // rest - kr with rest = n - 1 - base - 4 h (small integers, exact).
+        const int base = (int)(u * kBKV - blk * p.bn);
+        const int rest = (int)n - 1 - base - 4 * h;
+        const float frest = (float)rest;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int kr = 8 * (r >> 2) + (r & 3);
+            float w = 0.f;
+            if (x[r] != -INFINITY) {
+                const float e = __expf(x[r] - mt);
+                ps += e;
+                if (blk == 0)
+                    w = rest == kr ? e : 0.f;
+                else
+                    w = __expf((x[r] - mt) + (frest - (float)kr) * delta);
+            }
+            x[r] = w;
+        }
+    };
+    // O += W . V for tile u.  The scheduling groups keep the V reads a
+    // step ahead of their MFMAs instead of hoisting all of them (which
+    // would need 16 * ND registers at once).
+    auto pv = [&](const float (&x)[16], int64_t u) {
+        const float *vt = lv + (u % NVB) * kTile;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+#pragma unroll
+            for (int j = 0; j < ND; ++j)
+                o[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(attn::v_elem<DMAX>(vt, attn::key_of(r, h), h, c, j), x[r],
+                                                            o[j], 0, 0, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, ND / 2, 0);  // DS reads
+            __builtin_amdgcn_sched_group_barrier(0x008, ND, 0);      // MFMA
+        }
+    };
+    // Block blk from tiles u0 .. u0 + nt - 1 (nt = 1 or 2), their scores in
+    // sa (first of two) and sv.
+    auto finish = [&](float (&sa_)[16], float (&sv_)[16], int64_t u0, int nt, int64_t blk) {
+        const int64_t n = min(p.bn, p.sk - blk * p.bn);
+        float bmx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) bmx = fmaxf(bmx, sv_[r]);
+        if (nt == 2) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) bmx = fmaxf(bmx, sa_[r]);
+        }
+        bmx = fmaxf(bmx, __shfl_xor(bmx, 32));
+        const float mt = fmaxf(m, bmx);
+        // Key 0 is visible to every row, so m is finite from block 1 on.
+        const float delta = blk == 0 ? 0.f : m - mt;
+        float ps = 0.f;
+        if (nt == 2) weights(sa_, u0, blk, n, mt, delta, ps);
+        weights(sv_, u0 + nt - 1, blk, n, mt, delta, ps);
+        ps += __shfl_xor(ps, 32);
+        l = l * __expf(delta) + ps;
+        m = mt;
+        const float corr = __expf((float)n * delta);
+#pragma unroll
+        for (int j = 0; j < ND; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[j][r] *= corr;
+        if (nt == 2) pv(sa_, u0);
+        pv(sv_, u0 + nt - 1);
+    };
+    // A wave whose last query precedes a tile's first key skips it.
+    auto live = [&](int64_t u) { return !CAUSAL || u * kBKV <= wq0 + 31; };
+
+    issue(0);
+    attn::wait_vm0();
+    __syncthreads();
+    for (int64_t t = 0; t < ntiles; t += TPB) {
+        const int64_t blk = t / TPB;
+        float sv[16];
+        if (TPB == 2 && t + 1 < ntiles) {
+            // first tile of the block: scores wait in sa
+            issue(t + 1);
+            scores(t, sa);
+            attn::wait_vm0();
+            __syncthreads();
+            if (t + 2 < ntiles) issue(t + 2);
+            scores(t + 1, sv);
+            if (live(t) || live(t + 1)) finish(sa, sv, t, 2, blk);
+        } else {
+            if (t + 1 < ntiles) issue(t + 1);
+            scores(t, sv);
+            if (live(t)) finish(sa, sv, t, 1, blk);
+        }
+        attn::wait_vm0();
+        __syncthreads();
+    }
+
+    if (row_ok) {
+        float *orow = p.out + (b * p.sq + my_q) * p.d;
+#pragma unroll
+        for (int j = 0; j < ND; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int dim = 32 * j + 8 * i + 4 * h;
+                if (dim < p.d) {
+                    f32x4 v = {o[j][4 * i] / l, o[j][4 * i + 1] / l, o[j][4 * i + 2] / l, o[j][4 * i + 3] / l};
+                    *reinterpret_cast<f32x4 *>(orow + dim) = v;
+                }
+            }
+    }
+}
+
 __global__ void fa_zero_kernel(float *p, int64_t n) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
         p[i] = 0.f;
@@ -427,6 +645,28 @@ int launch_flash_attention_blockwise(const FlashAttnDesc &d, hipStream_t s) {
         p.nqb = (int)((d.sq + kFaBQ - 1) / kFaBQ);
         p.fold = d.causal && d.batch * p.nqb <= 2 * (int64_t)device_cu_count();
         const dim3 grid((unsigned)d.batch, (unsigned)p.nqb), block(kFaThreads);
+        if (d.block_n == 32 || d.block_n == 64) {
+#define GFH_FA_ONEPASS(DM, TPB)                                                                  \
+    do {                                                                                         \
+        if (d.causal)                                                                            \
+            hipLaunchKernelGGL((fa_onepass_kernel<DM, true, TPB>), grid, block, 0, s, p);        \
+        else                                                                                     \
+            hipLaunchKernelGGL((fa_onepass_kernel<DM, false, TPB>), grid, block, 0, s, p);       \
+    } while (0)
+            if (d.d <= 64) {
+                if (d.block_n == 32)
+                    GFH_FA_ONEPASS(64, 1);
+                else
+                    GFH_FA_ONEPASS(64, 2);
+            } else {
+                if (d.block_n == 32)
+                    GFH_FA_ONEPASS(128, 1);
+                else
+                    GFH_FA_ONEPASS(128, 2);
+            }
+#undef GFH_FA_ONEPASS
+            return check_launch("flash_attention (single pass)");
+        }
         if (d.d <= 64) {
             if (d.causal)
                 hipLaunchKernelGGL((fa_fused_kernel<64, true>), grid, block, 0, s, p);
