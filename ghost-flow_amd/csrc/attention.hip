@@ -168,6 +168,7 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(SdpaParams p) {
         gk.store(lk, tid);
         gv.store(lv, tid);
     }
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
     for (int64_t t = 0; t < ntiles; ++t) {

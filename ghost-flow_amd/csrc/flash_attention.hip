@@ -244,7 +244,7 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_fused_kernel(FaFused p) {
     float *const lv = lds + 2 * kTile;
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 31, h = lane >> 5;
     const int64_t b = blockIdx.x;
     // Causal: heaviest query blocks first, and for a grid resident all at
@@ -444,7 +444,7 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_onepass_kernel(FaFused p) {
     float *const lv = lds + 2 * kTile;
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 31, h = lane >> 5;
     const int64_t b = blockIdx.x;
     int qb = (int)blockIdx.y;
