@@ -70,6 +70,16 @@ void release_stream_state();
 // Compute units of the current device (queried once per device).
 int device_cu_count();
 
+// Workgroup w of a launch runs on XCD w % 8 (round-robin dispatch over the
+// 8 XCDs, each with its own L2).  This renumbering gives every XCD one
+// contiguous range of tile ids -- XCD x takes q + (x < r) of them from
+// x q + min(x, r), q = n / 8, r = n % 8 -- so tiles that share operand rows
+// (neighbours in tile order) share an L2.  A bijection on [0, n) for any n.
+__device__ __forceinline__ int xcd_chunked(int w, int n) {
+    const int q = n >> 3, r = n & 7, x = w & 7;
+    return x * q + (x < r ? x : r) + (w >> 3);
+}
+
 // ---- split-K arrival protocol ------------------------------------------------
 // Kernels that split K over workgroups (the decode GEMVs, the skinny int8 and
 // fp32 linears, KV-cache attention) combine their partials in the same

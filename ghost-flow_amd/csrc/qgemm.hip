@@ -329,7 +329,7 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
 
     const int nblk = p.tiles_m * p.tiles_n;
     int bid = blockIdx.x;
-    if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
+    bid = xcd_chunked(bid, nblk);
     const int group_size = kGroupM * p.tiles_n;
     const int group = bid / group_size;
     const int first_m = group * kGroupM;
