@@ -58,6 +58,7 @@ struct GemvParams {
     int64_t nstrips;
     int64_t slices;
     int64_t kslice;  // rows per slice: a multiple of 16, at most kMaxSlice
+    int xvec;        // x rows 16-byte aligned and k % 4 == 0 (fp32 kernel: staged 4 rows per load)
 };
 
 constexpr int kMaxSlice = 1024;  // int8 kernel
@@ -152,8 +153,16 @@ __device__ __forceinline__ void store_strip(const GemvParams &p, int64_t strip, 
 // NW waves per workgroup: 8 when the grid has at most one workgroup per CU,
 // so that twice the weight bytes are in flight per CU.  ROWS: the longest
 // slice the LDS staging of x holds.
-template <int MAXB, int U, bool VEC, int NW = kWaves, int ROWS = f32_max_rows<MAXB>()>
+// MF: the multiply-adds on the matrix cores instead of the VALU (groups of
+// 5-8 batch rows).  Each 16-byte weight load (4 rows x 64 columns per wave)
+// feeds four v_mfma_f32_16x16x4_f32: lane l holds W[row l / 16][4 (l % 16)
+// + e], the A operand (m = column, k = row) of MFMA e, and x[l % 16][row
+// l / 16] from LDS is the B operand (n = batch row), so MFMA e sums the
+// lane group's 4 rows for columns 4 i + e.  The VALU form costs 4 B FMAs per
+// load, 32 at B = 8 with packed f32 off; the MFMA form 4 MFMAs at any B.
+template <int MAXB, int U, bool VEC, int NW = kWaves, int ROWS = f32_max_rows<MAXB>(), bool MF = false>
 __global__ __launch_bounds__(64 * NW) void gemv_f32_kernel(GemvParams p) {
+    static_assert(!MF || (VEC && MAXB <= 16), "matrix-core form: 16-byte loads, at most 16 batch rows");
     constexpr int NT = 64 * NW;               // threads
     constexpr int EPL = 4;                    // floats per lane per load
     constexpr int SCOLS = kStripBytes / 4;    // strip columns
@@ -183,13 +192,28 @@ __global__ __launch_bounds__(64 * NW) void gemv_f32_kernel(GemvParams p) {
     // Activations first, from clamped in-range indices: loads complete in
     // issue order, so the staging below waits only for these while the
     // first weight batch (issued next) streams in behind them.
+    // With p.xvec (rows a multiple of 4, x rows 16-byte aligned) each
+    // thread loads 4 consecutive rows of one batch row per instruction.
     constexpr int kRowsPerThread = kMaxRows / NT;
+    constexpr int kQuads = (kMaxRows / 4 + NT - 1) / NT;  // 4-row groups per thread
+    const bool xvec = p.xvec != 0;
     float xv[kRowsPerThread][MAXB];
+    f32x4 xq[kQuads][MAXB];
+    if (xvec) {
 #pragma unroll
-    for (int i = 0; i < kRowsPerThread; ++i) {
-        const int rr = min((int)threadIdx.x + NT * i, rows - 1);
+        for (int i = 0; i < kQuads; ++i) {
+            const int qd = min((int)threadIdx.x + NT * i, rows / 4 - 1);
 #pragma unroll
-        for (int bi = 0; bi < MAXB; ++bi) xv[i][bi] = p.x[min<int64_t>(bi, nb - 1) * p.k + s_lo + rr];
+            for (int bi = 0; bi < MAXB; ++bi)
+                xq[i][bi] = *reinterpret_cast<const f32x4 *>(p.x + min<int64_t>(bi, nb - 1) * p.k + s_lo + 4 * qd);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < kRowsPerThread; ++i) {
+            const int rr = min((int)threadIdx.x + NT * i, rows - 1);
+#pragma unroll
+            for (int bi = 0; bi < MAXB; ++bi) xv[i][bi] = p.x[min<int64_t>(bi, nb - 1) * p.k + s_lo + rr];
+        }
     }
 
     // Each wave walks whole steps of its quarter of the slice.  Loads are
@@ -224,32 +248,59 @@ __global__ __launch_bounds__(64 * NW) void gemv_f32_kernel(GemvParams p) {
     // Stage x, zero past the slice and the batch (a mask, not a select: a
     // value used only under a condition lets the compiler sink its load into
     // a branch, which then waits for everything issued before it).
+    if (xvec) {
 #pragma unroll
-    for (int i = 0; i < kRowsPerThread; ++i) {
-        const int r = threadIdx.x + NT * i;
-        if (r >= rows_s) continue;
+        for (int i = 0; i < kQuads; ++i) {
+            const int qd = threadIdx.x + NT * i;
+            if (4 * qd >= rows_s) continue;
 #pragma unroll
-        for (int bi = 0; bi < MAXB; ++bi) {
-            const uint32_t keep = (r < rows && bi < nb) ? 0xffffffffu : 0u;
-            xs[r * MAXB + bi] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, xv[i][bi]) & keep);
+            for (int q = 0; q < 4; ++q) {
+#pragma unroll
+                for (int bi = 0; bi < MAXB; ++bi) {
+                    const uint32_t keep = (4 * qd + q < rows && bi < nb) ? 0xffffffffu : 0u;
+                    const float v = xq[i][bi][q];
+                    xs[(4 * qd + q) * MAXB + bi] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, v) & keep);
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < kRowsPerThread; ++i) {
+            const int r = threadIdx.x + NT * i;
+            if (r >= rows_s) continue;
+#pragma unroll
+            for (int bi = 0; bi < MAXB; ++bi) {
+                const uint32_t keep = (r < rows && bi < nb) ? 0xffffffffu : 0u;
+                xs[r * MAXB + bi] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, xv[i][bi]) & keep);
+            }
         }
     }
     __syncthreads();
 
-    float acc[MAXB][EPL];
+    float acc[MF ? 1 : MAXB][EPL];
 #pragma unroll
-    for (int bi = 0; bi < MAXB; ++bi)
+    for (int bi = 0; bi < (MF ? 1 : MAXB); ++bi)
 #pragma unroll
         for (int e = 0; e < EPL; ++e) acc[bi][e] = 0.f;
+    f32x4 macc[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) macc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int bq = lane & 15;  // MF: this lane's batch row (B operand column)
     auto fma_row = [&](const i32x4 &wv, int r) {
-        float x[MAXB];
-#pragma unroll
-        for (int bi = 0; bi < MAXB; ++bi) x[bi] = xs[r * MAXB + bi];
         const f32x4 wf = __builtin_bit_cast(f32x4, wv);
+        if constexpr (MF) {
+            const float xb = bq < MAXB ? xs[r * MAXB + (bq < MAXB ? bq : 0)] : 0.f;
 #pragma unroll
-        for (int bi = 0; bi < MAXB; ++bi)
+            for (int e = 0; e < EPL; ++e) macc[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(wf[e], xb, macc[e], 0, 0, 0);
+        } else {
+            float x[MAXB];
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) acc[bi][e] = fmaf(x[bi], wf[e], acc[bi][e]);  // explicit FMA
+            for (int bi = 0; bi < MAXB; ++bi) x[bi] = xs[r * MAXB + bi];
+#pragma unroll
+            for (int bi = 0; bi < MAXB; ++bi)
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) acc[bi][e] = fmaf(x[bi], wf[e], acc[bi][e]);  // explicit FMA
+        }
     };
     // The next step is requested before the current one is used.  Every
     // branch is wave-uniform and every block issues its loads
@@ -275,16 +326,27 @@ __global__ __launch_bounds__(64 * NW) void gemv_f32_kernel(GemvParams p) {
         r0 += kStep;
     }
 
-    // Reduce over the 4 row lanes of each column group, then over waves.
+    if constexpr (MF) {
+        // Lane l, register g of MFMA e: column 16 (l / 16) + 4 g + e of the
+        // strip, batch row l % 16 (its 4 rows already summed by the MFMA).
+        if (bq < MAXB) {
 #pragma unroll
-    for (int bi = 0; bi < MAXB; ++bi)
+            for (int e = 0; e < EPL; ++e)
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-            float v = acc[bi][e];
-            v += __shfl_xor(v, 16);
-            v += __shfl_xor(v, 32);
-            if (lane < 16) red[wave][bi][lane * EPL + e] = v;
+                for (int g = 0; g < 4; ++g) red[wave][bq][16 * (lane >> 4) + 4 * g + e] = macc[e][g];
         }
+    } else {
+        // Reduce over the 4 row lanes of each column group, then over waves.
+#pragma unroll
+        for (int bi = 0; bi < MAXB; ++bi)
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                float v = acc[bi][e];
+                v += __shfl_xor(v, 16);
+                v += __shfl_xor(v, 32);
+                if (lane < 16) red[wave][bi][lane * EPL + e] = v;
+            }
+    }
     __syncthreads();
     auto strip_value = [&](int bi, int c) {
         float v = red[0][bi][c];
@@ -597,16 +659,21 @@ template <int MAXB>
 void launch_f32(const GemvParams &p, bool vec, hipStream_t s) {
     constexpr int U = 8;
     const unsigned nwg = (unsigned)(p.nstrips * p.slices);
+    // Matrix cores for groups of 5-8 rows: W [4096, 14336] at 8 rows 46.1 ->
+    // 44.6 us; at 4 rows both forms take 42.7 us.
+    constexpr bool MF = MAXB >= 8;
     if constexpr (MAXB == 8) {
         if (vec && nwg <= 256 && p.kslice > f32_max_rows<8>()) {
-            hipLaunchKernelGGL((gemv_f32_kernel<8, U, true, 8, kWideRows8>), dim3(nwg), dim3(512), 0, s, p);
+            hipLaunchKernelGGL((gemv_f32_kernel<8, U, true, 8, kWideRows8, MF>), dim3(nwg), dim3(512), 0, s, p);
             return;
         }
     }
     if (vec && nwg <= 256)
-        hipLaunchKernelGGL((gemv_f32_kernel<MAXB, U, true, 8>), dim3(nwg), dim3(512), 0, s, p);
+        hipLaunchKernelGGL((gemv_f32_kernel<MAXB, U, true, 8, f32_max_rows<MAXB>(), MF>), dim3(nwg), dim3(512), 0, s,
+                           p);
     else if (vec)
-        hipLaunchKernelGGL((gemv_f32_kernel<MAXB, U, true>), dim3(nwg), dim3(kThreads), 0, s, p);
+        hipLaunchKernelGGL((gemv_f32_kernel<MAXB, U, true, kWaves, f32_max_rows<MAXB>(), MF>), dim3(nwg),
+                           dim3(kThreads), 0, s, p);
     else
         hipLaunchKernelGGL((gemv_f32_kernel<MAXB, U, false>), dim3(nwg), dim3(kThreads), 0, s, p);
 }
@@ -703,6 +770,7 @@ int launch_gemv_f32(const float *x, const float *w, float *y, int64_t b, int64_t
     p.n = n;
     p.nstrips = (n + kStripBytes / 4 - 1) / (kStripBytes / 4);
     const bool vec = n % 4 == 0 && aligned16(w);
+    p.xvec = (k % 4 == 0) && aligned16(x);
     return for_batch_groups(p, x, y, b, [&](GemvParams &q) {
         const int maxb = q.b == 1 ? 1 : q.b == 2 ? 2 : q.b <= 4 ? 4 : 8;
         int64_t max_rows = maxb == 1   ? f32_max_rows<1>()
