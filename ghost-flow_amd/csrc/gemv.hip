@@ -14,7 +14,8 @@
 //    fp32 or 256 int8 columns) over one K-slice; every load instruction
 //    covers 4 rows x 256 contiguous bytes (HBM streams 256-byte row runs at
 //    about 6 TB/s; 128-byte runs only reach ~5).  The slice's activations
-//    are staged in LDS once per workgroup.
+//    are staged in LDS once per workgroup (fp32 with aligned x: streamed
+//    with the weights instead, a step's rows at a time).
 //  * fp32 (gemv_f32_kernel): lane l reads 16 bytes of row l/16 of a 4-row
 //    group and the b multiply-adds run on the VALU; partial sums are reduced
 //    over the 4 row lanes with xor shuffles, then over the waves in LDS.
@@ -59,6 +60,7 @@ struct GemvParams {
     int64_t slices;
     int64_t kslice;  // rows per slice: a multiple of 16, at most kMaxSlice
     int xvec;        // x rows 16-byte aligned and k % 4 == 0 (fp32 kernel: staged 4 rows per load)
+    int off32;       // the weight is under 4 GB: byte offsets into it fit 32 bits
 };
 
 constexpr int kMaxSlice = 1024;  // int8 kernel
@@ -160,15 +162,33 @@ __device__ __forceinline__ void store_strip(const GemvParams &p, int64_t strip, 
 // l / 16] from LDS is the B operand (n = batch row), so MFMA e sums the
 // lane group's 4 rows for columns 4 i + e.  The VALU form costs 4 B FMAs per
 // load, 32 at B = 8 with packed f32 off; the MFMA form 4 MFMAs at any B.
-template <int MAXB, int U, bool VEC, int NW = kWaves, int ROWS = f32_max_rows<MAXB>(), bool MF = false>
+// XS: x is not staged for the whole slice before the loop but streamed with
+// the weights: with each step's weight loads a wave loads that step's
+// kStep rows of x (lane l: batch row l / 8, rows 4 (l % 8) .. + 3, one
+// 16-byte load) and passes them to its lanes through its own two LDS buffers
+// (no workgroup barrier: a wave's LDS accesses complete in issue order).
+// Needs p.xvec and p.off32.  The staged form's up-front wait for B x K floats per
+// workgroup (128 KB at B = 8, K = 4096) goes away.
+template <int MAXB, int U, bool VEC, int NW = kWaves, int ROWS = f32_max_rows<MAXB>(), bool MF = false,
+          bool XS = false>
 __global__ __launch_bounds__(64 * NW) void gemv_f32_kernel(GemvParams p) {
     static_assert(!MF || (VEC && MAXB <= 16), "matrix-core form: 16-byte loads, at most 16 batch rows");
+    static_assert(!XS || (VEC && MAXB <= 8 && U == 8),
+                  "streamed x: 16-byte loads (W under 4 GB), one x quad per lane and step");
     constexpr int NT = 64 * NW;               // threads
     constexpr int EPL = 4;                    // floats per lane per load
     constexpr int SCOLS = kStripBytes / 4;    // strip columns
     constexpr int kStep = 4 * U;              // rows per wave step
     constexpr int kMaxRows = ROWS;
-    __shared__ __attribute__((aligned(16))) float xs[kMaxRows * MAXB];  // this slice's x, [row][batch]
+    // XS buffers: [row][batch] for the VALU form; [batch][row] with a
+    // 36-float batch stride for the matrix-core form, whose 64 lanes (batch
+    // row l % 16, row l / 16) then read 64 distinct banks.
+    constexpr int kXsStride = 36;
+    constexpr int kXsBuf = MF ? kXsStride * MAXB : kStep * MAXB;
+    constexpr int kRStride = (XS && MF) ? 1 : MAXB;          // floats between rows
+    constexpr int kBStride = (XS && MF) ? kXsStride : 1;     // floats between batch rows
+    // Staged: this slice's x, [row][batch].  XS: two step buffers per wave.
+    __shared__ __attribute__((aligned(16))) float xs[XS ? NW * 2 * kXsBuf : kMaxRows * MAXB];
     __shared__ float red[NW][MAXB][SCOLS];
     __shared__ int last_flag;
 
@@ -199,7 +219,8 @@ __global__ __launch_bounds__(64 * NW) void gemv_f32_kernel(GemvParams p) {
     const bool xvec = p.xvec != 0;
     float xv[kRowsPerThread][MAXB];
     f32x4 xq[kQuads][MAXB];
-    if (xvec) {
+    if constexpr (XS) {
+    } else if (xvec) {
 #pragma unroll
         for (int i = 0; i < kQuads; ++i) {
             const int qd = min((int)threadIdx.x + NT * i, rows / 4 - 1);
@@ -225,7 +246,22 @@ __global__ __launch_bounds__(64 * NW) void gemv_f32_kernel(GemvParams p) {
     const int wb = min(wave * per, rows_s), we = min(wb + per, rows_s);
     const int64_t lcol = (VEC && col >= p.n) ? col0 : col;
     const float *base = W + s_lo * p.n + lcol;
+    // XS (W under 4 GB): addresses as the uniform base plus a 32-bit byte
+    // offset per lane, one multiply per step and an add and a clamp per
+    // load, instead of a 64-bit multiply per load: the fewer instructions
+    // between a step's loads, the sooner the next step's are issued.
+    const uint32_t row_bytes = (uint32_t)p.n * 4u;
+    const uint32_t lane_off = XS ? (uint32_t)((s_lo * p.n + lcol) * 4) : 0u;
+    const uint32_t last_off = lane_off + (uint32_t)(rows - 1) * row_bytes;  // this lane's 16 bytes of the last row
+    const char *const wbytes = reinterpret_cast<const char *>(W);
     auto load_step = [&](int r0, i32x4 (&w)[U]) {
+        if constexpr (XS) {
+            const uint32_t o = lane_off + (uint32_t)(r0 + rsub) * row_bytes;
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                w[u] = *reinterpret_cast<const i32x4 *>(wbytes + min(o + (uint32_t)(4 * u) * row_bytes, last_off));
+            return;
+        }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int r = max(min(r0 + 4 * u + rsub, rows - 1), 0);
@@ -240,15 +276,49 @@ __global__ __launch_bounds__(64 * NW) void gemv_f32_kernel(GemvParams p) {
             }
         }
     };
+    // XS: this lane's x quad of step r0, loaded from a clamped in-range
+    // address, and its store into the wave's buffer, zero for rows past the
+    // slice and batch rows past nb (rows % 4 == 0 with p.xvec, so a quad is
+    // all in or all out).  The mask is applied at the store: a use of the
+    // loaded value right after the load made the compiler wait for it there.
+    const int xb_row = lane >> 3, xq_off = 4 * (lane & 7);
+    const float *xsrc = p.x + min<int64_t>(xb_row, nb - 1) * p.k + s_lo;
+    auto load_x = [&](int r0) { return *reinterpret_cast<const f32x4 *>(xsrc + min(r0 + xq_off, rows - 4)); };
+    float *const xwave = xs + (XS ? wave * 2 * kXsBuf : 0);
+    auto put_x = [&](f32x4 v, int buf, int r0) {
+        const uint32_t keep = (r0 + xq_off < rows && xb_row < nb) ? 0xffffffffu : 0u;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float e = v[q];  // (a bit_cast of the element lvalue itself reads element 0)
+            v[q] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, e) & keep);
+        }
+        if (xb_row < MAXB) {
+            float *d = xwave + buf * kXsBuf;
+            if constexpr (MF) {
+                *reinterpret_cast<f32x4 *>(d + xb_row * kXsStride + xq_off) = v;
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) d[(xq_off + q) * MAXB + xb_row] = v[q];
+            }
+        }
+        // The other lanes of this wave read what was just written; a
+        // wave's LDS accesses complete in issue order.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
     __builtin_amdgcn_sched_barrier(0);
     i32x4 wa[U], wn[U];
+    f32x4 xa, xn;
+    if constexpr (XS) xa = load_x(wb);
     load_step(wb, wa);
     __builtin_amdgcn_sched_barrier(0);
 
     // Stage x, zero past the slice and the batch (a mask, not a select: a
     // value used only under a condition lets the compiler sink its load into
     // a branch, which then waits for everything issued before it).
-    if (xvec) {
+    if constexpr (XS) {
+    } else if (xvec) {
 #pragma unroll
         for (int i = 0; i < kQuads; ++i) {
             const int qd = threadIdx.x + NT * i;
@@ -275,7 +345,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_f32_kernel(GemvParams p) {
             }
         }
     }
-    __syncthreads();
+    if constexpr (!XS) __syncthreads();
 
     float acc[MF ? 1 : MAXB][EPL];
 #pragma unroll
@@ -286,16 +356,17 @@ __global__ __launch_bounds__(64 * NW) void gemv_f32_kernel(GemvParams p) {
 #pragma unroll
     for (int e = 0; e < EPL; ++e) macc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
     const int bq = lane & 15;  // MF: this lane's batch row (B operand column)
-    auto fma_row = [&](const i32x4 &wv, int r) {
+    // xr: x of the row, batch row bi at xr[bi * kBStride].
+    auto fma_row = [&](const i32x4 &wv, const float *xr) {
         const f32x4 wf = __builtin_bit_cast(f32x4, wv);
         if constexpr (MF) {
-            const float xb = bq < MAXB ? xs[r * MAXB + (bq < MAXB ? bq : 0)] : 0.f;
+            const float xb = bq < MAXB ? xr[(bq < MAXB ? bq : 0) * kBStride] : 0.f;
 #pragma unroll
             for (int e = 0; e < EPL; ++e) macc[e] = __builtin_amdgcn_mfma_f32_16x16x4f32(wf[e], xb, macc[e], 0, 0, 0);
         } else {
             float x[MAXB];
 #pragma unroll
-            for (int bi = 0; bi < MAXB; ++bi) x[bi] = xs[r * MAXB + bi];
+            for (int bi = 0; bi < MAXB; ++bi) x[bi] = xr[bi * kBStride];
 #pragma unroll
             for (int bi = 0; bi < MAXB; ++bi)
 #pragma unroll
@@ -305,25 +376,53 @@ __global__ __launch_bounds__(64 * NW) void gemv_f32_kernel(GemvParams p) {
     // The next step is requested before the current one is used.  Every
     // branch is wave-uniform and every block issues its loads
     // unconditionally, so the wait for a step never covers the next one.
-    auto fma_step = [&](const i32x4 (&w)[U], int r0) {
+    // Rows of step r0 from x rows xrow0 on: the staged slice (XS: the buffer).
+    auto fma_step = [&](const i32x4 (&w)[U], const float *xbase, int xrow0) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) fma_row(w[u], r0 + 4 * u + rsub);
+        for (int u = 0; u < U; ++u) fma_row(w[u], xbase + (xrow0 + 4 * u + rsub) * kRStride);
     };
-    for (int r0 = wb; r0 < we;) {
-        if (r0 + kStep >= we) {
-            fma_step(wa, r0);
-            break;
+    if constexpr (XS) {
+        // x of a step is requested before its weights, with the next step's
+        // loads in flight before the current step is used.
+        for (int r0 = wb; r0 < we;) {
+            if (r0 + kStep >= we) {
+                put_x(xa, 0, r0);
+                fma_step(wa, xwave, 0);
+                break;
+            }
+            xn = load_x(r0 + kStep);
+            load_step(r0 + kStep, wn);
+            put_x(xa, 0, r0);
+            fma_step(wa, xwave, 0);
+            r0 += kStep;
+            if (r0 + kStep >= we) {
+                put_x(xn, 1, r0);
+                fma_step(wn, xwave + kXsBuf, 0);
+                break;
+            }
+            xa = load_x(r0 + kStep);
+            load_step(r0 + kStep, wa);
+            put_x(xn, 1, r0);
+            fma_step(wn, xwave + kXsBuf, 0);
+            r0 += kStep;
         }
-        load_step(r0 + kStep, wn);
-        fma_step(wa, r0);
-        r0 += kStep;
-        if (r0 + kStep >= we) {
-            fma_step(wn, r0);
-            break;
+    } else {
+        for (int r0 = wb; r0 < we;) {
+            if (r0 + kStep >= we) {
+                fma_step(wa, xs, r0);
+                break;
+            }
+            load_step(r0 + kStep, wn);
+            fma_step(wa, xs, r0);
+            r0 += kStep;
+            if (r0 + kStep >= we) {
+                fma_step(wn, xs, r0);
+                break;
+            }
+            load_step(r0 + kStep, wa);
+            fma_step(wn, xs, r0);
+            r0 += kStep;
         }
-        load_step(r0 + kStep, wa);
-        fma_step(wn, r0);
-        r0 += kStep;
     }
 
     if constexpr (MF) {
@@ -662,6 +761,15 @@ void launch_f32(const GemvParams &p, bool vec, hipStream_t s) {
     // Matrix cores for groups of 5-8 rows: W [4096, 14336] at 8 rows 46.1 ->
     // 44.6 us; at 4 rows both forms take 42.7 us.
     constexpr bool MF = MAXB >= 8;
+    if (vec && p.xvec && p.off32) {  // x streamed with the weights, no staging
+        if (nwg <= 256)
+            hipLaunchKernelGGL((gemv_f32_kernel<MAXB, U, true, 8, f32_max_rows<MAXB>(), MF, true>), dim3(nwg),
+                               dim3(512), 0, s, p);
+        else
+            hipLaunchKernelGGL((gemv_f32_kernel<MAXB, U, true, kWaves, f32_max_rows<MAXB>(), MF, true>), dim3(nwg),
+                               dim3(kThreads), 0, s, p);
+        return;
+    }
     if constexpr (MAXB == 8) {
         if (vec && nwg <= 256 && p.kslice > f32_max_rows<8>()) {
             hipLaunchKernelGGL((gemv_f32_kernel<8, U, true, 8, kWideRows8, MF>), dim3(nwg), dim3(512), 0, s, p);
@@ -771,6 +879,8 @@ int launch_gemv_f32(const float *x, const float *w, float *y, int64_t b, int64_t
     p.nstrips = (n + kStripBytes / 4 - 1) / (kStripBytes / 4);
     const bool vec = n % 4 == 0 && aligned16(w);
     p.xvec = (k % 4 == 0) && aligned16(x);
+    // (64 rows of margin: a step's offsets are formed before the clamp to the last row)
+    p.off32 = ((double)k + 64.0) * (double)n * 4.0 < 4294967296.0;
     return for_batch_groups(p, x, y, b, [&](GemvParams &q) {
         const int maxb = q.b == 1 ? 1 : q.b == 2 ? 2 : q.b <= 4 ? 4 : 8;
         int64_t max_rows = maxb == 1   ? f32_max_rows<1>()
