@@ -37,6 +37,27 @@ def test_gemv_f32_integer_exact(torch_dev, b, k, n):
     np.testing.assert_array_equal(got, O.matmul(x, w))
 
 
+@pytest.mark.parametrize("b,k,n", [(1, 256, 4096), (4, 4096, 14336), (8, 1000, 2048), (3, 2048, 13000)])
+def test_gemv_f32_misaligned_x(torch_dev, b, k, n):
+    """x 4 bytes past a 16-byte boundary (a view at element offset 1 of a
+    larger buffer): the activations cannot be loaded 16 bytes at a time, so
+    the kernel stages them for the whole slice instead of streaming them
+    with the weights.  Integer data, exact; the aligned call agrees."""
+    import torch
+    gh, O = _gh(), _O()
+    rng = np.random.default_rng(b * 31 + k + n)
+    x = rng.integers(-8, 9, size=(b, k)).astype(np.float32)
+    w = rng.integers(-8, 9, size=(k, n)).astype(np.float32)
+    buf = torch.zeros(b * k + 4, dtype=torch.float32, device=torch_dev)
+    buf[1:1 + b * k] = to_dev(x.reshape(-1), torch_dev)
+    xv = buf[1:1 + b * k].view(b, k)
+    assert xv.data_ptr() % 16 == 4
+    dw = to_dev(w, torch_dev)
+    got = to_np(gh.gemv_f32(xv, dw))
+    np.testing.assert_array_equal(got, O.matmul(x, w))
+    np.testing.assert_array_equal(got, to_np(gh.gemv_f32(to_dev(x, torch_dev), dw)))
+
+
 def test_mv_reference_known_answer(torch_dev):
     """Tensor::mv [[1,2],[3,4]] . [1,2] = [5, 11] (matmul.rs:363-371), as
     x [1,2] . W^T with W^T = [[1,3],[2,4]]."""
