@@ -796,19 +796,38 @@ def comp_mha_decode(lib, torch, B=4, H=32, D=128, past=2047):
     bp = [t.data_ptr() for t in bias]
     ptrs = [([t.data_ptr() for t in w], kc.data_ptr(), vc.data_ptr()) for w, kc, vc in sets]
 
-    def f(i):
+    def step(i, stream):
         wp, kp, vp = ptrs[i % ncopy]
         L.gfh_mha_forward_with_cache_f32(x.data_ptr(), x.data_ptr(), x.data_ptr(), wp[0], bp[0], wp[1], bp[1],
                                          wp[2], bp[2], wp[3], bp[3], kp, vp, C, past, None, 0, 0,
                                          out.data_ptr(), None, B, 1, 1, E, H, ws.data_ptr(),
-                                         ws.numel() * 4, s)
-    ms = event_time_ms(torch, f, 100)
+                                         ws.numel() * 4, stream)
+
+    ms = event_time_ms(torch, lambda i: step(i, s), 100)
+    # The same step captured once per weight/cache set into a HIP graph and
+    # replayed (a serving loop's form: one launch per step).  Each stream
+    # gets its split-K buffers on its first call, so the capture stream runs
+    # every set once before capture.
+    cap = torch.cuda.Stream()
+    with torch.cuda.stream(cap):
+        for i in range(ncopy):
+            step(i, cap.cuda_stream)
+    cap.synchronize()
+    graphs = []
+    for i in range(ncopy):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap):
+            step(i, cap.cuda_stream)
+        graphs.append(g)
+    torch.cuda.synchronize()
+    gms = event_time_ms(torch, lambda i: graphs[i % ncopy].replay(), 100)
     byts = per_set + 4 * B * E * 6
     gbs = byts / ms / 1e6
-    del sets
+    del graphs, sets
     return {"name": f"mha_decode_step_b{B}_e{E}_h{H}_past{past}", "ms": ms, "value": gbs, "unit": "GB/s",
             "tokens_per_s": B / (ms * 1e-3), "frac": gbs * 1e9 / PEAK_HBM, "bound": "hbm",
-            "set_copies": ncopy}
+            "set_copies": ncopy, "graph_ms": gms, "graph_tokens_per_s": B / (gms * 1e-3),
+            "graph_frac": byts / gms / 1e6 * 1e9 / PEAK_HBM}
 
 
 def comp_swiglu(lib, torch, m, int8, H=4096, I=11008):

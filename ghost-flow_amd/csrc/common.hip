@@ -122,6 +122,38 @@ int optional_range(const void *p, size_t bytes, const char *name) {
     return require_range(p, bytes, name);
 }
 
+namespace {
+
+// Zeroes a new counter buffer on its stream.  A fill kernel rather than
+// hipMemsetAsync: where a stream is captured into a graph, memset nodes have
+// given wrong results on replays after the first.
+__global__ void zero_counters_kernel(int *p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0;
+}
+
+// The library's per-stream buffers (and stream-ordered scratch) are
+// allocated on first use.  On a stream that is being captured into a graph
+// that allocation would become part of the graph, so it is refused: the
+// caller runs the call once on the stream before capturing it (or passes a
+// workspace), and the captured calls then allocate nothing.
+int refuse_during_capture(hipStream_t s, const char *what) {
+    if (s == nullptr) return GFH_SUCCESS;  // the legacy default stream is never captured
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess) {
+        (void)hipGetLastError();
+        return GFH_SUCCESS;
+    }
+    if (st != hipStreamCaptureStatusNone)
+        return set_error(GFH_ALLOCATION_FAILED,
+                         "%s: the stream is being captured into a graph; run the call once on this stream before "
+                         "capturing it (per-stream buffers are allocated on first use) or pass a workspace",
+                         what);
+    return GFH_SUCCESS;
+}
+
+}  // namespace
+
 Scratch::~Scratch() {
     if (owned_ && p_) (void)hipFreeAsync(p_, s_);
 }
@@ -137,6 +169,7 @@ int Scratch::acquire(void *user, size_t user_bytes, size_t need, hipStream_t s) 
         owned_ = false;
         return GFH_SUCCESS;
     }
+    GFH_TRY(refuse_during_capture(s, "workspace"));
     hipError_t e = hipMallocAsync(&p_, need, s);
     if (e != hipSuccess) {
         (void)hipGetLastError();
@@ -175,11 +208,15 @@ int stream_counters(hipStream_t s, size_t count, int **out) {
     StreamState *st = nullptr;
     GFH_TRY(current_state(s, &st));
     if (st->ncounters < count) {
+        GFH_TRY(refuse_during_capture(s, "split-K counters"));
         size_t want = 4096;
         while (want < count) want *= 2;
         int *p = nullptr;
         hipError_t e = hipMallocAsync(reinterpret_cast<void **>(&p), want * sizeof(int), s);
-        if (e == hipSuccess) e = hipMemsetAsync(p, 0, want * sizeof(int), s);
+        if (e == hipSuccess) {
+            hipLaunchKernelGGL(zero_counters_kernel, dim3((unsigned)((want + 255) / 256)), dim3(256), 0, s, p, want);
+            e = hipGetLastError();
+        }
         if (e != hipSuccess) {
             (void)hipGetLastError();
             return set_error(GFH_ALLOCATION_FAILED, "counter buffer allocation failed: %s", hipGetErrorString(e));
@@ -209,6 +246,7 @@ int stream_workspace(hipStream_t s, size_t bytes, void **out) {
     StreamState *st = nullptr;
     GFH_TRY(current_state(s, &st));
     if (st->ws_bytes < bytes) {
+        GFH_TRY(refuse_during_capture(s, "split-K workspace"));
         size_t want = (size_t)1 << 20;
         while (want < bytes) want *= 2;
         void *p = nullptr;

@@ -28,6 +28,13 @@
  *  - Entry points are re-entrant.  Calls that take `workspace` use only that
  *    memory as scratch; when `workspace` is NULL they allocate stream-ordered
  *    scratch (hipMallocAsync/hipFreeAsync) on `stream`.
+ *  - HIP graphs: calls may be captured on a stream once the same call (same
+ *    or larger sizes) has run on that stream outside a capture, with caller
+ *    workspaces where a call takes one.  The library's per-stream split-K
+ *    buffers are allocated, and their counters zeroed by a kernel, on a
+ *    stream's first use; captured calls then allocate nothing and record no
+ *    memset.  A call that would allocate on a stream being captured fails
+ *    with GFH_ALLOCATION_FAILED before issuing any work.
  */
 #ifndef GHOSTFLOW_HIP_H
 #define GHOSTFLOW_HIP_H
