@@ -25,6 +25,7 @@
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "quant_math.hpp"
 
 // Every multiply and add below is its own f32 rounding, as in the reference
 // (rustc never contracts a*b+c into an FMA); the MFMA accumulation itself is
@@ -62,6 +63,12 @@ struct QParams {
     const int32_t *rowsum2;
     const float *bias2;
     float2 *hpart;
+    // Activations quantized inside the kernel (the 16-column skinny kernel
+    // only): fp32 x [m, k], quantized per tensor, asymmetric, from the
+    // (min, max) of all of x, or of the xpart partials when given.
+    const float *xf;
+    const float2 *xpart;
+    int nxpart;
 };
 
 // One 128 x BK byte stage of a K-contiguous int8 operand: 1024 16-byte
@@ -671,12 +678,26 @@ struct SkParams {
 // DUAL (SwiGLU gate/up): each wave multiplies the same x fragments with the
 // gate rows and the up rows of its 16 columns (D = 2 accumulator sets), and
 // the epilogue writes silu(gate) * up plus the workgroup's (min, max) of it.
-template <int MB, bool DUAL>
-__global__ __launch_bounds__(kThreads) void qlinear_skinny_kernel(SkParams sp) {
+// QX: the activations arrive in fp32 (p.xf) and are quantized per tensor
+// (asymmetric, quantize_activation, quantization.rs:280-287) by every
+// workgroup itself: the (min, max) of all of x (or the fold of p.xpart),
+// the scale and zero point, and the codes of this workgroup's K-slice into
+// LDS, with the quantize kernels' own arithmetic (quant_math.hpp), so the
+// codes are those of gfh_quantize_i8_per_tensor.  It replaces the two
+// quantize launches ahead of the INT8 linear at decode sizes.
+constexpr int kQxBytes = 32768;  // LDS for the codes: m x kslice bytes
+// (QX: four workgroups per CU, as without it -- at 136 registers three fit,
+// and N = 14336's 896 workgroups then needed a second round.)
+template <int MB, bool DUAL, bool QX = false>
+__global__ __launch_bounds__(kThreads, QX ? 4 : 1) void qlinear_skinny_kernel(SkParams sp) {
+    static_assert(!QX || MB == 1, "in-kernel quantization: at most 16 rows of x");
     constexpr int D = DUAL ? 2 : 1;
-    constexpr int kU = (DUAL && MB > 2) ? 4 : 8;  // k-steps in flight per lane
+    // k-steps in flight per lane (QX with two weights: 4, so that four
+    // workgroups fit per CU without spilling)
+    constexpr int kU = (DUAL && (MB > 2 || QX)) ? 4 : 8;
     const QParams &p = sp.q;
     __shared__ i32x4 red[kWaves - 1][D * MB][64];
+    __shared__ __attribute__((aligned(16))) int8_t xq[QX ? kQxBytes : 16];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t blk = blockIdx.x % sp.nblk, slice = blockIdx.x / sp.nblk;
     const int64_t n0 = blk * kCols;
@@ -697,6 +718,44 @@ __global__ __launch_bounds__(kThreads) void qlinear_skinny_kernel(SkParams sp) {
     if (DUAL) wsrc[D - 1] = p.qw2 + wrow;
     const int8_t *xsrc = p.qx + k_lo + kb;
 
+    float qx_scale = 0.f;
+    int32_t qx_zp = 0;
+    if constexpr (QX) {
+        float mn = INFINITY, mx = -INFINITY;
+        if (p.xpart) {
+            for (int i = threadIdx.x; i < p.nxpart; i += kThreads) {
+                const float2 v = p.xpart[i];
+                mn = fminf(mn, v.x);
+                mx = fmaxf(mx, v.y);
+            }
+        } else {
+            // x is [m, k] contiguous with k % 16 == 0 and 16-byte aligned.
+            const f32x4 *xv = reinterpret_cast<const f32x4 *>(p.xf);
+            const int64_t nv = p.m * p.k / 4;
+            for (int64_t i = threadIdx.x; i < nv; i += kThreads) {
+                const f32x4 v = xv[i];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float ve = v[e];
+                    mn = fminf(mn, ve);
+                    mx = fmaxf(mx, ve);
+                }
+            }
+        }
+        qmath::block_minmax<kThreads>(mn, mx);
+        int8_t zp8;
+        qmath::quant_params(mn, mx, false, qx_scale, zp8);
+        qx_zp = zp8;
+        // Codes of rows [0, m) x [k_lo, k_lo + kl), row r at xq + r * kslice.
+        const int q4 = kl / 4;
+        for (int i = threadIdx.x; i < (int)p.m * q4; i += kThreads) {
+            const int r = i / q4, c = 4 * (i - r * q4);
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(p.xf + r * p.k + k_lo + c);
+            *reinterpret_cast<uint32_t *>(xq + r * sp.kslice + c) = qmath::quant4(v, qx_scale, qx_zp);
+        }
+        __syncthreads();
+    }
+
     i32x4 acc[D][MB];
 #pragma unroll
     for (int d = 0; d < D; ++d)
@@ -714,8 +773,12 @@ __global__ __launch_bounds__(kThreads) void qlinear_skinny_kernel(SkParams sp) {
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
                 const int64_t row = mb * 16 + (lane & 15);
-                xf[u][mb] = (ok && row < p.m) ? *reinterpret_cast<const i32x4 *>(xsrc + row * p.k + off)
-                                              : i32x4{0, 0, 0, 0};
+                if constexpr (QX)
+                    xf[u][mb] = (ok && row < p.m) ? *reinterpret_cast<const i32x4 *>(xq + row * sp.kslice + off + kb)
+                                                  : i32x4{0, 0, 0, 0};
+                else
+                    xf[u][mb] = (ok && row < p.m) ? *reinterpret_cast<const i32x4 *>(xsrc + row * p.k + off)
+                                                  : i32x4{0, 0, 0, 0};
             }
         }
 #pragma unroll
@@ -751,14 +814,15 @@ __global__ __launch_bounds__(kThreads) void qlinear_skinny_kernel(SkParams sp) {
     // Zero-point-corrected accumulator of matrix d (0 = qw, 1 = qw2), and its
     // dequantized value plus bias.
     auto corrected = [&](int d, int64_t row, int32_t raw) -> int32_t {
-        if (!p.zx) return raw;
+        if (!QX && !p.zx) return raw;
         const int32_t *rs = d ? p.rowsum2 : p.rowsum;
-        return (int32_t)((uint32_t)raw - (uint32_t)((int32_t)p.zx[p.x_per_row ? row : 0] * rs[col]));
+        const int32_t zx = QX ? qx_zp : (int32_t)p.zx[p.x_per_row ? row : 0];
+        return (int32_t)((uint32_t)raw - (uint32_t)(zx * rs[col]));
     };
     auto dequant = [&](int d, int64_t row, int32_t a) -> float {
         const float *sw = d ? p.sw2 : p.sw;
         const float *bias = d ? p.bias2 : p.bias;
-        const float sc = p.sx[p.x_per_row ? row : 0] * sw[col];
+        const float sc = (QX ? qx_scale : p.sx[p.x_per_row ? row : 0]) * sw[col];
         float v = (float)a * sc;
         if (bias) v = v + bias[col];
         return v;
@@ -862,6 +926,13 @@ int64_t choose_kslice(int64_t nblk, int64_t k) {
     return (ks + 63) & ~(int64_t)63;
 }
 
+// Whether the in-kernel quantization of x serves this shape: at most 4 rows
+// (every workgroup reads all of x) whose codes of one K-slice fit the LDS.
+bool qx_fits(int64_t m, int64_t n, int64_t k) {
+    if (m < 1 || m > 4 || k <= 0 || k % 16 != 0 || n <= 0) return false;
+    return m * choose_kslice((n + kCols - 1) / kCols, k) <= kQxBytes;
+}
+
 template <bool DUAL>
 int launch(const QParams &p, hipStream_t s, int *npart = nullptr) {
     constexpr int D = DUAL ? 2 : 1;
@@ -870,6 +941,9 @@ int launch(const QParams &p, hipStream_t s, int *npart = nullptr) {
     sp.nblk = (p.n + kCols - 1) / kCols;
     sp.kslice = choose_kslice(sp.nblk, p.k);
     sp.slices = (p.k + sp.kslice - 1) / sp.kslice;
+    if (p.xf && (!qx_fits(p.m, p.n, p.k) || !aligned16(p.xf) || p.zx || p.x_per_row))
+        return set_error(GFH_INVALID_DATA, "qlinear_i8: in-kernel activation quantization does not serve m=%lld "
+                         "k=%lld", (long long)p.m, (long long)p.k);
     if (npart) *npart = (int)sp.nblk;
     if (sp.slices > 1) {
         void *ws = nullptr;
@@ -878,7 +952,9 @@ int launch(const QParams &p, hipStream_t s, int *npart = nullptr) {
         GFH_TRY(stream_counters(s, (size_t)sp.nblk, &sp.counters));
     }
     const dim3 grid((unsigned)(sp.nblk * sp.slices)), block(kThreads);
-    if (p.m <= 16)
+    if (p.xf)
+        hipLaunchKernelGGL((qlinear_skinny_kernel<1, DUAL, true>), grid, block, 0, s, sp);
+    else if (p.m <= 16)
         hipLaunchKernelGGL((qlinear_skinny_kernel<1, DUAL>), grid, block, 0, s, sp);
     else if (p.m <= 32)
         hipLaunchKernelGGL((qlinear_skinny_kernel<2, DUAL>), grid, block, 0, s, sp);
@@ -1269,6 +1345,8 @@ bool use_skinny_lds(int64_t m, int64_t n, int64_t k, bool dual) {
 
 }  // namespace
 
+bool qlinear_qx_fits(int64_t m, int64_t n, int64_t k) { return skinny::qx_fits(m, n, k); }
+
 int launch_qlinear_i8(const QLinearDesc &d, hipStream_t s) {
     QParams p{};
     p.qx = d.qx;
@@ -1284,6 +1362,13 @@ int launch_qlinear_i8(const QLinearDesc &d, hipStream_t s) {
     p.n = d.n;
     p.k = d.k;
     p.x_per_row = d.x_per_row ? 1 : 0;
+    p.xf = d.xf;
+    p.xpart = d.xpart;
+    p.nxpart = d.nxpart;
+    if (d.xf) {  // activations quantized in the kernel (qlinear_qx_fits)
+        if (!aligned16(d.qw)) return set_error(GFH_INVALID_DATA, "qlinear_i8: in-kernel quantization needs aligned qw");
+        return skinny::launch<false>(p, s);
+    }
     if (d.m <= 64 && d.k % 16 == 0 && d.k > 0 && aligned16(d.qx) && aligned16(d.qw))
         return use_skinny_lds(d.m, d.n, d.k, false) ? skinny_lds::launch<false>(p, s) : skinny::launch<false>(p, s);
     // Direct-to-LDS tiles need 16-byte aligned rows (K % 64 == 0) and 32-bit
@@ -1349,7 +1434,7 @@ int64_t qlinear_swiglu_partials(int64_t m, int64_t n) {
 
 int launch_qlinear_swiglu_i8(const QSwigluDesc &d, int *npart, hipStream_t s) {
     const QLinearDesc &g = d.g;
-    if (!qlinear_swiglu_fits(g.m, g.n, g.k) || g.x_per_row || !aligned16(g.qx) || !aligned16(g.qw) ||
+    if (!qlinear_swiglu_fits(g.m, g.n, g.k) || g.x_per_row || !(g.xf || aligned16(g.qx)) || !aligned16(g.qw) ||
         !aligned16(d.qw_up))
         return set_error(GFH_INVALID_DATA, "qlinear_swiglu_i8: shape or alignment not served by the fused kernel");
     QParams p{};
@@ -1369,6 +1454,10 @@ int launch_qlinear_swiglu_i8(const QSwigluDesc &d, int *npart, hipStream_t s) {
     p.rowsum2 = d.rowsum_up;
     p.bias2 = d.bias_up;
     p.hpart = d.hpart;
+    p.xf = g.xf;
+    p.xpart = g.xpart;
+    p.nxpart = g.nxpart;
+    if (g.xf) return skinny::launch<true>(p, s, npart);  // activations quantized in the kernel
     if (g.m <= 64)
         return use_skinny_lds(g.m, g.n, g.k, true) ? skinny_lds::launch<true>(p, s, npart)
                                                     : skinny::launch<true>(p, s, npart);

@@ -10,6 +10,7 @@
 // reduction passes: 16-byte loads, grid sized to fill the 256 CUs.
 #include "common.hpp"
 #include "kernels.hpp"
+#include "quant_math.hpp"
 
 // Every multiply and add below is its own f32 rounding, as in the reference
 // (rustc never contracts a*b+c into an FMA); the MFMA accumulation itself is
@@ -21,70 +22,13 @@ namespace {
 
 constexpr int kBlock = 256;
 
-__device__ __forceinline__ int32_t sat_f32_to_i32(float f) {
-    if (f != f) return 0;
-    if (f >= 2147483648.0f) return INT32_MAX;
-    if (f <= -2147483648.0f) return INT32_MIN;
-    return (int32_t)f;
-}
+using qmath::quant4;
+using qmath::quant_one;
+using qmath::quant_params;
+using qmath::sat_f32_to_i32;
+using qmath::sat_f32_to_i8;
 
-__device__ __forceinline__ int8_t sat_f32_to_i8(float f) {
-    if (f != f) return 0;
-    if (f >= 127.0f) return 127;
-    if (f <= -128.0f) return -128;
-    return (int8_t)(int32_t)f;
-}
-
-__device__ __forceinline__ void quant_params(float mn, float mx, bool symmetric, float &scale, int8_t &zp) {
-    if (symmetric) {
-        const float absmax = fmaxf(fabsf(mn), fabsf(mx));
-        scale = absmax / 127.0f;
-        zp = 0;
-    } else {
-        scale = (mx - mn) / 255.0f;
-        const float t = (-mn) / scale - 128.0f;
-        zp = sat_f32_to_i8(roundf(t));
-    }
-}
-
-__device__ __forceinline__ int8_t quant_one(float x, float scale, int32_t zp) {
-    const uint32_t sum = (uint32_t)sat_f32_to_i32(roundf(x / scale)) + (uint32_t)zp;
-    int32_t q = (int32_t)sum;
-    q = q < -128 ? -128 : (q > 127 ? 127 : q);
-    return (int8_t)q;
-}
-
-__device__ __forceinline__ uint32_t quant4(f32x4 v, float scale, int32_t zp) {
-    const uint32_t b0 = (uint8_t)quant_one(v[0], scale, zp);
-    const uint32_t b1 = (uint8_t)quant_one(v[1], scale, zp);
-    const uint32_t b2 = (uint8_t)quant_one(v[2], scale, zp);
-    const uint32_t b3 = (uint8_t)quant_one(v[3], scale, zp);
-    return b0 | (b1 << 8) | (b2 << 16) | (b3 << 24);
-}
-
-// Block-wide (min, max) reduction: wave shuffles, then LDS across waves.
-__device__ __forceinline__ void block_minmax(float &mn, float &mx) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        mn = fminf(mn, __shfl_xor(mn, off));
-        mx = fmaxf(mx, __shfl_xor(mx, off));
-    }
-    __shared__ float smn[kBlock / 64], smx[kBlock / 64];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) {
-        smn[wave] = mn;
-        smx[wave] = mx;
-    }
-    __syncthreads();
-    mn = smn[0];
-    mx = smx[0];
-#pragma unroll
-    for (int w = 1; w < kBlock / 64; ++w) {
-        mn = fminf(mn, smn[w]);
-        mx = fmaxf(mx, smx[w]);
-    }
-    __syncthreads();
-}
+__device__ __forceinline__ void block_minmax(float &mn, float &mx) { qmath::block_minmax<kBlock>(mn, mx); }
 
 // ---- per channel: one workgroup per row --------------------------------------
 template <bool VEC>

@@ -10,7 +10,7 @@
 // silu * up kernel) and in int8 (every Linear as the INT8 linear on
 // DynamicQuantization's scheme, quantization.rs:251-288: per-channel
 // symmetric weight codes, activations x and h quantized per tensor,
-// asymmetric, on the device).
+// asymmetric, on the device; at m <= 4 inside the two INT8 launches).
 #include <algorithm>
 
 #include "common.hpp"
@@ -138,6 +138,45 @@ int launch_swiglu_i8(const SwigluDesc &d, void *workspace, hipStream_t s) {
     int8_t *zh = reinterpret_cast<int8_t *>(hs + 4);
     void *hpart = take(h_partials_bytes(d.m, d.inter));
     float *h = d.h ? d.h : gate;
+
+    // Decode sizes (m <= 4): no quantize launches.  The gate/up kernel
+    // quantizes x itself (every workgroup from the min / max of all of x),
+    // and the down projection quantizes h from gate/up's (min, max) partials
+    // of it: the same codes as the quantize passes, two launches instead of
+    // five.
+    if (fused && qlinear_qx_fits(d.m, d.inter, d.hidden) && qlinear_qx_fits(d.m, d.hidden, d.inter) &&
+        aligned16(d.x) && aligned16(h)) {
+        QSwigluDesc f;
+        f.g.xf = d.x;
+        f.g.m = d.m;
+        f.g.n = d.inter;
+        f.g.k = d.hidden;
+        f.g.qw = d.qwg;
+        f.g.sw = d.swg;
+        f.g.w_rowsum = d.rsg;
+        f.g.bias = d.bg;
+        f.g.y = h;
+        f.qw_up = d.qwu;
+        f.sw_up = d.swu;
+        f.rowsum_up = d.rsu;
+        f.bias_up = d.bu;
+        f.hpart = static_cast<float2 *>(hpart);
+        int npart = 0;
+        GFH_TRY(launch_qlinear_swiglu_i8(f, &npart, s));
+        QLinearDesc q;
+        q.xf = h;
+        q.xpart = f.hpart;
+        q.nxpart = npart;
+        q.m = d.m;
+        q.n = d.hidden;
+        q.k = d.inter;
+        q.qw = d.qwd;
+        q.sw = d.swd;
+        q.w_rowsum = d.rsd;
+        q.bias = d.bd;
+        q.y = d.y;
+        return launch_qlinear_i8(q, s);
+    }
 
     GFH_TRY(launch_quantize_per_tensor(d.x, (int64_t)mh, false, qx, sx, zx, xpart, s));
     QLinearDesc q;
