@@ -632,6 +632,47 @@ def comp_qlinear(lib, torch, m, n, k, per_tensor=True):
             "bound": "mfma_i8" if attain == PEAK_I8 else "hbm", "weight_copies": ncopy}
 
 
+def comp_qlinear_dynamic(lib, torch, m, n, k):
+    """The INT8 linear on fp32 activations (gfh_qlinear_dynamic_i8):
+    DynamicQuantization's quantize_activation of x (per tensor, asymmetric)
+    and the INT8 linear in one call -- one launch at m <= 4, where
+    qlinear_i8_* above times the linear alone on codes quantized beforehand.
+    Same data as comp_qlinear; algorithmic bytes count x in fp32."""
+    dev = torch.device("cuda:0")
+    gh = lib.gh
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    x = torch.randn((m, k), device=dev, generator=g)
+    wbytes = n * k
+    ncopy = max(1, min(16, -(-2 * MALL_BYTES // wbytes)))
+    qws, sw = [], None
+    for _ in range(ncopy):
+        w = torch.randn((n, k), device=dev, generator=g) * 0.02
+        qw, sw, _zw = gh.quantize_per_channel(w, symmetric=True)
+        qws.append(qw)
+        del w
+    rs = [gh.qweight_rowsum(q) for q in qws]
+    y = torch.empty((m, n), device=dev)
+    nws = int(lib.L.gfh_qlinear_dynamic_i8_workspace_size(m, k))
+    ws = torch.empty((nws + 3) // 4, device=dev)
+    s = torch.cuda.current_stream(dev).cuda_stream
+    L = lib.L
+    ptrs = [(q.data_ptr(), r.data_ptr()) for q, r in zip(qws, rs)]
+
+    def f(i):
+        qp, rp = ptrs[i % ncopy]
+        L.gfh_qlinear_dynamic_i8(x.data_ptr(), qp, sw.data_ptr(), rp, None, y.data_ptr(), m, n, k,
+                                 ws.data_ptr(), ws.numel() * 4, s)
+    ms = event_time_ms(torch, f, 200)
+    ops = 2.0 * m * n * k
+    byts = 4 * m * k + n * k + 4 * m * n + 8 * n
+    gbs = byts / ms / 1e6
+    attain = min(PEAK_I8, ops / byts * PEAK_HBM)
+    return {"name": f"qlinear_dynamic_i8_m{m}_n{n}_k{k}", "ms": ms, "value": ops / ms / 1e9, "unit": "TOP/s",
+            "gbps": gbs, "frac": ops / (ms * 1e-3) / attain,
+            "bound": "mfma_i8" if attain == PEAK_I8 else "hbm", "weight_copies": ncopy}
+
+
 def comp_gemv(lib, torch, bsz, int8):
     dev = torch.device("cuda:0")
     K, N = 4096, 14336
@@ -1028,6 +1069,8 @@ def run_components(lib, torch, only, cpu=None):
         add(comp_qlinear, 4096, 4096, 4096, cpu_fn=lambda: cpu.qlinear(4096, 4096, 4096))
         for m in (1, 16, 256, 4096):
             add(comp_qlinear, m, 11008, 4096, cpu_fn=lambda m=m: cpu.qlinear(m, 11008, 4096))
+        for m in (1, 4):
+            add(comp_qlinear_dynamic, m, 11008, 4096, cpu_fn=lambda m=m: cpu.qlinear(m, 11008, 4096))
     if "quantize" in want:
         for m in (256, 4096):
             add(comp_quantize, m, cpu_fn=lambda m=m: cpu.quantize(m * 4096))

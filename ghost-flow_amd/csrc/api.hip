@@ -298,6 +298,70 @@ GFH_API int gfh_qlinear_i8(const int8_t *qx, const float *sx, const int8_t *zx, 
     });
 }
 
+namespace {
+// Workspace of gfh_qlinear_dynamic_i8's two-launch form: codes [m*k] | scale,
+// zero point | the quantize pass's min/max partials, each 256-byte aligned.
+size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
+size_t qdyn_workspace(int64_t m, int64_t k) {
+    const size_t mk = (size_t)m * (size_t)k;
+    return round256(mk) + 256 + round256(quantize_per_tensor_workspace((int64_t)mk));
+}
+}  // namespace
+
+GFH_API size_t gfh_qlinear_dynamic_i8_workspace_size(int64_t m, int64_t k) {
+    if (m <= 0 || k <= 0 || m > kMaxDim || k > kMaxDim) return 0;
+    return qdyn_workspace(m, k);
+}
+
+GFH_API int gfh_qlinear_dynamic_i8(const float *x, const int8_t *qw, const float *sw, const int32_t *w_rowsum,
+                                   const float *bias, float *y, int64_t m, int64_t n, int64_t k, void *workspace,
+                                   size_t workspace_bytes, gfh_stream_t stream) {
+    return guarded([&]() -> int {
+        if (m < 0 || n < 0 || k < 0 || m > kMaxDim || n > kMaxDim || k > kMaxDim)
+            return set_error(GFH_INVALID_SHAPE, "qlinear_dynamic: m=%lld n=%lld k=%lld out of range", (long long)m,
+                             (long long)n, (long long)k);
+        if (k > 65793)
+            return set_error(GFH_INVALID_SHAPE, "qlinear_dynamic: k=%lld exceeds the exact-int32 bound (65793)",
+                             (long long)k);
+        if (!y || !w_rowsum) return set_error(GFH_NULL_POINTER, "qlinear_dynamic: y and w_rowsum are required");
+        if (m == 0 || n == 0) return GFH_SUCCESS;
+        GFH_TRY(require_range(x, (size_t)m * (size_t)k * 4, "x"));
+        GFH_TRY(require_range(qw, (size_t)n * (size_t)k, "qw"));
+        GFH_TRY(require_range(sw, (size_t)n * 4, "sw"));
+        GFH_TRY(require_range(w_rowsum, (size_t)n * 4, "w_rowsum"));
+        GFH_TRY(optional_range(bias, (size_t)n * 4, "bias"));
+        GFH_TRY(require_range(y, (size_t)m * (size_t)n * 4, "y"));
+        GFH_TRY(ensure_init());
+        hipStream_t s = as_stream(stream);
+        QLinearDesc d;
+        d.qw = qw;
+        d.sw = sw;
+        d.w_rowsum = w_rowsum;
+        d.bias = bias;
+        d.y = y;
+        d.m = m;
+        d.n = n;
+        d.k = k;
+        if (qlinear_qx_fits(m, n, k, false) && aligned16(x) && aligned16(qw)) {
+            d.xf = x;  // one launch: the INT8 kernel quantizes x itself
+            return launch_qlinear_i8(d, s);
+        }
+        Scratch ws;
+        GFH_TRY(ws.acquire(workspace, workspace_bytes, qdyn_workspace(m, k), s));
+        char *base = static_cast<char *>(ws.ptr());
+        const size_t mk = (size_t)m * (size_t)k;
+        int8_t *qx = reinterpret_cast<int8_t *>(base);
+        float *sx = reinterpret_cast<float *>(base + round256(mk));
+        int8_t *zx = reinterpret_cast<int8_t *>(base + round256(mk) + 4);
+        void *part = base + round256(mk) + 256;
+        GFH_TRY(launch_quantize_per_tensor(x, (int64_t)mk, false, qx, sx, zx, part, s));
+        d.qx = qx;
+        d.sx = sx;
+        d.zx = zx;
+        return launch_qlinear_i8(d, s);
+    });
+}
+
 GFH_API int gfh_gemv_f32(const float *x, const float *w, float *y, int64_t b, int64_t k, int64_t n,
                          gfh_stream_t stream) {
     return guarded([&]() -> int {

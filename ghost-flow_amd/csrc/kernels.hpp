@@ -66,12 +66,12 @@ struct QLinearDesc {
     // In place of qx / sx / zx: fp32 activations [m, k] that the kernel
     // quantizes itself, per tensor and asymmetric, from the (min, max) of all
     // of them or of the nxpart partials xpart (a producer's); only where
-    // qlinear_qx_fits (m <= 4).
+    // qlinear_qx_fits (m <= 4 and few codes per workgroup).
     const float *xf = nullptr;
     const float2 *xpart = nullptr;
     int nxpart = 0;
 };
-bool qlinear_qx_fits(int64_t m, int64_t n, int64_t k);
+bool qlinear_qx_fits(int64_t m, int64_t n, int64_t k, bool partials);
 int launch_qlinear_i8(const QLinearDesc &d, hipStream_t s);
 // SwiGLU gate/up in one launch: h = silu(x.Wg^T + bg) * (x.Wu^T + bu) with x
 // quantized per tensor (g.zx per tensor, g.x_per_row false); g carries x,

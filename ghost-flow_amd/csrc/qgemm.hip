@@ -926,11 +926,19 @@ int64_t choose_kslice(int64_t nblk, int64_t k) {
     return (ks + 63) & ~(int64_t)63;
 }
 
-// Whether the in-kernel quantization of x serves this shape: at most 4 rows
-// (every workgroup reads all of x) whose codes of one K-slice fit the LDS.
-bool qx_fits(int64_t m, int64_t n, int64_t k) {
+// Whether the in-kernel quantization of x pays: every workgroup computes
+// the codes of its K-slice itself (m * kslice correctly rounded divisions),
+// and without producer partials also reads all of x for the min / max.
+// Measured against the quantize launches + INT8 linear (us, fused /
+// separate): N = 11008, K = 4096: m = 1 14.8 / 18.5, m = 2 19.4 / 18.9, m = 4
+// 27.4 / 19.8; N = 4096, K = 4096: m = 2 13.1 / 15.0, m = 3 16.2 / 15.9;
+// N = 4096, K = 11008, m = 1 19.9 / 20.3.  With partials (the SwiGLU down
+// projection, kslice 5504 / 7168 at m = 1) it paid too.
+constexpr int64_t kQxCodes = 4096, kQxCodesPartials = 8192;
+bool qx_fits(int64_t m, int64_t n, int64_t k, bool partials) {
     if (m < 1 || m > 4 || k <= 0 || k % 16 != 0 || n <= 0) return false;
-    return m * choose_kslice((n + kCols - 1) / kCols, k) <= kQxBytes;
+    const int64_t codes = m * choose_kslice((n + kCols - 1) / kCols, k);
+    return codes <= (partials ? kQxCodesPartials : kQxCodes) && codes <= kQxBytes;
 }
 
 template <bool DUAL>
@@ -941,7 +949,7 @@ int launch(const QParams &p, hipStream_t s, int *npart = nullptr) {
     sp.nblk = (p.n + kCols - 1) / kCols;
     sp.kslice = choose_kslice(sp.nblk, p.k);
     sp.slices = (p.k + sp.kslice - 1) / sp.kslice;
-    if (p.xf && (!qx_fits(p.m, p.n, p.k) || !aligned16(p.xf) || p.zx || p.x_per_row))
+    if (p.xf && (!qx_fits(p.m, p.n, p.k, p.xpart != nullptr) || !aligned16(p.xf) || p.zx || p.x_per_row))
         return set_error(GFH_INVALID_DATA, "qlinear_i8: in-kernel activation quantization does not serve m=%lld "
                          "k=%lld", (long long)p.m, (long long)p.k);
     if (npart) *npart = (int)sp.nblk;
@@ -1345,7 +1353,7 @@ bool use_skinny_lds(int64_t m, int64_t n, int64_t k, bool dual) {
 
 }  // namespace
 
-bool qlinear_qx_fits(int64_t m, int64_t n, int64_t k) { return skinny::qx_fits(m, n, k); }
+bool qlinear_qx_fits(int64_t m, int64_t n, int64_t k, bool partials) { return skinny::qx_fits(m, n, k, partials); }
 
 int launch_qlinear_i8(const QLinearDesc &d, hipStream_t s) {
     QParams p{};

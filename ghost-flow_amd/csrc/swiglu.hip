@@ -139,13 +139,13 @@ int launch_swiglu_i8(const SwigluDesc &d, void *workspace, hipStream_t s) {
     void *hpart = take(h_partials_bytes(d.m, d.inter));
     float *h = d.h ? d.h : gate;
 
-    // Decode sizes (m <= 4): no quantize launches.  The gate/up kernel
-    // quantizes x itself (every workgroup from the min / max of all of x),
-    // and the down projection quantizes h from gate/up's (min, max) partials
-    // of it: the same codes as the quantize passes, two launches instead of
-    // five.
-    if (fused && qlinear_qx_fits(d.m, d.inter, d.hidden) && qlinear_qx_fits(d.m, d.hidden, d.inter) &&
-        aligned16(d.x) && aligned16(h)) {
+    // Decode sizes (m = 1 at the LLaMA / Mistral widths): no quantize
+    // launches.  The gate/up kernel quantizes x itself (every workgroup from
+    // the min / max of all of x), and the down projection quantizes h from
+    // gate/up's (min, max) partials of it: the same codes as the quantize
+    // passes, two launches instead of five.
+    if (fused && qlinear_qx_fits(d.m, d.inter, d.hidden, false) &&
+        qlinear_qx_fits(d.m, d.hidden, d.inter, true) && aligned16(d.x) && aligned16(h)) {
         QSwigluDesc f;
         f.g.xf = d.x;
         f.g.m = d.m;

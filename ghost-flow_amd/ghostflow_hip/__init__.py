@@ -25,6 +25,7 @@ from .ops import (  # noqa: F401
     mha_forward_with_cache,
     mha_workspace_size,
     qlinear,
+    qlinear_dynamic,
     qswiglu,
     quantize_per_channel,
     quantize_per_tensor,

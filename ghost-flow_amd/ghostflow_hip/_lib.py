@@ -54,6 +54,8 @@ SIGNATURES = {
     "gfh_dequantize_i8": (_i, [_p, _i64, _i64, _p, _p, _i64, _p, _p]),
     "gfh_qweight_rowsum": (_i, [_p, _i64, _i64, _p, _p]),
     "gfh_qlinear_i8": (_i, [_p, _p, _p, _i, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
+    "gfh_qlinear_dynamic_i8_workspace_size": (_sz, [_i64, _i64]),
+    "gfh_qlinear_dynamic_i8": (_i, [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p, _sz, _p]),
     "gfh_gemv_f32": (_i, [_p, _p, _p, _i64, _i64, _i64, _p]),
     "gfh_gemv_w8": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "gfh_gemv_w8_noalloc": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),

@@ -204,6 +204,28 @@ def qlinear(qx, sx, zx, qw, sw, *, x_per_row=False, w_rowsum=None, bias=None, wa
     return y, acc
 
 
+def qlinear_dynamic(x, qw, sw, w_rowsum, *, bias=None, out=None, workspace=None):
+    """The INT8 linear on fp32 activations x [m, k]: quantize_activation
+    (per tensor, asymmetric, quantization.rs:280-287) then qlinear with the
+    per-channel weight codes qw [n, k]; y [m, n].  Same codes and outputs as
+    quantize_per_tensor followed by qlinear, in one launch for m <= 4."""
+    _need(x, torch.float32, "x")
+    _need(qw, torch.int8, "qw")
+    _need(sw, torch.float32, "sw")
+    _need(w_rowsum, torch.int32, "w_rowsum")
+    _need(bias, torch.float32, "bias")
+    m, k = x.shape
+    n = qw.shape[0]
+    if qw.shape[1] != k:
+        raise GhostFlowError(_lib.INVALID_SHAPE, f"ShapeMismatch expected [{m}, {k}] got [{qw.shape[1]}, {n}]")
+    y = torch.empty((m, n), dtype=torch.float32, device=x.device) if out is None else out
+    ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(),
+                                                             workspace.numel() * workspace.element_size())
+    _check(lib().gfh_qlinear_dynamic_i8(x.data_ptr(), qw.data_ptr(), sw.data_ptr(), w_rowsum.data_ptr(),
+                                        _ptr(bias), y.data_ptr(), m, n, k, ws_ptr, ws_bytes, _stream(x.device)))
+    return y
+
+
 # ---- GEMV ---------------------------------------------------------------------
 
 def gemv_f32(x, w, out=None):

@@ -9,10 +9,10 @@ computed on the device by the bit-exact kernels of quant.hip:
   DynamicQuantization         :251-294 per-channel symmetric weights,
                                        per-tensor asymmetric activations
 
-DynamicQuantization.quantized_linear runs the INT8 linear
-(gfh_qlinear_i8) on its stored weights and a dynamically quantized
-activation -- the layer the reference only expresses as get_weights +
-fp32 matmul.  FP16 raises NotImplementedError, as the reference's
+DynamicQuantization.quantized_linear runs the INT8 linear on its stored
+weights and a dynamically quantized activation (gfh_qlinear_dynamic_i8:
+quantize_activation then gfh_qlinear_i8, one launch at decode sizes) -- the
+layer the reference only expresses as get_weights + fp32 matmul.  FP16 raises NotImplementedError, as the reference's
 unimplemented!() does (quantization.rs:155-158, :167-168).
 """
 from __future__ import annotations
@@ -23,7 +23,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .ops import (GhostFlowError, dequantize, qlinear, quantize_per_channel, quantize_per_tensor,
+from .ops import (GhostFlowError, dequantize, qlinear_dynamic, quantize_per_channel, quantize_per_tensor,
                   qweight_rowsum)
 
 
@@ -128,7 +128,6 @@ class DynamicQuantization:
         q = self.weight_quantized[name]
         if len(q.shape) != 2:
             raise GhostFlowError(_lib.INVALID_SHAPE, f"{name} is not a [out, in] weight")
-        xq = self.quantize_activation(x.reshape(-1, x.shape[-1]).contiguous())
-        y, _ = qlinear(xq.data, xq.scales, xq.zero_points, q.data, q.scales, w_rowsum=self._rowsums[name],
-                       bias=bias)
+        y = qlinear_dynamic(x.reshape(-1, x.shape[-1]).contiguous(), q.data, q.scales, self._rowsums[name],
+                            bias=bias)
         return y.reshape(*x.shape[:-1], q.shape[0])

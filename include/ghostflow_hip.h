@@ -172,6 +172,22 @@ GFH_API int gfh_qlinear_i8(const int8_t *qx, const float *sx, const int8_t *zx,
                            int32_t *acc_out, int64_t m, int64_t n, int64_t k,
                            gfh_stream_t stream);
 
+/* The same layer on fp32 activations x [m, k]: DynamicQuantization::
+ * quantize_activation (per tensor, asymmetric, quantization.rs:280-287) of x
+ * followed by gfh_qlinear_i8 with x_per_row = 0.  The codes, and so y, are
+ * exactly those of gfh_quantize_i8_per_tensor(symmetric = 0) followed by
+ * gfh_qlinear_i8.  For m <= 4 (k % 16 == 0, aligned x and qw) it is one
+ * launch: every workgroup finds the min / max of x and quantizes its part
+ * itself, and no workspace is used.  Otherwise the quantize pass writes the
+ * codes to workspace (nullable; at least
+ * gfh_qlinear_dynamic_i8_workspace_size(m, k) bytes, 16-byte aligned).
+ * w_rowsum is required. */
+GFH_API size_t gfh_qlinear_dynamic_i8_workspace_size(int64_t m, int64_t k);
+GFH_API int gfh_qlinear_dynamic_i8(const float *x, const int8_t *qw, const float *sw,
+                                   const int32_t *w_rowsum, const float *bias, float *y,
+                                   int64_t m, int64_t n, int64_t k, void *workspace,
+                                   size_t workspace_bytes, gfh_stream_t stream);
+
 /* ---- decode GEMV --------------------------------------------------------- */
 
 /* y[b, n] = sum_k x[b, k] * W[k, n], W [k, n] row-major, b <= 64.
