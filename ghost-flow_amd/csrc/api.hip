@@ -267,6 +267,10 @@ GFH_API int gfh_qlinear_i8(const int8_t *qx, const float *sx, const int8_t *zx, 
         if (zx && !w_rowsum)
             return set_error(GFH_NULL_POINTER, "qlinear: w_rowsum is required when zero points are given");
         if (m == 0 || n == 0) return GFH_SUCCESS;
+        int64_t t;
+        if (!mul_ok(m, k, &t) || !mul_ok(n, k, &t) || !mul_ok(m, n, &t))
+            return set_error(GFH_INVALID_SHAPE, "qlinear: m=%lld n=%lld k=%lld overflow", (long long)m, (long long)n,
+                             (long long)k);
         const int64_t nx = x_per_row ? m : 1;
         GFH_TRY(require_range(qx, (size_t)m * (size_t)k, "qx"));
         GFH_TRY(require_range(qw, (size_t)n * (size_t)k, "qw"));
@@ -309,7 +313,8 @@ size_t qdyn_workspace(int64_t m, int64_t k) {
 }  // namespace
 
 GFH_API size_t gfh_qlinear_dynamic_i8_workspace_size(int64_t m, int64_t k) {
-    if (m <= 0 || k <= 0 || m > kMaxDim || k > kMaxDim) return 0;
+    int64_t t;
+    if (m <= 0 || k <= 0 || m > kMaxDim || k > kMaxDim || !mul_ok(m, k, &t)) return 0;
     return qdyn_workspace(m, k);
 }
 
@@ -325,6 +330,10 @@ GFH_API int gfh_qlinear_dynamic_i8(const float *x, const int8_t *qw, const float
                              (long long)k);
         if (!y || !w_rowsum) return set_error(GFH_NULL_POINTER, "qlinear_dynamic: y and w_rowsum are required");
         if (m == 0 || n == 0) return GFH_SUCCESS;
+        int64_t t;
+        if (!mul_ok(m, k, &t) || !mul_ok(n, k, &t) || !mul_ok(m, n, &t))
+            return set_error(GFH_INVALID_SHAPE, "qlinear_dynamic: m=%lld n=%lld k=%lld overflow", (long long)m,
+                             (long long)n, (long long)k);
         GFH_TRY(require_range(x, (size_t)m * (size_t)k * 4, "x"));
         GFH_TRY(require_range(qw, (size_t)n * (size_t)k, "qw"));
         GFH_TRY(require_range(sw, (size_t)n * 4, "sw"));

@@ -92,6 +92,21 @@ def test_qlinear_k_bound_and_outputs():
     assert lib.gfh_qlinear_i8(None, None, None, 0, None, None, None, None, None, None, 4, 4, 64, None) == 3
 
 
+def test_qlinear_dynamic_rules():
+    """gfh_qlinear_dynamic_i8 validates on the host before any device work:
+    the exact-int32 K bound, the required y / w_rowsum, element counts
+    whose byte sizes would overflow, and the workspace size query."""
+    lib = _lib()
+    f = lib.gfh_qlinear_dynamic_i8
+    assert f(None, None, None, None, None, None, 4, 4, 70000, None, 0, None) == 1   # K beyond 65793
+    assert f(None, None, None, None, None, None, 4, 4, 64, None, 0, None) == 3      # y, w_rowsum NULL
+    y = C.c_void_p(16)
+    assert f(None, None, None, y, None, y, 2**31 - 1, 2**31 - 1, 64, None, 0, None) == 1  # m*n bytes overflow
+    assert f(None, None, None, y, None, y, 0, 16, 64, None, 0, None) == 0             # empty: no work
+    assert lib.gfh_qlinear_dynamic_i8_workspace_size(0, 64) == 0
+    assert lib.gfh_qlinear_dynamic_i8_workspace_size(4, 4096) >= 4 * 4096
+
+
 def test_gemv_batch_limit():
     lib = _lib()
     assert lib.gfh_gemv_f32(None, None, None, 65, 16, 16, None) == 1
