@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <climits>
 #include <cmath>
+#include <initializer_list>
 #include <new>
 
 #include "common.hpp"
@@ -24,6 +25,15 @@ bool mul_ok(int64_t a, int64_t b, int64_t *out) {
     __int128 r = (__int128)a * (__int128)b;
     if (r > (__int128)INT64_MAX / 8) return false;
     *out = (int64_t)r;
+    return true;
+}
+
+// Whether the product of dims (each >= 0) stays far from int64 / size_t
+// overflow, so that byte sizes computed from it are exact.
+bool count_ok(std::initializer_list<int64_t> dims) {
+    int64_t c = 1;
+    for (int64_t d : dims)
+        if (!mul_ok(c, d, &c)) return false;
     return true;
 }
 
@@ -378,6 +388,8 @@ GFH_API int gfh_gemv_f32(const float *x, const float *w, float *y, int64_t b, in
             return set_error(GFH_INVALID_SHAPE, "gemv_f32: b=%lld (<= 64) k=%lld n=%lld out of range",
                              (long long)b, (long long)k, (long long)n);
         if (b == 0 || n == 0) return GFH_SUCCESS;
+        if (!count_ok({k, n}))
+            return set_error(GFH_INVALID_SHAPE, "gemv: k=%lld n=%lld overflow", (long long)k, (long long)n);
         GFH_TRY(require_range(x, (size_t)b * (size_t)k * 4, "x"));
         GFH_TRY(require_range(w, (size_t)k * (size_t)n * 4, "w"));
         GFH_TRY(require_range(y, (size_t)b * (size_t)n * 4, "y"));
@@ -393,6 +405,8 @@ GFH_API int gfh_gemv_w8(const float *x, const int8_t *qw, const float *scales, c
             return set_error(GFH_INVALID_SHAPE, "gemv_w8: b=%lld (<= 64) k=%lld n=%lld out of range",
                              (long long)b, (long long)k, (long long)n);
         if (b == 0 || n == 0) return GFH_SUCCESS;
+        if (!count_ok({k, n}))
+            return set_error(GFH_INVALID_SHAPE, "gemv: k=%lld n=%lld overflow", (long long)k, (long long)n);
         GFH_TRY(require_range(x, (size_t)b * (size_t)k * 4, "x"));
         GFH_TRY(require_range(qw, (size_t)k * (size_t)n, "qw"));
         GFH_TRY(require_range(scales, (size_t)k * 4, "scales"));
@@ -410,6 +424,8 @@ GFH_API int gfh_gemv_w8_noalloc(const float *x, const int8_t *qw, const float *s
             return set_error(GFH_INVALID_SHAPE, "gemv_w8_noalloc: b=%lld (<= 64) k=%lld n=%lld out of range",
                              (long long)b, (long long)k, (long long)n);
         if (b == 0 || n == 0) return GFH_SUCCESS;
+        if (!count_ok({k, n}))
+            return set_error(GFH_INVALID_SHAPE, "gemv: k=%lld n=%lld overflow", (long long)k, (long long)n);
         GFH_TRY(require_range(x, (size_t)b * (size_t)k * 4, "x"));
         GFH_TRY(require_range(qw, (size_t)k * (size_t)n, "qw"));
         GFH_TRY(require_range(scales, (size_t)k * 4, "scales"));
@@ -510,6 +526,9 @@ GFH_API int gfh_sdpa_f32(const float *q, const float *k, const float *v, float *
         if (mask && mask_numel <= 0) return set_error(GFH_INVALID_SHAPE, "sdpa: mask_numel must be > 0");
         if (b == 0 || h == 0 || sq == 0) return GFH_SUCCESS;
         if (skv == 0) return set_error(GFH_INVALID_SHAPE, "sdpa: empty key sequence");
+        if (!count_ok({b, h, sq, skv}) || !count_ok({b, h, skv, d}))
+            return set_error(GFH_INVALID_SHAPE, "sdpa: b=%lld h=%lld sq=%lld skv=%lld overflow", (long long)b,
+                             (long long)h, (long long)sq, (long long)skv);
         const size_t bh = (size_t)b * (size_t)h;
         GFH_TRY(require_range(q, bh * (size_t)sq * (size_t)d * 4, "q"));
         GFH_TRY(require_range(k, bh * (size_t)skv * (size_t)d * 4, "k"));

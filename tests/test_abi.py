@@ -111,6 +111,10 @@ def test_gemv_batch_limit():
     lib = _lib()
     assert lib.gfh_gemv_f32(None, None, None, 65, 16, 16, None) == 1
     assert lib.gfh_gemv_w8(None, None, None, None, None, 65, 16, 16, None) == 1
+    # k * n elements whose byte size would overflow
+    big = 2**31 - 1
+    assert lib.gfh_gemv_f32(None, None, None, 1, big, big, None) == 1
+    assert lib.gfh_gemv_w8(None, None, None, None, None, 1, big, big, None) == 1
 
 
 def test_flash_attention_shape_rules():
