@@ -207,7 +207,8 @@ GFH_API int gfh_quantize_i8_per_channel(const float *x, int64_t rows, int64_t co
 }
 
 GFH_API size_t gfh_quantize_i8_per_tensor_workspace_size(int64_t n) {
-    return quantize_per_tensor_workspace(n < 0 ? 0 : n);
+    if (n < 0 || n > ((int64_t)1 << 40)) return 0;
+    return quantize_per_tensor_workspace(n);
 }
 
 GFH_API int gfh_quantize_i8_per_tensor(const float *x, int64_t n, int symmetric, int8_t *q, float *scale,
@@ -452,7 +453,9 @@ GFH_API int gfh_softmax_lastdim_f32(const float *x, float *y, int64_t rows, int6
 }
 
 GFH_API size_t gfh_flash_attention_workspace_size(int64_t batch, int64_t seq_len_q, int64_t seq_len_k) {
-    if (batch <= 0 || seq_len_q <= 0 || seq_len_k <= 0) return 0;
+    if (batch <= 0 || seq_len_q <= 0 || seq_len_k <= 0 || batch > kMaxDim || seq_len_q > kMaxDim ||
+        seq_len_k > kMaxDim)
+        return 0;
     int64_t t, u;
     if (!mul_ok(batch, seq_len_q, &t) || !mul_ok(t, seq_len_k, &u)) return 0;
     return (size_t)u * sizeof(float);
@@ -523,7 +526,8 @@ GFH_API int gfh_sdpa_f32(const float *q, const float *k, const float *v, float *
                              "sdpa: causal attention needs sq == skv (got %lld, %lld); the top-left causal rule of "
                              "FlashAttention::forward for sq != skv is gfh_flash_attention_f32",
                              (long long)sq, (long long)skv);
-        if (mask && mask_numel <= 0) return set_error(GFH_INVALID_SHAPE, "sdpa: mask_numel must be > 0");
+        if (mask && (mask_numel <= 0 || !count_ok({mask_numel})))
+            return set_error(GFH_INVALID_SHAPE, "sdpa: mask_numel=%lld out of range", (long long)mask_numel);
         if (b == 0 || h == 0 || sq == 0) return GFH_SUCCESS;
         if (skv == 0) return set_error(GFH_INVALID_SHAPE, "sdpa: empty key sequence");
         if (!count_ok({b, h, sq, skv}) || !count_ok({b, h, skv, d}))
@@ -579,13 +583,15 @@ GFH_API int gfh_kv_attention_f32(const float *q, int64_t ldq, const float *k, co
         if (causal && kv_len < sq)
             return set_error(GFH_INVALID_SHAPE, "kv_attention: causal needs kv_len >= sq (got %lld < %lld)",
                              (long long)kv_len, (long long)sq);
-        if (mask && mask_numel <= 0) return set_error(GFH_INVALID_SHAPE, "kv_attention: mask_numel must be > 0");
+        if (mask && (mask_numel <= 0 || !count_ok({mask_numel})))
+            return set_error(GFH_INVALID_SHAPE, "kv_attention: mask_numel=%lld out of range", (long long)mask_numel);
         if (b == 0 || h == 0 || sq == 0) return GFH_SUCCESS;
         if (kv_len == 0) return set_error(GFH_INVALID_SHAPE, "kv_attention: empty key sequence");
-        int64_t bs, bhs, eq, ekv, eo, ew, t;
+        int64_t bs, bhs, eq, ekv, eo, ew, t, one;
         if (!mul_ok(b, sq, &bs) || !mul_ok(bs, h, &bhs) || !extent2d(bs, hd, ldq, &eq) ||
-            !extent2d(bs, hd, ldo, &eo) || !mul_ok(capacity, ldkv, &t) ||
-            !extent_batched((kv_len - 1) * ldkv + hd, b, t, &ekv) || !mul_ok(bhs, kv_len, &ew))
+            !extent2d(bs, hd, ldo, &eo) || !mul_ok(capacity, ldkv, &t) || !extent2d(kv_len, hd, ldkv, &one) ||
+            !extent_batched(one, b, t, &ekv) || !mul_ok(bhs, kv_len, &ew) || !count_ok({sq, ldq}) ||
+            !count_ok({sq, ldo}))
             return set_error(GFH_INVALID_SHAPE, "kv_attention: operand extent overflows");
         GFH_TRY(require_range(q, (size_t)eq * 4, "q"));
         GFH_TRY(require_range(k, (size_t)ekv * 4, "k"));
@@ -653,7 +659,8 @@ GFH_API int gfh_mha_forward_with_cache_f32(const float *query, const float *key,
         const int64_t kv_len = past_len + sk;
         if (causal && kv_len < sq)
             return set_error(GFH_INVALID_SHAPE, "mha: causal needs past_len + sk >= sq");
-        if (mask && mask_numel <= 0) return set_error(GFH_INVALID_SHAPE, "mha: mask_numel must be > 0");
+        if (mask && (mask_numel <= 0 || !count_ok({mask_numel})))
+            return set_error(GFH_INVALID_SHAPE, "mha: mask_numel=%lld out of range", (long long)mask_numel);
         if (b == 0 || sq == 0) return GFH_SUCCESS;
         if (kv_len == 0) return set_error(GFH_INVALID_SHAPE, "mha: empty key sequence");
         int64_t bsq, bsk, ww, cache, bh, bhs, wts;
@@ -728,20 +735,27 @@ GFH_API int gfh_silu_mul_f32(const float *gate, const float *up, float *out, int
 }
 
 namespace {
+// SwiGLU dims in [0, INT32_MAX] whose operand element counts (m x hidden,
+// m x inter, hidden x inter) stay far from overflow.
+bool swiglu_dims_ok(int64_t m, int64_t hidden, int64_t inter, int64_t *mh, int64_t *mi, int64_t *wi) {
+    return m >= 0 && hidden >= 0 && inter >= 0 && m <= kMaxDim && hidden <= kMaxDim && inter <= kMaxDim &&
+           mul_ok(m, hidden, mh) && mul_ok(m, inter, mi) && mul_ok(hidden, inter, wi);
+}
+
 // Shape checks shared by both SwiGLU entry points.
 int swiglu_shapes(const char *what, int64_t m, int64_t hidden, int64_t inter, int64_t *mh, int64_t *mi,
                   int64_t *wi) {
-    if (m < 0 || hidden < 0 || inter < 0 || m > kMaxDim || hidden > kMaxDim || inter > kMaxDim)
+    if (!swiglu_dims_ok(m, hidden, inter, mh, mi, wi))
         return set_error(GFH_INVALID_SHAPE, "%s: m=%lld hidden=%lld inter=%lld out of range", what, (long long)m,
                          (long long)hidden, (long long)inter);
-    if (!mul_ok(m, hidden, mh) || !mul_ok(m, inter, mi) || !mul_ok(hidden, inter, wi))
-        return set_error(GFH_INVALID_SHAPE, "%s: operand extent overflows", what);
     return GFH_SUCCESS;
 }
 }  // namespace
 
 GFH_API size_t gfh_swiglu_f32_workspace_size(int64_t m, int64_t inter) {
-    return swiglu_f32_workspace_bytes(m < 0 ? 0 : m, inter < 0 ? 0 : inter);
+    int64_t a, b, c;
+    if (!swiglu_dims_ok(m, 0, inter, &a, &b, &c)) return 0;
+    return swiglu_f32_workspace_bytes(m, inter);
 }
 
 GFH_API int gfh_swiglu_f32(const float *x, int64_t m, int64_t hidden, int64_t inter, const float *wg,
@@ -784,7 +798,9 @@ GFH_API int gfh_swiglu_f32(const float *x, int64_t m, int64_t hidden, int64_t in
 }
 
 GFH_API size_t gfh_swiglu_i8_workspace_size(int64_t m, int64_t hidden, int64_t inter) {
-    return swiglu_i8_workspace_bytes(m < 0 ? 0 : m, hidden < 0 ? 0 : hidden, inter < 0 ? 0 : inter);
+    int64_t a, b, c;
+    if (!swiglu_dims_ok(m, hidden, inter, &a, &b, &c)) return 0;
+    return swiglu_i8_workspace_bytes(m, hidden, inter);
 }
 
 GFH_API int gfh_swiglu_i8(const float *x, int64_t m, int64_t hidden, int64_t inter, const int8_t *qwg,

@@ -27,7 +27,8 @@
  *    the host before any launch; nothing is launched when a call fails.
  *  - Entry points are re-entrant.  Calls that take `workspace` use only that
  *    memory as scratch; when `workspace` is NULL they allocate stream-ordered
- *    scratch (hipMallocAsync/hipFreeAsync) on `stream`.
+ *    scratch (hipMallocAsync/hipFreeAsync) on `stream`.  The *_workspace_size
+ *    queries return 0 for shapes their entry point rejects as out of range.
  *  - HIP graphs: calls may be captured on a stream once the same call (same
  *    or larger sizes) has run on that stream outside a capture, with caller
  *    workspaces where a call takes one.  The library's per-stream split-K

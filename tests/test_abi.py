@@ -174,6 +174,19 @@ def test_kv_attention_rejects_bad_shapes():
     # causal with more queries than keys
     assert lib.gfh_kv_attention_f32(p, 16, p, p, 8, 16, p, 16, None, 1, 2, 4, 3, 8, 1.0, 1, None, 0, None) == 1
     assert b"causal" in lib.gfh_last_error()
+    # a key leading dimension whose extent over kv_len rows would overflow
+    big = 2**62
+    assert lib.gfh_kv_attention_f32(p, 16, p, p, 8, big, p, 16, None, 1, 2, 1, 8, 8, 1.0, 0, None, 0, None) == 1
+    assert b"overflows" in lib.gfh_last_error()
+    # a mask whose byte size would overflow
+    assert lib.gfh_kv_attention_f32(p, 16, p, p, 8, 16, p, 16, None, 1, 2, 1, 8, 8, 1.0, 0, p, big, None) == 1
+    assert b"mask_numel" in lib.gfh_last_error()
+    assert lib.gfh_sdpa_f32(p, p, p, p, None, 1, 1, 8, 8, 16, 1.0, 0, p, big, None) == 1
+    assert b"mask_numel" in lib.gfh_last_error()
+    w = [p] * 8  # wq, bq, wk, bk, wv, bv, wo, bo
+    assert lib.gfh_mha_forward_with_cache_f32(p, p, p, *w, p, p, 16, 0, p, big, 0, p, None, 1, 1, 1, 16, 2,
+                                              None, 0, None) == 1
+    assert b"mask_numel" in lib.gfh_last_error()
 
 
 def test_swiglu_rejects_bad_shapes():
@@ -202,7 +215,12 @@ def test_swiglu_workspace_sizes():
     assert lib.gfh_swiglu_i8_workspace_size(4, 64, 96) >= 4 * 64 + 4 * 96 * 4 + 4 * 96
     # unfused (hidden = 80): gate and up in fp32 as well
     assert lib.gfh_swiglu_i8_workspace_size(70, 80, 96) >= 70 * 80 + 2 * 70 * 96 * 4 + 70 * 96
-    assert lib.gfh_swiglu_i8_workspace_size(-1, -1, -1) >= 0
+    # shapes the entry points reject as out of range size to 0
+    assert lib.gfh_swiglu_i8_workspace_size(-1, -1, -1) == 0
+    assert lib.gfh_swiglu_f32_workspace_size(2**40, 2**40) == 0
+    assert lib.gfh_swiglu_i8_workspace_size(2**31 - 1, 2**31 - 1, 16) == 0
+    assert lib.gfh_quantize_i8_per_tensor_workspace_size(2**41) == 0
+    assert lib.gfh_flash_attention_workspace_size(2**33, 1, 1) == 0
 
 
 def test_matmul_backward_rejects_bad_dims():
