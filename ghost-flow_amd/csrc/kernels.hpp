@@ -22,10 +22,15 @@ struct SgemmDesc {
     const float *bias = nullptr;
 };
 int launch_sgemm(const SgemmDesc &d, hipStream_t s);
-// gemv_nt.hip: the NT form at m <= 8 (Linear at decode sizes); launch_sgemm
-// uses it when gemv_nt_fits.
+// gemv_nt.hip: the NT form at m <= kNtSkinnyMinM (Linear at decode sizes);
+// launch_sgemm uses it when gemv_nt_fits.  The grouped form runs up to
+// kNtMaxGroups unbatched NT products of one shape (m, n, k, lda, ldb, alpha,
+// beta) with their own operands, bias and ldc in one launch.
 bool gemv_nt_fits(const SgemmDesc &d);
 int launch_gemv_nt(const SgemmDesc &d, hipStream_t s);
+constexpr int kNtMaxGroups = 3;
+bool gemv_nt_group_fits(const SgemmDesc *d, int count);
+int launch_gemv_nt_group(const SgemmDesc *d, int count, hipStream_t s);
 // gemm_nt_skinny.hip: the NT form at kNtSkinnyMinM < m <= 64 on f32 MFMA
 // with the weight streamed into registers; launch_sgemm uses it when
 // gemm_nt_skinny_fits.

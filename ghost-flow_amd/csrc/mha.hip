@@ -10,8 +10,9 @@
 //                                              -> workspace [b*sq, e]
 //   out = attn . Wo^T + bo
 //
-// The projections are launch_sgemm NT calls (the row-dot GEMV when at most
-// 8 rows, the MFMA tile GEMM otherwise).  Attention reads q, K and V in the
+// The projections are launch_sgemm NT calls (the row-dot GEMV up to 4 rows,
+// with q, k and v in one grouped launch when their shapes agree; the skinny
+// MFMA GEMM up to 64 rows; the MFMA tile GEMM beyond).  Attention reads q, K and V in the
 // [B, S, E] layout where head h is a block of columns -- the storage of the
 // reference's reshape_for_attention view (:146-150) -- with the decode
 // kernel (kv_attention.hip) for up to 16 queries and the tiled SDPA kernel
@@ -35,7 +36,7 @@ int launch_mha_forward(const MhaDesc &d, void *workspace, hipStream_t s) {
     float *qbuf = static_cast<float *>(workspace);
     float *abuf = reinterpret_cast<float *>(static_cast<char *>(workspace) + one);
 
-    auto linear = [&](const float *x, int64_t m, const float *w, const float *bias, float *y, int64_t ldc) {
+    auto linear_desc = [&](const float *x, int64_t m, const float *w, const float *bias, float *y, int64_t ldc) {
         SgemmDesc g;
         g.trans_b = true;
         g.m = m;
@@ -48,15 +49,15 @@ int launch_mha_forward(const MhaDesc &d, void *workspace, hipStream_t s) {
         g.c = y;
         g.ldc = ldc;
         g.bias = bias;
-        return launch_sgemm(g, s);
+        return g;
     };
     // New keys / values into cache rows [past, past + sk) of every batch.
-    auto project_into_cache = [&](const float *x, const float *w, const float *bias, float *cache) {
+    auto cache_desc = [&](const float *x, const float *w, const float *bias, float *cache) {
         float *dst = cache + d.past_len * e;
         if (d.sk == 1)  // one row per batch: rows e apart in x, capacity*e apart in the cache
-            return linear(x, d.b, w, bias, dst, d.capacity * e);
+            return linear_desc(x, d.b, w, bias, dst, d.capacity * e);
         if (d.b == 1 || d.capacity == d.sk)  // the batch's rows are contiguous in the cache
-            return linear(x, d.b * d.sk, w, bias, dst, e);
+            return linear_desc(x, d.b * d.sk, w, bias, dst, e);
         SgemmDesc g;  // one slice per batch, the weight shared (batch_b = 1)
         g.trans_b = true;
         g.m = d.sk;
@@ -73,13 +74,19 @@ int launch_mha_forward(const MhaDesc &d, void *workspace, hipStream_t s) {
         g.stride_c = d.capacity * e;
         g.batch = d.b;
         g.bias = bias;
-        return launch_sgemm(g, s);
+        return g;
     };
 
-    GFH_TRY(linear(d.query, d.b * d.sq, d.wq, d.bq, qbuf, e));
-    if (d.sk > 0) {
-        GFH_TRY(project_into_cache(d.key, d.wk, d.bk, d.k_cache));
-        GFH_TRY(project_into_cache(d.value, d.wv, d.bv, d.v_cache));
+    const SgemmDesc proj[3] = {linear_desc(d.query, d.b * d.sq, d.wq, d.bq, qbuf, e),
+                               cache_desc(d.key, d.wk, d.bk, d.k_cache), cache_desc(d.value, d.wv, d.bv, d.v_cache)};
+    const int nproj = d.sk > 0 ? 3 : 1;
+    // At decode sizes (the same few rows of query, key and value) the three
+    // projections share one GEMV launch: 3x the columns fill the GPU better
+    // than one projection does, and two launch tails go away.
+    if (gemv_nt_group_fits(proj, nproj)) {
+        GFH_TRY(launch_gemv_nt_group(proj, nproj, s));
+    } else {
+        for (int i = 0; i < nproj; ++i) GFH_TRY(launch_sgemm(proj[i], s));
     }
     const int64_t kv_len = d.past_len + d.sk;
     if (d.sq <= 16) {
@@ -127,7 +134,7 @@ int launch_mha_forward(const MhaDesc &d, void *workspace, hipStream_t s) {
         a.o_bs = d.sq * e, a.o_hs = hd, a.o_rs = e;
         GFH_TRY(launch_sdpa(a, s));
     }
-    return linear(abuf, d.b * d.sq, d.wo, d.bo, d.out, e);
+    return launch_sgemm(linear_desc(abuf, d.b * d.sq, d.wo, d.bo, d.out, e), s);
 }
 
 }  // namespace gfh

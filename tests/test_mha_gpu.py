@@ -162,3 +162,42 @@ def test_module_forward_is_self_attention(torch_dev):
     params = [to_np(t) for t in mha.parameters()]
     xn = to_np(x)
     assert_rel(y, O.mha_forward_with_cache(xn, xn, xn, *params, h)[0])
+
+
+@pytest.mark.parametrize("b,sq,sk,p", [
+    (4, 1, 1, 300),  # a decode step: q, k and v projected in one grouped launch
+    (1, 3, 3, 5),    # one sequence, 3 new rows: grouped as well
+    (2, 1, 1, 0),    # no past
+    (3, 2, 2, 4),    # k / v rows strided per batch in the cache: three launches
+    (6, 1, 1, 7),    # 6 rows: the skinny MFMA GEMM, three launches
+])
+def test_projections_equal_separate_linears(torch_dev, b, sq, sk, p):
+    """Where the q / k / v projections share one launch, each must still
+    equal the same Linear (gfh_sgemm NT) run alone, bit for bit: the cache
+    rows written, and the output against Linear -> kv_attention -> Linear
+    composed from separate calls."""
+    import torch
+    gh = _gh()
+    e, h, cap = 256, 4, 16 + 300
+    params = _dev(_params(e, 17 + b), torch_dev)
+    wq, bq, wk, bk, wv, bv, wo, bo = params
+    rng = np.random.default_rng(b * 100 + sq)
+    q_in, k_in, v_in = (to_dev(rng.normal(0, 1, (b, s, e)).astype(np.float32), torch_dev) for s in (sq, sk, sk))
+    kc = to_dev(rng.normal(0, 1, (b, cap, e)).astype(np.float32), torch_dev)
+    vc = to_dev(rng.normal(0, 1, (b, cap, e)).astype(np.float32), torch_dev)
+    kc0, vc0 = kc.clone(), vc.clone()
+    out = gh.mha_forward_cached(q_in, k_in, v_in, wq, bq, wk, bk, wv, bv, wo, bo, h, kc, vc, p)
+    torch.cuda.synchronize()
+    if sk == 1 or b == 1:  # the new rows of every batch projected as one [b * sk, e] product
+        kn = gh.linear(k_in.reshape(b * sk, e), wk, bk).reshape(b, sk, e)
+        vn = gh.linear(v_in.reshape(b * sk, e), wv, bv).reshape(b, sk, e)
+    else:  # one [sk, e] product per batch (the rows are strided in the cache)
+        kn = torch.stack([gh.linear(k_in[i], wk, bk) for i in range(b)])
+        vn = torch.stack([gh.linear(v_in[i], wv, bv) for i in range(b)])
+    assert torch.equal(kc[:, p:p + sk], kn) and torch.equal(vc[:, p:p + sk], vn)
+    assert torch.equal(kc[:, :p], kc0[:, :p]) and torch.equal(kc[:, p + sk:], kc0[:, p + sk:])
+    assert torch.equal(vc[:, :p], vc0[:, :p]) and torch.equal(vc[:, p + sk:], vc0[:, p + sk:])
+    q = gh.linear(q_in.reshape(b * sq, e), wq, bq).reshape(b, sq, e)
+    attn = gh.ops.kv_attention(q, kc, vc, p + sk, h)
+    ref = gh.linear(attn.reshape(b * sq, e), wo, bo).reshape(b, sq, e)
+    assert torch.equal(out, ref)
