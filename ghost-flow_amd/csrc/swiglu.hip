@@ -66,6 +66,8 @@ size_t swiglu_f32_workspace_bytes(int64_t m, int64_t inter) {
 }
 
 // fp32: gate and up into the workspace, h over gate (or into d.h), then down.
+// Each product is a launch_sgemm NT call (the grouped GEMV for gate and up
+// together when m <= 4).
 int launch_swiglu_f32(const SwigluDesc &d, void *workspace, hipStream_t s) {
     const size_t one = round_up((size_t)d.m * (size_t)d.inter * 4);
     float *gate = static_cast<float *>(workspace);
@@ -84,12 +86,20 @@ int launch_swiglu_f32(const SwigluDesc &d, void *workspace, hipStream_t s) {
         g.c = y;
         g.ldc = n;
         g.bias = bias;
-        return launch_sgemm(g, s);
+        return g;
     };
-    GFH_TRY(linear(d.x, d.wg, d.bg, gate, d.inter, d.hidden));
-    GFH_TRY(linear(d.x, d.wu, d.bu, up, d.inter, d.hidden));
+    // Gate and up read the same x: at decode sizes (m <= 4) they share one
+    // grouped GEMV launch, otherwise one launch each.
+    const SgemmDesc gu[2] = {linear(d.x, d.wg, d.bg, gate, d.inter, d.hidden),
+                             linear(d.x, d.wu, d.bu, up, d.inter, d.hidden)};
+    if (gemv_nt_group_fits(gu, 2)) {
+        GFH_TRY(launch_gemv_nt_group(gu, 2, s));
+    } else {
+        GFH_TRY(launch_sgemm(gu[0], s));
+        GFH_TRY(launch_sgemm(gu[1], s));
+    }
     GFH_TRY(launch_silu_mul(gate, up, h, d.m * d.inter, s));
-    return linear(h, d.wd, d.bd, d.y, d.hidden, d.inter);
+    return launch_sgemm(linear(h, d.wd, d.bd, d.y, d.hidden, d.inter), s);
 }
 
 // Workspace of the int8 block, each region 256-byte aligned:

@@ -224,3 +224,20 @@ def test_swiglu_modules(torch_dev):
     assert torch.equal(yq.reshape(6, 128), gh.qswiglu(x.reshape(6, 128), ql.gate, ql.up, ql.down))
     # int8 stays near the fp32 layer
     assert float((yq - y).abs().max()) <= 0.05 * float(y.abs().max())
+
+
+@pytest.mark.parametrize("m", [1, 3, 6])
+def test_swiglu_f32_equals_its_linears(torch_dev, m):
+    """Gate and up share one grouped launch at m <= 4 (separate launches at
+    m = 6); either way h and y must equal the same Linears and silu * up run
+    as separate calls, bit for bit."""
+    import torch
+    gh = _gh()
+    rng = np.random.default_rng(70 + m)
+    hidden, inter = 512, 1376
+    x = to_dev(rng.normal(0, 1, (m, hidden)).astype(F), torch_dev)
+    wg, bg, wu, bu, wd, bd = (to_dev(a, torch_dev) for a in _fp32_layer(rng, hidden, inter))
+    y, h = gh.swiglu(x, wg, bg, wu, bu, wd, bd, want_h=True)
+    hh = gh.silu_mul(gh.linear(x, wg, bg), gh.linear(x, wu, bu))
+    assert torch.equal(h, hh)
+    assert torch.equal(y, gh.linear(hh, wd, bd))
