@@ -64,8 +64,16 @@ struct SkNtParams {
     int64_t m, n, k;
     float alpha, beta;
     int64_t ngrp, kslice, slices;
-    float *part;    // [slices][m][n] partial sums (slices > 1, batch 1)
-    int *counters;  // one per 16-column block, zero at rest (slices > 1)
+    float *part;    // [groups][slices][m][n] partial sums (slices > 1, batch 1)
+    int *counters;  // [groups][16-column blocks], zero at rest (slices > 1)
+    // ngroups > 0: blockIdx.y selects product g of a grouped launch, with
+    // the operands below (m, n, k, lda, ldb, alpha and beta are shared).
+    int ngroups;
+    const float *gx[kNtMaxGroups];
+    const float *gw[kNtMaxGroups];
+    float *gy[kNtMaxGroups];
+    const float *gbias[kNtMaxGroups];
+    int64_t gldc[kNtMaxGroups];
 };
 
 template <int N>
@@ -87,12 +95,17 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_nt_skinny_kernel(SkNtPara
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t grp = blockIdx.x % p.ngrp, slice = blockIdx.x / p.ngrp;
     const int64_t n0 = grp * kGroupCols + 16 * wave;  // this wave's first weight row
-    // batch slice blockIdx.y with the reference's modulo indexing
-    // (matmul.rs:147-149)
+    // blockIdx.y: product z of a grouped launch, else batch slice z with the
+    // reference's modulo indexing (matmul.rs:147-149)
     const uint32_t z = blockIdx.y;
-    const float *xb = p.x + (int64_t)(z % (uint32_t)p.batch_a) * p.stride_a;
-    const float *wb = p.w + (int64_t)(z % (uint32_t)p.batch_b) * p.stride_b;
-    float *yb = p.y + (int64_t)z * p.stride_c;
+    const bool grouped = p.ngroups > 0;
+    const float *xb = grouped ? p.gx[z] : p.x + (int64_t)(z % (uint32_t)p.batch_a) * p.stride_a;
+    const float *wb = grouped ? p.gw[z] : p.w + (int64_t)(z % (uint32_t)p.batch_b) * p.stride_b;
+    float *yb = grouped ? p.gy[z] : p.y + (int64_t)z * p.stride_c;
+    const float *bias = grouped ? p.gbias[z] : p.bias;
+    const int64_t ldc = grouped ? p.gldc[z] : p.ldc;
+    float *part = grouped ? p.part + (int64_t)z * p.slices * p.m * p.n : p.part;
+    int *counters = grouped ? p.counters + (int64_t)z * p.ngrp * kWaves : p.counters;
 
     const int64_t k_lo = slice * p.kslice;
     const int kl = (int)min(p.kslice, p.k - k_lo);  // > 0, a multiple of 4
@@ -232,10 +245,10 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_nt_skinny_kernel(SkNtPara
     const int64_t col = n0 + (lane & 15);
     auto row_of = [&](int mb, int r) -> int64_t { return (int64_t)mb * 16 + 4 * (lane >> 4) + r; };
     auto epilogue = [&](int64_t row, float sum) {
-        float *dst = yb + row * p.ldc + col;
+        float *dst = yb + row * ldc + col;
         float v = p.alpha * sum;
         if (p.beta != 0.f) v = v + p.beta * *dst;
-        if (p.bias) v = v + p.bias[col];
+        if (bias) v = v + bias[col];
         *dst = v;
     };
     const bool col_ok = col < p.n;
@@ -260,7 +273,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_nt_skinny_kernel(SkNtPara
         for (int r = 0; r < 4; ++r) {
             const int64_t row = row_of(mb, r);
             if (row < p.m && col_ok)
-                __hip_atomic_store(p.part + (slice * p.m + row) * p.n + col, acc[mb][r], __ATOMIC_RELAXED,
+                __hip_atomic_store(part + (slice * p.m + row) * p.n + col, acc[mb][r], __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
         }
     // split-K arrival protocol (common.hpp): steps 2-4
@@ -269,7 +282,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_nt_skinny_kernel(SkNtPara
     const int64_t blk = n0 / 16;
     int last = 0;
     if (lane == 0)
-        last = __hip_atomic_fetch_add(p.counters + blk, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+        last = __hip_atomic_fetch_add(counters + blk, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                (int)p.slices - 1;
     last = __shfl(last, 0);
     if (!last) return;
@@ -286,7 +299,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_nt_skinny_kernel(SkNtPara
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int64_t row = row_of(mb, r);
-            src[mb][r] = (row < p.m && col_ok) ? p.part + row * p.n + col : nullptr;
+            src[mb][r] = (row < p.m && col_ok) ? part + row * p.n + col : nullptr;
             sum[mb][r] = 0.f;
         }
     for (int64_t j0 = 0; j0 < p.slices; j0 += kGroup) {
@@ -314,7 +327,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_nt_skinny_kernel(SkNtPara
 #pragma unroll
         for (int r = 0; r < 4; ++r)
             if (src[mb][r]) epilogue(row_of(mb, r), sum[mb][r]);
-    if (lane == 0) __hip_atomic_store(p.counters + blk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (lane == 0) __hip_atomic_store(counters + blk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // K elements per workgroup: all of K with at least ~kTargetWgs workgroups
@@ -351,6 +364,32 @@ bool gemm_nt_skinny_fits(const SgemmDesc &d) {
            (d.batch_a <= 1 || d.stride_a % 4 == 0) && (d.batch_b <= 1 || d.stride_b % 4 == 0) && d.batch <= 65535;
 }
 
+namespace {
+// Slicing, split-K buffers and the launch for `gy` products (grid.y).
+int launch_params(SkNtParams &p, int64_t gy, hipStream_t s) {
+    const int64_t prods = p.ngroups > 0 ? p.ngroups : 1;
+    p.ngrp = (p.n + kGroupCols - 1) / kGroupCols;
+    p.kslice = choose_kslice(p.ngrp * prods, p.k, p.ngroups > 0 ? 1 : gy, p.m);
+    p.slices = (p.k + p.kslice - 1) / p.kslice;
+    if (p.slices > 1) {
+        void *ws = nullptr;
+        GFH_TRY(stream_workspace(s, sizeof(float) * (size_t)(prods * p.slices * p.m * p.n), &ws));
+        p.part = static_cast<float *>(ws);
+        GFH_TRY(stream_counters(s, (size_t)(prods * p.ngrp * kWaves), &p.counters));
+    }
+    const dim3 grid((unsigned)(p.ngrp * p.slices), (unsigned)gy), block(64 * kWaves);
+    if (p.m <= 16)
+        hipLaunchKernelGGL((gemm_nt_skinny_kernel<1, kDepth>), grid, block, 0, s, p);
+    else if (p.m <= 32)
+        hipLaunchKernelGGL((gemm_nt_skinny_kernel<2, kDepth>), grid, block, 0, s, p);
+    else if (p.m <= 48)
+        hipLaunchKernelGGL((gemm_nt_skinny_kernel<3, kDepth>), grid, block, 0, s, p);
+    else
+        hipLaunchKernelGGL((gemm_nt_skinny_kernel<4, kDepth>), grid, block, 0, s, p);
+    return check_launch("sgemm (NT skinny MFMA)");
+}
+}  // namespace
+
 int launch_gemm_nt_skinny(const SgemmDesc &d, hipStream_t s) {
     SkNtParams p{};
     p.x = d.a;
@@ -370,26 +409,39 @@ int launch_gemm_nt_skinny(const SgemmDesc &d, hipStream_t s) {
     p.k = d.k;
     p.alpha = d.alpha;
     p.beta = d.beta;
-    const int64_t batch = std::max<int64_t>(d.batch, 1);
-    p.ngrp = (d.n + kGroupCols - 1) / kGroupCols;
-    p.kslice = choose_kslice(p.ngrp, d.k, batch, d.m);
-    p.slices = (d.k + p.kslice - 1) / p.kslice;
-    if (p.slices > 1) {
-        void *ws = nullptr;
-        GFH_TRY(stream_workspace(s, sizeof(float) * (size_t)(p.slices * d.m * d.n), &ws));
-        p.part = static_cast<float *>(ws);
-        GFH_TRY(stream_counters(s, (size_t)(p.ngrp * kWaves), &p.counters));
+    return launch_params(p, std::max<int64_t>(d.batch, 1), s);
+}
+
+bool gemm_nt_skinny_group_fits(const SgemmDesc *d, int count) {
+    if (count < 1 || count > kNtMaxGroups) return false;
+    for (int g = 0; g < count; ++g) {
+        const SgemmDesc &e = d[g];
+        if (!gemm_nt_skinny_fits(e) || e.batch > 1 || e.m != d[0].m || e.n != d[0].n || e.k != d[0].k ||
+            e.lda != d[0].lda || e.ldb != d[0].ldb || e.alpha != d[0].alpha || e.beta != d[0].beta)
+            return false;
     }
-    const dim3 grid((unsigned)(p.ngrp * p.slices), (unsigned)batch), block(64 * kWaves);
-    if (d.m <= 16)
-        hipLaunchKernelGGL((gemm_nt_skinny_kernel<1, kDepth>), grid, block, 0, s, p);
-    else if (d.m <= 32)
-        hipLaunchKernelGGL((gemm_nt_skinny_kernel<2, kDepth>), grid, block, 0, s, p);
-    else if (d.m <= 48)
-        hipLaunchKernelGGL((gemm_nt_skinny_kernel<3, kDepth>), grid, block, 0, s, p);
-    else
-        hipLaunchKernelGGL((gemm_nt_skinny_kernel<4, kDepth>), grid, block, 0, s, p);
-    return check_launch("sgemm (NT skinny MFMA)");
+    return true;
+}
+
+int launch_gemm_nt_skinny_group(const SgemmDesc *d, int count, hipStream_t s) {
+    SkNtParams p{};
+    p.lda = d[0].lda;
+    p.ldb = d[0].ldb;
+    p.batch_a = p.batch_b = 1;
+    p.m = d[0].m;
+    p.n = d[0].n;
+    p.k = d[0].k;
+    p.alpha = d[0].alpha;
+    p.beta = d[0].beta;
+    p.ngroups = count;
+    for (int g = 0; g < count; ++g) {
+        p.gx[g] = d[g].a;
+        p.gw[g] = d[g].b;
+        p.gy[g] = d[g].c;
+        p.gbias[g] = d[g].bias;
+        p.gldc[g] = d[g].ldc;
+    }
+    return launch_params(p, count, s);
 }
 
 }  // namespace gfh

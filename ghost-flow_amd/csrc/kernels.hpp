@@ -33,10 +33,17 @@ bool gemv_nt_group_fits(const SgemmDesc *d, int count);
 int launch_gemv_nt_group(const SgemmDesc *d, int count, hipStream_t s);
 // gemm_nt_skinny.hip: the NT form at kNtSkinnyMinM < m <= 64 on f32 MFMA
 // with the weight streamed into registers; launch_sgemm uses it when
-// gemm_nt_skinny_fits.
+// gemm_nt_skinny_fits.  Grouped like the row-dot form.
 constexpr int64_t kNtSkinnyMinM = 4;
 bool gemm_nt_skinny_fits(const SgemmDesc &d);
 int launch_gemm_nt_skinny(const SgemmDesc &d, hipStream_t s);
+bool gemm_nt_skinny_group_fits(const SgemmDesc *d, int count);
+int launch_gemm_nt_skinny_group(const SgemmDesc *d, int count, hipStream_t s);
+// sgemm.hip: up to kNtMaxGroups NT products of one shape at m <= 64 in one
+// launch (whichever of the two forms above serves m), or false / an error
+// when they do not fit one.
+bool sgemm_nt_group_fits(const SgemmDesc *d, int count);
+int launch_sgemm_nt_group(const SgemmDesc *d, int count, hipStream_t s);
 // sgemm_big.hip: NT and NN (A [m, k]) on direct-to-LDS tiles -- 256 x 256 or
 // 128 x 128 when they fill the GPU, else 64 x 64 (K % 32 == 0, batch 1; NN
 // with n % 4 == 0).

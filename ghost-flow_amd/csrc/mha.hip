@@ -11,8 +11,8 @@
 //   out = attn . Wo^T + bo
 //
 // The projections are launch_sgemm NT calls (the row-dot GEMV up to 4 rows,
-// with q, k and v in one grouped launch when their shapes agree; the skinny
-// MFMA GEMM up to 64 rows; the MFMA tile GEMM beyond).  Attention reads q, K and V in the
+// the skinny MFMA GEMM up to 64, the MFMA tile GEMM beyond), with q, k and v
+// in one grouped launch up to 64 rows when their shapes agree.  Attention reads q, K and V in the
 // [B, S, E] layout where head h is a block of columns -- the storage of the
 // reference's reshape_for_attention view (:146-150) -- with the decode
 // kernel (kv_attention.hip) for up to 16 queries and the tiled SDPA kernel
@@ -80,11 +80,11 @@ int launch_mha_forward(const MhaDesc &d, void *workspace, hipStream_t s) {
     const SgemmDesc proj[3] = {linear_desc(d.query, d.b * d.sq, d.wq, d.bq, qbuf, e),
                                cache_desc(d.key, d.wk, d.bk, d.k_cache), cache_desc(d.value, d.wv, d.bv, d.v_cache)};
     const int nproj = d.sk > 0 ? 3 : 1;
-    // At decode sizes (the same few rows of query, key and value) the three
-    // projections share one GEMV launch: 3x the columns fill the GPU better
-    // than one projection does, and two launch tails go away.
-    if (gemv_nt_group_fits(proj, nproj)) {
-        GFH_TRY(launch_gemv_nt_group(proj, nproj, s));
+    // Up to 64 rows (the same rows of query, key and value) the three
+    // projections share one launch: 3x the columns fill the GPU better than
+    // one projection does, and two launch tails go away.
+    if (sgemm_nt_group_fits(proj, nproj)) {
+        GFH_TRY(launch_sgemm_nt_group(proj, nproj, s));
     } else {
         for (int i = 0; i < nproj; ++i) GFH_TRY(launch_sgemm(proj[i], s));
     }

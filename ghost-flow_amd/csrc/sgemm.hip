@@ -273,6 +273,16 @@ int launch_variant(const SgemmParams &p, int64_t batch, hipStream_t s) {
 
 }  // namespace
 
+bool sgemm_nt_group_fits(const SgemmDesc *d, int count) {
+    return gemv_nt_group_fits(d, count) || gemm_nt_skinny_group_fits(d, count);
+}
+
+int launch_sgemm_nt_group(const SgemmDesc *d, int count, hipStream_t s) {
+    if (gemv_nt_group_fits(d, count)) return launch_gemv_nt_group(d, count, s);
+    if (gemm_nt_skinny_group_fits(d, count)) return launch_gemm_nt_skinny_group(d, count, s);
+    return set_error(GFH_INVALID_SHAPE, "sgemm: these products do not share one launch");
+}
+
 int launch_sgemm(const SgemmDesc &d, hipStream_t s) {
     // x . W^T with at most 8 rows of x: a tile of this kernel would leave
     // most of its MFMA rows empty and its grid far too small to stream W.

@@ -66,8 +66,8 @@ size_t swiglu_f32_workspace_bytes(int64_t m, int64_t inter) {
 }
 
 // fp32: gate and up into the workspace, h over gate (or into d.h), then down.
-// Each product is a launch_sgemm NT call (the grouped GEMV for gate and up
-// together when m <= 4).
+// Each product is a launch_sgemm NT call (gate and up as one grouped launch
+// when m <= 64).
 int launch_swiglu_f32(const SwigluDesc &d, void *workspace, hipStream_t s) {
     const size_t one = round_up((size_t)d.m * (size_t)d.inter * 4);
     float *gate = static_cast<float *>(workspace);
@@ -88,12 +88,12 @@ int launch_swiglu_f32(const SwigluDesc &d, void *workspace, hipStream_t s) {
         g.bias = bias;
         return g;
     };
-    // Gate and up read the same x: at decode sizes (m <= 4) they share one
-    // grouped GEMV launch, otherwise one launch each.
+    // Gate and up read the same x: up to 64 rows they share one grouped
+    // launch, otherwise one launch each.
     const SgemmDesc gu[2] = {linear(d.x, d.wg, d.bg, gate, d.inter, d.hidden),
                              linear(d.x, d.wu, d.bu, up, d.inter, d.hidden)};
-    if (gemv_nt_group_fits(gu, 2)) {
-        GFH_TRY(launch_gemv_nt_group(gu, 2, s));
+    if (sgemm_nt_group_fits(gu, 2)) {
+        GFH_TRY(launch_sgemm_nt_group(gu, 2, s));
     } else {
         GFH_TRY(launch_sgemm(gu[0], s));
         GFH_TRY(launch_sgemm(gu[1], s));

@@ -164,18 +164,23 @@ def test_module_forward_is_self_attention(torch_dev):
     assert_rel(y, O.mha_forward_with_cache(xn, xn, xn, *params, h)[0])
 
 
-@pytest.mark.parametrize("b,sq,sk,p", [
-    (4, 1, 1, 300),  # a decode step: q, k and v projected in one grouped launch
-    (1, 3, 3, 5),    # one sequence, 3 new rows: grouped as well
-    (2, 1, 1, 0),    # no past
-    (3, 2, 2, 4),    # k / v rows strided per batch in the cache: three launches
-    (6, 1, 1, 7),    # 6 rows: the skinny MFMA GEMM, three launches
+@pytest.mark.parametrize("b,sq,sk,p,exact", [
+    (4, 1, 1, 300, True),  # a decode step: q, k and v in one grouped row-dot launch
+    (1, 3, 3, 5, True),    # one sequence, 3 new rows: grouped as well
+    (2, 1, 1, 0, True),    # no past
+    (3, 2, 2, 4, True),    # k / v rows strided per batch in the cache: three launches
+    (6, 1, 1, 7, False),   # 6 rows: one grouped skinny MFMA launch
+    (40, 1, 1, 3, False),  # 40 rows: the same, three row blocks
 ])
-def test_projections_equal_separate_linears(torch_dev, b, sq, sk, p):
-    """Where the q / k / v projections share one launch, each must still
-    equal the same Linear (gfh_sgemm NT) run alone, bit for bit: the cache
-    rows written, and the output against Linear -> kv_attention -> Linear
-    composed from separate calls."""
+def test_projections_equal_separate_linears(torch_dev, b, sq, sk, p, exact):
+    """Where the q / k / v projections share one launch, each must equal the
+    same Linear (gfh_sgemm NT) run alone: the cache rows written, and the
+    output against Linear -> kv_attention -> Linear composed from separate
+    calls.  Bit for bit up to 4 rows (the row-dot form splits K only inside
+    a workgroup, so grouping changes nothing) and where the products are not
+    grouped; from 5 rows the grouped skinny launch chooses its K split for
+    the whole group, so its sums may differ from a lone launch's in the last
+    bits: within the GEMM bound, and the output within the attention bar."""
     import torch
     gh = _gh()
     e, h, cap = 256, 4, 16 + 300
@@ -194,10 +199,18 @@ def test_projections_equal_separate_linears(torch_dev, b, sq, sk, p):
     else:  # one [sk, e] product per batch (the rows are strided in the cache)
         kn = torch.stack([gh.linear(k_in[i], wk, bk) for i in range(b)])
         vn = torch.stack([gh.linear(v_in[i], wv, bv) for i in range(b)])
-    assert torch.equal(kc[:, p:p + sk], kn) and torch.equal(vc[:, p:p + sk], vn)
+    if exact:
+        assert torch.equal(kc[:, p:p + sk], kn) and torch.equal(vc[:, p:p + sk], vn)
+    else:
+        for got, ref, xin, w in ((kc[:, p:p + sk], kn, k_in, wk), (vc[:, p:p + sk], vn, v_in, wv)):
+            tol = gemm_tol(e, to_np(xin), to_np(w))
+            assert float((got - ref).abs().max()) <= 2 * tol
     assert torch.equal(kc[:, :p], kc0[:, :p]) and torch.equal(kc[:, p + sk:], kc0[:, p + sk:])
     assert torch.equal(vc[:, :p], vc0[:, :p]) and torch.equal(vc[:, p + sk:], vc0[:, p + sk:])
     q = gh.linear(q_in.reshape(b * sq, e), wq, bq).reshape(b, sq, e)
     attn = gh.ops.kv_attention(q, kc, vc, p + sk, h)
     ref = gh.linear(attn.reshape(b * sq, e), wo, bo).reshape(b, sq, e)
-    assert torch.equal(out, ref)
+    if exact:
+        assert torch.equal(out, ref)
+    else:
+        assert_rel(to_np(out), to_np(ref).astype(np.float64))

@@ -226,11 +226,14 @@ def test_swiglu_modules(torch_dev):
     assert float((yq - y).abs().max()) <= 0.05 * float(y.abs().max())
 
 
-@pytest.mark.parametrize("m", [1, 3, 6])
+@pytest.mark.parametrize("m", [1, 3])
 def test_swiglu_f32_equals_its_linears(torch_dev, m):
-    """Gate and up share one grouped launch at m <= 4 (separate launches at
-    m = 6); either way h and y must equal the same Linears and silu * up run
-    as separate calls, bit for bit."""
+    """Gate and up share one grouped row-dot launch up to 4 rows; h and y
+    must equal the same Linears and silu * up run as separate calls, bit for
+    bit (the row-dot form splits K only inside a workgroup, so grouping
+    changes nothing).  From 5 rows the grouped launch is the skinny MFMA
+    kernel, whose K split is chosen for the group: test_swiglu_f32_stages
+    holds it to the oracle."""
     import torch
     gh = _gh()
     rng = np.random.default_rng(70 + m)
