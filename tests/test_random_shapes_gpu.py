@@ -13,7 +13,11 @@ oracle at the bars of the hand-picked cases:
     or two): bit for bit against quantize_activation + the INT8 linear;
   * attention over a KV cache (a few new queries, causal or masked, the
     cache partly filled): within 1e-4 relative of the oracle's SDPA on the
-    filled rows.
+    filled rows;
+  * softmax (1e-4 relative per element), per-channel and per-tensor
+    quantization (bit for bit), matmul_backward (GEMM bound),
+    MultiHeadAttention::forward_with_cache (1e-4 relative) and
+    FlashAttention::forward's blockwise recurrence (its normwise bar).
 The shapes are drawn once from fixed seeds, so every run checks the same
 cases; they land on ragged tiles, odd K, split-K boundaries and tiny sizes
 that the hand-picked shapes may not."""
@@ -252,3 +256,130 @@ def test_kv_attention_random(torch_dev, b, h, sq, kv_len, cap, d, mode):
     np.testing.assert_array_equal(np.isfinite(got), finite)
     if finite.any():
         assert_rel(got[finite], ref[finite])
+
+
+def _softmax_cases():
+    rng = np.random.default_rng(20268)
+    return [(_dim(rng, 1, 3000), _dim(rng, 1, 5000)) for _ in range(16)]
+
+
+@pytest.mark.parametrize("rows,cols", _softmax_cases())
+def test_softmax_random(torch_dev, rows, cols):
+    """Tensor::softmax(-1): 1e-4 relative per element (the reference sums a
+    row sequentially, the GPU in a tree)."""
+    gh, O = _gh(), _O()
+    x = np.random.default_rng(rows * 7 + cols).normal(0, 3, (rows, cols)).astype(np.float32)
+    got = to_np(gh.softmax_lastdim(to_dev(x, torch_dev)))
+    np.testing.assert_allclose(got, O.softmax_lastdim(x), rtol=1e-4, atol=1e-12)
+
+
+def _quant_cases():
+    rng = np.random.default_rng(20269)
+    return [(_dim(rng, 1, 500), _dim(rng, 1, 3000), bool(rng.integers(2))) for _ in range(16)]
+
+
+@pytest.mark.parametrize("rows,cols,symmetric", _quant_cases())
+def test_quantize_random(torch_dev, rows, cols, symmetric):
+    """quantize_per_channel_int8 and quantize_per_tensor_int8: codes, scales
+    and zero points bit for bit."""
+    gh, O = _gh(), _O()
+    x = np.random.default_rng(rows * 13 + cols).normal(0, 2, (rows, cols)).astype(np.float32)
+    dx = to_dev(x, torch_dev)
+    for got, ref in ((gh.quantize_per_channel(dx, symmetric), O.quantize_per_channel(x, symmetric)),
+                     (gh.quantize_per_tensor(dx, symmetric), O.quantize_per_tensor(x, symmetric))):
+        q, s, z = (to_np(t) for t in got)
+        rq, rs, rz = ref
+        np.testing.assert_array_equal(q.reshape(-1), np.asarray(rq).reshape(-1))
+        np.testing.assert_array_equal(s.reshape(-1).view(np.uint32),
+                                      np.atleast_1d(np.asarray(rs, np.float32)).view(np.uint32))
+        np.testing.assert_array_equal(z.reshape(-1), np.atleast_1d(np.asarray(rz, np.int8)))
+
+
+def _backward_cases():
+    rng = np.random.default_rng(20270)
+    return [(_dim(rng, 1, 400), _dim(rng, 1, 400), _dim(rng, 1, 400)) for _ in range(12)]
+
+
+@pytest.mark.parametrize("m,k,n", _backward_cases())
+def test_matmul_backward_random(torch_dev, m, k, n):
+    """matmul_backward: grad . b^T and a^T . grad within the GEMM bound."""
+    gh, O = _gh(), _O()
+    rng = np.random.default_rng(m * 3 + k * 5 + n * 7)
+    g = rng.normal(0, 1, (m, n)).astype(np.float32)
+    a = rng.normal(0, 1, (m, k)).astype(np.float32)
+    b = rng.normal(0, 1, (k, n)).astype(np.float32)
+    ga, gb = gh.matmul_backward(to_dev(g, torch_dev), to_dev(a, torch_dev), to_dev(b, torch_dev))
+    ra, rb = O.matmul_backward(g, a, b)
+    assert np.abs(to_np(ga) - ra).max() <= gemm_tol(n, g, b)
+    assert np.abs(to_np(gb) - rb).max() <= gemm_tol(m, a, g)
+
+
+def _mha_cases():
+    rng = np.random.default_rng(20271)
+    cases = []
+    for _ in range(14):
+        h = int(rng.integers(1, 9))
+        e = h * 4 * int(rng.integers(1, 33))
+        sq = int(rng.integers(1, 40))
+        cases.append((int(rng.integers(1, 4)), sq, sq, int(rng.integers(0, 60)), e, h, bool(rng.integers(2))))
+    return cases
+
+
+@pytest.mark.parametrize("b,sq,sk,p,e,h,with_mask", _mha_cases())
+def test_mha_random(torch_dev, b, sq, sk, p, e, h, with_mask):
+    """MultiHeadAttention::forward_with_cache: output and weights within 1e-4
+    relative (fully masked rows NaN, as the reference), new keys / values
+    within the GEMM bound."""
+    gh, O = _gh(), _O()
+    rng = np.random.default_rng(b * 17 + sq * 101 + p * 7 + e)
+    bound, bb = np.sqrt(6.0 / e), 1.0 / np.sqrt(e)
+    ws = [rng.uniform(-bound, bound, (e, e)).astype(np.float32) for _ in range(4)]
+    bs = [rng.uniform(-bb, bb, e).astype(np.float32) for _ in range(4)]
+    params = [t for pair in zip(ws, bs) for t in pair]
+    query, key, value = (rng.standard_normal((b, s, e)).astype(np.float32) for s in (sq, sk, sk))
+    pk = rng.standard_normal((b, p, e)).astype(np.float32) if p else None
+    pv = rng.standard_normal((b, p, e)).astype(np.float32) if p else None
+    mask = None
+    if with_mask:
+        mask = (rng.random(int(rng.integers(1, sq * (p + sk) + 4))) > 0.3).astype(np.float32)
+        mask[0] = 1.0
+    ref = O.mha_forward_with_cache(query, key, value, *params, h, mask=mask, past_key=pk, past_value=pv)
+    dev = lambda t: None if t is None else to_dev(t, torch_dev)  # noqa: E731
+    got = gh.mha_forward_with_cache(dev(query), dev(key), dev(value), *[dev(t) for t in params], h,
+                                    mask=dev(mask), past_key=dev(pk), past_value=dev(pv))
+    out, w = to_np(got[0].contiguous()), to_np(got[1].contiguous())
+    live = ~np.isnan(ref[0])
+    assert (np.isnan(out) == ~live).all()
+    if live.any():
+        assert_rel(out[live], ref[0][live])
+    assert_rel(np.nan_to_num(w, nan=-1.0), np.nan_to_num(ref[1], nan=-1.0))
+    kn = to_np(got[2]).transpose(0, 2, 1, 3).reshape(b, sk, e)
+    assert np.abs(kn - ref[2]).max() <= gemm_tol(e, key, ws[1]) + np.abs(bs[1]).max() * 1e-6
+
+
+def _flash_cases():
+    rng = np.random.default_rng(20272)
+    cases = []
+    for _ in range(12):
+        bm = int(rng.choice([1, 7, 16, 32, 64, 100]))
+        bn = int(rng.choice([1, 5, 32, 64, 96, 128]))
+        sk = _dim(rng, 1, 400)
+        if bn == 1:
+            sk = min(sk, 300)
+        cases.append((int(rng.integers(1, 4)), _dim(rng, 1, 400), sk, int(rng.integers(1, 129)), bm, bn,
+                      bool(rng.integers(2)), float(rng.uniform(0.05, 0.5))))
+    return cases
+
+
+@pytest.mark.parametrize("bsz,sq,sk,d,bm,bn,causal,scale", _flash_cases())
+def test_flash_attention_blockwise_random(torch_dev, bsz, sq, sk, d, bm, bn, causal, scale):
+    """FlashAttention::forward's blockwise recurrence: max|err| <= 1e-4
+    max|ref|, and what the reference leaves at exactly 0 is exactly 0."""
+    gh, O = _gh(), _O()
+    rng = np.random.default_rng(bsz * 5 + sq * 11 + sk * 13 + d)
+    q, k, v = (rng.normal(0, 1, (bsz, s, d)).astype(np.float32) for s in (sq, sk, sk))
+    ref = O.flash_attention_blockwise(q, k, v, bm, bn, causal, scale)
+    got = to_np(gh.flash_attention_blockwise(to_dev(q, torch_dev), to_dev(k, torch_dev), to_dev(v, torch_dev),
+                                             block_size_m=bm, block_size_n=bn, causal=causal, scale=scale))
+    np.testing.assert_array_equal(got == 0.0, ref == 0.0)
+    assert float(np.abs(got.astype(np.float64) - ref).max()) <= 1e-4 * float(np.abs(ref).max(initial=0.0))
