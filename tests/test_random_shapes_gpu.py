@@ -16,8 +16,9 @@ oracle at the bars of the hand-picked cases:
     filled rows;
   * softmax (1e-4 relative per element), per-channel and per-tensor
     quantization (bit for bit), matmul_backward (GEMM bound),
-    MultiHeadAttention::forward_with_cache (1e-4 relative) and
-    FlashAttention::forward's blockwise recurrence (its normwise bar).
+    MultiHeadAttention::forward_with_cache (1e-4 relative),
+    FlashAttention::forward's blockwise recurrence (its normwise bar) and
+    SwiGLU::forward in fp32 and int8 (the bars of its stage tests).
 The shapes are drawn once from fixed seeds, so every run checks the same
 cases; they land on ragged tiles, odd K, split-K boundaries and tiny sizes
 that the hand-picked shapes may not."""
@@ -383,3 +384,52 @@ def test_flash_attention_blockwise_random(torch_dev, bsz, sq, sk, d, bm, bn, cau
                                              block_size_m=bm, block_size_n=bn, causal=causal, scale=scale))
     np.testing.assert_array_equal(got == 0.0, ref == 0.0)
     assert float(np.abs(got.astype(np.float64) - ref).max()) <= 1e-4 * float(np.abs(ref).max(initial=0.0))
+
+
+def _swiglu_cases():
+    rng = np.random.default_rng(20273)
+    return [(_dim(rng, 1, 700), 16 * _dim(rng, 1, 64), 16 * _dim(rng, 1, 96), bool(rng.integers(2)),
+             bool(rng.integers(2))) for _ in range(16)]
+
+
+@pytest.mark.parametrize("m,hidden,inter,int8,bias", _swiglu_cases())
+def test_swiglu_random(torch_dev, m, hidden, inter, int8, bias):
+    """SwiGLU::forward.  fp32: h = silu(gate) * up within the bound that the
+    GEMM bound of gate and up implies, y within the GEMM bound of h . Wd^T.
+    int8 (DynamicQuantization's scheme per Linear): h within 4 ulp of the
+    oracle's silu * up of its bit-exact gate and up, y bit for bit against
+    the oracle's quantize + INT8 linear of the GPU's own h."""
+    gh, O = _gh(), _O()
+    rng = np.random.default_rng(m * 19 + hidden * 7 + inter)
+    x = rng.normal(0, 1, (m, hidden)).astype(np.float32)
+    sc = np.float32(np.sqrt(6.0 / hidden)), np.float32(np.sqrt(6.0 / inter))
+    wg = (rng.uniform(-1, 1, (inter, hidden)) * sc[0]).astype(np.float32)
+    wu = (rng.uniform(-1, 1, (inter, hidden)) * sc[0]).astype(np.float32)
+    wd = (rng.uniform(-1, 1, (hidden, inter)) * sc[1]).astype(np.float32)
+    bg, bu, bd = ((rng.uniform(-0.05, 0.05, n).astype(np.float32) if bias else None) for n in (inter, inter, hidden))
+    dev = lambda a: None if a is None else to_dev(a, torch_dev)  # noqa: E731
+    if not int8:
+        y, h = (to_np(t) for t in gh.swiglu(dev(x), dev(wg), dev(bg), dev(wu), dev(bu), dev(wd), dev(bd), want_h=True))
+        gate, up = O.linear_forward(x, wg, bg), O.linear_forward(x, wu, bu)
+        h_ref = O.silu_mul(gate, up)
+        tg, tu = gemm_tol(hidden, x, wg), gemm_tol(hidden, x, wu)
+        sg = np.abs(h_ref / np.where(up == 0, 1, up))
+        bound = 1.1 * np.abs(up) * tg + (sg + 1.1 * tg) * tu + 4 * np.spacing(np.abs(h_ref))
+        assert (np.abs(h.astype(np.float64) - h_ref) <= bound).all()
+        assert np.abs(y - O.linear_forward(h, wd, bd)).max() <= gemm_tol(inter, h, wd)
+        return
+    q = {}
+    for name, w, b in (("g", wg, bg), ("u", wu, bu), ("d", wd, bd)):
+        codes, scales, _ = O.quantize_per_channel(w, True)
+        cd = to_dev(codes, torch_dev)
+        q[name] = (codes, scales, b, (cd, to_dev(scales, torch_dev), gh.qweight_rowsum(cd), dev(b)))
+    y, h = (to_np(t) for t in gh.qswiglu(dev(x), q["g"][3], q["u"][3], q["d"][3], want_h=True))
+    qx, sx, zx = O.quantize_per_tensor(x, symmetric=False)
+    lin = lambda w: O.qlinear_i8(qx, sx, np.atleast_1d(zx), False, w[0], w[1], w[2], want_acc=False)[0]  # noqa: E731
+    h_ref = O.silu_mul(lin(q["g"]), lin(q["u"]))
+    same = (h == h_ref) | (np.isnan(h) & np.isnan(h_ref))
+    err = np.abs(h.astype(np.float64) - h_ref.astype(np.float64))
+    assert (same | (err <= 4 * np.spacing(np.abs(h_ref)).astype(np.float64))).all()
+    qh, sh, zh = O.quantize_per_tensor(h, symmetric=False)
+    y_ref, _ = O.qlinear_i8(qh, sh, np.atleast_1d(zh), False, q["d"][0], q["d"][1], q["d"][2], want_acc=False)
+    np.testing.assert_array_equal(y.view(np.uint32), y_ref.view(np.uint32))
