@@ -104,8 +104,9 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_nt_skinny_kernel(SkNtPara
     float *yb = grouped ? p.gy[z] : p.y + (int64_t)z * p.stride_c;
     const float *bias = grouped ? p.gbias[z] : p.bias;
     const int64_t ldc = grouped ? p.gldc[z] : p.ldc;
-    float *part = grouped ? p.part + (int64_t)z * p.slices * p.m * p.n : p.part;
-    int *counters = grouped ? p.counters + (int64_t)z * p.ngrp * kWaves : p.counters;
+    // (split-K buffers exist only when K is split)
+    float *part = grouped && p.part ? p.part + (int64_t)z * p.slices * p.m * p.n : p.part;
+    int *counters = grouped && p.counters ? p.counters + (int64_t)z * p.ngrp * kWaves : p.counters;
 
     const int64_t k_lo = slice * p.kslice;
     const int kl = (int)min(p.kslice, p.k - k_lo);  // > 0, a multiple of 4
