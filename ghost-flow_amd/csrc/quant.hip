@@ -8,6 +8,8 @@
 // is half away from zero, `as` casts saturate with NaN -> 0, and the i32 add
 // wraps as in a release build.  All kernels are HBM-bound elementwise or
 // reduction passes: 16-byte loads, grid sized to fill the 256 CUs.
+#include <cstdlib>
+
 #include "common.hpp"
 #include "kernels.hpp"
 #include "quant_math.hpp"
@@ -170,6 +172,123 @@ __global__ __launch_bounds__(kBlock) void quant_per_tensor_kernel(const float *_
     }
 }
 
+// ---- small tensors in one launch ---------------------------------------------
+// Up to kResMaxGroups workgroups of 1024 threads, each thread holding one
+// float4 of x in registers, do both passes in one launch:
+//   1. each workgroup loads its share and folds its (min, max);
+//   2. it publishes the pair and counts its arrival with the split-K
+//      arrival protocol (common.hpp: agent-scope stores, vmcnt(0), agent-scope
+//      fetch_add on counters[0]);
+//   3. it waits until every workgroup has arrived, then folds all pairs
+//      (agent-scope loads), so every workgroup derives the same (scale, zp);
+//   4. it writes its codes from the registers.
+// counters[1] counts the workgroups done with the pairs; the last one returns
+// both counters to 0.  The wait is bounded: it only lasts while a workgroup
+// of the grid has not started, which needs other kernels holding every CU.
+// A workgroup that gives up waiting folds all of x itself, which gives the
+// same (min, max) as the pairs (exact folds; zeros of either sign give the
+// same codes), so the codes are right either way and every wave exits.
+constexpr int kResThreads = 1024;
+constexpr int kResMaxGroups = 16;
+// Wait rounds (s_sleep 2, ~128 clocks, plus one agent-scope load each)
+// before a workgroup gives up: well over 0.1 s.  GFH_QUANT_WAIT_ROUNDS
+// overrides it (0: every workgroup takes the fold-everything path; used by
+// the tests of that path).
+constexpr int kResSpinLimit = 1 << 20;
+
+__global__ __launch_bounds__(kResThreads) void quant_small_kernel(const float *__restrict__ x, int64_t n,
+                                                                 bool symmetric, float *__restrict__ partials,
+                                                                 int *__restrict__ counters, int8_t *__restrict__ q,
+                                                                 float *__restrict__ scale_out,
+                                                                 int8_t *__restrict__ zp_out, int spin_limit) {
+    const int tid = threadIdx.x;
+    const int nwg = gridDim.x;
+    const int nfull4 = (int)(n / 4);  // kResThreads <= nfull4 <= kResThreads * kResMaxGroups (host check)
+    const int i4 = blockIdx.x * kResThreads + tid;
+    const f32x4 *xv = reinterpret_cast<const f32x4 *>(x);
+    // Load from a clamped index; past the last whole float4 the elements are
+    // replaced afterwards (NaN is neutral for the NaN-ignoring folds).
+    f32x4 v = xv[i4 < nfull4 ? i4 : nfull4 - 1];
+    if (i4 >= nfull4) {
+        float e[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) e[c] = (int64_t)i4 * 4 + c < n ? x[(int64_t)i4 * 4 + c] : NAN;
+        v = f32x4{e[0], e[1], e[2], e[3]};
+    }
+    float mn = fminf(fminf(v[0], v[1]), fminf(v[2], v[3]));
+    float mx = fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3]));
+    qmath::block_minmax<kResThreads>(mn, mx);
+
+    __shared__ int s_gave_up;
+    if (tid == 0) {
+        __hip_atomic_store(partials + 2 * blockIdx.x, mn, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(partials + 2 * blockIdx.x + 1, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the pair is at the coherence point
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        // Its return value is waited for: this arrival is counted before the
+        // wait, and before counters[1] below.
+        int arrived = __hip_atomic_fetch_add(counters, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+        for (int spin = 0; arrived < nwg && spin < spin_limit; ++spin) {
+            __builtin_amdgcn_s_sleep(2);
+            arrived = __hip_atomic_load(counters, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        s_gave_up = arrived < nwg;
+    }
+    __syncthreads();
+    float gmn = INFINITY, gmx = -INFINITY;
+    if (!s_gave_up) {
+        if (tid < nwg) {
+            gmn = __hip_atomic_load(partials + 2 * tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            gmx = __hip_atomic_load(partials + 2 * tid + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    } else {
+        for (int64_t i = tid; i < n; i += kResThreads) {
+            gmn = fminf(gmn, x[i]);
+            gmx = fmaxf(gmx, x[i]);
+        }
+    }
+    qmath::block_minmax<kResThreads>(gmn, gmx);  // its barrier: every load above has been used
+    if (tid == 0) {
+        const int done = __hip_atomic_fetch_add(counters + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (done == nwg - 1) {  // every workgroup has left the wait
+            __hip_atomic_store(counters, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(counters + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    float scale;
+    int8_t zp;
+    quant_params(gmn, gmx, symmetric, scale, zp);
+    if (blockIdx.x == 0 && tid == 0) {
+        *scale_out = scale;
+        *zp_out = zp;
+    }
+    if (i4 < nfull4) {
+        reinterpret_cast<uint32_t *>(q)[i4] = quant4(v, scale, zp);
+    } else {
+        const float e[4] = {v[0], v[1], v[2], v[3]};
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if ((int64_t)i4 * 4 + c < n) q[(int64_t)i4 * 4 + c] = quant_one(e[c], scale, zp);
+    }
+}
+
+// Workgroups of the one-launch form for n elements, or 0 when n is outside
+// its range.  Measured (µs, one launch / two): 16384 elements 5.7 / 6.5-7.0;
+// at 262144 (64 workgroups) 7.9 / 7.0, and larger grids lose more.
+int small_groups(int64_t n) {
+    if (n < 4 * (int64_t)kResThreads) return 0;
+    const int64_t g = ((n + 3) / 4 + kResThreads - 1) / kResThreads;
+    return g <= kResMaxGroups ? (int)g : 0;
+}
+
+int spin_limit() {
+    const char *e = getenv("GFH_QUANT_WAIT_ROUNDS");
+    if (e == nullptr || *e == '\0') return kResSpinLimit;
+    const long v = strtol(e, nullptr, 10);
+    return v < 0 ? 0 : (v > kResSpinLimit ? kResSpinLimit : (int)v);
+}
+
 // ---- dequantize -------------------------------------------------------------------
 // out = ((float)q - (float)zp) * scale, per tensor (nscales == 1) or per row.
 template <bool VEC>
@@ -242,6 +361,15 @@ int launch_quantize_per_tensor(const float *x, int64_t n, bool symmetric, int8_t
     const int nb = per_tensor_blocks(n);
     float2 *partials = static_cast<float2 *>(ws);
     const bool vec = aligned16(x) && ((reinterpret_cast<uintptr_t>(q) & 3u) == 0);
+    const int groups = vec ? small_groups(n) : 0;
+    if (groups) {
+        // One launch; its grid never exceeds nb, so the workspace holds its pairs.
+        int *counters = nullptr;
+        GFH_TRY(stream_counters(s, 2, &counters));
+        hipLaunchKernelGGL(quant_small_kernel, dim3(groups), dim3(kResThreads), 0, s, x, n, symmetric,
+                           reinterpret_cast<float *>(partials), counters, q, scale, zp, spin_limit());
+        return check_launch("quantize_per_tensor/one_launch");
+    }
     if (vec) {
         hipLaunchKernelGGL(minmax_partial_kernel<true>, dim3(nb), dim3(kBlock), 0, s, x, n, partials);
         GFH_TRY(check_launch("quantize_per_tensor/minmax"));

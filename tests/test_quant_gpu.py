@@ -93,6 +93,81 @@ def test_per_tensor_random(torch_dev, n, symmetric):
     assert int(to_np(z)[0]) == int(rz)
 
 
+# Sizes around the one-launch form for small tensors (up to 16 workgroups of
+# 1024 threads, one float4 each, so 4096 <= n <= 65536) and its edges: a
+# single workgroup, a last workgroup with a ragged share or a partial
+# float4, and the sizes just outside its range (two launches).
+ONE_LAUNCH_SIZES = [4095, 4096, 4097, 16384, 40000 + 3, 65533, 65536, 65537]
+
+
+@pytest.mark.parametrize("n", ONE_LAUNCH_SIZES)
+def test_per_tensor_one_launch_sizes(torch_dev, n):
+    gh, O = _gh(), _O()
+    x = gh.normal((n,), seed=5, tensor_id=0)
+    for symmetric in (False, True):
+        q, s, z = gh.quantize_per_tensor(to_dev(x, torch_dev), symmetric)
+        rq, rs, rz = O.quantize_per_tensor(x, symmetric)
+        np.testing.assert_array_equal(to_np(q), rq)
+        assert _same_f32(to_np(s), np.atleast_1d(rs))
+        assert int(to_np(z)[0]) == int(rz)
+
+
+def test_per_tensor_consecutive_calls(torch_dev):
+    """Calls in a row on one stream with different sizes and data: each
+    launch must see only its own workgroups' (min, max) pairs, so the
+    arrival counters are back at zero after every call."""
+    gh, O = _gh(), _O()
+    for i, n in enumerate([65536, 4097, (1 << 20) + 1, 16384, 4096, 65533, 40003]):
+        x = gh.normal((n,), 0.0, 1.0 + i, seed=40 + i, tensor_id=0)
+        q, s, z = gh.quantize_per_tensor(to_dev(x, torch_dev), False)
+        rq, rs, rz = O.quantize_per_tensor(x, False)
+        np.testing.assert_array_equal(to_np(q), rq, err_msg=str(n))
+        assert _same_f32(to_np(s), np.atleast_1d(rs)), n
+        assert int(to_np(z)[0]) == int(rz), n
+
+
+@pytest.mark.parametrize("n", [4097, 16384, 65533])
+def test_per_tensor_workgroups_that_stop_waiting(torch_dev, n, monkeypatch):
+    """With a wait limit of 0 every workgroup of the one-launch form gives up
+    waiting for the others and folds all of x itself: the same codes."""
+    gh, O = _gh(), _O()
+    monkeypatch.setenv("GFH_QUANT_WAIT_ROUNDS", "0")
+    x = gh.normal((n,), seed=9, tensor_id=0)
+    x[n // 3] = 40.0
+    x[-1] = -35.0
+    for symmetric in (False, True):
+        q, s, z = gh.quantize_per_tensor(to_dev(x, torch_dev), symmetric)
+        rq, rs, rz = O.quantize_per_tensor(x, symmetric)
+        np.testing.assert_array_equal(to_np(q), rq)
+        assert _same_f32(to_np(s), np.atleast_1d(rs))
+        assert int(to_np(z)[0]) == int(rz)
+    monkeypatch.delenv("GFH_QUANT_WAIT_ROUNDS")
+    q, s, z = gh.quantize_per_tensor(to_dev(x, torch_dev), False)
+    rq, rs, rz = O.quantize_per_tensor(x, False)
+    np.testing.assert_array_equal(to_np(q), rq)
+
+
+def test_special_values_one_launch(torch_dev):
+    """The special-value patterns at sizes the one-launch form serves, with
+    the extreme values in different workgroups and in the ragged tail."""
+    gh, O = _gh(), _O()
+    n = 65533
+    base = gh.normal((n,), seed=12, tensor_id=0)
+    cases = {"zeros": np.zeros(n, np.float32), "nan_only": np.full(n, np.nan, np.float32)}
+    x = base.copy(); x[::797] = np.nan; cases["nans"] = x
+    x = base.copy(); x[12347] = np.inf; cases["inf"] = x
+    x = base.copy(); x[-1] = -np.inf; cases["neg_inf_in_tail"] = x
+    x = base.copy(); x[-2] = 1e30; x[5] = -1e30; cases["huge"] = x
+    cases["constant"] = np.full(n, -3.0, np.float32)
+    for name, x in cases.items():
+        for sym in (True, False):
+            q, s, z = gh.quantize_per_tensor(to_dev(x, torch_dev), sym)
+            rq, rs, rz = O.quantize_per_tensor(x, sym)
+            np.testing.assert_array_equal(to_np(q), rq, err_msg=f"{name} sym={sym}")
+            assert _same_f32(to_np(s), np.atleast_1d(rs)), (name, sym)
+            assert int(to_np(z)[0]) == int(rz), (name, sym)
+
+
 def test_per_tensor_unaligned_view(torch_dev):
     """An offset (non 16-byte aligned) input takes the scalar path."""
     gh, O = _gh(), _O()
