@@ -23,9 +23,15 @@
 //    the weight is), x made every workgroup move m / 16 times the weight
 //    bytes again: a read-only probe of the weight stream at [4096, 4096]
 //    took 12.8 us alone and 18.2 us with the x reads of m = 16;
-//  * the weight chunks go to registers two chunks ahead of the MFMAs (three
-//    register sets), so 8 KB per wave stay in flight while it computes (at
-//    [4096, 4096], m = 8-64: three or four chunks ahead were 1-2 us slower);
+//  * the weight chunks go through an LDS ring of their own, two chunks ahead
+//    of the MFMAs: each wave fills its 16 rows with global_load_lds_dwordx4,
+//    4 rows x 256 bytes (whole 128-byte lines) per instruction, swizzled as
+//    x is, and reads its MFMA fragments back with ds_read_b128.  Loaded
+//    straight into the fragments' registers, one instruction covered 16
+//    rows x 64 bytes (half lines); at [4096, 4096] the ring took 18.5 / 18.6
+//    / 21.8 / 30.6 us at m = 8 / 16 / 32 / 64 against 19.2 / 19.2 / 22.7 /
+//    34.3 us, the fp32 SwiGLU at m = 16 126.9 against 130.2 us, and three
+//    chunks ahead were slower than two (18.8 against 18.5 us at m = 8);
 //  * with fewer than ~512 workgroups K is also split over workgroups: each
 //    wave publishes its partial block with agent-scope stores and counts
 //    its arrival on its 16-column block, and the last one adds the slices
@@ -83,14 +89,17 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // MB: 16-row blocks of x (m <= 16 MB); D: chunks in flight ahead of the
-// MFMAs (D + 1 ring stages and register sets).
+// MFMAs (D + 1 stages of each ring).  LDS: 12 KB x MB + 48 KB, so two
+// workgroups per CU up to 32 rows and one above.
 template <int MB, int D>
-__global__ __launch_bounds__(64 * kWaves, 2) void gemm_nt_skinny_kernel(SkNtParams p) {
+__global__ __launch_bounds__(64 * kWaves, MB <= 2 ? 2 : 1) void gemm_nt_skinny_kernel(SkNtParams p) {
     constexpr int kXRows = 16 * MB;
     constexpr int kStageBytes = kXRows * kRowBytes;
+    constexpr int kWStageBytes = kGroupCols * kRowBytes;
     constexpr int kStages = D + 1;
     constexpr int kOps = MB + 4;  // vector memory instructions per chunk and wave
-    __shared__ __attribute__((aligned(1024))) char xs[kStages * kStageBytes];
+    __shared__ __attribute__((aligned(1024))) char xs[kStages * (kStageBytes + kWStageBytes)];
+    char *const wsm = xs + kStages * kStageBytes;  // the weight ring
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t grp = blockIdx.x % p.ngrp, slice = blockIdx.x / p.ngrp;
@@ -131,13 +140,25 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_nt_skinny_kernel(SkNtPara
             __builtin_amdgcn_global_load_lds((glb_ptr)(xsrc[j] + min(i * kKC + xcol[j], kl - 4)),
                                              (lds_ptr)(stage + 4 * (wave * MB + j) * kRowBytes), 16, 0, 0);
     };
-    // W: rows past n read row n - 1 (never stored).
-    const float *wsrc = wb + min<int64_t>(n0 + (lane & 15), p.n - 1) * p.ldb + k_lo;
-    const int kq = 4 * (lane >> 4);
-    auto load_w = [&](int i, f32x4(&R)[4]) __attribute__((always_inline)) {
+    // W: instruction j of wave w fills its rows 4 j .. 4 j + 3 of the stage;
+    // lane l fills slot l % 16 of row 4 j + l / 16 from logical chunk
+    // (l % 16) ^ row, the swizzle of the x ring.  Rows past n read row n - 1
+    // (never stored); elements past the slice read its last four (masked in
+    // the tail).
+    const float *wrow[4];
+    int wcol[4];
 #pragma unroll
-        for (int s = 0; s < 4; ++s)
-            R[s] = *reinterpret_cast<const f32x4 *>(wsrc + min(i * kKC + 16 * s + kq, kl - 4));
+    for (int j = 0; j < 4; ++j) {
+        const int r = 4 * j + (lane >> 4);
+        wrow[j] = wb + min<int64_t>(n0 + r, p.n - 1) * p.ldb + k_lo;
+        wcol[j] = 4 * ((lane & 15) ^ r);
+    }
+    auto issue_w = [&](int i, int slot) __attribute__((always_inline)) {
+        char *stage = wsm + slot * kWStageBytes + wave * 16 * kRowBytes;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            __builtin_amdgcn_global_load_lds((glb_ptr)(wrow[j] + min(i * kKC + wcol[j], kl - 4)),
+                                             (lds_ptr)(stage + 4 * j * kRowBytes), 16, 0, 0);
     };
 
     f32x4 acc[MB];
@@ -145,10 +166,14 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_nt_skinny_kernel(SkNtPara
     for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
     // Fragment of x block mb, step s: row 16 mb + l % 16, logical chunk
     // 4 s + l / 16 (block rows start at multiples of 16, so the swizzle is
-    // the lane's own l % 16).
+    // the lane's own l % 16); the weight fragment is the same slot of row
+    // l % 16 of the wave's rows in the weight stage.
     const int xrd = (lane & 15) * kRowBytes;
-    auto compute = [&](int i, f32x4(&R)[4], auto tail) __attribute__((always_inline)) {
-        const char *stage = xs + (i % kStages) * kStageBytes;
+    const int lane_sw = lane & 15;
+    const int kq = 4 * (lane >> 4);  // the lane's k offset within a step
+    auto compute = [&](int u, auto tail, int i) __attribute__((always_inline)) {
+        const char *stage = xs + u * kStageBytes;
+        const char *wstage = wsm + u * kWStageBytes + wave * 16 * kRowBytes + xrd;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             f32x4 xv[MB];
@@ -156,7 +181,7 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_nt_skinny_kernel(SkNtPara
             for (int mb = 0; mb < MB; ++mb)
                 xv[mb] = *reinterpret_cast<const f32x4 *>(stage + mb * 16 * kRowBytes + xrd +
                                                           (((4 * s + (lane >> 4)) ^ (lane & 15)) << 4));
-            f32x4 wv = R[s];
+            f32x4 wv = *reinterpret_cast<const f32x4 *>(wstage + (((4 * s + (lane >> 4)) ^ lane_sw) << 4));
             if constexpr (decltype(tail)::value) {
                 // k % 4 == 0: a lane's 4 elements are all inside the slice or
                 // all past it; past it both operands are zero (a zero x alone
@@ -177,67 +202,46 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_nt_skinny_kernel(SkNtPara
         }
     };
 
-    // Chunk i: wait for its x and W (the next D - 1 chunks' loads stay in
-    // flight), barrier (its x is visible, and every wave is done with chunk
-    // i - 1, whose ring stage and register set now refill), issue chunk
-    // i + D, compute chunk i.  The issue is unconditional -- past the last
-    // chunk it repeats the last one (an L2 hit) into the free stage and set
-    // -- so every chunk issues the same kOps instructions per wave, in the
-    // same order, and the register sets rotate without copies.  The
-    // compiler drops the register loads of repeats that no MFMA reads, so
-    // the last D - 1 chunks count only what is left behind their x: their
-    // own W, the x of the D - 1 chunks issued after them and the W of those
-    // that exist (a load the compiler keeps only makes the wait longer).
+    // Chunk i (ring stage u = i % kStages): wait for its x and W (the next
+    // D - 1 chunks' loads stay in flight), barrier (its x is visible, and
+    // every wave is done with chunk i - 1, whose stages now refill), issue
+    // chunk i + D, compute chunk i.  The issue is unconditional -- past the
+    // last chunk it repeats the last one (an L2 hit) into the free stages --
+    // so every chunk issues the same kOps instructions per wave, in the same
+    // order, and the wait count is a constant.
     const bool ragged = (kl % kKC) != 0;
-    auto wait_chunk = [&](int i) __attribute__((always_inline)) {
-        static_assert(D >= 1 && D <= 4, "the tail waits below cover D <= 4");
-        const int rem = nch - 1 - i;  // chunks after chunk i
-        constexpr int kBase = 4 + (D - 1) * MB;
-        if (rem >= D - 1)
-            wait_vmcnt<(D - 1) * kOps>();
-        else if (rem == 0)
-            wait_vmcnt<kBase>();
-        else if (rem == 1)
-            wait_vmcnt<kBase + 4>();
-        else
-            wait_vmcnt<kBase + 8>();
-    };
-    auto step = [&](int i, f32x4(&Rc)[4], f32x4(&Rn)[4]) __attribute__((always_inline)) {
-        wait_chunk(i);
+    auto step = [&](int i, int u) __attribute__((always_inline)) {
+        static_assert(D >= 1 && (D - 1) * kOps < 64, "the wait count must fit vmcnt");
+        wait_vmcnt<(D - 1) * kOps>();
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         const int nx = min(i + D, nch - 1);
-        issue_x(nx, (i + D) % kStages);
-        // x before W: the instructions after a chunk's x then always include
-        // its own W and the next chunks' x.
+        issue_x(nx, (u + D) % kStages);
         __builtin_amdgcn_sched_barrier(0);
-        load_w(nx, Rn);
+        issue_w(nx, (u + D) % kStages);
         __builtin_amdgcn_sched_barrier(0);
         if (ragged && i + 1 == nch)
-            compute(i, Rc, std::true_type{});
+            compute(u, std::true_type{}, i);
         else
-            compute(i, Rc, std::false_type{});
+            compute(u, std::false_type{}, i);
     };
-    f32x4 R[kStages][4];
 #pragma unroll
     for (int c = 0; c < D; ++c) {
         issue_x(min(c, nch - 1), c);
         __builtin_amdgcn_sched_barrier(0);
-        load_w(min(c, nch - 1), R[c]);
+        issue_w(min(c, nch - 1), c);
         __builtin_amdgcn_sched_barrier(0);
     }
-    // Whole rounds of kStages chunks in a loop without exits (an exit
-    // between steps gives the compiler a path on which a register set is
-    // still being loaded at the loop head, and it then waits for every load
-    // there), then the chunks left, in the same rotation.
+    // Whole rounds of kStages chunks (stage indices known at compile time),
+    // then the chunks left.
     int i = 0;
     for (; i + kStages <= nch; i += kStages) {
 #pragma unroll
-        for (int u = 0; u < kStages; ++u) step(i + u, R[u], R[(u + D) % kStages]);
+        for (int u = 0; u < kStages; ++u) step(i + u, u);
     }
 #pragma unroll
     for (int u = 0; u + 1 < kStages; ++u)
-        if (i + u < nch) step(i + u, R[u], R[(u + D) % kStages]);
+        if (i + u < nch) step(i + u, u);
     wait_vmcnt<0>();  // no load may still be writing the ring
     if (n0 >= p.n) return;  // a wave past the last column (after every barrier)
 
@@ -339,19 +343,21 @@ __global__ __launch_bounds__(64 * kWaves, 2) void gemm_nt_skinny_kernel(SkNtPara
 // 41.7 us (m = 8 / 32 / 64) with 16.  Of the 18.7 us at m = 16, about 2.7
 // us are the split-K tail (partial stores, arrival count, the last
 // arriver's reads: three memory round trips) and 1 us the x staging.
-// Above 48 rows (four row blocks, a 16 KB x stage per chunk) half as many
-// workgroups: m = 64 took 29.1 / 33.8 us at 4 slices against 32.0 / 34.4 us
-// at 8 in two sweeps, while m <= 32 prefers 8.
+// Above 32 rows (three or four row blocks: one workgroup per CU, its LDS
+// rings 84-96 KB) half as many workgroups, one round of them: m = 40 / 48 /
+// 64 took 25.7 / 25.6 / 30.6 us against 28.5 / 28.9 / 34.3 us with the
+// weights in registers and 512 workgroups for m <= 48, while m <= 32
+// prefers 8 slices.
 constexpr int64_t kTargetWgs = 512;
 constexpr int kDepth = 2;
-// Up to 48 rows the slice count is rounded down: at N = 11008 (172 groups),
+// Up to 32 rows the slice count is rounded down: at N = 11008 (172 groups),
 // K = 4096, 2 slices took 45.9 / 46.8 / 56.8 us at m = 8 / 16 / 32 against
 // 49.9 / 50.3 / 57.4 with 3 (uneven: 1536, 1536, 1024 rows) and 57.6 /
 // 57.8 / 68.3 with none.
 int64_t choose_kslice(int64_t ngrp, int64_t k, int64_t batch, int64_t m) {
     const int64_t kc = ((k + kKC - 1) / kKC) * kKC;
     if (batch > 1) return kc;
-    int64_t s = m > 48 ? (kTargetWgs / 2 + ngrp - 1) / ngrp : kTargetWgs / ngrp;
+    int64_t s = m > 32 ? (kTargetWgs / 2 + ngrp - 1) / ngrp : kTargetWgs / ngrp;
     s = std::max<int64_t>(1, std::min<int64_t>(s, k / (4 * kKC)));
     const int64_t ks = (k + s - 1) / s;
     return (ks + kKC - 1) / kKC * kKC;
