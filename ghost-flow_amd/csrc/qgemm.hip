@@ -986,8 +986,12 @@ int launch(const QParams &p, hipStream_t s, int *npart = nullptr) {
 //    v_mfma_i32_16x16x64_i8;
 //  * x: global_load_lds_dwordx4 fills 4 rows x 256 bytes per instruction,
 //    16-byte slots swizzled by row (conflict-free fragment reads); the
-//    weight chunks (both matrices in DUAL mode) go to registers two chunks
-//    ahead of the MFMAs in three rotating register sets;
+//    weight chunks (both matrices in DUAL mode) go through a ring of their
+//    own the same way, each wave filling its 16 rows, two chunks ahead of
+//    the MFMAs.  Loaded straight into the fragment registers, one
+//    instruction covered 16 rows x 64 bytes (half lines): N = 11008, K =
+//    4096, M = 16 / 32 / 64 took 14.6 / 16.5 / 20.9 us against 12.5 / 14.3
+//    / 18.3 us with the ring (same box);
 //  * with fewer than ~512 workgroups K is also split over workgroups; each
 //    wave publishes its exact int32 partials, counts its arrival on its
 //    16-column block, and the last one adds the slices (exact in any order)
@@ -1002,7 +1006,7 @@ typedef __attribute__((address_space(1))) void *glb_ptr;
 constexpr int kWaves = 4;
 constexpr int kGroupCols = 16 * kWaves;  // output columns per workgroup
 constexpr int kChunk = 256;              // k bytes per chunk
-constexpr int kStages = 3;               // x ring (two chunks in flight)
+constexpr int kStages = 3;               // x and weight rings (two chunks in flight)
 
 struct Params {
     QParams q;
@@ -1018,11 +1022,13 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 template <int MB, bool DUAL>
-__global__ __launch_bounds__(64 * kWaves, 2) void qlinear_skinny_lds_kernel(Params sp) {
+__global__ __launch_bounds__(64 * kWaves, (MB <= 2 && !DUAL) ? 2 : 1) void qlinear_skinny_lds_kernel(Params sp) {
     constexpr int D = DUAL ? 2 : 1;
     constexpr int kStageBytes = 16 * MB * kChunk;
+    constexpr int kWStageBytes = D * kGroupCols * kChunk;  // [D][wave][16 rows][kChunk]
     constexpr int kOps = MB + 4 * D;  // vector memory instructions per chunk and wave
-    __shared__ __attribute__((aligned(1024))) int8_t xs[kStages * kStageBytes];
+    __shared__ __attribute__((aligned(1024))) int8_t xs[kStages * (kStageBytes + kWStageBytes)];
+    int8_t *const wsm = xs + kStages * kStageBytes;  // the weight ring
     const QParams &p = sp.q;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1051,18 +1057,33 @@ __global__ __launch_bounds__(64 * kWaves, 2) void qlinear_skinny_lds_kernel(Para
             __builtin_amdgcn_global_load_lds((glb_ptr)(xsrc[j] + min(i * kChunk + xcol[j], kl - 16)),
                                              (lds_ptr)(stage + 4 * (wave * MB + j) * kChunk), 16, 0, 0);
     };
-    // W: rows past n read row n - 1 (never stored).
-    const int64_t wrow = min<int64_t>(n0 + (lane & 15), p.n - 1) * p.k + k_lo;
-    const int8_t *wsrc[D];
-    wsrc[0] = p.qw + wrow;
-    if (DUAL) wsrc[D - 1] = p.qw2 + wrow;
-    const int kq = 16 * (lane >> 4);
-    auto load_w = [&](int i, i32x4(&R)[D][4]) __attribute__((always_inline)) {
+    // W goes through an LDS ring of its own (4 rows x 256 bytes, whole
+    // 128-byte lines, per instruction; loaded straight into the fragment
+    // registers one instruction covered 16 rows x 64 bytes): instruction j
+    // of wave w fills its rows 4 j .. 4 j + 3 of weight d's stage; lane l
+    // fills slot l % 16 of row 4 j + l / 16 from logical chunk (l % 16) ^
+    // row, the swizzle of x.  Rows past n read row n - 1 (never stored);
+    // bytes past the slice read its last 16 (masked in the tail).
+    const int8_t *wsrc[D][4];
+    int wcol[4];
 #pragma unroll
-        for (int d = 0; d < D; ++d)
+    for (int j = 0; j < 4; ++j) {
+        const int r = 4 * j + (lane >> 4);
+        const int64_t wrow = min<int64_t>(n0 + r, p.n - 1) * p.k + k_lo;
+        wsrc[0][j] = p.qw + wrow;
+        if (DUAL) wsrc[D - 1][j] = p.qw2 + wrow;
+        wcol[j] = 16 * ((lane & 15) ^ r);
+    }
+    const int kq = 16 * (lane >> 4);  // the lane's k offset within a step
+    auto issue_w = [&](int i, int slot) __attribute__((always_inline)) {
 #pragma unroll
-            for (int s = 0; s < 4; ++s)
-                R[d][s] = *reinterpret_cast<const i32x4 *>(wsrc[d] + min(i * kChunk + 64 * s + kq, kl - 16));
+        for (int d = 0; d < D; ++d) {
+            int8_t *stage = wsm + slot * kWStageBytes + (d * kWaves + wave) * 16 * kChunk;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                __builtin_amdgcn_global_load_lds((glb_ptr)(wsrc[d][j] + min(i * kChunk + wcol[j], kl - 16)),
+                                                 (lds_ptr)(stage + 4 * j * kChunk), 16, 0, 0);
+        }
     };
 
     i32x4 acc[D][MB];
@@ -1072,18 +1093,22 @@ __global__ __launch_bounds__(64 * kWaves, 2) void qlinear_skinny_lds_kernel(Para
         for (int mb = 0; mb < MB; ++mb) acc[d][mb] = i32x4{0, 0, 0, 0};
     // Fragment of x block mb, step s: row 16 mb + l % 16, logical chunk
     // 4 s + l / 16.
+    // The weight fragment is the same slot of row l % 16 of the wave's rows
+    // in weight d's stage.
     const int xrd = (lane & 15) * kChunk;
-    auto compute = [&](int i, i32x4(&R)[D][4], auto tail) __attribute__((always_inline)) {
-        const int8_t *stage = xs + (i % kStages) * kStageBytes;
+    auto compute = [&](int u, auto tail, int i) __attribute__((always_inline)) {
+        const int8_t *stage = xs + u * kStageBytes;
+        const int8_t *wstage = wsm + u * kWStageBytes + wave * 16 * kChunk + xrd;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             i32x4 xv[MB], wv[D];
+            const int sw = ((4 * s + (lane >> 4)) ^ (lane & 15)) << 4;
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb)
-                xv[mb] = *reinterpret_cast<const i32x4 *>(stage + mb * 16 * kChunk + xrd +
-                                                          (((4 * s + (lane >> 4)) ^ (lane & 15)) << 4));
+                xv[mb] = *reinterpret_cast<const i32x4 *>(stage + mb * 16 * kChunk + xrd + sw);
 #pragma unroll
-            for (int d = 0; d < D; ++d) wv[d] = R[d][s];
+            for (int d = 0; d < D; ++d)
+                wv[d] = *reinterpret_cast<const i32x4 *>(wstage + d * kWaves * 16 * kChunk + sw);
             if constexpr (decltype(tail)::value) {
                 // K % 16 == 0: a lane's 16 bytes are all inside the slice or
                 // all past it; past it both operands are zero.
@@ -1104,50 +1129,44 @@ __global__ __launch_bounds__(64 * kWaves, 2) void qlinear_skinny_lds_kernel(Para
         }
     };
 
-    // Chunk i: wait for its x and W (the next chunk's loads stay in flight),
-    // barrier (its x is visible, and every wave is done with chunk i - 1,
-    // whose ring stage and register set now refill), issue chunk i + 2
-    // (unconditionally: past the last chunk it repeats the last one into the
-    // free stage and set, so the counts stay constant and the register sets
-    // rotate without copies), compute chunk i.  The compiler drops the
-    // register loads of repeats that no MFMA reads, so the last chunk counts
-    // only its own W and the repeated x behind its x.
+    // Chunk i (ring stage u = i % kStages): wait for its x and W (the next
+    // chunk's loads stay in flight), barrier (its x is visible, and every
+    // wave is done with chunk i - 1, whose stages now refill), issue chunk
+    // i + 2 (unconditionally: past the last chunk it repeats the last one
+    // into the free stages, so the wait count is one constant), compute
+    // chunk i.
     const bool ragged = (kl % kChunk) != 0;
-    auto step = [&](int i, i32x4(&Rc)[D][4], i32x4(&Rn)[D][4]) __attribute__((always_inline)) {
-        if (i + 1 < nch)
-            wait_vmcnt<kOps>();
-        else
-            wait_vmcnt<4 * D + MB>();
+    auto step = [&](int i, int u) __attribute__((always_inline)) {
+        wait_vmcnt<kOps>();
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);
         const int nx = min(i + 2, nch - 1);
-        issue_x(nx, (i + 2) % kStages);
+        issue_x(nx, (u + 2) % kStages);
         __builtin_amdgcn_sched_barrier(0);  // x before W
-        load_w(nx, Rn);
+        issue_w(nx, (u + 2) % kStages);
         __builtin_amdgcn_sched_barrier(0);
         if (ragged && i + 1 == nch)
-            compute(i, Rc, std::true_type{});
+            compute(u, std::true_type{}, i);
         else
-            compute(i, Rc, std::false_type{});
+            compute(u, std::false_type{}, i);
     };
-    i32x4 R[kStages][D][4];
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
         issue_x(min(c, nch - 1), c);
         __builtin_amdgcn_sched_barrier(0);
-        load_w(min(c, nch - 1), R[c]);
+        issue_w(min(c, nch - 1), c);
         __builtin_amdgcn_sched_barrier(0);
     }
-    // Whole rounds of three chunks in a loop without exits, then the one or
-    // two left, in the same rotation.
+    // Whole rounds of three chunks (stage indices known at compile time),
+    // then the one or two left.
     int i = 0;
     for (; i + kStages <= nch; i += kStages) {
 #pragma unroll
-        for (int u = 0; u < kStages; ++u) step(i + u, R[u], R[(u + 2) % kStages]);
+        for (int u = 0; u < kStages; ++u) step(i + u, u);
     }
 #pragma unroll
     for (int u = 0; u + 1 < kStages; ++u)
-        if (i + u < nch) step(i + u, R[u], R[(u + 2) % kStages]);
+        if (i + u < nch) step(i + u, u);
     wait_vmcnt<0>();          // no load may still be writing the ring
     if (n0 >= p.n) return;  // a wave past the last column (after every barrier)
 
@@ -1324,7 +1343,7 @@ int launch(const QParams &p, hipStream_t s, int *npart = nullptr) {
         hipLaunchKernelGGL((qlinear_skinny_lds_kernel<1, DUAL>), grid, block, 0, s, sp);
     else if (p.m <= 32)
         hipLaunchKernelGGL((qlinear_skinny_lds_kernel<2, DUAL>), grid, block, 0, s, sp);
-    else if constexpr (!DUAL) {  // (two weight streams at 3-4 row blocks would spill)
+    else if constexpr (!DUAL) {  // (the two-weight form serves up to 32 rows)
         if (p.m <= 48)
             hipLaunchKernelGGL((qlinear_skinny_lds_kernel<3, DUAL>), grid, block, 0, s, sp);
         else
