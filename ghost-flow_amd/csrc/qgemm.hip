@@ -1343,14 +1343,10 @@ int launch(const QParams &p, hipStream_t s, int *npart = nullptr) {
         hipLaunchKernelGGL((qlinear_skinny_lds_kernel<1, DUAL>), grid, block, 0, s, sp);
     else if (p.m <= 32)
         hipLaunchKernelGGL((qlinear_skinny_lds_kernel<2, DUAL>), grid, block, 0, s, sp);
-    else if constexpr (!DUAL) {  // (the two-weight form serves up to 32 rows)
-        if (p.m <= 48)
-            hipLaunchKernelGGL((qlinear_skinny_lds_kernel<3, DUAL>), grid, block, 0, s, sp);
-        else
-            hipLaunchKernelGGL((qlinear_skinny_lds_kernel<4, DUAL>), grid, block, 0, s, sp);
-    } else {
-        return set_error(GFH_INVALID_SHAPE, "qlinear_swiglu_i8: shared-x skinny kernel serves M <= 32");
-    }
+    else if (p.m <= 48)
+        hipLaunchKernelGGL((qlinear_skinny_lds_kernel<3, DUAL>), grid, block, 0, s, sp);
+    else
+        hipLaunchKernelGGL((qlinear_skinny_lds_kernel<4, DUAL>), grid, block, 0, s, sp);
     return check_launch(DUAL ? "qlinear_swiglu_i8 (skinny, shared x)" : "qlinear_i8 (skinny, shared x)");
 }
 
@@ -1362,12 +1358,12 @@ int launch(const QParams &p, hipStream_t s, int *npart = nullptr) {
 // K = 4096: M = 8 14.2 / 14.1, 16 16.3 / 14.0, 32 22.9 / 15.5, gate/up M =
 // 16 25.8 / 22.5, 32 33.2 / 24.9; N = 4096, K = 11008: M = 16 19.6 / 16.9,
 // 32 28.7 / 19.7; N = 4096, K = 4096, M = 16 11.2 / 9.2.  Up to 4 rows x is
-// cheap to re-read; the two-weight (gate / up) form of the shared-x kernel
-// would spill registers above 32 rows.
+// cheap to re-read.
 bool use_skinny_lds(int64_t m, int64_t n, int64_t k, bool dual) {
     (void)n;
     (void)k;
-    return m > 4 && !(dual && m > 32);
+    (void)dual;
+    return m > 4;
 }
 
 }  // namespace

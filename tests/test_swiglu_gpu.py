@@ -122,7 +122,7 @@ def _int8_layer(rng, hidden, inter, bias):
 # above 512: 256 x (128 + 128) tiles; hidden = 80 (not a multiple of 64)
 # takes the unfused path.
 @pytest.mark.parametrize("m,hidden,inter", [(1, 64, 96), (3, 1040, 208), (4, 4096, 11008), (7, 128, 352),
-                                            (5, 4096, 256), (16, 4096, 11008),
+                                            (5, 4096, 256), (16, 4096, 11008), (40, 4096, 1024), (56, 2048, 768),
                                             (64, 256, 512), (70, 80, 208), (100, 256, 208), (200, 192, 320),
                                             (300, 256, 512), (600, 320, 256), (1024, 512, 768)])
 @pytest.mark.parametrize("bias", [True, False])
