@@ -123,6 +123,7 @@ def _int8_layer(rng, hidden, inter, bias):
 # takes the unfused path.
 @pytest.mark.parametrize("m,hidden,inter", [(1, 64, 96), (3, 1040, 208), (4, 4096, 11008), (7, 128, 352),
                                             (5, 4096, 256), (16, 4096, 11008), (40, 4096, 1024), (56, 2048, 768),
+                                            (7, 256, 9008), (24, 512, 8240),
                                             (64, 256, 512), (70, 80, 208), (100, 256, 208), (200, 192, 320),
                                             (300, 256, 512), (600, 320, 256), (1024, 512, 768)])
 @pytest.mark.parametrize("bias", [True, False])
