@@ -1307,8 +1307,11 @@ __global__ __launch_bounds__(64 * kWaves, (MB <= 2 && !DUAL) ? 2 : 1) void qline
 }
 
 // K bytes per workgroup: all of K with at least 128 column groups (half
-// the CUs), otherwise enough slices for about 512 workgroups, each at least
-// 4 chunks, a multiple of the chunk.  At N = 11008 (172 groups), K = 4096,
+// the CUs), otherwise enough slices for about 256 workgroups, each at least
+// 4 chunks, a multiple of the chunk.  At N = 4096 (64 groups), K = 11008,
+// M = 8 / 16 / 32 / 64: 14.1 / 14.3 / 16.1 / 20.9 us with 4 slices against
+// 15.9 / 16.3 / 19.5 / 27.6 with 8 (a 512 target) and 16.9 / 17.1 / 19.4 /
+// 25.0 with 2; K = 14336, M = 16 / 48: 16.1 / 19.9 against 17.1 / 24.4.  At N = 11008 (172 groups), K = 4096,
 // no split beat 2 / 3 / 4 slices at every M measured: M = 8 / 16 / 32 14.1 /
 // 14.0 / 15.5 us against 14.9-17.6 / 15.2-18.2 / 18.1-21.5 (the gate/up form
 // 22.4 / 22.5 / 24.9 against 25.0-27.8 / 25.7-27.7 / 29.4-33.8): the split
@@ -1316,7 +1319,7 @@ __global__ __launch_bounds__(64 * kWaves, (MB <= 2 && !DUAL) ? 2 : 1) void qline
 int64_t choose_kslice(int64_t ngrp, int64_t k) {
     const int64_t kc = (k + kChunk - 1) / kChunk * kChunk;
     if (ngrp >= 128) return kc;
-    int64_t s = (512 + ngrp - 1) / ngrp;
+    int64_t s = (256 + ngrp - 1) / ngrp;
     s = std::max<int64_t>(1, std::min<int64_t>(s, k / (4 * kChunk)));
     if (s == 1) return kc;
     const int64_t ks = (k + s - 1) / s;
