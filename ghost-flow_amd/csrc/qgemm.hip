@@ -917,9 +917,14 @@ __global__ __launch_bounds__(kThreads, QX ? 4 : 1) void qlinear_skinny_kernel(Sk
 }
 
 // K bytes per workgroup: all of K when there are at least ~512 column
-// blocks, otherwise enough slices for ~512 workgroups, each at least 1024
-// bytes (4 waves x 4 k-steps), a multiple of 64.
+// blocks, or at least 256 with K <= 4096; otherwise enough slices for ~512
+// workgroups, each at least 1024 bytes (4 waves x 4 k-steps), a multiple
+// of 64.  N = 4096, K = 4096 (256 blocks), no split / 2 slices: M = 1 6.3 /
+// 7.9 us, M = 4 7.3 / 10.7 us.  At K = 11008 and 14336 two slices stay
+// ahead at M = 1 (13.8 / 14.5 and 15.3 / 16.6 us) and in the SwiGLU, whose
+// down projection quantizes its slice of h in each workgroup.
 int64_t choose_kslice(int64_t nblk, int64_t k) {
+    if (nblk >= 256 && k <= 4096) return (k + 63) & ~(int64_t)63;
     int64_t s = (512 + nblk - 1) / nblk;
     s = std::max<int64_t>(1, std::min<int64_t>(s, k / 1024));
     int64_t ks = (k + s - 1) / s;
