@@ -1365,13 +1365,20 @@ int launch(const QParams &p, hipStream_t s, int *npart = nullptr) {
 // it once per workgroup.  Measured (us, 16-column / shared x): N = 11008,
 // K = 4096: M = 8 14.2 / 14.1, 16 16.3 / 14.0, 32 22.9 / 15.5, gate/up M =
 // 16 25.8 / 22.5, 32 33.2 / 24.9; N = 4096, K = 11008: M = 16 19.6 / 16.9,
-// 32 28.7 / 19.7; N = 4096, K = 4096, M = 16 11.2 / 9.2.  Up to 4 rows x is
-// cheap to re-read.
+// 32 28.7 / 19.7; N = 4096, K = 4096, M = 16 11.2 / 9.2.  At 2-4 rows the
+// shared-x kernel (with its weight ring) also wins, except where it would
+// split K and the 16-column kernel would not: M = 2 / 4, N = 11008, K =
+// 4096 11.8 / 12.3 against 12.5 / 13.4 us; N = 4096, K = 11008 13.5 / 14.1
+// against 14.9 / 17.4 us; but N = 4096, K = 4096 8.8 / 9.3 against 6.7 /
+// 7.3 us.  One row stays on the 16-column kernel (its in-kernel
+// quantization serves the decode SwiGLU and the dynamic linear).
 bool use_skinny_lds(int64_t m, int64_t n, int64_t k, bool dual) {
-    (void)n;
-    (void)k;
     (void)dual;
-    return m > 4;
+    if (m > 4) return true;
+    if (m < 2) return false;
+    const bool lds_splits = skinny_lds::choose_kslice((n + skinny_lds::kGroupCols - 1) / skinny_lds::kGroupCols, k) < k;
+    const bool cols16_splits = skinny::choose_kslice((n + skinny::kCols - 1) / skinny::kCols, k) < k;
+    return !(lds_splits && !cols16_splits);
 }
 
 }  // namespace
