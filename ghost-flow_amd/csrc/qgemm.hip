@@ -1370,12 +1370,12 @@ int launch(const QParams &p, hipStream_t s, int *npart = nullptr) {
 // split K and the 16-column kernel would not: M = 2 / 4, N = 11008, K =
 // 4096 11.8 / 12.3 against 12.5 / 13.4 us; N = 4096, K = 11008 13.5 / 14.1
 // against 14.9 / 17.4 us; but N = 4096, K = 4096 8.8 / 9.3 against 6.7 /
-// 7.3 us.  One row stays on the 16-column kernel (its in-kernel
-// quantization serves the decode SwiGLU and the dynamic linear).
+// 7.3 us; M = 1 the same way (N = 11008, K = 4096 11.6 against 12.0 us).
+// Activations quantized in the kernel (the decode SwiGLU, the dynamic
+// linear) take the 16-column kernel before this choice.
 bool use_skinny_lds(int64_t m, int64_t n, int64_t k, bool dual) {
     (void)dual;
     if (m > 4) return true;
-    if (m < 2) return false;
     const bool lds_splits = skinny_lds::choose_kslice((n + skinny_lds::kGroupCols - 1) / skinny_lds::kGroupCols, k) < k;
     const bool cols16_splits = skinny::choose_kslice((n + skinny::kCols - 1) / skinny::kCols, k) < k;
     return !(lds_splits && !cols16_splits);
