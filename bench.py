@@ -1178,13 +1178,53 @@ def main():
                 if ln.startswith("bytes_per_launch:"):
                     traffic = int(ln.split(":", 1)[1])
 
+    host = host_record(torch)
+    detail_path = args.detail or os.path.join(ROOT, "gpurun_out", "bench_detail.json")
+    line = headline_line(args.steps, args.warmup, h, cpu, traffic, host, components,
+                         os.path.relpath(detail_path, ROOT))
+    detail = dict(line)
+    detail["host"] = host
+    detail["components"] = [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in c.items()}
+                            for c in components]
+    try:
+        os.makedirs(os.path.dirname(detail_path), exist_ok=True)
+        with open(detail_path, "w") as fh:
+            json.dump(detail, fh, indent=1)
+    except OSError as e:
+        log(f"bench: could not write {detail_path}: {e}")
+    print(json.dumps(line), flush=True)
+
+
+# Components whose fraction of roofline the north star sets a target for:
+# fp32 GEMM >= 0.60 of f32 MFMA at 4096^3, INT8 >= 0.50 of i8 MFMA at
+# 4096^3, decode GEMV >= 0.70 of HBM at B = 1/4/8.
+NORTH_STAR_COMPONENTS = {
+    "sgemm_nn_4096": 0.60,
+    "qlinear_i8_m4096_n4096_k4096": 0.50,
+    "gemv_f32_b1": 0.70, "gemv_f32_b4": 0.70, "gemv_f32_b8": 0.70,
+    "gemv_w8_b1": 0.70, "gemv_w8_b4": 0.70, "gemv_w8_b8": 0.70,
+}
+# The result line must stay well inside what a log tail keeps.
+LINE_LIMIT = 2048
+
+
+def headline_line(steps, warmup, h, cpu, traffic, host, components, detail_rel):
+    """The one stdout JSON line: the headline and its roofline and CPU
+    baseline, the host in brief, and for the north star's target components
+    only [microseconds, fraction of roofline, target].  Every component with
+    its own CPU baseline goes to stderr and to the detail file instead."""
+    ns = {}
+    for c in components:
+        t = NORTH_STAR_COMPONENTS.get(c.get("name"))
+        if t is not None and "ms" in c:
+            ns[c["name"]] = [round(c["ms"] * 1e3, 1), round(c.get("frac", 0.0), 3), t]
     line = {
         "metric": METRIC,
         "value": round(h["value"], 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": round(h["ms_per_step"], 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -1197,14 +1237,14 @@ def main():
                      "unit": "TFLOP/s", "frac": round(h["achieved"] / (PEAK_F32 / 1e12), 4),
                      "traffic": traffic},
         "cpu_baseline": None if cpu is None else {k: cpu[k] for k in ("value", "unit", "cores", "kind", "sample")},
-        "host": host_record(torch),
-        "components": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in c.items()}
-                       for c in components],
+        "host": {k: host[k] for k in ("nproc", "cpu_model", "ram_gib", "rocm", "gpu") if k in host},
+        "north_star": ns,
+        "components": {"count": len(components), "file": detail_rel},
     }
-    if args.detail:
-        with open(args.detail, "w") as fh:
-            json.dump(line, fh, indent=1)
-    print(json.dumps(line), flush=True)
+    if len(json.dumps(line)) > LINE_LIMIT:
+        # the sample text is the only free-form field of any length
+        line["cpu_baseline"]["sample"] = line["cpu_baseline"]["sample"][:240]
+    return line
 
 
 if __name__ == "__main__":

@@ -503,6 +503,8 @@ GFH_API int gfh_flash_attention_f32(const float *q, const float *k, const float 
         d.block_n = block_size_n;
         d.causal = causal != 0;
         d.scale = scale;
+        if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 7) != 0)
+            return set_error(GFH_INVALID_DATA, "flash_attention: workspace must be 8-byte aligned");
         Scratch ws;
         GFH_TRY(ws.acquire(workspace, workspace_bytes, flash_attention_workspace_bytes(d), s));
         d.ws = static_cast<float *>(ws.ptr());

@@ -31,10 +31,14 @@
 //   3. O = W . V                             (gfh_sgemm NN).
 // Causal masking uses absolute indices, key j visible to row i iff j <= i
 // (top-left, :193-196), and key blocks starting at or past the end of the
-// row's query block are skipped (:150-152).  The result is the reference's
-// within fp32 rounding (different summation orders, and c^e evaluated as
-// exp(e delta)); non-finite inputs are outside that contract.  With
-// block_n = 1 the recurrence is exact softmax attention.
+// row's query block are skipped (:150-152).  The block maxima M_t are
+// exact (fp64 scores of their keys, kept in fp64: see exact_dot), so the
+// result differs from the exact value of the recurrence only by the
+// rounding of each key's own fp32 score and weight -- closer to it than the
+// reference's own fp32 evaluation, whose max errors the recurrence amplifies
+// -- and from the reference by that amount (different summation orders, c^e
+// evaluated as exp(e delta)); non-finite inputs are outside that contract.
+// With block_n = 1 the recurrence is exact softmax attention.
 #include <algorithm>
 #include <cmath>
 
@@ -52,21 +56,23 @@ namespace {
 constexpr int kFaThreads = 256;
 
 struct FaRow {
-    float *w;  // [rows][sk] scores in, weights out
-    int64_t sq, sk, bm, bn;
+    float *w;            // [rows][sk] scores in, weights out
+    const float *q, *k;  // [batch][sq][d], [batch][sk][d]: exact block maxima
+    int64_t sq, sk, d, bm, bn;
+    float scale;
     int causal;
 };
 
-// Inclusive scan of one float per thread over the workgroup with `op`
+// Inclusive scan of one value per thread over the workgroup with `op`
 // (Hillis-Steele through LDS); every thread gets its own prefix.
-template <typename Op>
-__device__ __forceinline__ float wg_inclusive_scan(float v, float *buf, Op op) {
+template <typename T, typename Op>
+__device__ __forceinline__ T wg_inclusive_scan(T v, T *buf, Op op) {
     const int tid = threadIdx.x;
     buf[tid] = v;
     __syncthreads();
 #pragma unroll
     for (int off = 1; off < kFaThreads; off <<= 1) {
-        const float o = tid >= off ? buf[tid - off] : v;
+        const T o = tid >= off ? buf[tid - off] : v;
         __syncthreads();
         if (tid >= off) v = op(v, o);
         buf[tid] = v;
@@ -75,17 +81,22 @@ __device__ __forceinline__ float wg_inclusive_scan(float v, float *buf, Op op) {
     return v;
 }
 
-// NB: LDS capacity for per-block state (block maxima, suffix sums).
+// NB: LDS capacity for per-block state (block maxima, suffix sums), kept in
+// fp64: each block's maximum is the exact score of its key with the largest
+// fp32 score (q . k summed in fp64, times the scale), for the reason given
+// with tile_argmax / exact_dot below.
 template <int NB>
 __global__ __launch_bounds__(kFaThreads) void fa_weights_kernel(FaRow p) {
-    __shared__ float M[NB];  // block max, then the running max after each block
-    __shared__ float E[NB];  // sum over later processed blocks of n * delta
-    __shared__ float buf[kFaThreads];
+    __shared__ double M[NB];  // block max, then the running max after each block
+    __shared__ double E[NB];  // sum over later processed blocks of n * delta
+    __shared__ double buf[kFaThreads];
     __shared__ float red[kFaThreads / 64];
     const int tid = threadIdx.x;
     const int64_t row = blockIdx.x;
     const int64_t i = row % p.sq;
     float *s = p.w + row * p.sk;
+    const float *qrow = p.q + row * p.d;
+    const float *kb = p.k + (row / p.sq) * p.sk * p.d;
     const int64_t nb = (p.sk + p.bn - 1) / p.bn;
     // Processed key blocks: all, or (causal) those starting before the end
     // of this row's query block.  Visible keys: j < jv.
@@ -97,8 +108,20 @@ __global__ __launch_bounds__(kFaThreads) void fa_weights_kernel(FaRow p) {
     for (int64_t t = tid; t < np; t += kFaThreads) {
         const int64_t j0 = t * p.bn, j1 = std::min<int64_t>(std::min<int64_t>(j0 + p.bn, p.sk), jv);
         float mx = -INFINITY;
-        for (int64_t j = j0; j < j1; ++j) mx = fmaxf(mx, s[j]);
-        M[t] = mx;
+        int64_t jm = -1;
+        for (int64_t j = j0; j < j1; ++j)
+            if (s[j] > mx) {
+                mx = s[j];
+                jm = j;
+            }
+        double ex = -INFINITY;
+        if (jm >= 0) {
+            const float *krow = kb + jm * p.d;
+            double dot = 0.0;
+            for (int64_t e = 0; e < p.d; ++e) dot = fma((double)qrow[e], (double)krow[e], dot);
+            ex = dot * (double)p.scale;
+        }
+        M[t] = ex;
     }
     __syncthreads();
 
@@ -107,14 +130,13 @@ __global__ __launch_bounds__(kFaThreads) void fa_weights_kernel(FaRow p) {
     // rewritten with the prefix from the chunks before it.
     const int64_t chunk = (np + kFaThreads - 1) / kFaThreads;
     const int64_t lo = std::min<int64_t>(tid * chunk, np), hi = std::min<int64_t>(lo + chunk, np);
-    float run = -INFINITY;
-    for (int64_t t = lo; t < hi; ++t) run = fmaxf(run, M[t]);
-    const float incl = wg_inclusive_scan(run, buf, [](float a, float b) { return fmaxf(a, b); });
-    float before = tid > 0 ? buf[tid - 1] : -INFINITY;
-    (void)incl;
+    double run = -INFINITY;
+    for (int64_t t = lo; t < hi; ++t) run = fmax(run, M[t]);
+    (void)wg_inclusive_scan(run, buf, [](double a, double b) { return fmax(a, b); });
+    double before = tid > 0 ? buf[tid - 1] : -INFINITY;
     __syncthreads();
     for (int64_t t = lo; t < hi; ++t) {
-        before = fmaxf(before, M[t]);
+        before = fmax(before, M[t]);
         M[t] = before;
     }
     __syncthreads();
@@ -122,22 +144,21 @@ __global__ __launch_bounds__(kFaThreads) void fa_weights_kernel(FaRow p) {
     // 3. E[t] = sum over processed t' > t of n_t' (M[t'-1] - M[t']): the
     // chunk sums scanned from the back (suffix), then each chunk walked
     // backwards.
-    auto term = [&](int64_t t) -> float {
-        const float n = (float)std::min<int64_t>(p.bn, p.sk - t * p.bn);
+    auto term = [&](int64_t t) -> double {
+        const double n = (double)std::min<int64_t>(p.bn, p.sk - t * p.bn);
         return n * (M[t - 1] - M[t]);
     };
-    float part = 0.f;
+    double part = 0.0;
     for (int64_t t = std::max<int64_t>(lo, 1); t < hi; ++t) part = part + term(t);
     // suffix scan = prefix scan over reversed thread order
     buf[kFaThreads - 1 - tid] = part;
     __syncthreads();
-    const float mine = buf[tid];
+    const double mine = buf[tid];
     __syncthreads();
-    const float rincl = wg_inclusive_scan(mine, buf, [](float a, float b) { return a + b; });
-    (void)rincl;
+    (void)wg_inclusive_scan(mine, buf, [](double a, double b) { return a + b; });
     // exclusive suffix of thread tid = inclusive prefix of reversed index (255 - tid) - 1
     const int rt = kFaThreads - 1 - tid;
-    float after = rt > 0 ? buf[rt - 1] : 0.f;
+    double after = rt > 0 ? buf[rt - 1] : 0.0;
     __syncthreads();
     for (int64_t t = hi - 1; t >= lo; --t) {
         E[t] = after;
@@ -146,7 +167,7 @@ __global__ __launch_bounds__(kFaThreads) void fa_weights_kernel(FaRow p) {
     __syncthreads();
 
     // 4. l = sum of exp(s_j - m_last) over the visible keys
-    const float m_last = np > 0 ? M[np - 1] : -INFINITY;
+    const float m_last = np > 0 ? (float)M[np - 1] : -INFINITY;
     float ls = 0.f;
     for (int64_t j = tid; j < jv; j += kFaThreads) ls = ls + expf(s[j] - m_last);
     ls = wave_sum(ls);
@@ -163,9 +184,9 @@ __global__ __launch_bounds__(kFaThreads) void fa_weights_kernel(FaRow p) {
             const int64_t n = std::min<int64_t>(p.bn, p.sk - t * p.bn);
             float lw;
             if (t == 0)
-                lw = idx == n - 1 ? (s[j] - M[0]) + E[0] : -INFINITY;
+                lw = idx == n - 1 ? (s[j] - (float)M[0]) + (float)E[0] : -INFINITY;
             else
-                lw = ((s[j] - M[t]) + (float)(n - 1 - idx) * (M[t - 1] - M[t])) + E[t];
+                lw = ((s[j] - (float)M[t]) + (float)(n - 1 - idx) * (float)(M[t - 1] - M[t])) + (float)E[t];
             const float e = expf(lw);
             out = l > 0.f ? e / l : e;
         }
@@ -200,13 +221,76 @@ __global__ __launch_bounds__(kFaThreads) void fa_weights_kernel(FaRow p) {
 struct FaFused {
     const float *q, *k, *v;
     float *out;
-    float *mblk;  // [batch * sq][nbw]
+    double *mblk;  // [batch * sq][nbw] exact running maxima
     int64_t sq, sk, d, bn, nbw;
     float scale;
     int nqb, fold;
 };
 
 constexpr int kFaBQ = 128;  // queries per workgroup
+
+// ---- exact block maxima ---------------------------------------------------------
+//
+// The recurrence multiplies the output by exp(M_{t-1} - M_t) once per key, so
+// an error in a running max M enters the exponent up to block_n times (and
+// the later blocks' sizes times more).  An fp32 score of a length-d dot
+// product is off from the exact one by ~1e-6 of its size (the reference's
+// own fp32 evaluation suffers the same), enough for relative errors of
+// ~1e-5 after that amplification.  So every block maximum is recomputed
+// exactly: the key with the largest fp32 score has q . k summed in fp64
+// (a product of two fp32 values is exact in fp64), times the fp32 scale,
+// and the running maxima and their differences are kept in fp64.  The
+// weights then carry only the unamplified rounding of each key's own score.
+
+// This row's largest fp32 score of a 32-key tile, and its key: lanes (c, 0)
+// and (c, 1) hold keys key_of(r, 0) / key_of(r, 1) and both get the same
+// answer (ties go to lane half 0, then to the lower register).  A row with
+// no visible key gets -inf and key 0.
+__device__ __forceinline__ int tile_argmax(const float (&x)[16], int h, float &mx) {
+    float m = x[0];
+    int rb = 0;
+#pragma unroll
+    for (int r = 1; r < 16; ++r)
+        if (x[r] > m) {
+            m = x[r];
+            rb = r;
+        }
+    const int kb = m == -INFINITY ? 0 : attn::key_of(rb, h);
+    const float pm = __shfl_xor(m, 32);
+    const int pk = __shfl_xor(kb, 32);
+    const float m0 = h ? pm : m, m1 = h ? m : pm;
+    const int k0 = h ? pk : kb, k1 = h ? kb : pk;
+    const bool first = m0 >= m1;
+    mx = first ? m0 : m1;
+    return first ? k0 : k1;
+}
+
+// q . k in fp64 for this row: each lane sums its own dims (chunks 2 g + h,
+// `chunk(g)` points at those 4 floats of the key), and the two halves are
+// added (the same sum in both lanes).
+// The query's fp64 copies are made afresh at every call (an empty volatile
+// asm on each value keeps the compiler from hoisting 2 x 64 registers of
+// them out of the key loop), and at most four chunks are read ahead, so the
+// sum costs a few registers beside the kernels' live accumulators.
+template <int NG, typename F>
+__device__ __forceinline__ double exact_dot(const f32x4 (&qf)[NG], F chunk) {
+    double acc = 0.0;
+#pragma unroll
+    for (int g0 = 0; g0 < NG; g0 += 4) {
+        f32x4 kv[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) kv[g] = *reinterpret_cast<const f32x4 *>(chunk(g0 + g));
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                float qv = qf[g0 + g][s];
+                asm volatile("" : "+v"(qv));
+                acc = fma((double)qv, (double)kv[g][s], acc);
+            }
+    }
+    return acc + __shfl_xor(acc, 32);
+}
 
 template <int DMAX, bool CAUSAL>
 __device__ __forceinline__ void fa_tile_scores(const FaFused &p, const float *ks, const f32x4 (&qf)[DMAX / 8],
@@ -261,7 +345,7 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_fused_kernel(FaFused p) {
     const float *Q = p.q + b * p.sq * p.d;
     const float *K = p.k + b * p.sk * p.d;
     const float *V = p.v + b * p.sk * p.d;
-    float *mrow = p.mblk + (b * p.sq + (row_ok ? my_q : p.sq - 1)) * p.nbw;
+    double *mrow = p.mblk + (b * p.sq + (row_ok ? my_q : p.sq - 1)) * p.nbw;
 
     f32x4 qf[NG];
 #pragma unroll
@@ -280,7 +364,8 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_fused_kernel(FaFused p) {
     gk.load(K, 0, p.sk, p.d, p.d, tid);
     gk.store(lk, tid);
     __syncthreads();
-    float m = -INFINITY, l = 0.f;
+    double m = -INFINITY;  // exact running max
+    float l = 0.f;
     for (int64_t t = 0; t < ntiles; ++t) {
         const int cur = t & 1;
         const bool more = t + 1 < ntiles;
@@ -288,17 +373,18 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_fused_kernel(FaFused p) {
         const int64_t k0 = t * kBKV;
         if (!CAUSAL || k0 <= wq0 + 31) {
             float sv[16];
-            fa_tile_scores<DMAX, CAUSAL>(p, lk + cur * kTile, qf, k0, my_q, lane, sv);
-            float mt = sv[0];
-#pragma unroll
-            for (int r = 1; r < 16; ++r) mt = fmaxf(mt, sv[r]);
-            mt = fmaxf(mt, __shfl_xor(mt, 32));
-            const float m_new = fmaxf(m, mt);
+            const float *ks = lk + cur * kTile;
+            fa_tile_scores<DMAX, CAUSAL>(p, ks, qf, k0, my_q, lane, sv);
+            float mx;
+            const int kw = tile_argmax(sv, h, mx);
+            const double dot = exact_dot(qf, [&](int g) { return ks + kw * kStride + 8 * g + 4 * h; });
+            const double m_new = mx != -INFINITY ? fmax(m, dot * (double)p.scale) : m;
             const bool dead = (m_new == -INFINITY);
-            const float alpha = dead ? 1.f : __expf(m - m_new);
+            const float alpha = dead ? 1.f : __expf((float)(m - m_new));
+            const float mn = (float)m_new;
             float ps = 0.f;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) ps += dead ? 0.f : __expf(sv[r] - m_new);
+            for (int r = 0; r < 16; ++r) ps += dead ? 0.f : __expf(sv[r] - mn);
             ps += __shfl_xor(ps, 32);
             l = l * alpha + ps;
             m = m_new;
@@ -316,9 +402,9 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_fused_kernel(FaFused p) {
     // ---- pass 2: the weights from M, and O = W . V ----
     const int64_t jv = CAUSAL ? min(p.sk, my_q + 1) : p.sk;  // visible keys of this row
     const int64_t vb = (jv - 1) / p.bn;                         // last block with one
-    const float m_v = m;
-    const float m_v1 = vb >= 1 ? mrow[vb - 1] : 0.f;
-    const float e_tail = vb >= 1 ? (float)min(p.bn, p.sk - vb * p.bn) * (m_v1 - m_v) : 0.f;
+    const double m_v = m;
+    const double m_v1 = vb >= 1 ? mrow[vb - 1] : 0.0;
+    const double e_tail = vb >= 1 ? (double)min(p.bn, p.sk - vb * p.bn) * (m_v1 - m_v) : 0.0;
     f32x16 o[ND];
 #pragma unroll
     for (int j = 0; j < ND; ++j)
@@ -340,13 +426,14 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_fused_kernel(FaFused p) {
         const int64_t k0 = t * kBKV;
         if (!CAUSAL || k0 <= wq0 + 31) {
             const int64_t blk = k0 / p.bn;
-            const float mt = mrow[blk];
-            const float mp = blk >= 1 ? mrow[blk - 1] : 0.f;
+            const double mt64 = mrow[blk];
+            const double mp64 = blk >= 1 ? mrow[blk - 1] : 0.0;
             float sv[16];
             fa_tile_scores<DMAX, CAUSAL>(p, lk + cur * kTile, qf, k0, my_q, lane, sv);
             const int64_t n = min(p.bn, p.sk - blk * p.bn);
-            const float e = blk < vb ? (float)p.bn * (mt - m_v1) + e_tail : 0.f;
-            const float delta = mp - mt;
+            const float e = blk < vb ? (float)((double)p.bn * (mt64 - m_v1) + e_tail) : 0.f;
+            const float delta = (float)(mp64 - mt64);
+            const float mt = (float)mt64;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int64_t idx = k0 + attn::key_of(r, h) - blk * p.bn;
@@ -473,8 +560,10 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_onepass_kernel(FaFused p) {
     for (int j = 0; j < ND; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[j][r] = 0.f;
-    float m = -INFINITY, l = 0.f;
+    double m = -INFINITY;  // exact running max
+    float l = 0.f;
     float sa[16];  // scores of a two-tile block's first tile
+    double xa = -INFINITY, xv = -INFINITY;  // exact maxima of sa / sv
 #pragma unroll
     for (int r = 0; r < 16; ++r) sa[r] = -INFINITY;
 
@@ -486,10 +575,18 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_onepass_kernel(FaFused p) {
         KL::issue(K, u * kBKV, p.sk, p.d, p.d, lk + (u & 1) * kTile, wave, lane);
         VL::issue(V, u * kBKV, p.sk, p.d, p.d, lv + (u % NVB) * kTile, wave, lane);
     };
-    auto scores = [&](int64_t u, float (&x)[16]) {
+    // Scores of tile u into x, and the exact value of this row's largest
+    // one into ex (-inf without a visible key).
+    auto scores = [&](int64_t u, float (&x)[16], double &ex) {
         const int64_t k0 = u * kBKV;
+        ex = -INFINITY;
         if (!CAUSAL || k0 <= wq0 + 31) {
-            fa_scores_lds<DMAX, CAUSAL>(p, lk + (u & 1) * kTile, qf, k0, my_q, lane, x);
+            const float *ks = lk + (u & 1) * kTile;
+            fa_scores_lds<DMAX, CAUSAL>(p, ks, qf, k0, my_q, lane, x);
+            float mx;
+            const int kw = tile_argmax(x, h, mx);
+            const double dot = exact_dot(qf, [&](int g) { return ks + (2 * g + h) * (4 * kBKV) + 4 * kw; });
+            if (mx != -INFINITY) ex = dot * (double)p.scale;
         } else {
 #pragma unroll
             for (int r = 0; r < 16; ++r) x[r] = -INFINITY;
@@ -536,25 +633,20 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_onepass_kernel(FaFused p) {
     };
     // Block blk from tiles u0 .. u0 + nt - 1 (nt = 1 or 2), their scores in
     // sa (first of two) and sv.
-    auto finish = [&](float (&sa_)[16], float (&sv_)[16], int64_t u0, int nt, int64_t blk) {
+    // (exact maxima of the two tiles in xa_ / xv_)
+    auto finish = [&](float (&sa_)[16], float (&sv_)[16], double xa_, double xv_, int64_t u0, int nt,
+                      int64_t blk) {
         const int64_t n = min(p.bn, p.sk - blk * p.bn);
-        float bmx = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) bmx = fmaxf(bmx, sv_[r]);
-        if (nt == 2) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) bmx = fmaxf(bmx, sa_[r]);
-        }
-        bmx = fmaxf(bmx, __shfl_xor(bmx, 32));
-        const float mt = fmaxf(m, bmx);
+        const double mt64 = fmax(m, nt == 2 ? fmax(xa_, xv_) : xv_);
         // Key 0 is visible to every row, so m is finite from block 1 on.
-        const float delta = blk == 0 ? 0.f : m - mt;
+        const float delta = blk == 0 ? 0.f : (float)(m - mt64);
+        const float mt = (float)mt64;
         float ps = 0.f;
         if (nt == 2) weights(sa_, u0, blk, n, mt, delta, ps);
         weights(sv_, u0 + nt - 1, blk, n, mt, delta, ps);
         ps += __shfl_xor(ps, 32);
         l = l * __expf(delta) + ps;
-        m = mt;
+        m = mt64;
         const float corr = __expf((float)n * delta);
 #pragma unroll
         for (int j = 0; j < ND; ++j)
@@ -575,16 +667,16 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_onepass_kernel(FaFused p) {
         if (TPB == 2 && t + 1 < ntiles) {
             // first tile of the block: scores wait in sa
             issue(t + 1);
-            scores(t, sa);
+            scores(t, sa, xa);
             attn::wait_vm0();
             __syncthreads();
             if (t + 2 < ntiles) issue(t + 2);
-            scores(t + 1, sv);
-            if (live(t) || live(t + 1)) finish(sa, sv, t, 2, blk);
+            scores(t + 1, sv, xv);
+            if (live(t) || live(t + 1)) finish(sa, sv, xa, xv, t, 2, blk);
         } else {
             if (t + 1 < ntiles) issue(t + 1);
-            scores(t, sv);
-            if (live(t)) finish(sa, sv, t, 1, blk);
+            scores(t, sv, xv);
+            if (live(t)) finish(sa, sv, xa, xv, t, 1, blk);
         }
         attn::wait_vm0();
         __syncthreads();
@@ -623,7 +715,7 @@ bool flash_attention_fused_fits(const FlashAttnDesc &d) {
 
 size_t flash_attention_workspace_bytes(const FlashAttnDesc &d) {
     if (d.sk > 0 && flash_attention_fused_fits(d))
-        return sizeof(float) * (size_t)d.batch * (size_t)d.sq * (size_t)((d.sk + d.block_n - 1) / d.block_n);
+        return sizeof(double) * (size_t)d.batch * (size_t)d.sq * (size_t)((d.sk + d.block_n - 1) / d.block_n);
     return sizeof(float) * (size_t)d.batch * (size_t)d.sq * (size_t)d.sk;
 }
 
@@ -635,7 +727,7 @@ int launch_flash_attention_blockwise(const FlashAttnDesc &d, hipStream_t s) {
         p.k = d.k;
         p.v = d.v;
         p.out = d.out;
-        p.mblk = d.ws;
+        p.mblk = reinterpret_cast<double *>(d.ws);
         p.sq = d.sq;
         p.sk = d.sk;
         p.d = d.d;
@@ -726,6 +818,10 @@ int launch_flash_attention_blockwise(const FlashAttnDesc &d, hipStream_t s) {
         // 2. blockwise weights, in place
         FaRow r;
         r.w = d.ws;
+        r.q = d.q;
+        r.k = d.k;
+        r.d = d.d;
+        r.scale = d.scale;
         r.sq = d.sq;
         r.sk = d.sk;
         r.bm = d.block_m;

@@ -36,8 +36,11 @@
 #include "common.hpp"
 #include "kernels.hpp"
 
-// Every f32 product and sum is its own rounding, as in the reference CPU
-// path (no FMA contraction).
+// No implicit contraction of a*b+c: where this file writes a separate
+// product and sum they round separately.  The fp32 accumulation itself is
+// deliberately fused -- explicit fmaf on the VALU path and MFMA on the
+// matrix-core paths -- under the GEMM error bound the tests apply, not
+// the reference's separate roundings.
 #pragma clang fp contract(off)
 
 namespace gfh {

@@ -190,11 +190,14 @@ __global__ __launch_bounds__(kBlock) void quant_per_tensor_kernel(const float *_
 // same codes), so the codes are right either way and every wave exits.
 constexpr int kResThreads = 1024;
 constexpr int kResMaxGroups = 16;
-// Wait rounds (s_sleep 2, ~128 clocks, plus one agent-scope load each)
-// before a workgroup gives up: well over 0.1 s.  GFH_QUANT_WAIT_ROUNDS
-// overrides it (0: every workgroup takes the fold-everything path; used by
-// the tests of that path).
-constexpr int kResSpinLimit = 1 << 20;
+// Wait rounds (s_sleep 2, ~128 clocks, plus one agent-scope load of a few
+// hundred ns each) before a workgroup gives up: a few ms at most, far above
+// the few microseconds the whole grid needs to start when the GPU is free,
+// and a bounded cost when other streams hold the CUs (the fold-everything
+// path then reads all of x, at most 256 KiB, per workgroup).
+// GFH_QUANT_WAIT_ROUNDS lowers it (0: every workgroup takes the
+// fold-everything path; used by the tests of that path).
+constexpr int kResSpinLimit = 1 << 12;
 
 __global__ __launch_bounds__(kResThreads) void quant_small_kernel(const float *__restrict__ x, int64_t n,
                                                                  bool symmetric, float *__restrict__ partials,

@@ -35,6 +35,23 @@ def _ptr(t):
     return None if t is None else t.data_ptr()
 
 
+def _workspace_bytes(ws):
+    """Bytes a caller workspace holds, whatever its dtype: numel times the
+    element size.  The workspace must be a contiguous device tensor."""
+    if ws is None:
+        return 0
+    if not ws.is_cuda:
+        raise GhostFlowError(_lib.INVALID_DATA, "workspace must be a device tensor")
+    if not ws.is_contiguous():
+        raise GhostFlowError(_lib.INVALID_DATA, "workspace must be contiguous")
+    return ws.numel() * ws.element_size()
+
+
+def _workspace(ws):
+    """(pointer, bytes) of a caller workspace, (None, 0) without one."""
+    return (None, 0) if ws is None else (ws.data_ptr(), _workspace_bytes(ws))
+
+
 def _need(t, dtype, name):
     if t is None:
         return
@@ -150,7 +167,7 @@ def quantize_per_tensor(x, symmetric=False, workspace=None):
     q = torch.empty(x.shape, dtype=torch.int8, device=x.device)
     s = torch.empty(1, dtype=torch.float32, device=x.device)
     z = torch.empty(1, dtype=torch.int8, device=x.device)
-    ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(), workspace.numel() * workspace.element_size())
+    ws_ptr, ws_bytes = _workspace(workspace)
     _check(lib().gfh_quantize_i8_per_tensor(x.data_ptr(), x.numel(), int(bool(symmetric)),
                                             q.data_ptr(), s.data_ptr(), z.data_ptr(),
                                             ws_ptr, ws_bytes, _stream(x.device)))
@@ -219,8 +236,7 @@ def qlinear_dynamic(x, qw, sw, w_rowsum, *, bias=None, out=None, workspace=None)
     if qw.shape[1] != k:
         raise GhostFlowError(_lib.INVALID_SHAPE, f"ShapeMismatch expected [{m}, {k}] got [{qw.shape[1]}, {n}]")
     y = torch.empty((m, n), dtype=torch.float32, device=x.device) if out is None else out
-    ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(),
-                                                             workspace.numel() * workspace.element_size())
+    ws_ptr, ws_bytes = _workspace(workspace)
     _check(lib().gfh_qlinear_dynamic_i8(x.data_ptr(), qw.data_ptr(), sw.data_ptr(), w_rowsum.data_ptr(),
                                         _ptr(bias), y.data_ptr(), m, n, k, ws_ptr, ws_bytes, _stream(x.device)))
     return y
@@ -303,8 +319,7 @@ def flash_attention_blockwise(q, k, v, *, block_size_m=64, block_size_n=64, caus
     o = torch.empty_like(q) if out is None else out
     _check(lib().gfh_flash_attention_f32(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), b, sq, sk, d,
                                          int(block_size_m), int(block_size_n), int(bool(causal)), float(scale),
-                                         _ptr(workspace), 0 if workspace is None else workspace.numel() * 4,
-                                         _stream(q.device)))
+                                         _ptr(workspace), _workspace_bytes(workspace), _stream(q.device)))
     return o
 
 
@@ -369,8 +384,7 @@ def mha_forward_cached(query, key, value, wq, bq, wk, bk, wv, bv, wo, bo, num_he
     o = torch.empty_like(query) if out is None else out
     w = (torch.empty((b, num_heads, sq, kv_len), dtype=torch.float32, device=query.device)
          if want_weights else None)
-    ws_ptr, ws_bytes = (None, 0) if workspace is None else (workspace.data_ptr(),
-                                                             workspace.numel() * workspace.element_size())
+    ws_ptr, ws_bytes = _workspace(workspace)
     _check(lib().gfh_mha_forward_with_cache_f32(
         query.data_ptr(), key.data_ptr(), value.data_ptr(), wq.data_ptr(), _ptr(bq), wk.data_ptr(), _ptr(bk),
         wv.data_ptr(), _ptr(bv), wo.data_ptr(), _ptr(bo), k_cache.data_ptr(), v_cache.data_ptr(), cap, past_len,

@@ -273,11 +273,14 @@ GFH_API int gfh_sdpa_f32(const float *q, const float *k, const float *v, float *
  *     only its last key, and a block whose max rises scales the earlier
  *     output by the correction to the power of its key count;
  *   - rows with row_sum == 0 are left undivided (:166-172); no keys gives 0.
- * Within fp32 rounding of the reference (1e-4 relative) for finite inputs.
- * Block sizes must be positive (the reference's step_by(0) panics) and
- * ceil(seq_len_k / block_size_n) <= 8192.  Workspace: gfh_flash_attention_
- * workspace_size(batch, seq_len_q, seq_len_k) bytes (nullable, see
- * conventions).  For softmax attention use gfh_sdpa_f32. */
+ * Within fp32 rounding of the reference (1e-4 relative) for finite inputs;
+ * the block maxima are exact (fp64 scores of their keys), so the result is
+ * nearer the exact value of the recurrence than the reference's own fp32
+ * evaluation.  Block sizes must be positive (the reference's step_by(0)
+ * panics) and ceil(seq_len_k / block_size_n) <= 8192.  Workspace:
+ * gfh_flash_attention_workspace_size(batch, seq_len_q, seq_len_k) bytes,
+ * 8-byte aligned (nullable, see conventions).  For softmax attention use
+ * gfh_sdpa_f32. */
 GFH_API int gfh_flash_attention_f32(const float *q, const float *k, const float *v,
                                     float *out, int64_t batch, int64_t seq_len_q,
                                     int64_t seq_len_k, int64_t d_model,

@@ -181,3 +181,18 @@ def test_reference_unit_test_shapes():
     assert O.flash_attention_blockwise(q, k, v, 64, 64, False, 1.0).shape == (2, 8, 16)
     q, k, v = _data(1, 4, 4, 8, 0)
     assert O.flash_attention_blockwise(q, k, v, 64, 64, True, 1.0).shape == (1, 4, 8)
+
+
+@pytest.mark.parametrize("bm,bn,sq,sk,causal", [(64, 64, 20, 20, False), (4, 8, 21, 37, False),
+                                                (4, 8, 21, 37, True), (8, 4, 37, 21, True),
+                                                (3, 5, 13, 13, True), (64, 16, 70, 70, True),
+                                                (5, 7, 1, 30, False), (2, 3, 30, 1, True),
+                                                (16, 1, 9, 40, False), (7, 5, 29, 31, True)])
+def test_vectorized_closed_form(bm, bn, sq, sk, causal):
+    """The vectorized fp64 closed form the GPU tests use as the exact value
+    agrees with the per-row loop above (itself pinned against the oracle)."""
+    from _flash_exact import flash_blockwise_exact
+    q, k, v = _data(2, sq, sk, 6, bm * 13 + bn * 5 + sq + sk)
+    a = flash_blockwise_exact(q, k, v, bm, bn, causal, 0.45)
+    b = _closed_form(q, k, v, bm, bn, causal, 0.45)
+    np.testing.assert_allclose(a, b, rtol=1e-12, atol=1e-14)
