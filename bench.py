@@ -492,6 +492,75 @@ class CpuRef:
                            f"oracle quantize_activation (per tensor, asymmetric) of {n} elements, full: "
                            f"{full * 1e3:.1f} ms per call")
 
+    def kv_attention(self, B=4, H=32, D=128, kv_len=2048):
+        """The attention step of MultiHeadAttention::forward_with_cache for
+        one new token over kv_len - 1 cached positions (attention.rs:100-144):
+        concat_tensors of the cached and new keys and of the values
+        (:214-247), the head split of reshape_for_attention (:146-150) and
+        scaled_dot_product_attention (:11-49), timed in full on one thread.
+        Same algorithmic bytes as the GPU component (K, V, q, out)."""
+        np, O = self.np, self.O
+        E = H * D
+        past_k, past_v = self._randn((B, kv_len - 1, E)), self._randn((B, kv_len - 1, E))
+        k_new, v_new, q = self._randn((B, 1, E)), self._randn((B, 1, E)), self._randn((B, 1, E))
+
+        def heads(t, n):  # [B, n, E] -> [B, H, n, D], one head at a time
+            src = t.reshape(B, n, H, D)
+            out = np.empty((B, H, n, D), np.float32)
+            for hh in range(H):
+                out[:, hh] = src[:, :, hh, :]
+            return out
+
+        def step():
+            kc = np.concatenate([past_k, k_new], axis=1)
+            vc = np.concatenate([past_v, v_new], axis=1)
+            O.sdpa(heads(q, 1), heads(kc, kv_len), heads(vc, kv_len))
+        step()
+        full = self._t(step)
+        byts = 2 * 4 * B * kv_len * E + 8 * B * E
+        return self.result(byts / full / 1e9, "GB/s", full,
+                           f"oracle concat_tensors (K, V) + reshape_for_attention + scaled_dot_product_attention "
+                           f"over {kv_len} positions, B={B}, {H} heads of {D}, full: {full * 1e3:.1f} ms per step")
+
+    def mha_decode(self, B=4, H=32, D=128, past=2047):
+        """One decode step of MultiHeadAttention::forward_with_cache
+        (attention.rs:100-144): the q / k / v projections (Linear::forward,
+        W^T gather + matmul_blocked + bias), the cache concatenation, SDPA
+        and out_proj, through the oracle's composite, timed in full."""
+        np, O = self.np, self.O
+        E = H * D
+        w = [self._randn((E, E)) * np.float32(1 / 64) for _ in range(4)]
+        bias = [self._randn((E,)) * np.float32(1 / 64) for _ in range(4)]
+        x = self._randn((B, 1, E))
+        pk, pv = self._randn((B, past, E)), self._randn((B, past, E))
+
+        def step():
+            O.mha_forward_with_cache(x, x, x, w[0], bias[0], w[1], bias[1], w[2], bias[2], w[3], bias[3], H,
+                                     past_key=pk, past_value=pv)
+        full = self._t(step)
+        byts = 4 * 4 * E * E + 2 * 4 * B * (past + 1) * E + 4 * B * E * 6
+        return self.result(byts / full / 1e9, "GB/s", full,
+                           f"oracle MultiHeadAttention::forward_with_cache, B={B}, 1 new token, {past} cached "
+                           f"positions, E={E}, {H} heads (4 Linear + concat + SDPA), full: "
+                           f"{full * 1e3:.1f} ms per step", tokens_per_s=B / full)
+
+    def state_dict_load(self, path):
+        """load_state_dict + read_tensor (serialize.rs:48-88,124-167) of a
+        file already in the page cache, restated byte for byte
+        (oracle/ghostflw.py): the file read and the little-endian decode of
+        every tensor into host memory, timed in full on one thread."""
+        from oracle import ghostflw
+        nbytes = os.path.getsize(path)
+
+        def load():
+            with open(path, "rb") as fh:
+                ghostflw.load_bytes(fh.read())
+        load()
+        full = min(self._t(load) for _ in range(3))
+        return self.result(nbytes / full / 1e9, "GB/s", full,
+                           f"oracle GHOSTFLW/GHOSTFLQ reader (read + decode into host memory) of a {nbytes / 1e6:.0f} "
+                           f"MB file from the page cache, full, best of 3: {full * 1e3:.1f} ms")
+
     def linear(self, m, n, k):
         full, rows, meas = self.matmul_s(m, k, n, b_transposed=True)
         t_bias = self._copy_s(4 * m * n)  # the broadcast add writes a new [m, n] tensor (same traffic)
@@ -934,7 +1003,7 @@ def comp_swiglu(lib, torch, m, int8, H=4096, I=11008):
             "bound": ("mfma_i8" if int8 else "mfma_f32") if attain == peak else "hbm", "weight_sets": ncopy}
 
 
-def comp_state_dict_load(lib, torch, int8):
+def comp_state_dict_load(lib, torch, int8, cpu=None):
     """Weight load, file -> HBM: the three LLaMA-7B MLP weights (4096 x 11008
     each) as a GHOSTFLW state dict (fp32, 541 MB) or a GHOSTFLQ file of their
     int8 codes + scales (135 MB), read from the page cache through
@@ -982,11 +1051,20 @@ def comp_state_dict_load(lib, torch, int8):
             a, b = (state[k], outs[k]) if not int8 else (state[k][0], outs[k][0])
             if not torch.equal(a, b):
                 raise RuntimeError(f"state dict reload mismatch in {k}")
+        cpu_res = None
+        if cpu is not None:  # the reference's reader on the same file, while it exists
+            try:
+                cpu_res = cpu.state_dict_load(path)
+            except Exception as e:  # noqa: BLE001
+                cpu_res = {"error": str(e)}
     finally:
         os.unlink(path)
     gbs = nbytes / sec / 1e9
-    return {"name": f"state_dict_load_{'ghostflq_i8' if int8 else 'ghostflw_f32'}_llama7b_mlp", "ms": sec * 1e3,
-            "value": gbs, "unit": "GB/s", "bytes": nbytes, "frac": gbs / 64.0, "bound": "pcie5_x16"}
+    r = {"name": f"state_dict_load_{'ghostflq_i8' if int8 else 'ghostflw_f32'}_llama7b_mlp", "ms": sec * 1e3,
+         "value": gbs, "unit": "GB/s", "bytes": nbytes, "frac": gbs / 64.0, "bound": "pcie5_x16"}
+    if cpu_res is not None:
+        r["cpu_baseline"] = cpu_res
+    return r
 
 
 def comp_quantize(lib, torch, m, k=4096):
@@ -1064,7 +1142,7 @@ def run_components(lib, torch, only, cpu=None):
 
     if "io" in want:
         for int8 in (False, True):
-            add(comp_state_dict_load, int8)
+            add(comp_state_dict_load, int8, cpu=cpu)
     if "qlinear" in want:
         add(comp_qlinear, 4096, 4096, 4096, cpu_fn=lambda: cpu.qlinear(4096, 4096, 4096))
         for m in (1, 16, 256, 4096):
@@ -1090,8 +1168,8 @@ def run_components(lib, torch, only, cpu=None):
     if "decode" in want:
         for m in (1, 4, 8, 16, 64):
             add(comp_linear_decode, m, cpu_fn=lambda m=m: _cpu_linear_result(cpu, m, 4096, 4096))
-        add(comp_kv_attention)
-        add(comp_mha_decode)
+        add(comp_kv_attention, cpu_fn=lambda: cpu.kv_attention())
+        add(comp_mha_decode, cpu_fn=lambda: cpu.mha_decode())
     if "swiglu" in want:
         for m in (1, 16, 256, 4096):
             add(comp_swiglu, m, True, cpu_fn=lambda m=m: cpu.swiglu(m, True))

@@ -248,8 +248,12 @@ def mha_forward_with_cache(query, key, value, wq, bq, wk, bk, wv, bv, wo, bo, nu
         kc, vc = k, v
     skv = kc.shape[1]
 
-    def heads(t, n):  # [B, n, E] -> [B, H, n, D]
-        return np.ascontiguousarray(t.reshape(b, n, h, d).transpose(0, 2, 1, 3))
+    def heads(t, n):  # [B, n, E] -> [B, H, n, D], one head at a time (row copies of D floats)
+        src = t.reshape(b, n, h, d)
+        out = np.empty((b, h, n, d), np.float32)
+        for hh in range(h):
+            out[:, hh] = src[:, :, hh, :]
+        return out
 
     out, w = sdpa(heads(q, s), heads(kc, skv), heads(vc, skv), mask=mask, want_weights=True)
     attn = np.ascontiguousarray(out.transpose(0, 2, 1, 3)).reshape(b * s, e)
