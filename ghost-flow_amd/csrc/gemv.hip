@@ -474,25 +474,34 @@ __global__ __launch_bounds__(64 * NW) void gemv_f32_kernel(GemvParams p) {
 //    two byte permutes per pair of weights; one packed f16 add of
 //    -(1152 + zp) per pair of rows leaves q - zp, exact (|q - zp| <= 255).
 //  * B: each workgroup scales its slice of xs by a power of two 2^e so that
-//    max |xs| 2^e lies in [2^14, 2^15), then splits it into two f16, hi =
-//    f16(xs 2^e) and lo = f16(xs 2^e - hi): hi + lo carries 22 significant
-//    bits, and hi * w, lo * w are exact in the fp32 accumulators.  Split
-//    column n = b holds hi of batch row b and n = 8 + b its lo, so 8 batch
-//    rows fill the 16 columns of one MFMA.
+//    max |xs| 2^e lies in [2^14, 2^15), then splits it into three f16, hi =
+//    f16(X), mid = f16(X - hi), lo = f16(X - hi - mid) with X = xs 2^e (each
+//    difference exact in fp32): hi + mid + lo carries 33 significant bits,
+//    more than X's own 24, so X is carried exactly unless its last bits fall
+//    below f16's subnormal step (|X| < 2^-1, i.e. below 2^-16 of the slice
+//    maximum), and hi * w, mid * w, lo * w are exact products in the fp32
+//    accumulators.  Up to 4 batch rows the three pieces of batch row b sit
+//    in split columns b, MAXB + b and 2 MAXB + b of one MFMA; 8 batch rows
+//    take two MFMAs per weight fragment, hi / mid in columns b / 8 + b of
+//    the first and lo in column b of the second.
 // Sums are fp32 in a fixed order, as in the VALU form; the result is within
 // the fp32 GEMM bound of the reference, not bit-identical to it.
 namespace w8mf {
 
 constexpr int kBlockRows = 32;           // rows per MFMA step of a wave
 constexpr int kXStride = kMaxSlice + 8;  // f16 per split column: +16 bytes keeps B reads conflict-free
-constexpr int kXBytes = 16 * kXStride * 2;
+// B operands (16 split columns each) per weight fragment
+template <int MAXB>
+constexpr int nbops() { return MAXB <= 4 ? 1 : 2; }
+template <int MAXB>
+constexpr int xbytes() { return 16 * nbops<MAXB>() * kXStride * 2; }
 // Wave partials [wave][batch][column], aliased onto the split activations:
 // 2 words of padding per 64 columns and a 264-word row put the 32 lanes
 // that store together on 32 distinct banks.
 constexpr int kRedStride = 264;
-template <int NW>
+template <int NW, int MAXB>
 constexpr int lds_bytes() {
-    return kXBytes > NW * 8 * kRedStride * 4 ? kXBytes : NW * 8 * kRedStride * 4;
+    return xbytes<MAXB>() > NW * 8 * kRedStride * 4 ? xbytes<MAXB>() : NW * 8 * kRedStride * 4;
 }
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -502,10 +511,13 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ int red_index(int w, int b, int col) { return (w * 8 + b) * kRedStride + col + 2 * (col >> 6); }
 
 template <int MAXB, bool VEC, int NW>
-__global__ __launch_bounds__(64 * NW, (VEC && NW == 4) ? 2 : 1) void gemv_w8_mfma_kernel(GemvParams p) {
+__global__ __launch_bounds__(64 * NW, (VEC && NW == 4 && MAXB <= 4) ? 2 : 1) void gemv_w8_mfma_kernel(GemvParams p) {
     constexpr int SCOLS = kStripBytes;
     constexpr int NT = 64 * NW;
-    __shared__ __attribute__((aligned(16))) unsigned char lds[lds_bytes<NW>()];
+    constexpr int NBO = nbops<MAXB>();
+    // split column of piece 0 / 1 / 2 (hi / mid / lo) of batch row b
+    constexpr int kMidCol = NBO == 1 ? MAXB : 8, kLoCol = NBO == 1 ? 2 * MAXB : 16;
+    __shared__ __attribute__((aligned(16))) unsigned char lds[lds_bytes<NW, MAXB>()];
     __shared__ __attribute__((aligned(16))) uint32_t zph[kMaxSlice / 2];  // -(1152 + zp) of row pairs, f16x2
     __shared__ float amax_red[NW];
     __shared__ int last_flag;
@@ -661,18 +673,27 @@ __global__ __launch_bounds__(64 * NW, (VEC && NW == 4) ? 2 : 1) void gemv_w8_mfm
             const float X = ldexpf(xv[i][bi], ex);
             const _Float16 hi = (_Float16)X;
             const bool fin = __builtin_isfinite(X);
+            const float r1 = fin ? X - (float)hi : 0.f;
+            const _Float16 mid = (_Float16)r1;
+            const _Float16 lo = (_Float16)(r1 - (float)mid);
             xsh[bi * kXStride + r] = hi;
-            xsh[(8 + bi) * kXStride + r] = fin ? (_Float16)(X - (float)hi) : (_Float16)0.f;
+            xsh[(kMidCol + bi) * kXStride + r] = mid;
+            xsh[(kLoCol + bi) * kXStride + r] = lo;
         }
     }
     __syncthreads();
 
     // Stream the weights in 32-row blocks, kBufs blocks in flight.
-    f32x4 acc[16];
+    f32x4 acc[NBO][16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int o = 0; o < NBO; ++o)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[o][j] = f32x4{0.f, 0.f, 0.f, 0.f};
     auto compute_block = [&](const i32x4 (&R)[8], int r0) {
-        const half8 bx = *reinterpret_cast<const half8 *>(xsh + c * kXStride + r0 + 8 * g);
+        half8 bx[NBO];
+#pragma unroll
+        for (int o = 0; o < NBO; ++o)
+            bx[o] = *reinterpret_cast<const half8 *>(xsh + (16 * o + c) * kXStride + r0 + 8 * g);
         const u32x4 zq = *reinterpret_cast<const u32x4 *>(zph + (r0 + 8 * g) / 2);
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
@@ -693,9 +714,11 @@ __global__ __launch_bounds__(64 * NW, (VEC && NW == 4) ? 2 : 1) void gemv_w8_mfm
                 a[3][i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2, __builtin_amdgcn_perm(t1, 0x64646464u, 0x00070006u)) + z);
             }
 #pragma unroll
-            for (int jj = 0; jj < 4; ++jj)
-                acc[4 * d + jj] =
-                    __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a[jj]), bx, acc[4 * d + jj], 0, 0, 0);
+            for (int o = 0; o < NBO; ++o)
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj)
+                    acc[o][4 * d + jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a[jj]), bx[o],
+                                                                                acc[o][4 * d + jj], 0, 0, 0);
         }
     };
     // While more than kBufs blocks remain, a buffer is refilled with the
@@ -717,19 +740,35 @@ __global__ __launch_bounds__(64 * NW, (VEC && NW == 4) ? 2 : 1) void gemv_w8_mfm
     for (int j = 0; j < kBufs; ++j)
         if (i + j < cnt) compute_block(R[j], block_row(i + j));
 
-    // acc[j][i] of lane (g, c) is column 16 (4g + i) + j for split column c;
-    // hi (c) and lo (c + 8) of batch row c meet with a rotation by 8 lanes
-    // within each row of 16 (DPP row_ror:8).
+    // acc[o][j][i] of lane (g, c) is column 16 (4g + i) + j for split
+    // column c of B operand o.  The pieces of batch row c < MAXB meet in
+    // lane c of each row of 16, summed (hi + mid) + lo: up to 4 batch rows
+    // from lanes c + MAXB and c + 2 MAXB of the same row, 8 batch rows from
+    // lane c + 8 and the second operand.  DPP row_ror:r gives lane i the
+    // value of lane (i - r) mod 16 of its row (checked on gfx950), so lane
+    // c + M is row_ror:(16 - M).
     __syncthreads();  // every wave is done with the split activations
     float *red = reinterpret_cast<float *>(lds);
+    constexpr int kRorMid = 0x120 + (16 - kMidCol), kRorLo = 0x120 + (16 - kLoCol) % 16;
+    auto from_lane = [](float v, auto ctrl) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), decltype(ctrl)::value,
+                                                                  0xf, 0xf, false));
+    };
 #pragma unroll
     for (int j = 0; j < 16; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float v = acc[j][i];
-            const float o = __builtin_bit_cast(
-                float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xf, 0xf, false));
-            if (c < MAXB) red[red_index(wave, c, 16 * (4 * g + i) + j)] = v + o;
+            const float v = acc[0][j][i];
+            float t;
+            if constexpr (NBO == 1) {
+                const float vm = from_lane(v, std::integral_constant<int, kRorMid>{});
+                const float vl = from_lane(v, std::integral_constant<int, kRorLo>{});
+                t = (v + vm) + vl;
+            } else {
+                const float vm = from_lane(v, std::integral_constant<int, kRorMid>{});
+                t = (v + vm) + acc[NBO - 1][j][i];
+            }
+            if (c < MAXB) red[red_index(wave, c, 16 * (4 * g + i) + j)] = t;
         }
     __syncthreads();
     auto strip_value = [&](int bi, int cc) {
@@ -931,10 +970,19 @@ int gemv_w8_common(const float *x, const int8_t *qw, const float *scales, const 
         const bool wide = vec && q.nstrips * q.slices <= 256;
         auto go = [&](auto maxb) {
             constexpr int MB = decltype(maxb)::value;
-            if (wide)
-                w8mf::launch<MB, 8>(q, vec, s);
-            else
+            // 8 batch rows carry two accumulator sets (the activations'
+            // three pieces take 24 split columns): 4 waves with a whole SIMD
+            // each (19.5 us at [4096, 14336]), where 8 waves spill (8 waves
+            // with one block in flight: 20.3 us; 4 waves with 3 or 4 blocks in
+            // flight: 20.1 / 20.4 us).
+            if constexpr (MB <= 4) {
+                if (wide)
+                    w8mf::launch<MB, 8>(q, vec, s);
+                else
+                    w8mf::launch<MB, 4>(q, vec, s);
+            } else {
                 w8mf::launch<MB, 4>(q, vec, s);
+            }
         };
         if (q.b == 1)
             go(std::integral_constant<int, 1>{});

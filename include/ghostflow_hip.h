@@ -205,10 +205,11 @@ GFH_API int gfh_gemv_f32(const float *x, const float *w, float *y, int64_t b,
  * by Tensor::matmul, without materializing the fp32 weight. b <= 64.
  * Precision: the products are regrouped as (x[b, k] * s[k]) * (q - zp).  Per
  * K-slice of up to 1024 rows, x * s is scaled by a power of two so that its
- * largest finite magnitude lies in [2^14, 2^15), then carried as two f16
- * (hi + lo: 22 significant bits near the slice maximum; values far below it
- * keep an absolute error under 2^-39 times that maximum).  The multiply-adds
- * are exact in fp32 and summed in fp32, so y stays within the fp32 GEMM
+ * largest finite magnitude lies in [2^14, 2^15), then carried as three f16
+ * (hi + mid + lo: 33 significant bits, so every fp32 x * s down to 2^-16
+ * times the slice maximum is carried exactly; smaller values keep an
+ * absolute error under 2^-39 times that maximum, f16's subnormal step).  The
+ * products are exact and summed in fp32, so y stays within the fp32 GEMM
  * bound of the reference but is not bit-identical to it.  An infinite or
  * NaN x * s is carried unchanged and gives inf / NaN as the reference does. */
 GFH_API int gfh_gemv_w8(const float *x, const int8_t *qw, const float *scales,

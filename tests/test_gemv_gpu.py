@@ -168,11 +168,34 @@ def test_split_k_counters_reset_across_calls_and_streams(torch_dev):
     np.testing.assert_array_equal(to_np(y2), first)
 
 
+@pytest.mark.parametrize("b", [1, 4, 8])
+def test_gemv_w8_activation_precision(torch_dev, b):
+    """x * s is carried in full: its three f16 pieces hold 33 bits, more
+    than the 24 of the fp32 product.  With exactly one non-zero weight per
+    column, y[b, n] = x s (q - zp) has no sum over k, so the result carries
+    only the rounding of x * s and of adding the three pieces' products:
+    within 3 * 2^-24 relative of the exact value (two f16 pieces, 22 bits,
+    are off by up to 2^-22 relative and fail this).  b = 8 takes the two-
+    operand form, b <= 4 the one-operand form."""
+    gh = _gh()
+    rng = np.random.default_rng(40 + b)
+    k, n = 1024, 512
+    x = (rng.uniform(1.0, 2.0, size=(b, k)) * rng.choice([-1.0, 1.0], size=(b, k))).astype(np.float32)
+    s = rng.uniform(0.5, 2.0, size=k).astype(np.float32)
+    q = np.zeros((k, n), np.int8)
+    rows = rng.integers(0, k, size=n)
+    q[rows, np.arange(n)] = (rng.integers(1, 128, size=n) * rng.choice([-1, 1], size=n)).astype(np.int8)
+    got = to_np(gh.gemv_w8(to_dev(x, torch_dev), to_dev(q, torch_dev), to_dev(s, torch_dev))).astype(np.float64)
+    exact = x.astype(np.float64)[:, rows] * s.astype(np.float64)[rows] * q[rows, np.arange(n)].astype(np.float64)
+    rel = np.abs(got - exact) / np.abs(exact)
+    assert rel.max() <= 3.01 * 2.0 ** -24, rel.max()
+
+
 def test_gemv_w8_wide_dynamic_range(torch_dev):
     """One K-slice whose |x s| spans more than 2^30 (log-uniform magnitudes
-    from 2^-16 to 2^15, random signs): the f16 hi + lo carry of x s loses
-    relative precision only far below the slice maximum, so the result must
-    stay within the GEMM bound of the reference's dequantize + matmul."""
+    from 2^-16 to 2^15, random signs): the f16 pieces of x s lose relative
+    precision only far below the slice maximum, so the result must stay
+    within the GEMM bound of the reference's dequantize + matmul."""
     gh, O = _gh(), _O()
     rng = np.random.default_rng(21)
     b, k, n = 3, 1024, 768
