@@ -41,6 +41,7 @@
 // With block_n = 1 the recurrence is exact softmax attention.
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #include "attn_tiles.hpp"
 #include "common.hpp"
@@ -571,27 +572,37 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_onepass_kernel(FaFused p) {
     const int64_t ntiles = (kv_end + kBKV - 1) / kBKV;
 
     // Requests tile u (K and V) into its buffers.
+    auto issue_k = [&](int64_t u) { KL::issue(K, u * kBKV, p.sk, p.d, p.d, lk + (u & 1) * kTile, wave, lane); };
+    auto issue_v = [&](int64_t u) { VL::issue(V, u * kBKV, p.sk, p.d, p.d, lv + (u % NVB) * kTile, wave, lane); };
     auto issue = [&](int64_t u) {
-        KL::issue(K, u * kBKV, p.sk, p.d, p.d, lk + (u & 1) * kTile, wave, lane);
-        VL::issue(V, u * kBKV, p.sk, p.d, p.d, lv + (u % NVB) * kTile, wave, lane);
+        issue_k(u);
+        issue_v(u);
     };
-    // Scores of tile u into x, and the exact value of this row's largest
-    // one into ex (-inf without a visible key).
-    auto scores = [&](int64_t u, float (&x)[16], double &ex) {
+    // The exact score of key kw of K tile u for this row.
+    auto exact_score = [&](int64_t u, int kw) {
+        const float *ks = lk + (u & 1) * kTile;
+        return exact_dot(qf, [&](int g) { return ks + (2 * g + h) * (4 * kBKV) + 4 * kw; }) * (double)p.scale;
+    };
+    // Scores of tile u into x; with EXACT also the exact value of this
+    // row's largest one into ex (-inf without a visible key).
+    auto scores = [&](int64_t u, float (&x)[16], double &ex, auto exact) {
         const int64_t k0 = u * kBKV;
         ex = -INFINITY;
         if (!CAUSAL || k0 <= wq0 + 31) {
-            const float *ks = lk + (u & 1) * kTile;
-            fa_scores_lds<DMAX, CAUSAL>(p, ks, qf, k0, my_q, lane, x);
-            float mx;
-            const int kw = tile_argmax(x, h, mx);
-            const double dot = exact_dot(qf, [&](int g) { return ks + (2 * g + h) * (4 * kBKV) + 4 * kw; });
-            if (mx != -INFINITY) ex = dot * (double)p.scale;
+            fa_scores_lds<DMAX, CAUSAL>(p, lk + (u & 1) * kTile, qf, k0, my_q, lane, x);
+            if constexpr (decltype(exact)::value) {
+                float mx;
+                const int kw = tile_argmax(x, h, mx);
+                const double e = exact_score(u, kw);
+                if (mx != -INFINITY) ex = e;
+            }
         } else {
 #pragma unroll
             for (int r = 0; r < 16; ++r) x[r] = -INFINITY;
         }
     };
+    const std::true_type with_exact{};
+    const std::false_type no_exact{};
     // Weights of tile u of block blk in place (scores in x); adds
     // exp(s - mt) of its visible keys to ps.
     auto weights = [&](float (&x)[16], int64_t u, int64_t blk, int64_t n, float mt, float delta, float &ps) {
@@ -665,17 +676,30 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_onepass_kernel(FaFused p) {
         const int64_t blk = t / TPB;
         float sv[16];
         if (TPB == 2 && t + 1 < ntiles) {
-            // first tile of the block: scores wait in sa
+            // First tile of the block: scores wait in sa.  The block's
+            // exact max is taken once, from its key with the largest fp32
+            // score in either tile, so the first tile's K stays in its
+            // buffer until every wave has that score: the next block's
+            // first K tile (same buffer) is requested after a barrier.
             issue(t + 1);
-            scores(t, sa, xa);
+            scores(t, sa, xa, no_exact);
             attn::wait_vm0();
             __syncthreads();
-            if (t + 2 < ntiles) issue(t + 2);
-            scores(t + 1, sv, xv);
+            if (t + 2 < ntiles) issue_v(t + 2);
+            scores(t + 1, sv, xv, no_exact);
+            float mxa, mxv;
+            const int kwa = tile_argmax(sa, h, mxa);
+            const int kwv = tile_argmax(sv, h, mxv);
+            const bool first = mxa >= mxv;  // the same in both lanes of a row
+            const double e = exact_score(first ? t : t + 1, first ? kwa : kwv);
+            xa = -INFINITY;
+            xv = (first ? mxa : mxv) != -INFINITY ? e : -INFINITY;
+            __syncthreads();
+            if (t + 2 < ntiles) issue_k(t + 2);
             if (live(t) || live(t + 1)) finish(sa, sv, xa, xv, t, 2, blk);
         } else {
             if (t + 1 < ntiles) issue(t + 1);
-            scores(t, sv, xv);
+            scores(t, sv, xv, with_exact);
             if (live(t)) finish(sa, sv, xa, xv, t, 1, blk);
         }
         attn::wait_vm0();
