@@ -564,7 +564,6 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_onepass_kernel(FaFused p) {
     double m = -INFINITY;  // exact running max
     float l = 0.f;
     float sa[16];  // scores of a two-tile block's first tile
-    double xa = -INFINITY, xv = -INFINITY;  // exact maxima of sa / sv
 #pragma unroll
     for (int r = 0; r < 16; ++r) sa[r] = -INFINITY;
 
@@ -644,11 +643,10 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_onepass_kernel(FaFused p) {
     };
     // Block blk from tiles u0 .. u0 + nt - 1 (nt = 1 or 2), their scores in
     // sa (first of two) and sv.
-    // (exact maxima of the two tiles in xa_ / xv_)
-    auto finish = [&](float (&sa_)[16], float (&sv_)[16], double xa_, double xv_, int64_t u0, int nt,
-                      int64_t blk) {
+    // (bx: the block's exact max, -inf without a visible key)
+    auto finish = [&](float (&sa_)[16], float (&sv_)[16], double bx, int64_t u0, int nt, int64_t blk) {
         const int64_t n = min(p.bn, p.sk - blk * p.bn);
-        const double mt64 = fmax(m, nt == 2 ? fmax(xa_, xv_) : xv_);
+        const double mt64 = fmax(m, bx);
         // Key 0 is visible to every row, so m is finite from block 1 on.
         const float delta = blk == 0 ? 0.f : (float)(m - mt64);
         const float mt = (float)mt64;
@@ -682,25 +680,26 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_onepass_kernel(FaFused p) {
             // buffer until every wave has that score: the next block's
             // first K tile (same buffer) is requested after a barrier.
             issue(t + 1);
-            scores(t, sa, xa, no_exact);
+            double unused;
+            scores(t, sa, unused, no_exact);
             attn::wait_vm0();
             __syncthreads();
             if (t + 2 < ntiles) issue_v(t + 2);
-            scores(t + 1, sv, xv, no_exact);
+            scores(t + 1, sv, unused, no_exact);
             float mxa, mxv;
             const int kwa = tile_argmax(sa, h, mxa);
             const int kwv = tile_argmax(sv, h, mxv);
             const bool first = mxa >= mxv;  // the same in both lanes of a row
             const double e = exact_score(first ? t : t + 1, first ? kwa : kwv);
-            xa = -INFINITY;
-            xv = (first ? mxa : mxv) != -INFINITY ? e : -INFINITY;
+            const double bx = (first ? mxa : mxv) != -INFINITY ? e : -INFINITY;
             __syncthreads();
             if (t + 2 < ntiles) issue_k(t + 2);
-            if (live(t) || live(t + 1)) finish(sa, sv, xa, xv, t, 2, blk);
+            if (live(t) || live(t + 1)) finish(sa, sv, bx, t, 2, blk);
         } else {
             if (t + 1 < ntiles) issue(t + 1);
-            scores(t, sv, xv, with_exact);
-            if (live(t)) finish(sa, sv, xa, xv, t, 1, blk);
+            double bx;
+            scores(t, sv, bx, with_exact);
+            if (live(t)) finish(sa, sv, bx, t, 1, blk);
         }
         attn::wait_vm0();
         __syncthreads();
