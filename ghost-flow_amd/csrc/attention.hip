@@ -16,8 +16,12 @@
 //   * a row whose scores are all -inf yields NaN, as softmax over all -inf
 //     does in the reference (max = -inf, exp(NaN)).
 //
-// Layout (one 256-thread workgroup = 4 wave64s per 128 queries of one
-// (b, h); K/V streamed in 32-key tiles through double-buffered LDS):
+// Two kernels: sdpa_set_kernel (below) for every call without a weights
+// output -- 16-query sets on 16x16x4 MFMAs, light and heavy causal query
+// groups paired per SIMD, four waves per SIMD -- and sdpa_fwd_kernel, which
+// also writes the [sq, skv] weights.  sdpa_fwd_kernel's layout (one
+// 256-thread workgroup = 4 wave64s per 128 queries of one (b, h); K/V
+// streamed in 32-key tiles through double-buffered LDS):
 //   * S^T = K . Q^T on v_mfma_f32_32x32x2_f32: keys are the MFMA rows and
 //     queries the columns, so lane l owns query l%32 and holds 16 of the 32
 //     keys of a tile (the other 16 sit in lane l^32).  Row max / row sum are
@@ -265,6 +269,244 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(SdpaParams p) {
     }
 }
 
+// ---- balanced 16-query sets (no weights output) ------------------------------
+//
+// The same recurrence over 16-query sets on v_mfma_f32_16x16x4_f32 (same
+// rate per SIMD as the 32x32x2 form), one set per wave, eight waves per
+// workgroup.  The query groups of a (b, h) slice (G = ceil(sq / 16)) are
+// paired as (G - 1 - p, p): waves 0-3 take the light groups p = 4 blockIdx.y
+// + w, waves 4-7 the heavy groups G - 1 - p.  Under causal masking a pair
+// covers about (sq + 32) / 32 (16-query x 32-key) tile units whatever p is,
+// so every workgroup, and every SIMD (waves w and w + 4 share one), carries
+// the same load; with 32-query waves over 128-query blocks the heaviest
+// blocks set the critical path.  One set needs at most 128 registers, so two
+// 64 KB workgroups per CU put four waves on each SIMD, which hides the
+// softmax, LDS and barrier stalls that two waves per SIMD left exposed
+// (B=4, H=32, D=128 causal: S=512 88 us, S=2048 1.14 ms; with two sets per
+// wave and two waves per SIMD, 91 us and 1.17 ms).
+//
+// Fragment layouts (lane l, c = l % 16, quarter h = l / 16):
+//  * S^T = K . Q^T: A = K (row = key, k = dim), B = Q^T.  The four dims a
+//    lane supplies over steps e = 0..3 of dim group u are 16u + 4h + e, so a
+//    lane's K and Q operands for a group are one 16-byte read each.  The
+//    accumulator of key block kb (keys 16kb .. 16kb + 15) holds, in register
+//    r, key 16kb + 4h + r for query c.
+//  * O^T = V^T . P^T: step r of key block kb takes key 16kb + 4h + r in
+//    quarter h, so its B operand is register r of that block's scores and P
+//    never moves; the A operand is V[key][16b + c], one ds_read_b32.
+//  * O block b (dims 16b .. 16b + 15): lane holds dims 16b + 4h + r of query c.
+//  * K and V tiles are requested straight into LDS (global_load_lds, no
+//    staging registers).  K is chunk-major (16-byte chunk q of key r at slot
+//    32q + r: a fragment read is 256 contiguous bytes per quarter); V is
+//    key-major with chunk q of key r at q ^ (4 * bits 2-3 of r), so the four
+//    quarters of a V read (keys 4 apart, 16 dims each) fall on disjoint
+//    16-bank groups: quarter h finds dims 16b .. 16b + 15 at 16 (b ^ h).
+constexpr int kSetQ = 16;  // queries per set
+constexpr int kSetThreads = 512;
+
+// Max / sum over the four lanes c, c + 16, c + 32, c + 48 (one query's
+// scores), with gfx950's lane swaps: v_permlane16_swap pairs lane l with
+// l ^ 16 and v_permlane32_swap pairs it with l ^ 32 (both halves of each
+// result hold the two values), VALU ops instead of LDS-path permutes.
+__device__ __forceinline__ float quarter_max(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float quarter_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+template <int DMAX>
+struct QuerySet {
+    static constexpr int NU = DMAX / 16;  // 16-dim groups
+    f32x4 qf[NU];
+    f32x4 o[NU];
+    float m, l;
+    int q;       // this lane's query
+    int kv_end;  // keys this set reads (causal: up to its last query)
+    bool valid;
+};
+
+// One 32-key tile for a set.  kq = this lane's K fragment base; vb[j] = its
+// V base for the dim blocks b with b % 4 == j (the quarter swizzle above).
+template <int DMAX, bool CAUSAL, bool MASK>
+__device__ __forceinline__ void set_tile(const SdpaParams &p, QuerySet<DMAX> &st, const float *kq,
+                                         const float *(&vb)[4], int k0, int h) {
+    constexpr int NU = DMAX / 16;
+    f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    // The MFMA phases run at raised wave priority, so that another wave of
+    // the SIMD in its softmax does not delay their issue.
+    __builtin_amdgcn_s_setprio(1);
+    // K fragments one dim group ahead of the MFMAs that use them: chunk
+    // 4u + h of key 16kb + c (kq already holds h and c).
+    auto kfrag = [&](int u, int kb) { return *reinterpret_cast<const f32x4 *>(kq + 4 * (128 * u + 16 * kb)); };
+    f32x4 kf[2][2];
+    kf[0][0] = kfrag(0, 0);
+    kf[0][1] = kfrag(0, 1);
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+        if (u + 1 < NU) {
+            kf[(u + 1) & 1][0] = kfrag(u + 1, 0);
+            kf[(u + 1) & 1][1] = kfrag(u + 1, 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of these MFMAs
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+                acc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[u & 1][kb][e], st.qf[u][e], acc[kb], 0, 0, 0);
+    }
+    __builtin_amdgcn_s_setprio(0);
+
+    // Scale, mask, online softmax.  lim = the last key of the tile the query
+    // keeps, relative to k0 (clamped to the tile: 32-bit comparisons).
+    int last = (int)p.skv - 1;
+    if (CAUSAL) last = min(last, st.q + (int)p.causal_off);
+    const int lim = max(-1, min(kBKV, last - k0));
+    float pv[8];
+    float mb = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int j = 16 * (i >> 2) + 4 * h + (i & 3);
+        const float v = acc[i >> 2][i & 3] * p.scale;
+        bool keep = j <= lim;
+        if (MASK && keep) {
+            const int64_t f = ((int64_t)blockIdx.x * p.sq + st.q) * p.skv + (k0 + j);
+            keep = p.mask[f % p.mask_numel] > 0.5f;
+        }
+        pv[i] = keep ? v : -INFINITY;
+        mb = fmaxf(mb, pv[i]);
+    }
+    const float m_new = fmaxf(st.m, quarter_max(mb));
+    const bool dead = (m_new == -INFINITY);  // every score so far masked
+    const float alpha = dead ? 1.f : __expf(st.m - m_new);
+    float psum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        pv[i] = dead ? 0.f : __expf(pv[i] - m_new);
+        psum += pv[i];
+    }
+    st.l = st.l * alpha + quarter_sum(psum);
+    st.m = m_new;
+#pragma unroll
+    for (int b = 0; b < NU; ++b) st.o[b] *= alpha;
+
+    // P.V step i = 4 kb + r: key 16kb + 4h + r (4h is in vb), dim 16b + c;
+    // the V elements of step i + 1 are read while step i's MFMAs run.
+    auto vload = [&](int i, float (&va)[NU]) {
+#pragma unroll
+        for (int b = 0; b < NU; ++b) va[b] = vb[b & 3][(16 * (i >> 2) + (i & 3)) * DMAX + 64 * (b >> 2)];
+    };
+    __builtin_amdgcn_s_setprio(1);
+    float va[2][NU];
+    vload(0, va[0]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        if (i + 1 < 8) vload(i + 1, va[(i + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int b = 0; b < NU; ++b)
+            st.o[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[i & 1][b], pv[i], st.o[b], 0, 0, 0);
+    }
+    __builtin_amdgcn_s_setprio(0);
+}
+
+// At most 128 registers per lane (the second bound is waves per SIMD):
+// two workgroups per CU, four waves per SIMD.
+template <int DMAX, bool CAUSAL, bool MASK>
+__global__ __launch_bounds__(kSetThreads, 4) void sdpa_set_kernel(SdpaParams p) {
+    static_assert(DMAX == 64 || DMAX == 128, "direct-to-LDS tiles cover 64 or 128 dims");
+    constexpr int NU = DMAX / 16;
+    constexpr int kTile = kBKV * DMAX;
+    using KLoad = attn::KvLds<DMAX, kSetThreads, false>;
+    using VLoad = attn::KvLds<DMAX, kSetThreads, true, true>;
+    __shared__ __attribute__((aligned(16))) float lds[4 * kTile];  // K0 K1 V0 V1
+    float *const lk = lds;
+    float *const lv = lds + 2 * kTile;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: set bounds and LDS targets in SGPRs
+    const int c = lane & 15, h = lane >> 4;
+    const int64_t bh = blockIdx.x;
+    const int64_t bb = bh / p.h, hh = bh % p.h;
+    const float *Q = p.q + bb * p.q_bs + hh * p.q_hs;
+    const float *K = p.k + bb * p.kv_bs + hh * p.kv_hs;
+    const float *V = p.v + bb * p.kv_bs + hh * p.kv_hs;
+
+    // Indices are 32-bit (the launcher requires sq, skv < 2^31).  The heavy
+    // wave holds group G - 1 - pair (the middle group of an odd G included),
+    // the light wave group pair when it is smaller; neither exists for pairs
+    // past the last.
+    const int sq = (int)p.sq, skv = (int)p.skv;
+    const int ngroups = (sq + kSetQ - 1) / kSetQ;
+    const int pair = (int)blockIdx.y * 4 + (wave & 3);
+    const bool heavy = wave >= 4;
+    auto kv_end_of = [&](int g) -> int {
+        return CAUSAL ? min(skv, min((g + 1) * kSetQ, sq) + (int)p.causal_off) : skv;
+    };
+    QuerySet<DMAX> st;
+    const int g = heavy ? ngroups - 1 - pair : pair;
+    st.valid = heavy ? ngroups - 1 - pair >= pair : ngroups - 1 - pair > pair;
+    st.q = g * kSetQ + c;
+    st.kv_end = kv_end_of(g);
+    st.m = -INFINITY;
+    st.l = 0.f;
+#pragma unroll
+    for (int u = 0; u < NU; ++u) {
+        const int dim = 16 * u + 4 * h;
+        // Branch-free: a clamped address, zero where there is no query or dim.
+        const bool in = st.valid && st.q < sq && dim < p.d;
+        const int64_t row = st.valid ? min(st.q, sq - 1) : 0;
+        const f32x4 v = *reinterpret_cast<const f32x4 *>(Q + row * p.q_rs + (dim < p.d ? dim : 0));
+        st.qf[u] = in ? v : f32x4{0.f, 0.f, 0.f, 0.f};
+        st.o[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // The workgroup streams the keys of its heaviest set: wave 4's.
+    const int kv_end = kv_end_of(ngroups - 1 - (int)blockIdx.y * 4);
+    const int ntiles = (kv_end + kBKV - 1) / kBKV;
+
+    if (ntiles > 0) {
+        KLoad::issue(K, 0, skv, p.d, p.kv_rs, lk, wave, lane);
+        VLoad::issue(V, 0, skv, p.d, p.kv_rs, lv, wave, lane);
+    }
+    attn::wait_vm0();
+    __syncthreads();
+
+    for (int t = 0; t < ntiles; ++t) {
+        const int cur = t & 1;
+        // The other buffers were last read before the previous barrier.
+        if (t + 1 < ntiles) {
+            KLoad::issue(K, (t + 1) * kBKV, skv, p.d, p.kv_rs, lk + (cur ^ 1) * kTile, wave, lane);
+            VLoad::issue(V, (t + 1) * kBKV, skv, p.d, p.kv_rs, lv + (cur ^ 1) * kTile, wave, lane);
+        }
+        const int k0 = t * kBKV;
+        const float *kq = lk + cur * kTile + 4 * (32 * h + c);
+        const float *vt = lv + cur * kTile + 4 * h * DMAX + c;
+        const float *vb[4] = {vt + 16 * (0 ^ h), vt + 16 * (1 ^ h), vt + 16 * (2 ^ h), vt + 16 * (3 ^ h)};
+        if (st.valid && k0 < st.kv_end) set_tile<DMAX, CAUSAL, MASK>(p, st, kq, vb, k0, h);
+        attn::wait_vm0();
+        __syncthreads();
+    }
+
+    // O = O / l; lane (query c, quarter h) holds dims 16b + 4h .. + 3.
+    if (st.valid && st.q < sq) {
+        const float inv_l = 1.0f / st.l;
+        float *orow = p.out + bb * p.o_bs + hh * p.o_hs + (int64_t)st.q * p.o_rs;
+#pragma unroll
+        for (int b = 0; b < NU; ++b) {
+            const int dim = 16 * b + 4 * h;
+            if (dim < p.d) *reinterpret_cast<f32x4 *>(orow + dim) = st.o[b] * inv_l;
+        }
+    }
+}
+
 // ---- row softmax (Tensor::softmax(-1)) ---------------------------------------
 // Per row, as activation.rs:188-212: a max fold from -inf (NaN-ignoring, like
 // f32::max), the sum of exp(x - max), then exp(x - max) / sum with a true
@@ -363,8 +605,32 @@ void launch_sdpa_variant(const SdpaParams &p, dim3 grid, bool weights, hipStream
         hipLaunchKernelGGL((sdpa_fwd_kernel<DMAX, CAUSAL, MASK, false>), grid, dim3(kThreads), 0, s, p);
 }
 
+// Head dims up to 32 run the 64-dim tiles (the direct-to-LDS loader's
+// smallest row).
+template <int DMAX, bool CAUSAL>
+void launch_sdpa_sets(const SdpaParams &p, bool mask, hipStream_t s) {
+    constexpr int DP = DMAX < 64 ? 64 : DMAX;
+    const int64_t groups = (p.sq + kSetQ - 1) / kSetQ;
+    const int64_t pairs = (groups + 1) / 2;
+    const dim3 grid((unsigned)p.bh, (unsigned)((pairs + 3) / 4));
+    if (mask)
+        hipLaunchKernelGGL((sdpa_set_kernel<DP, CAUSAL, true>), grid, dim3(kSetThreads), 0, s, p);
+    else
+        hipLaunchKernelGGL((sdpa_set_kernel<DP, CAUSAL, false>), grid, dim3(kSetThreads), 0, s, p);
+}
+
 template <int DMAX>
 void launch_sdpa_d(const SdpaParams &p, dim3 grid, bool causal, bool mask, bool weights, hipStream_t s) {
+    // The balanced kernel serves every call without a weights output whose
+    // indices fit 32 bits; the 32-query kernel writes the weights.
+    constexpr int64_t kMax32 = (int64_t)1 << 31;
+    if (!weights && p.sq + p.causal_off < kMax32 && p.skv < kMax32 - kBKV) {
+        if (causal)
+            launch_sdpa_sets<DMAX, true>(p, mask, s);
+        else
+            launch_sdpa_sets<DMAX, false>(p, mask, s);
+        return;
+    }
     if (causal) {
         if (mask)
             launch_sdpa_variant<DMAX, true, true>(p, grid, weights, s);

@@ -38,6 +38,22 @@ struct KvStage {
             r[i] = v;
         }
     }
+    // The same tile without branches: every lane loads from an address
+    // clamped into the operand (the last key, chunk 0 of the row) and keeps
+    // zero where load() would skip the load (nkeys >= 1).
+    __device__ __forceinline__ void load_clamped(const float *__restrict__ base, int64_t key0, int64_t nkeys,
+                                                 int64_t d, int64_t rs, int tid) {
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int idx = tid + i * NT;
+            const int key = idx / (DMAX / 4);
+            const int dim = (idx % (DMAX / 4)) * 4;
+            const bool in = key0 + key < nkeys && dim < d;
+            const int64_t row = min(key0 + key, nkeys - 1);
+            const f32x4 v = *reinterpret_cast<const f32x4 *>(base + row * rs + (dim < d ? dim : 0));
+            r[i] = in ? v : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
     __device__ __forceinline__ void store(float *lds, int tid) const {
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
@@ -69,7 +85,10 @@ struct KvStage {
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 typedef __attribute__((address_space(1))) void *glb_ptr_t;
 
-template <int DMAX, int NT, bool IS_V>
+// VQ4 (V tiles only): chunk q of key r at q ^ (4 * bits 2-3 of r) instead,
+// for readers whose four lane quarters take keys 4 apart (16 consecutive dims
+// each): the quarters then fall on four disjoint 16-bank groups.
+template <int DMAX, int NT, bool IS_V, bool VQ4 = false>
 struct KvLds {
     static_assert(DMAX == 64 || DMAX == 128, "direct-to-LDS tiles cover 64 or 128 dims");
     static constexpr int kTileFloats = kBKV * DMAX;
@@ -88,7 +107,7 @@ struct KvLds {
             int row, lc;
             if (IS_V) {
                 row = ins * (64 / kChunks) + lane / kChunks;
-                lc = (lane % kChunks) ^ (8 * ((row >> 2) & 1));
+                lc = VQ4 ? (lane % kChunks) ^ (4 * ((row >> 2) & 3)) : (lane % kChunks) ^ (8 * ((row >> 2) & 1));
             } else {
                 row = lane & 31;
                 lc = 2 * ins + (lane >> 5);

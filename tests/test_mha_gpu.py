@@ -94,11 +94,19 @@ def test_causal_flag_equals_lower_triangular_mask(torch_dev, sq, p):
     kc[:, :p] = to_dev(pk, torch_dev)
     vc[:, :p] = to_dev(pv, torch_dev)
     dx = to_dev(x, torch_dev)
+    dm = to_dev(mask, torch_dev)
+    # with the weights output (the 32-query kernel) and without it (the
+    # balanced-set kernel): the flag and the mask agree bit for bit on each
     out, w = gh.mha_forward_cached(dx, dx, dx, *dev, h, kc, vc, p, causal=True, want_weights=True)
     assert_rel(to_np(out), ref[0])
     assert_rel(to_np(w), ref[1])
-    out2 = gh.mha_forward_cached(dx, dx, dx, *dev, h, kc, vc, p, mask=to_dev(mask, torch_dev))
-    np.testing.assert_array_equal(to_np(out2), to_np(out))
+    out_m, w_m = gh.mha_forward_cached(dx, dx, dx, *dev, h, kc, vc, p, mask=dm, want_weights=True)
+    np.testing.assert_array_equal(to_np(out_m), to_np(out))
+    np.testing.assert_array_equal(to_np(w_m), to_np(w))
+    out_c = gh.mha_forward_cached(dx, dx, dx, *dev, h, kc, vc, p, causal=True)
+    assert_rel(to_np(out_c), ref[0])
+    out2 = gh.mha_forward_cached(dx, dx, dx, *dev, h, kc, vc, p, mask=dm)
+    np.testing.assert_array_equal(to_np(out2), to_np(out_c))
 
 
 def test_incremental_decoding_matches_full_causal_forward(torch_dev):
