@@ -304,22 +304,8 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(SdpaParams p) {
 constexpr int kSetQ = 16;  // queries per set
 constexpr int kSetThreads = 512;
 
-// Max / sum over the four lanes c, c + 16, c + 32, c + 48 (one query's
-// scores), with gfx950's lane swaps: v_permlane16_swap pairs lane l with
-// l ^ 16 and v_permlane32_swap pairs it with l ^ 32 (both halves of each
-// result hold the two values), VALU ops instead of LDS-path permutes.
-__device__ __forceinline__ float quarter_max(float x) {
-    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
-    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
-}
-__device__ __forceinline__ float quarter_sum(float x) {
-    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
+using attn::quarter_max;
+using attn::quarter_sum;
 
 template <int DMAX>
 struct QuerySet {
@@ -424,7 +410,7 @@ __global__ __launch_bounds__(kSetThreads, 4) void sdpa_set_kernel(SdpaParams p) 
     constexpr int NU = DMAX / 16;
     constexpr int kTile = kBKV * DMAX;
     using KLoad = attn::KvLds<DMAX, kSetThreads, false>;
-    using VLoad = attn::KvLds<DMAX, kSetThreads, true, true>;
+    using VLoad = attn::KvLds<DMAX, kSetThreads, true>;
     __shared__ __attribute__((aligned(16))) float lds[4 * kTile];  // K0 K1 V0 V1
     float *const lk = lds;
     float *const lv = lds + 2 * kTile;

@@ -4,6 +4,8 @@
 // register holds.
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace gfh {
@@ -76,19 +78,16 @@ struct KvStage {
 //    fragment read (ds_read_b128; 16 lanes on keys 0..15 at one chunk) is
 //    256 contiguous bytes, and the address is a lane base plus a constant
 //    per chunk.  Instruction i loads chunks 2i, 2i + 1 of all 32 keys.
-//  * V tiles are key-major, chunk q of key r at chunk q ^ (8 * bit 2 of r):
-//    the two lane halves of a P.V operand read (ds_read_b32 of 32
-//    consecutive dims of keys k and k + 4) hit disjoint halves of the 64
-//    banks.  Instruction i loads 1024 / (4 DMAX) whole keys.
+//  * V tiles are key-major, chunk q of key r at chunk q ^ (4 * bits 2-3 of
+//    r): a P.V operand read of the 16x16x4 layouts (four lane quarters on
+//    keys 4 apart, 16 consecutive dims each) then falls on four disjoint
+//    16-bank groups.  Instruction i loads 1024 / (4 DMAX) whole keys.
 // Keys past nkeys read the last key and chunks past d read chunk 0 of the
 // row: finite values that meet a -inf score (weight 0) or a zero query dim.
 typedef __attribute__((address_space(3))) void *lds_ptr_t;
 typedef __attribute__((address_space(1))) void *glb_ptr_t;
 
-// VQ4 (V tiles only): chunk q of key r at q ^ (4 * bits 2-3 of r) instead,
-// for readers whose four lane quarters take keys 4 apart (16 consecutive dims
-// each): the quarters then fall on four disjoint 16-bank groups.
-template <int DMAX, int NT, bool IS_V, bool VQ4 = false>
+template <int DMAX, int NT, bool IS_V>
 struct KvLds {
     static_assert(DMAX == 64 || DMAX == 128, "direct-to-LDS tiles cover 64 or 128 dims");
     static constexpr int kTileFloats = kBKV * DMAX;
@@ -107,7 +106,7 @@ struct KvLds {
             int row, lc;
             if (IS_V) {
                 row = ins * (64 / kChunks) + lane / kChunks;
-                lc = VQ4 ? (lane % kChunks) ^ (4 * ((row >> 2) & 3)) : (lane % kChunks) ^ (8 * ((row >> 2) & 1));
+                lc = (lane % kChunks) ^ (4 * ((row >> 2) & 3));
             } else {
                 row = lane & 31;
                 lc = 2 * ins + (lane >> 5);
@@ -120,17 +119,62 @@ struct KvLds {
     }
 };
 
-// Score operand: dims 8 g + 4 h .. + 3 of key c of a K tile (chunk 2 g + h).
-template <int DMAX>
-__device__ __forceinline__ f32x4 k_frag(const float *ks, int c, int h, int g) {
-    return *reinterpret_cast<const f32x4 *>(ks + (2 * g + h) * (4 * kBKV) + 4 * c);
+// ---- one query's four lanes (16x16x4 layouts) ---------------------------------
+//
+// In the 16-query layouts (lane l holds query l % 16 in quarter l / 16) a
+// query's values sit in lanes c, c + 16, c + 32, c + 48.  These fold them
+// with gfx950's lane swaps: v_permlane16_swap pairs lane l with l ^ 16 and
+// v_permlane32_swap pairs it with l ^ 32 (both halves of each result hold
+// the two values), VALU ops instead of LDS-path permutes.  Every lane of the
+// query ends with the same result.
+__device__ __forceinline__ float quarter_max(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
-
-// P.V operand: dim 32 j + c of key row `key` of a V tile, for the lane half
-// h = bit 2 of key.
-template <int DMAX>
-__device__ __forceinline__ float v_elem(const float *vt, int key, int h, int c, int j) {
-    return vt[key * DMAX + 32 * (j ^ h) + c];
+__device__ __forceinline__ float quarter_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+// The partner's copy of x across lane bit 4 (l ^ 16) or bit 5 (l ^ 32).
+template <int BIT>
+__device__ __forceinline__ unsigned swap_partner(unsigned x, int lane) {
+    const auto a = BIT == 4 ? __builtin_amdgcn_permlane16_swap(x, x, false, false)
+                            : __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    // a holds {lower lane's value, upper lane's value} of the pair
+    return ((lane >> BIT) & 1) ? a[0] : a[1];
+}
+// fp64 sum over the query's four lanes, in a fixed order for every lane:
+// (quarter 0 + quarter 1) + (quarter 2 + quarter 3).
+__device__ __forceinline__ double quarter_sum_f64(double x, int lane) {
+    auto partner = [&](double v, auto bit) {
+        constexpr int B = decltype(bit)::value;
+        const unsigned long long u = __double_as_longlong(v);
+        const unsigned lo = swap_partner<B>((unsigned)u, lane), hi = swap_partner<B>((unsigned)(u >> 32), lane);
+        return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+    };
+    const double y = partner(x, std::integral_constant<int, 4>{});
+    x = ((lane >> 4) & 1) ? y + x : x + y;
+    const double z = partner(x, std::integral_constant<int, 5>{});
+    return ((lane >> 5) & 1) ? z + x : x + z;
+}
+// The largest value over the query's four lanes and its key; ties go to
+// the smaller key, so every lane picks the same one.
+__device__ __forceinline__ void quarter_argmax(float &v, int &key, int lane) {
+    auto pick = [&](auto bit) {
+        constexpr int B = decltype(bit)::value;
+        const float pv = __uint_as_float(swap_partner<B>(__float_as_uint(v), lane));
+        const int pk = (int)swap_partner<B>((unsigned)key, lane);
+        if (pv > v || (pv == v && pk < key)) {
+            v = pv;
+            key = pk;
+        }
+    };
+    pick(std::integral_constant<int, 4>{});
+    pick(std::integral_constant<int, 5>{});
 }
 
 // s_waitcnt vmcnt(0): this wave's global loads (and LDS-bound requests) are done.

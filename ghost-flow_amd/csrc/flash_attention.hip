@@ -16,8 +16,8 @@
 //   o = sum_t sum_{j in t} p_j c_t^(n_t - 1 - idx_j) prod_{t' > t} c_t'^n_t' v_j
 // where the first block has c_0 = exp(-inf) = 0 (only its last key survives),
 // and l = sum_j exp(s_j - m_last).  Three forms compute it:
-//   * fa_onepass_kernel (block_n = 32 or 64): the recurrence per key block
-//     in closed form, one pass (below);
+//   * fa_set_kernel (block_n = 32 or 64): the recurrence per key block in
+//     closed form, one pass, on 16-query sets (below);
 //   * fa_fused_kernel (other multiples of 32): two passes, the block maxima
 //     first (below);
 //   * otherwise three steps:
@@ -492,231 +492,309 @@ __global__ __launch_bounds__(kFaThreads, 2) void fa_fused_kernel(FaFused p) {
 // scores wait in registers until the second gives the block max.  K tiles
 // are double-buffered and V tiles triple-buffered through LDS (tile u in V
 // buffer u % 3), all requested straight into LDS one tile ahead; 80 KB per
-// workgroup at d <= 128, two workgroups per CU.
-template <int DMAX, bool CAUSAL>
-__device__ __forceinline__ void fa_scores_lds(const FaFused &p, const float *ks, const f32x4 (&qf)[DMAX / 8],
-                                              int64_t k0, int64_t my_q, int lane, float (&sv)[16]) {
-    constexpr int NG = DMAX / 8;
-    constexpr int kBKV = attn::kBKV;
-    const int c = lane & 31, h = lane >> 5;
-    f32x16 acc;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-        const f32x4 kf = attn::k_frag<DMAX>(ks, c, h, g);
-#pragma unroll
-        for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[s], qf[g][s], acc, 0, 0, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // MFMA
-    }
-    // keys k0 + i with i < lim are visible to this row
-    int64_t lim64 = p.sk - k0;
-    if (CAUSAL) lim64 = min(lim64, my_q - k0 + 1);
-    const int lim = (int)max<int64_t>(0, min<int64_t>(lim64, kBKV));
-#pragma unroll
-    for (int r = 0; r < 16; ++r) sv[r] = attn::key_of(r, h) < lim ? acc[r] * p.scale : -INFINITY;
-}
+// workgroup at d <= 128.
+//
+// Laid out as the balanced SDPA kernel:
+// 16-query sets on v_mfma_f32_16x16x4_f32, one set per wave, eight waves per
+// workgroup.  The query groups of a batch element (G = ceil(sq / 16)) are
+// paired as (G - 1 - p, p): waves 0-3 take the light groups p = 4 blockIdx.y
+// + w, waves 4-7 the heavy groups G - 1 - p, so under causal masking every
+// workgroup and every SIMD (waves w and w + 4 share one) carries the same
+// load.  A set walks the key blocks up to the one holding its last visible
+// key (blocks past it are fully masked for every row of the set and change
+// neither M nor O).  At most 128 registers per lane: two 80 KB workgroups
+// per CU, four waves per SIMD.
+//
+// Per lane (c = l % 16, quarter h = l / 16): dims 16u + 4h .. + 3 of query c
+// for the scores (S^T = K . Q^T), keys 16kb + 4h + r of a tile in score
+// register 4kb + r, dims 16b + 4h + r of the output.  The block's exact max
+// is the fp64 q . k of the query's largest fp32 score (its four lanes agree
+// on the key: quarter_argmax), each lane summing its own 8 x 4 dims and the
+// four partial sums added in a fixed order.  K tiles are chunk-major, V
+// tiles key-major with the 4-way swizzle of the quarter reads.
+constexpr int kFaSetThreads = 512;
 
 template <int DMAX, bool CAUSAL, int TPB>
-__global__ __launch_bounds__(kFaThreads, 2) void fa_onepass_kernel(FaFused p) {
+__global__ __launch_bounds__(kFaSetThreads, 4) void fa_set_kernel(FaFused p) {
     static_assert(TPB == 1 || TPB == 2, "32- or 64-key blocks");
-    constexpr int NG = DMAX / 8, ND = DMAX / 32;
+    constexpr int NU = DMAX / 16;
     constexpr int kBKV = attn::kBKV;
     constexpr int kTile = kBKV * DMAX;
     constexpr int NVB = TPB + 1;  // V tile buffers
-    using KL = attn::KvLds<DMAX, kFaThreads, false>;
-    using VL = attn::KvLds<DMAX, kFaThreads, true>;
+    using KL = attn::KvLds<DMAX, kFaSetThreads, false>;
+    using VL = attn::KvLds<DMAX, kFaSetThreads, true>;
     __shared__ __attribute__((aligned(1024))) float lds[(2 + NVB) * kTile];
     float *const lk = lds;
     float *const lv = lds + 2 * kTile;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int c = lane & 31, h = lane >> 5;
+    const int c = lane & 15, h = lane >> 4;
     const int64_t b = blockIdx.x;
-    int qb = (int)blockIdx.y;
-    if (CAUSAL) {
-        const int y = (int)blockIdx.y, half = (p.nqb + 1) / 2;
-        qb = (p.fold && y >= half) ? y - half : p.nqb - 1 - y;
-    }
-    const int64_t q0 = (int64_t)qb * kFaBQ;
-    const int64_t wq0 = q0 + wave * 32;
-    const int64_t my_q = wq0 + c;
-    const bool row_ok = my_q < p.sq;
+    // 32-bit indices (the launcher checks sq, sk < 2^31)
+    const int sq = (int)p.sq, sk = (int)p.sk, bn = (int)p.bn;
+    const int ngroups = (sq + 15) / 16;
+    const int pair = (int)blockIdx.y * 4 + (wave & 3);
+    const bool heavy = wave >= 4;
+    const int g = heavy ? ngroups - 1 - pair : pair;
+    const bool valid = heavy ? ngroups - 1 - pair >= pair : ngroups - 1 - pair > pair;
+    const int my_q = 16 * g + c;
+    const int last_q = min(16 * g + 15, sq - 1);  // the set's last query
+    auto blocks_of = [&](int gg) {
+        const int end = CAUSAL ? min(sk, min(16 * gg + 16, sq)) : sk;
+        return (end + bn - 1) / bn;
+    };
+    const int my_blocks = valid ? blocks_of(g) : 0;
+    const int ntiles = min((sk + kBKV - 1) / kBKV, blocks_of(ngroups - 1 - (int)blockIdx.y * 4) * TPB);
     const float *Q = p.q + b * p.sq * p.d;
     const float *K = p.k + b * p.sk * p.d;
     const float *V = p.v + b * p.sk * p.d;
 
-    f32x4 qf[NG];
+    f32x4 qf[NU], o[NU];
 #pragma unroll
-    for (int g = 0; g < NG; ++g) {
-        const int dim = 8 * g + 4 * h;
-        f32x4 v = {0.f, 0.f, 0.f, 0.f};
-        if (row_ok && dim < p.d) v = *reinterpret_cast<const f32x4 *>(Q + my_q * p.d + dim);
-        qf[g] = v;
+    for (int u = 0; u < NU; ++u) {
+        const int dim = 16 * u + 4 * h;
+        // Branch-free: a clamped address, zero where there is no query or dim.
+        const bool in = valid && my_q < sq && dim < p.d;
+        const int64_t row = valid ? min(my_q, sq - 1) : 0;
+        const f32x4 v = *reinterpret_cast<const f32x4 *>(Q + row * p.d + (dim < p.d ? dim : 0));
+        qf[u] = in ? v : f32x4{0.f, 0.f, 0.f, 0.f};
+        o[u] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    f32x16 o[ND];
-#pragma unroll
-    for (int j = 0; j < ND; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[j][r] = 0.f;
     double m = -INFINITY;  // exact running max
     float l = 0.f;
-    float sa[16];  // scores of a two-tile block's first tile
-#pragma unroll
-    for (int r = 0; r < 16; ++r) sa[r] = -INFINITY;
 
-    const int64_t kv_end = CAUSAL ? min(p.sk, q0 + kFaBQ) : p.sk;
-    const int64_t ntiles = (kv_end + kBKV - 1) / kBKV;
-
-    // Requests tile u (K and V) into its buffers.
-    auto issue_k = [&](int64_t u) { KL::issue(K, u * kBKV, p.sk, p.d, p.d, lk + (u & 1) * kTile, wave, lane); };
-    auto issue_v = [&](int64_t u) { VL::issue(V, u * kBKV, p.sk, p.d, p.d, lv + (u % NVB) * kTile, wave, lane); };
-    auto issue = [&](int64_t u) {
+    // The requests' per-lane addresses are recomputed at every call (a few
+    // VALU ops per tile): hoisted out of the key loop they would hold two
+    // registers per request for the whole loop, which this kernel's 128
+    // cannot spare.
+    auto fresh_lane = [&]() {
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        return ln;
+    };
+    auto issue_k = [&](int u) {
+        KL::issue(K, u * kBKV, p.sk, p.d, p.d, lk + (u & 1) * kTile, wave, fresh_lane());
+    };
+    auto issue_v = [&](int u) {
+        VL::issue(V, u * kBKV, p.sk, p.d, p.d, lv + (u % NVB) * kTile, wave, fresh_lane());
+    };
+    auto issue = [&](int u) {
         issue_k(u);
         issue_v(u);
     };
-    // The exact score of key kw of K tile u for this row.
-    auto exact_score = [&](int64_t u, int kw) {
-        const float *ks = lk + (u & 1) * kTile;
-        return exact_dot(qf, [&](int g) { return ks + (2 * g + h) * (4 * kBKV) + 4 * kw; }) * (double)p.scale;
-    };
-    // Scores of tile u into x; with EXACT also the exact value of this
-    // row's largest one into ex (-inf without a visible key).
-    auto scores = [&](int64_t u, float (&x)[16], double &ex, auto exact) {
-        const int64_t k0 = u * kBKV;
-        ex = -INFINITY;
-        if (!CAUSAL || k0 <= wq0 + 31) {
-            fa_scores_lds<DMAX, CAUSAL>(p, lk + (u & 1) * kTile, qf, k0, my_q, lane, x);
-            if constexpr (decltype(exact)::value) {
-                float mx;
-                const int kw = tile_argmax(x, h, mx);
-                const double e = exact_score(u, kw);
-                if (mx != -INFINITY) ex = e;
-            }
-        } else {
+    // Scores of tile u (scaled; -inf where the key is not visible).
+    auto scores = [&](int u, float (&x)[8]) {
+        const int k0 = u * kBKV;
+        if (CAUSAL && k0 > last_q) {  // past every query of the set
 #pragma unroll
-            for (int r = 0; r < 16; ++r) x[r] = -INFINITY;
+            for (int i = 0; i < 8; ++i) x[i] = -INFINITY;
+            return;
+        }
+        // lane-derived values recomputed here (a reload from scratch in the
+        // loop would also wait for the tiles in flight)
+        int ln = (int)__lane_id();
+        asm volatile("" : "+v"(ln));
+        const int h = ln >> 4, c = ln & 15;
+        const float *kq = lk + (u & 1) * kTile + 4 * (32 * h + c);
+        auto kfrag = [&](int uu, int kb) { return *reinterpret_cast<const f32x4 *>(kq + 4 * (128 * uu + 16 * kb)); };
+        f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        __builtin_amdgcn_s_setprio(1);
+        f32x4 kf[2][2];
+        kf[0][0] = kfrag(0, 0);
+        kf[0][1] = kfrag(0, 1);
+#pragma unroll
+        for (int uu = 0; uu < NU; ++uu) {
+            if (uu + 1 < NU) {
+                kf[(uu + 1) & 1][0] = kfrag(uu + 1, 0);
+                kf[(uu + 1) & 1][1] = kfrag(uu + 1, 1);
+            }
+            __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of these MFMAs
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+                    acc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[uu & 1][kb][e], qf[uu][e], acc[kb], 0, 0, 0);
+        }
+        __builtin_amdgcn_s_setprio(0);
+        // keys k0 + j with j < lim are visible to this row
+        int lim = sk - k0;
+        if (CAUSAL) lim = min(lim, 16 * g + c - k0 + 1);  // this row's query + 1 - k0
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int j = 16 * (i >> 2) + 4 * h + (i & 3);
+            x[i] = j < lim ? acc[i >> 2][i & 3] * p.scale : -INFINITY;
         }
     };
-    const std::true_type with_exact{};
-    const std::false_type no_exact{};
-    // Weights of tile u of block blk in place (scores in x); adds
-    // exp(s - mt) of its visible keys to ps.
-    auto weights = [&](float (&x)[16], int64_t u, int64_t blk, int64_t n, float mt, float delta, float &ps) {
-        // key_of(r, h) = 4 h + kr, kr = 8 (r / 4) + r % 4; the key's
-        // position in its block is base + 4 h + kr, so n - 1 - idx =
-        // rest - kr with rest = n - 1 - base - 4 h (small integers, exact).
-        const int base = (int)(u * kBKV - blk * p.bn);
-        const int rest = (int)n - 1 - base - 4 * h;
-        const float frest = (float)rest;
+    // This row's largest fp32 score over the block's NT tiles and its key
+    // in the block (the same in the query's four lanes); the exact score of
+    // that key (tile t0 + key / 32), or -inf without a visible key.
+    auto block_max = [&](const float (&xa)[8], const float (&xb)[8], auto ntc, int t0) -> double {
+        constexpr int NT = decltype(ntc)::value;
+        // lane, quarter and column recomputed here (cheaper than holding
+        // them through the loop, where a reload from scratch would also wait
+        // for the tiles in flight)
+        int ln = (int)__lane_id();
+        asm volatile("" : "+v"(ln));
+        const int h = ln >> 4;
+        float mv = -INFINITY;
+        int mk = 0;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int kr = 8 * (r >> 2) + (r & 3);
+        for (int ti = 0; ti < NT; ++ti)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float x = ti == 0 && NT == 2 ? xa[i] : xb[i];
+                if (x > mv) {  // keys rise with (ti, i): ties keep the smaller
+                    mv = x;
+                    mk = 32 * ti + 16 * (i >> 2) + 4 * h + (i & 3);
+                }
+            }
+        attn::quarter_argmax(mv, mk, ln);
+        const float *ks = lk + ((t0 + (mk >> 5)) & 1) * kTile;
+        const int kw = mk & 31;
+        // this lane's dims: chunk 4u + h of key kw at slot (4u + h) * 32 + kw
+        double acc = 0.0;
+#pragma unroll
+        for (int u0 = 0; u0 < NU; u0 += 2) {
+            f32x4 kv[2];
+#pragma unroll
+            for (int uu = 0; uu < 2; ++uu)
+                kv[uu] = *reinterpret_cast<const f32x4 *>(ks + 4 * ((4 * (u0 + uu) + h) * 32 + kw));
+#pragma unroll
+            for (int uu = 0; uu < 2; ++uu)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float qv = qf[u0 + uu][e];
+                    asm volatile("" : "+v"(qv));  // fp64 copies made here, not hoisted out of the key loop
+                    acc = fma((double)qv, (double)kv[uu][e], acc);
+                }
+        }
+        const double ex = attn::quarter_sum_f64(acc, ln) * (double)p.scale;
+        return mv == -INFINITY ? -INFINITY : ex;
+    };
+    // Weights of tile u of block blk in place (scores in x); adds exp(s - mt)
+    // of its visible keys to ps.  The key's position in its block is
+    // base + 16kb + 4h + r, so n - 1 - idx = rest - (16kb + r) with
+    // rest = n - 1 - base - 4h (small integers, exact in fp32).
+    auto weights = [&](float (&x)[8], int u, int blk, int n, float mt, float delta, float &ps) {
+        const int rest = n - 1 - (u * kBKV - blk * bn) - 4 * h;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int kr = 16 * (i >> 2) + (i & 3);
             float w = 0.f;
-            if (x[r] != -INFINITY) {
-                const float e = __expf(x[r] - mt);
+            if (x[i] != -INFINITY) {
+                const float e = __expf(x[i] - mt);
                 ps += e;
                 if (blk == 0)
                     w = rest == kr ? e : 0.f;
                 else
-                    w = __expf((x[r] - mt) + (frest - (float)kr) * delta);
+                    w = __expf((x[i] - mt) + (float)(rest - kr) * delta);
             }
-            x[r] = w;
+            x[i] = w;
         }
     };
-    // O += W . V for tile u.  The scheduling groups keep the V reads a
-    // step ahead of their MFMAs instead of hoisting all of them (which
-    // would need 16 * ND registers at once).
-    auto pv = [&](const float (&x)[16], int64_t u) {
-        const float *vt = lv + (u % NVB) * kTile;
+    // O += W . V for tile u: step i = 4kb + r takes key 16kb + 4h + r and
+    // dim 16b + c (quarter h finds dim block b at 16 (b ^ h) of the
+    // swizzled row); the V elements of step i + 1 are read during step i.
+    auto pv = [&](const float (&x)[8], int u) {
+        const float *vt = lv + (u % NVB) * kTile + 4 * h * DMAX + c;
+        const float *vb[4] = {vt + 16 * (0 ^ h), vt + 16 * (1 ^ h), vt + 16 * (2 ^ h), vt + 16 * (3 ^ h)};
+        auto vload = [&](int i, float (&va)[NU]) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
+            for (int bb = 0; bb < NU; ++bb) va[bb] = vb[bb & 3][(16 * (i >> 2) + (i & 3)) * DMAX + 64 * (bb >> 2)];
+        };
+        __builtin_amdgcn_s_setprio(1);
+        float va[2][NU];
+        vload(0, va[0]);
 #pragma unroll
-            for (int j = 0; j < ND; ++j)
-                o[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(attn::v_elem<DMAX>(vt, attn::key_of(r, h), h, c, j), x[r],
-                                                            o[j], 0, 0, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, ND / 2, 0);  // DS reads
-            __builtin_amdgcn_sched_group_barrier(0x008, ND, 0);      // MFMA
+        for (int i = 0; i < 8; ++i) {
+            if (i + 1 < 8) vload(i + 1, va[(i + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int bb = 0; bb < NU; ++bb)
+                o[bb] = __builtin_amdgcn_mfma_f32_16x16x4f32(va[i & 1][bb], x[i], o[bb], 0, 0, 0);
         }
+        __builtin_amdgcn_s_setprio(0);
     };
-    // Block blk from tiles u0 .. u0 + nt - 1 (nt = 1 or 2), their scores in
-    // sa (first of two) and sv.
-    // (bx: the block's exact max, -inf without a visible key)
-    auto finish = [&](float (&sa_)[16], float (&sv_)[16], double bx, int64_t u0, int nt, int64_t blk) {
-        const int64_t n = min(p.bn, p.sk - blk * p.bn);
+    // Block blk from tiles u0 .. u0 + NT - 1, scores in xa (first of two)
+    // and xb, exact block max bx.
+    auto finish = [&](float (&xa)[8], float (&xb)[8], double bx, int u0, auto ntc, int blk) {
+        constexpr int NT = decltype(ntc)::value;
+        const int n = min(bn, sk - blk * bn);
         const double mt64 = fmax(m, bx);
         // Key 0 is visible to every row, so m is finite from block 1 on.
         const float delta = blk == 0 ? 0.f : (float)(m - mt64);
         const float mt = (float)mt64;
         float ps = 0.f;
-        if (nt == 2) weights(sa_, u0, blk, n, mt, delta, ps);
-        weights(sv_, u0 + nt - 1, blk, n, mt, delta, ps);
-        ps += __shfl_xor(ps, 32);
-        l = l * __expf(delta) + ps;
+        if (NT == 2) weights(xa, u0, blk, n, mt, delta, ps);
+        weights(xb, u0 + NT - 1, blk, n, mt, delta, ps);
+        l = l * __expf(delta) + attn::quarter_sum(ps);
         m = mt64;
         const float corr = __expf((float)n * delta);
 #pragma unroll
-        for (int j = 0; j < ND; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[j][r] *= corr;
-        if (nt == 2) pv(sa_, u0);
-        pv(sv_, u0 + nt - 1);
+        for (int bb = 0; bb < NU; ++bb) o[bb] *= corr;
+        if (NT == 2) pv(xa, u0);
+        pv(xb, u0 + NT - 1);
     };
-    // A wave whose last query precedes a tile's first key skips it.
-    auto live = [&](int64_t u) { return !CAUSAL || u * kBKV <= wq0 + 31; };
+    const std::integral_constant<int, 1> one{};
+    const std::integral_constant<int, 2> two{};
 
-    issue(0);
+    if (ntiles > 0) issue(0);
     attn::wait_vm0();
     __syncthreads();
-    for (int64_t t = 0; t < ntiles; t += TPB) {
-        const int64_t blk = t / TPB;
-        float sv[16];
-        if (TPB == 2 && t + 1 < ntiles) {
-            // First tile of the block: scores wait in sa.  The block's
-            // exact max is taken once, from its key with the largest fp32
-            // score in either tile, so the first tile's K stays in its
-            // buffer until every wave has that score: the next block's
-            // first K tile (same buffer) is requested after a barrier.
+    // Whole blocks of TPB tiles, then (TPB = 2) a last block of one tile.
+    // Every wave passes the same barriers; a wave whose set ends earlier
+    // only requests its share of the tiles.
+    int t = 0;
+    for (; t + TPB <= ntiles; t += TPB) {
+        const int blk = t / TPB;
+        const bool mine = blk < my_blocks;
+        float xa[8], xb[8];
+        if constexpr (TPB == 2) {
+            // The block's exact max needs both tiles' scores, and its K
+            // tiles stay in their buffers until every wave has it: the next
+            // block's first K tile (same buffer as this block's first) is
+            // requested after a barrier.
             issue(t + 1);
-            double unused;
-            scores(t, sa, unused, no_exact);
+            if (mine) scores(t, xa);
             attn::wait_vm0();
             __syncthreads();
             if (t + 2 < ntiles) issue_v(t + 2);
-            scores(t + 1, sv, unused, no_exact);
-            float mxa, mxv;
-            const int kwa = tile_argmax(sa, h, mxa);
-            const int kwv = tile_argmax(sv, h, mxv);
-            const bool first = mxa >= mxv;  // the same in both lanes of a row
-            const double e = exact_score(first ? t : t + 1, first ? kwa : kwv);
-            const double bx = (first ? mxa : mxv) != -INFINITY ? e : -INFINITY;
+            double bx = -INFINITY;
+            if (mine) {
+                scores(t + 1, xb);
+                bx = block_max(xa, xb, two, t);
+            }
             __syncthreads();
             if (t + 2 < ntiles) issue_k(t + 2);
-            if (live(t) || live(t + 1)) finish(sa, sv, bx, t, 2, blk);
+            if (mine) finish(xa, xb, bx, t, two, blk);
         } else {
             if (t + 1 < ntiles) issue(t + 1);
-            double bx;
-            scores(t, sv, bx, with_exact);
-            if (live(t)) finish(sa, sv, bx, t, 1, blk);
+            if (mine) {
+                scores(t, xb);
+                const double bx = block_max(xb, xb, one, t);
+                finish(xb, xb, bx, t, one, blk);
+            }
         }
         attn::wait_vm0();
         __syncthreads();
     }
+    if (TPB == 2 && t < ntiles) {  // the last block holds one tile (its keys end the sequence)
+        float xb[8];
+        if (t / TPB < my_blocks) {
+            scores(t, xb);
+            const double bx = block_max(xb, xb, one, t);
+            finish(xb, xb, bx, t, one, t / TPB);
+        }
+    }
 
-    if (row_ok) {
+    if (valid && my_q < sq) {
         float *orow = p.out + (b * p.sq + my_q) * p.d;
 #pragma unroll
-        for (int j = 0; j < ND; ++j)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int dim = 32 * j + 8 * i + 4 * h;
-                if (dim < p.d) {
-                    f32x4 v = {o[j][4 * i] / l, o[j][4 * i + 1] / l, o[j][4 * i + 2] / l, o[j][4 * i + 3] / l};
-                    *reinterpret_cast<f32x4 *>(orow + dim) = v;
-                }
-            }
+        for (int bb = 0; bb < NU; ++bb) {
+            const int dim = 16 * bb + 4 * h;
+            if (dim < p.d) *reinterpret_cast<f32x4 *>(orow + dim) = o[bb] / l;
+        }
     }
 }
 
@@ -761,12 +839,14 @@ int launch_flash_attention_blockwise(const FlashAttnDesc &d, hipStream_t s) {
         p.fold = d.causal && d.batch * p.nqb <= 2 * (int64_t)device_cu_count();
         const dim3 grid((unsigned)d.batch, (unsigned)p.nqb), block(kFaThreads);
         if (d.block_n == 32 || d.block_n == 64) {
+            const int64_t groups = (d.sq + 15) / 16;
+            const dim3 sgrid((unsigned)d.batch, (unsigned)(((groups + 1) / 2 + 3) / 4)), sblock(kFaSetThreads);
 #define GFH_FA_ONEPASS(DM, TPB)                                                                  \
     do {                                                                                         \
         if (d.causal)                                                                            \
-            hipLaunchKernelGGL((fa_onepass_kernel<DM, true, TPB>), grid, block, 0, s, p);        \
+            hipLaunchKernelGGL((fa_set_kernel<DM, true, TPB>), sgrid, sblock, 0, s, p);          \
         else                                                                                     \
-            hipLaunchKernelGGL((fa_onepass_kernel<DM, false, TPB>), grid, block, 0, s, p);       \
+            hipLaunchKernelGGL((fa_set_kernel<DM, false, TPB>), sgrid, sblock, 0, s, p);         \
     } while (0)
             if (d.d <= 64) {
                 if (d.block_n == 32)
