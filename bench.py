@@ -1120,11 +1120,19 @@ def comp_softmax(lib, torch, S, B=4, H=32):
 def run_components(lib, torch, only, cpu=None):
     """Every component's GPU figure, each with the reference CPU path's
     figure for the same workload (`cpu_baseline`) when `cpu` is given.  The
-    square fp32 GEMMs run last, so the headline Linear (the same kernel)
-    starts on a settled clock right after them."""
+    square fp32 GEMMs run last among the GPU figures (the headline Linear
+    settles the clock again itself).
+
+    The CPU baselines run after every GPU figure is taken: numpy's BLAS
+    threads keep spinning on the host cores for a while after a call, and
+    the components whose calls take a few microseconds on the GPU are bound
+    by how fast the host submits them (the per-tensor quantize of a [256,
+    4096] activation measured 24.9 us per call right after a CPU baseline,
+    7.5 us without one)."""
     want = set(filter(None, only.split(","))) or {"sgemm", "qlinear", "gemv", "sdpa", "flash", "softmax",
                                                   "quantize", "decode", "swiglu", "io"}
     out = []
+    pending = []  # (record, cpu_fn): CPU baselines, run after the GPU figures
 
     def add(fn, *a, cpu_fn=None, **kw):
         try:
@@ -1133,12 +1141,19 @@ def run_components(lib, torch, only, cpu=None):
             r = {"name": fn.__name__ + repr(a), "error": str(e)}
         torch.cuda.empty_cache()
         if cpu is not None and cpu_fn is not None and "error" not in r:
+            pending.append((r, cpu_fn))
+        log("  " + json.dumps(r))
+        out.append(r)
+
+    def cpu_baselines():
+        if pending:
+            log("bench: CPU baselines of the components")
+        for r, cpu_fn in pending:
             try:
                 r["cpu_baseline"] = cpu_fn()
             except Exception as e:  # noqa: BLE001
                 r["cpu_baseline"] = {"error": str(e)}
-        log("  " + json.dumps(r))
-        out.append(r)
+            log("  " + json.dumps({"name": r["name"], "cpu_baseline": r["cpu_baseline"]}))
 
     if "io" in want:
         for int8 in (False, True):
@@ -1183,6 +1198,7 @@ def run_components(lib, torch, only, cpu=None):
     if "sgemm" in want:
         for n in (1024, 2048, 4096, 8192):
             add(comp_sgemm, n, cpu_fn=lambda n=n: cpu.sgemm(n))
+    cpu_baselines()
     return out
 
 
