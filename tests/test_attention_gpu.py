@@ -151,6 +151,23 @@ def test_config5_s2048_sampled_slices(torch_dev):
         assert_rel(got[bi, hi], ref)
 
 
+def test_long_sequence_s4096(torch_dev):
+    """S=4096, d=128, causal, 2 (b,h) slices: 128 key tiles per heavy query
+    set and 64 workgroups per slice in the balanced-set kernel, against the
+    oracle; the last query row is the mean-weighted sum over all 4096 keys."""
+    gh, O = _gh(), _O()
+    shape = (1, 2, 4096, 128)
+    q = gh.normal(shape, seed=3, tensor_id=0)
+    k = gh.normal(shape, seed=3, tensor_id=1)
+    v = gh.normal(shape, seed=3, tensor_id=2)
+    got = to_np(gh.sdpa(to_dev(q, torch_dev), to_dev(k, torch_dev), to_dev(v, torch_dev), causal=True))
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(2) as pool:  # the oracle's C call releases the GIL
+        refs = list(pool.map(lambda h: O.flash_attention(q[0, h], k[0, h], v[0, h], _scale(128), True), range(2)))
+    for h, ref in enumerate(refs):
+        assert_rel(got[0, h], ref)
+
+
 @pytest.mark.parametrize("rows,cols", [(1, 3), (1, 4), (7, 1000), (300, 2048), (3, 70000), (5, 260), (9, 4096),
                                        (40000, 512), (2, 4100), (9000, 5), (3, 8)])
 def test_softmax_vs_oracle(torch_dev, rows, cols):

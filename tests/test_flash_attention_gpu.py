@@ -71,6 +71,7 @@ CASES = [
     (2, 181, 250, 128, 64, 64, False, 0.09),    # non-causal, ragged key blocks
     (2, 40, 20, 16, 64, 64, True, 0.3),         # every key in block 0 (sk < block_n)
     (1, 2048, 2048, 128, 64, 64, True, 0.0883883476),  # the bench's sequence length
+    (1, 4096, 4096, 128, 64, 64, True, 0.0883883476),  # 64 key blocks for the heaviest query sets
     (2, 77, 333, 128, 128, 256, True, 0.09),    # block_n larger than a workgroup's queries
 ]
 
