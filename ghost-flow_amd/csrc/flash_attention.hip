@@ -531,7 +531,8 @@ __global__ __launch_bounds__(kFaSetThreads, 4) void fa_set_kernel(FaFused p) {
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int c = lane & 15, h = lane >> 4;
     const int64_t b = blockIdx.x;
-    // 32-bit indices (the launcher checks sq, sk < 2^31)
+    // 32-bit indices: the entry point bounds sq below 2^31 and sk to 8192
+    // key blocks (at most 2^19 keys with block_n <= 64)
     const int sq = (int)p.sq, sk = (int)p.sk, bn = (int)p.bn;
     const int ngroups = (sq + 15) / 16;
     const int pair = (int)blockIdx.y * 4 + (wave & 3);
