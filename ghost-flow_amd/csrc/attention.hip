@@ -304,9 +304,6 @@ __global__ __launch_bounds__(kThreads, 2) void sdpa_fwd_kernel(SdpaParams p) {
 constexpr int kSetQ = 16;  // queries per set
 constexpr int kSetThreads = 512;
 
-using attn::quarter_max;
-using attn::quarter_sum;
-
 template <int DMAX>
 struct QuerySet {
     static constexpr int NU = DMAX / 16;  // 16-dim groups

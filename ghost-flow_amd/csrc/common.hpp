@@ -5,6 +5,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <type_traits>
 
 #include "ghostflow_hip.h"
 
@@ -153,6 +154,64 @@ __device__ __forceinline__ float half_wave_sum(float v) {
     const float lo = readlane_f(v, 0) + readlane_f(v, 16);
     const float hi = readlane_f(v, 32) + readlane_f(v, 48);
     return (threadIdx.x & 32) ? hi : lo;
+}
+
+// ---- four lanes c, c + 16, c + 32, c + 48 -----------------------------------
+//
+// In the 16x16x4 MFMA layouts (lane l holds column l % 16 in quarter l / 16)
+// a column's values sit in lanes c, c + 16, c + 32, c + 48.  These fold them
+// with gfx950's lane swaps: v_permlane16_swap pairs lane l with l ^ 16 and
+// v_permlane32_swap pairs it with l ^ 32 (both halves of each result hold
+// the two values), VALU ops instead of LDS-path permutes.  Every lane of the
+// four ends with the same result.
+__device__ __forceinline__ float quarter_max(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float quarter_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+// The partner's copy of x across lane bit 4 (l ^ 16) or bit 5 (l ^ 32).
+template <int BIT>
+__device__ __forceinline__ unsigned swap_partner(unsigned x, int lane) {
+    const auto a = BIT == 4 ? __builtin_amdgcn_permlane16_swap(x, x, false, false)
+                            : __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    // a holds {lower lane's value, upper lane's value} of the pair
+    return ((lane >> BIT) & 1) ? a[0] : a[1];
+}
+// fp64 sum over the four lanes, in a fixed order for every lane:
+// (quarter 0 + quarter 1) + (quarter 2 + quarter 3).
+__device__ __forceinline__ double quarter_sum_f64(double x, int lane) {
+    auto partner = [&](double v, auto bit) {
+        constexpr int B = decltype(bit)::value;
+        const unsigned long long u = __double_as_longlong(v);
+        const unsigned lo = swap_partner<B>((unsigned)u, lane), hi = swap_partner<B>((unsigned)(u >> 32), lane);
+        return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+    };
+    const double y = partner(x, std::integral_constant<int, 4>{});
+    x = ((lane >> 4) & 1) ? y + x : x + y;
+    const double z = partner(x, std::integral_constant<int, 5>{});
+    return ((lane >> 5) & 1) ? z + x : x + z;
+}
+// The largest value over the four lanes and its key; ties go to
+// the smaller key, so every lane picks the same one.
+__device__ __forceinline__ void quarter_argmax(float &v, int &key, int lane) {
+    auto pick = [&](auto bit) {
+        constexpr int B = decltype(bit)::value;
+        const float pv = __uint_as_float(swap_partner<B>(__float_as_uint(v), lane));
+        const int pk = (int)swap_partner<B>((unsigned)key, lane);
+        if (pv > v || (pv == v && pk < key)) {
+            v = pv;
+            key = pk;
+        }
+    };
+    pick(std::integral_constant<int, 4>{});
+    pick(std::integral_constant<int, 5>{});
 }
 
 // silu(g) * up as the reference computes it (activation.rs:117-122 and

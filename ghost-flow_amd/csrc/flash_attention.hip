@@ -650,7 +650,7 @@ __global__ __launch_bounds__(kFaSetThreads, 4) void fa_set_kernel(FaFused p) {
                     mk = 32 * ti + 16 * (i >> 2) + 4 * h + (i & 3);
                 }
             }
-        attn::quarter_argmax(mv, mk, ln);
+        quarter_argmax(mv, mk, ln);
         const float *ks = lk + ((t0 + (mk >> 5)) & 1) * kTile;
         const int kw = mk & 31;
         // this lane's dims: chunk 4u + h of key kw at slot (4u + h) * 32 + kw
@@ -670,7 +670,7 @@ __global__ __launch_bounds__(kFaSetThreads, 4) void fa_set_kernel(FaFused p) {
                     acc = fma((double)qv, (double)kv[uu][e], acc);
                 }
         }
-        const double ex = attn::quarter_sum_f64(acc, ln) * (double)p.scale;
+        const double ex = quarter_sum_f64(acc, ln) * (double)p.scale;
         return mv == -INFINITY ? -INFINITY : ex;
     };
     // Weights of tile u of block blk in place (scores in x); adds exp(s - mt)
@@ -729,7 +729,7 @@ __global__ __launch_bounds__(kFaSetThreads, 4) void fa_set_kernel(FaFused p) {
         float ps = 0.f;
         if (NT == 2) weights(xa, u0, blk, n, mt, delta, ps);
         weights(xb, u0 + NT - 1, blk, n, mt, delta, ps);
-        l = l * __expf(delta) + attn::quarter_sum(ps);
+        l = l * __expf(delta) + quarter_sum(ps);
         m = mt64;
         const float corr = __expf((float)n * delta);
 #pragma unroll

@@ -438,14 +438,14 @@ __global__ __launch_bounds__(64 * NW) void gemv_f32_kernel(GemvParams p) {
                 for (int g = 0; g < 4; ++g) red[wave][bq][16 * (lane >> 4) + 4 * g + e] = macc[e][g];
         }
     } else {
-        // Reduce over the 4 row lanes of each column group, then over waves.
+        // Reduce over the 4 row lanes of each column group (lanes l, l ^ 16,
+        // l ^ 32, l ^ 48: lane swaps, (l + (l ^ 16)) + ((l ^ 32) + (l ^ 48))),
+        // then over waves.
 #pragma unroll
         for (int bi = 0; bi < MAXB; ++bi)
 #pragma unroll
             for (int e = 0; e < EPL; ++e) {
-                float v = acc[bi][e];
-                v += __shfl_xor(v, 16);
-                v += __shfl_xor(v, 32);
+                const float v = quarter_sum(acc[bi][e]);
                 if (lane < 16) red[wave][bi][lane * EPL + e] = v;
             }
     }
