@@ -40,22 +40,6 @@ struct KvStage {
             r[i] = v;
         }
     }
-    // The same tile without branches: every lane loads from an address
-    // clamped into the operand (the last key, chunk 0 of the row) and keeps
-    // zero where load() would skip the load (nkeys >= 1).
-    __device__ __forceinline__ void load_clamped(const float *__restrict__ base, int64_t key0, int64_t nkeys,
-                                                 int64_t d, int64_t rs, int tid) {
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            const int idx = tid + i * NT;
-            const int key = idx / (DMAX / 4);
-            const int dim = (idx % (DMAX / 4)) * 4;
-            const bool in = key0 + key < nkeys && dim < d;
-            const int64_t row = min(key0 + key, nkeys - 1);
-            const f32x4 v = *reinterpret_cast<const f32x4 *>(base + row * rs + (dim < d ? dim : 0));
-            r[i] = in ? v : f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-    }
     __device__ __forceinline__ void store(float *lds, int tid) const {
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
