@@ -1454,9 +1454,14 @@ int launch_qlinear_i8(const QLinearDesc &d, hipStream_t s) {
 //
 // Decode sizes (m <= 64) use the skinny kernel with two weight streams;
 // larger m the direct-to-LDS tiles with gate and up rows interleaved in
-// 32-row blocks (256 x (128 + 128) above m = 512, 128 x (64 + 64) below, the
-// latter as a 4 x 2 wave grid so that every wave holds both halves of its
-// columns).
+// 32-row blocks: 128 x (64 + 64) up to m = 128, 256 x (64 + 64) up to 256
+// (both a 4 x 2 wave grid, so that every wave holds both halves of its
+// columns), 256 x (128 + 128) above.  Each workgroup takes one CU (its ring
+// is 128-160 KB), so the tile is the one with the fewest operand bytes per
+// CU over the whole launch: rounds of 256 workgroups x bytes per tile.  At
+// N = 11008, K = 4096, m = 256 the 128-row tile needs two rounds of 1 MB
+// (344 workgroups), the 256-row tile one round of 1.5 MB (172); at m = 512
+// the 256 x 256 tile one round of 2 MB against three of 1 MB (688).
 
 bool qlinear_swiglu_fits(int64_t m, int64_t n, int64_t k) {
     if (m <= 0 || n <= 0 || k <= 0 || k % 16 != 0) return false;
@@ -1466,7 +1471,8 @@ bool qlinear_swiglu_fits(int64_t m, int64_t n, int64_t k) {
 
 int64_t qlinear_swiglu_partials(int64_t m, int64_t n) {
     if (m <= 64) return (n + skinny::kCols - 1) / skinny::kCols;
-    if (m > 512) return ((m + 255) / 256) * ((n + 127) / 128);
+    if (m > 256) return ((m + 255) / 256) * ((n + 127) / 128);
+    if (m > 128) return ((m + 255) / 256) * ((n + 63) / 64);
     return ((m + 127) / 128) * ((n + 63) / 64);
 }
 
@@ -1500,11 +1506,15 @@ int launch_qlinear_swiglu_i8(const QSwigluDesc &d, int *npart, hipStream_t s) {
         return use_skinny_lds(g.m, g.n, g.k, true) ? skinny_lds::launch<true>(p, s, npart)
                                                     : skinny::launch<true>(p, s, npart);
     const bool bk128 = g.k % 128 == 0;
-    if (g.m > 512)
+    if (g.m > 256)
         return bk128 ? big::launch_tiles_dual<256, 256, 128, 3, 2, 2, 4>(p, s, npart)
                      : big::launch_tiles_dual<256, 256, 64, 4, 4, 2, 4>(p, s, npart);
+    if (g.m > 128)
+        return bk128 ? big::launch_tiles_dual<256, 128, 128, 3, 3, 4, 2>(p, s, npart)
+                     : big::launch_tiles_dual<256, 128, 64, 4, 4, 4, 2>(p, s, npart);
     // (a 4-deep ring: M = 128 / 256 / 512 at N = 11008, K = 4096 28.6 / 51.4
-    // / 80.1 us against 29.2 / 54.1 / 85.2 with 3; 64-row tiles were slower)
+    // / 80.1 us against 29.2 / 54.1 / 85.2 with 3 on this tile; 64-row tiles
+    // were slower)
     return bk128 ? big::launch_tiles_dual<128, 128, 128, 4, 4, 4, 2>(p, s, npart)
                  : big::launch_tiles_dual<128, 128, 64, 4, 4, 4, 2>(p, s, npart);
 }

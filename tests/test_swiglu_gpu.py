@@ -118,9 +118,9 @@ def _int8_layer(rng, hidden, inter, bias):
 
 
 # m <= 64: the skinny gate/up kernel (5 x 4096 x 256 splits K over workgroups);
-# 100..512: 128 x (64 + 64) tiles (hidden % 128 == 64 -> 64-byte stages);
-# above 512: 256 x (128 + 128) tiles; hidden = 80 (not a multiple of 64)
-# takes the unfused path.
+# 65..128: 128 x (64 + 64) tiles; 129..256: 256 x (64 + 64) (hidden % 128 ==
+# 64 -> 64-byte stages: m = 200); above 256: 256 x (128 + 128) tiles; hidden
+# = 80 (not a multiple of 64) takes the unfused path.
 @pytest.mark.parametrize("m,hidden,inter", [(1, 64, 96), (3, 1040, 208), (4, 4096, 11008), (7, 128, 352),
                                             (5, 4096, 256), (16, 4096, 11008), (40, 4096, 1024), (56, 2048, 768),
                                             (7, 256, 9008), (24, 512, 8240),
@@ -176,11 +176,11 @@ def test_swiglu_f32_mistral_ffn(torch_dev, m):
     assert np.abs(y - y_ref).max() <= gemm_tol(inter, h, wd), float(np.abs(y - y_ref).max())
 
 
-@pytest.mark.parametrize("m", [1, 16, 300, 600])
+@pytest.mark.parametrize("m", [1, 16, 256, 300, 600])
 def test_swiglu_i8_mistral_ffn(torch_dev, m):
     """Mistral's 4096 x 14336 feed-forward block in int8 (DynamicQuantization
-    codes, biases): skinny gate/up at m <= 64, 128 x (64 + 64) tiles at 300,
-    256 x (128 + 128) at 600.  h within 4 ulp of the oracle's silu * up of its
+    codes, biases): skinny gate/up at m <= 64, 256 x (64 + 64) tiles at 256,
+    256 x (128 + 128) at 300 and 600.  h within 4 ulp of the oracle's silu * up of its
     bit-exact gate and up; y bit-exact against the oracle's quantize + INT8
     linear of the GPU's own h."""
     gh = _gh()
