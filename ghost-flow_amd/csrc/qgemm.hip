@@ -69,6 +69,14 @@ struct QParams {
     const float *xf;
     const float2 *xpart;
     int nxpart;
+    // K split over workgroups (the tile kernel, slices > 1): slice j covers K
+    // elements [j kslice, (j + 1) kslice) of every tile; each publishes its
+    // int32 accumulators to part and the last to arrive on counters[tile]
+    // adds them and runs the epilogue.
+    int slices;
+    int64_t kslice;
+    int32_t *part;
+    int *counters;
 };
 
 // One 128 x BK byte stage of a K-contiguous int8 operand: 1024 16-byte
@@ -335,8 +343,12 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
     const int wn0 = (wave % NWN) * WN;
 
     const int nblk = p.tiles_m * p.tiles_n;
-    int bid = blockIdx.x;
-    bid = xcd_chunked(bid, nblk);
+    // Workgroup -> (slice, tile): each XCD takes a contiguous range of
+    // slice-major ids, so tiles of one slice that share rows of x or W run
+    // under one L2.
+    const int vid = xcd_chunked(blockIdx.x, nblk * p.slices);
+    const int slice = vid / nblk;
+    const int bid = vid - slice * nblk;
     const int group_size = kGroupM * p.tiles_n;
     const int group = bid / group_size;
     const int first_m = group * kGroupM;
@@ -351,7 +363,8 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
     // +RPL-1; lane l fills LDS slot l of that 1 KB run (row l / CPR, physical
     // chunk l % CPR) from logical chunk (l % CPR) ^ swz(row).  The host
     // guarantees BM * K < 2^32.
-    const int8_t *a_base = p.qx + m0 * p.k;
+    const int64_t k_lo = (int64_t)slice * p.kslice;  // a multiple of BK
+    const int8_t *a_base = p.qx + m0 * p.k + k_lo;
     const int8_t *b_src[T::kLB];  // per load instruction: its matrix at row n0 (uniform)
     uint32_t a_off[T::kLA], b_off[T::kLB];
 #pragma unroll
@@ -364,10 +377,10 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
         const int r0 = wave * (BN / NW) + j * RPL;  // multiple of RPL: one 32-row block per instruction
         const int r = r0 + lane / CPR;
         const int rl = DUAL ? ((r >> 6) << 5) + (r & 31) : r;  // row of its matrix, from n0
-        b_src[j] = (DUAL && ((r0 >> 5) & 1) ? p.qw2 : p.qw) + n0 * p.k;
+        b_src[j] = (DUAL && ((r0 >> 5) & 1) ? p.qw2 : p.qw) + n0 * p.k + k_lo;
         b_off[j] = (uint32_t)((min(n0 + rl, p.n - 1) - n0) * p.k) + (uint32_t)(((lane % CPR) ^ swz<BK>(r)) * 16);
     }
-    const int nk = (int)(p.k / BK);
+    const int nk = (int)(min(p.kslice, p.k - k_lo) / BK);
 
     // Ring slots: A stages at [0, SA * kABytes), B stages after them.
     int8_t *const ring_b = lds + SA * T::kABytes;
@@ -466,6 +479,67 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
     mfmas((T::kSteps - 1) & 1);
     // No load may still be writing the ring when the workgroup moves on.
     wait_vmcnt<0>();
+
+    if constexpr (!DUAL) {
+        if (p.slices > 1) {
+            // Split K: publish this slice's int32 accumulators (register r of
+            // thread t at [slot][r][t], 2 KB per register and workgroup, so
+            // the stores and loads are coalesced), count the arrival, and
+            // let the last slice of the tile add the others' (integer, so
+            // exact in any order) and run the epilogue.  The arrival
+            // protocol is common.hpp's.
+            constexpr int REGS = FM * FN * 16;
+            constexpr int NT = T::kNT;
+            int32_t *mine = p.part + ((int64_t)slice * nblk + bid) * (REGS * NT) + tid;
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        __hip_atomic_store(mine + ((i * FN + j) * 16 + r) * NT, acc[i][j][r], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            wait_vmcnt<0>();  // this thread's partial stores are complete
+            // (the flag goes through the operand ring: after this barrier no
+            // wave reads a fragment from it any more)
+            int *last_flag = reinterpret_cast<int *>(lds);
+            __syncthreads();
+            if (tid == 0)
+                *last_flag = __hip_atomic_fetch_add(p.counters + bid, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                             p.slices - 1;
+            __syncthreads();
+            if (!*last_flag) return;
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            // The other slices' partials, G slices at a time with every load
+            // of a group requested before the first add.
+            constexpr int G = REGS >= 96 ? 1 : 96 / REGS;
+            for (int j0 = 0; j0 < p.slices; j0 += G) {
+                int32_t t[G][REGS];
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const int j = j0 + g;
+                    const bool use = j < p.slices && j != slice;
+                    const int32_t *src = p.part + ((int64_t)(use ? j : slice) * nblk + bid) * (REGS * NT) + tid;
+#pragma unroll
+                    for (int r = 0; r < REGS; ++r)
+                        t[g][r] = use ? __hip_atomic_load(src + r * NT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                      : 0;
+                }
+#pragma unroll
+                for (int g = 0; g < G; ++g)
+#pragma unroll
+                    for (int i = 0; i < FM; ++i)
+#pragma unroll
+                        for (int jj = 0; jj < FN; ++jj)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r)
+                                acc[i][jj][r] = (int32_t)((uint32_t)acc[i][jj][r] +
+                                                          (uint32_t)t[g][(i * FN + jj) * 16 + r]);
+            }
+            if (tid == 0) __hip_atomic_store(p.counters + bid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
 
     if constexpr (DUAL) {
         // Lane l, register r of block (i, j): row 8*(r/4) + 4*(l/32) + r%4,
@@ -612,11 +686,27 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
     }
 }
 
+// slices > 1: K split into that many slices of whole BK stages (the caller
+// keeps tiles x slices within one round of workgroups).
 template <int BM, int BN, int BK, int SA, int SB, int NWM = 2, int NWN = 2>
-int launch_tiles(QParams p, hipStream_t s) {
+int launch_tiles(QParams p, hipStream_t s, int slices = 1) {
+    using T = Tile<BM, BN, BK, SA, SB, NWM, NWN>;
     p.tiles_m = (int)((p.m + BM - 1) / BM);
     p.tiles_n = (int)((p.n + BN - 1) / BN);
-    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n)), block(Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT);
+    const int64_t stages = p.k / BK;
+    if (slices > stages) slices = (int)stages;
+    p.kslice = slices > 1 ? (stages + slices - 1) / slices * BK : p.k;
+    p.slices = slices > 1 ? (int)((p.k + p.kslice - 1) / p.kslice) : 1;
+    p.part = nullptr;
+    p.counters = nullptr;
+    const int64_t nblk = (int64_t)p.tiles_m * p.tiles_n;
+    if (p.slices > 1) {
+        void *ws = nullptr;
+        GFH_TRY(stream_workspace(s, sizeof(int32_t) * (size_t)(p.slices * nblk) * BM * BN, &ws));
+        p.part = static_cast<int32_t *>(ws);
+        GFH_TRY(stream_counters(s, (size_t)nblk, &p.counters));
+    }
+    const dim3 grid((unsigned)(nblk * p.slices)), block(T::kNT);
     if (p.x_per_row) {
         if (p.acc)
             hipLaunchKernelGGL((qlinear_tile_kernel<BM, BN, BK, SA, SB, NWM, NWN, true, true>), grid, block, 0, s, p);
@@ -637,6 +727,8 @@ template <int BM, int BN, int BK, int SA, int SB, int NWM, int NWN>
 int launch_tiles_dual(QParams p, hipStream_t s, int *npart) {
     p.tiles_m = (int)((p.m + BM - 1) / BM);
     p.tiles_n = (int)((p.n + BN / 2 - 1) / (BN / 2));
+    p.slices = 1;
+    p.kslice = p.k;
     *npart = p.tiles_m * p.tiles_n;
     const dim3 grid((unsigned)(p.tiles_m * p.tiles_n)), block(Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT);
     hipLaunchKernelGGL((qlinear_tile_kernel<BM, BN, BK, SA, SB, NWM, NWN, false, false, true>), grid, block, 0, s, p);
@@ -1432,6 +1524,26 @@ int launch_qlinear_i8(const QLinearDesc &d, hipStream_t s) {
         // 256, N = 4096, K = 4096 17.2 / 10.4 / 8.2; M = 256, N = 11008, K =
         // 4096 26.0 / 31.7 / 29.8; M = 128, N = 11008 24.0 / 19.1 / 21.8.
         auto tiles = [&](int64_t bm, int64_t bn) { return ((d.m + bm - 1) / bm) * ((d.n + bn - 1) / bn); };
+        // Long K with few tiles: split K over workgroups so that the grid
+        // is one round of 256 (int32 partials, exact; the last slice of a
+        // tile adds them).  The fewest slices that fill the round: 64 x 64
+        // tiles when they leave room for two, else 128 x 128 ones (a 64 x 64
+        // split needs a round of 512, slower).  Measured on uniform random
+        // codes (us, unsplit / split): M = 128, N = 4096, K = 11008 29.3 /
+        // 23.0 (64 x 64 in 2; 128 x 128 in 8: 26.3); M = 256, N = 4096
+        // (64 x 64 unsplit against 128 x 128 in 4): K = 11008 32.0 / 29.2,
+        // K = 14336 40.3 / 34.5, but K = 8192 24.2 / 24.6 and K = 4096 13.5 /
+        // 22.4 -- the last slice's reads of the others' 64 KB partials cost
+        // what a shorter K no longer saves.  Grids of 512 (two 128 x 128
+        // workgroups per CU with 2-stage rings, or one per CU in two rounds)
+        // took 1.4-1.7x as long.
+        if (d.k >= 8192) {
+            const int64_t t64 = tiles(64, 64), t128 = tiles(128, 128);
+            if (2 * t64 <= 256)
+                return big::launch_tiles<64, 64, 128, 4, 4, 2, 2>(p, s, (int)(256 / t64));
+            if (t128 <= 128 && d.k >= 10240)
+                return big::launch_tiles<128, 128, 128, 3, 3, 2, 4>(p, s, (int)(256 / t128));
+        }
         constexpr int64_t kFill = 160;
         if (tiles(128, 128) >= kFill)
             return tiles(128, 128) <= 256 ? big::launch_tiles<128, 128, 128, 3, 3, 2, 4>(p, s)

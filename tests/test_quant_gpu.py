@@ -390,6 +390,49 @@ def test_qlinear_mid_m_tiles_bit_exact(torch_dev, m, n, k, x_per_row, with_zp):
     assert _same_f32(to_np(y), ry)
 
 
+def _qlinear_both_outputs(torch_dev, m, n, k, x_per_row, with_zp, seed):
+    """y alone and (y, acc) from the GPU, each bit-exact to the oracle."""
+    gh, O = _gh(), _O()
+    x = gh.normal((m, k), seed=seed, tensor_id=0)
+    w = gh.normal((n, k), 0.0, 0.02, seed=seed, tensor_id=1)
+    bias = gh.uniform((n,), -0.1, 0.1, seed=seed, tensor_id=2)
+    qw, sw, _ = O.quantize_per_channel(w, True)
+    if x_per_row:
+        qx, sx, zx = O.quantize_per_channel(x, not with_zp)
+    else:
+        qx, sx, zx = O.quantize_per_tensor(x, not with_zp)
+    sx, zx = np.atleast_1d(sx), np.atleast_1d(zx)
+    zx_arg = zx if with_zp else None
+    ry, racc = O.qlinear_i8(qx, sx, zx_arg, x_per_row, qw, sw, bias)
+    d = lambda a: None if a is None else to_dev(a, torch_dev)  # noqa: E731
+    args = (d(qx), d(sx), d(zx_arg), d(qw), d(sw))
+    y, acc = gh.qlinear(*args, x_per_row=x_per_row, bias=d(bias), want_acc=True)
+    np.testing.assert_array_equal(to_np(acc), racc)
+    assert _same_f32(to_np(y), ry)
+    y2, _ = gh.qlinear(*args, x_per_row=x_per_row, bias=d(bias), want_acc=False)
+    assert _same_f32(to_np(y2), ry)
+
+
+@pytest.mark.parametrize("m,n,k", [(130, 1000, 8320), (250, 777, 10240), (200, 3000, 12288)])
+@pytest.mark.parametrize("x_per_row,with_zp", [(False, True), (True, False), (True, True)])
+def test_qlinear_split_k_bit_exact(torch_dev, m, n, k, x_per_row, with_zp):
+    """64 < M <= 512 with K >= 8192 and few tiles splits K over workgroups
+    (int32 partials, added by the last slice of each tile): 64 x 64 tiles in
+    5 and 4 slices (the first two shapes), 128 x 128 in 5 with a shorter
+    last slice (the third); ragged M and N, every activation-scale variant,
+    both the accumulator output and the output-only path bit-exact."""
+    _qlinear_both_outputs(torch_dev, m, n, k, x_per_row, with_zp, seed=m + k)
+
+
+@pytest.mark.parametrize("m,k", [(128, 11008), (256, 11008), (256, 14336)])
+def test_qlinear_split_k_swiglu_down(torch_dev, m, k):
+    """The LLaMA / Mistral down projections at 128 and 256 rows (N = 4096):
+    64 x 64 tiles in 2 slices at m = 128, 128 x 128 in 4 at m = 256 (the
+    last one shorter at K = 11008, 86 stages); int32 accumulators and fp32
+    outputs bit-exact."""
+    _qlinear_both_outputs(torch_dev, m, 4096, k, False, True, seed=k)
+
+
 @pytest.mark.parametrize("m,n,k", [(1, 1000, 4096), (7, 130, 1088), (16, 520, 2048), (17, 300, 4096),
                                    (33, 1000, 2048), (64, 130, 1088)])
 @pytest.mark.parametrize("x_per_row,with_zp", [(False, True), (True, False), (True, True)])
