@@ -39,6 +39,7 @@
 //     (b,h) land on the same XCD and share its K/V in that L2.
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #include "attn_tiles.hpp"
 #include "common.hpp"
@@ -504,7 +505,9 @@ __global__ __launch_bounds__(kSetThreads, 4) void sdpa_set_kernel(SdpaParams p) 
 // Both walk the rows with a grid stride, so any row count fits one launch.
 constexpr int kSoftmaxGrid = 8 * 1024;  // workgroups: 32 per CU
 
-template <int NV>
+// NT: nontemporal loads and stores, for inputs that do not stay in the
+// 256 MB MALL anyway (chosen by the launcher).
+template <int NV, bool NT>
 __global__ __launch_bounds__(kThreads) void softmax_rows_wave_kernel(const float *__restrict__ x,
                                                                      float *__restrict__ y, int64_t rows,
                                                                      int64_t cols) {
@@ -517,7 +520,8 @@ __global__ __launch_bounds__(kThreads) void softmax_rows_wave_kernel(const float
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int64_t c = 4 * (lane + 64 * i);
-            v[i] = c < cols ? *reinterpret_cast<const f32x4 *>(xr + c)
+            const f32x4 *src = reinterpret_cast<const f32x4 *>(xr + c);
+            v[i] = c < cols ? (NT ? __builtin_nontemporal_load(src) : *src)
                             : f32x4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
         }
         float mx = -INFINITY;
@@ -545,7 +549,13 @@ __global__ __launch_bounds__(kThreads) void softmax_rows_wave_kernel(const float
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int64_t c = 4 * (lane + 64 * i);
-            if (c < cols) *reinterpret_cast<f32x4 *>(yr + c) = v[i] / sum;
+            if (c < cols) {
+                f32x4 *dst = reinterpret_cast<f32x4 *>(yr + c);
+                if (NT)
+                    __builtin_nontemporal_store(v[i] / sum, dst);
+                else
+                    *dst = v[i] / sum;
+            }
         }
     }
 }
@@ -635,16 +645,29 @@ int launch_softmax_lastdim(const float *x, float *y, int64_t rows, int64_t cols,
         const int64_t wgs = std::min<int64_t>((rows + kThreads / 64 - 1) / (kThreads / 64), kSoftmaxGrid);
         const dim3 grid((unsigned)wgs), block(kThreads);
         const int nv = (int)((cols / 4 + 63) / 64);  // f32x4 per lane
-        if (nv <= 1)
-            hipLaunchKernelGGL(softmax_rows_wave_kernel<1>, grid, block, 0, s, x, y, rows, cols);
-        else if (nv <= 2)
-            hipLaunchKernelGGL(softmax_rows_wave_kernel<2>, grid, block, 0, s, x, y, rows, cols);
-        else if (nv <= 4)
-            hipLaunchKernelGGL(softmax_rows_wave_kernel<4>, grid, block, 0, s, x, y, rows, cols);
-        else if (nv <= 8)
-            hipLaunchKernelGGL(softmax_rows_wave_kernel<8>, grid, block, 0, s, x, y, rows, cols);
+        // Nontemporal access when x and y together exceed the MALL: at
+        // [262144, 2048] (4.3 GB) 777 against 809 us per call (a plain device
+        // copy of the same bytes takes 870-950 us), while at [65536, 512]
+        // (268 MB, which stays in the MALL between calls) it took 42.2
+        // against 39.5 us.
+        const bool nt = (double)rows * (double)cols * 8.0 > 256.0 * 1024 * 1024;
+        auto go = [&](auto ntc) {
+            constexpr bool NT = decltype(ntc)::value;
+            if (nv <= 1)
+                hipLaunchKernelGGL((softmax_rows_wave_kernel<1, NT>), grid, block, 0, s, x, y, rows, cols);
+            else if (nv <= 2)
+                hipLaunchKernelGGL((softmax_rows_wave_kernel<2, NT>), grid, block, 0, s, x, y, rows, cols);
+            else if (nv <= 4)
+                hipLaunchKernelGGL((softmax_rows_wave_kernel<4, NT>), grid, block, 0, s, x, y, rows, cols);
+            else if (nv <= 8)
+                hipLaunchKernelGGL((softmax_rows_wave_kernel<8, NT>), grid, block, 0, s, x, y, rows, cols);
+            else
+                hipLaunchKernelGGL((softmax_rows_wave_kernel<16, NT>), grid, block, 0, s, x, y, rows, cols);
+        };
+        if (nt)
+            go(std::true_type{});
         else
-            hipLaunchKernelGGL(softmax_rows_wave_kernel<16>, grid, block, 0, s, x, y, rows, cols);
+            go(std::false_type{});
     } else {
         const dim3 grid((unsigned)std::min<int64_t>(rows, kSoftmaxGrid));
         hipLaunchKernelGGL(softmax_rows_kernel, grid, dim3(kThreads), 0, s, x, y, rows, cols);

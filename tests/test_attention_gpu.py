@@ -197,6 +197,22 @@ def test_softmax_vs_oracle(torch_dev, rows, cols):
     assert np.abs(got.astype(np.float64).sum(-1) - 1).max() < 1e-5
 
 
+def test_softmax_beyond_the_mall(torch_dev):
+    """[20000, 2048]: x and y together (328 MB) exceed the MALL, so the
+    wave-per-row kernel takes its nontemporal loads and stores.  Same
+    arithmetic as the cached form: the first rows equal, bit for bit, the
+    same rows softmaxed in a small call, and a row sample meets the 1e-4 bar
+    against the oracle."""
+    gh, O = _gh(), _O()
+    rows, cols = 20000, 2048
+    x = gh.normal((rows, cols), 0.0, 3.0, seed=11, tensor_id=0)
+    got = to_np(gh.softmax_lastdim(to_dev(x, torch_dev)))
+    small = to_np(gh.softmax_lastdim(to_dev(np.ascontiguousarray(x[:64]), torch_dev)))
+    np.testing.assert_array_equal(got[:64].view(np.uint32), small.view(np.uint32))
+    pick = np.random.default_rng(0).choice(rows, 256, replace=False)
+    np.testing.assert_allclose(got[pick], O.softmax_lastdim(np.ascontiguousarray(x[pick])), rtol=1e-4, atol=1e-12)
+
+
 @pytest.mark.parametrize("cols", [8, 7, 512])
 def test_softmax_special_values(torch_dev, cols):
     """-inf entries get probability 0, a row of only -inf gives NaN (0/0 as
