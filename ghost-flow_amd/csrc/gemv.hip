@@ -262,7 +262,8 @@ __global__ __launch_bounds__(64 * NW) void gemv_f32_kernel(GemvParams p) {
             const uint32_t o = lane_off + (uint32_t)(r0 + rsub) * row_bytes;
 #pragma unroll
             for (int u = 0; u < U; ++u)
-                w[u] = *reinterpret_cast<const i32x4 *>(wbytes + min(o + (uint32_t)(4 * u) * row_bytes, last_off));
+                w[u] = __builtin_nontemporal_load(
+                    reinterpret_cast<const i32x4 *>(wbytes + min(o + (uint32_t)(4 * u) * row_bytes, last_off)));
             return;
         }
 #pragma unroll
@@ -589,7 +590,7 @@ __global__ __launch_bounds__(64 * NW, (VEC && NW == 4 && MAXB <= 4) ? 2 : 1) voi
             const int r = max(min(r0 + 8 * g + i, rows - 1), 0);  // row within the slice
             const int8_t *src = base + (int64_t)r * p.n;
             if constexpr (VEC) {
-                R[i] = *reinterpret_cast<const i32x4 *>(src);
+                R[i] = __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(src));
             } else {
                 int8_t tmp[16];
 #pragma unroll
