@@ -123,6 +123,12 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
 
+// Cache-policy operand of __builtin_amdgcn_global_load_lds that sets the
+// instruction's nt bit (gfx950: global_load_lds_dwordx4 ... nt), the hint
+// __builtin_nontemporal_load gives an ordinary load: for streams read once,
+// such as a weight whose every byte one workgroup consumes.
+constexpr int kNtHint = 2;
+
 // ---- cross-lane sums without LDS round trips ---------------------------
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float x) {

@@ -158,7 +158,7 @@ __global__ __launch_bounds__(64 * kWaves, MB <= 2 ? 2 : 1) void gemm_nt_skinny_k
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             __builtin_amdgcn_global_load_lds((glb_ptr)(wrow[j] + min(i * kKC + wcol[j], kl - 4)),
-                                             (lds_ptr)(stage + 4 * j * kRowBytes), 16, 0, 0);
+                                             (lds_ptr)(stage + 4 * j * kRowBytes), 16, 0, kNtHint);
     };
 
     f32x4 acc[MB];

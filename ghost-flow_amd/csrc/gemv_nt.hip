@@ -113,7 +113,7 @@ __global__ __launch_bounds__(64 * kNtWaves, 2) void gemv_nt_ksplit_kernel(NtPara
         for (int u = 0; u < U; ++u) {
 #pragma unroll
             for (int r = 0; r < R; ++r)
-                wv[u][r] = *reinterpret_cast<const f32x4 *>(wr[r] + (t + kNtWaves * u) * 256);
+                wv[u][r] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(wr[r] + (t + kNtWaves * u) * 256));
 #pragma unroll
             for (int b = 0; b < MB; ++b)
                 xv[u][b] = *reinterpret_cast<const f32x4 *>(xr[b] + (t + kNtWaves * u) * 256);
@@ -124,7 +124,7 @@ __global__ __launch_bounds__(64 * kNtWaves, 2) void gemv_nt_ksplit_kernel(NtPara
     for (; t < full; t += kNtWaves) {
         f32x4 wv[R], xv[MB];
 #pragma unroll
-        for (int r = 0; r < R; ++r) wv[r] = *reinterpret_cast<const f32x4 *>(wr[r] + t * 256);
+        for (int r = 0; r < R; ++r) wv[r] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(wr[r] + t * 256));
 #pragma unroll
         for (int b = 0; b < MB; ++b) xv[b] = *reinterpret_cast<const f32x4 *>(xr[b] + t * 256);
         fma4(wv, xv);
@@ -136,7 +136,7 @@ __global__ __launch_bounds__(64 * kNtWaves, 2) void gemv_nt_ksplit_kernel(NtPara
         f32x4 wv[R], xv[MB];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const f32x4 v = *reinterpret_cast<const f32x4 *>(wr[r] + off);
+            const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(wr[r] + off));
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float ve = v[e];  // (a bit cast of the element lvalue would read element 0)

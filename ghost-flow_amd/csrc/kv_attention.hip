@@ -114,8 +114,8 @@ __global__ __launch_bounds__(kKvThreads, 2) void kv_attention_kernel(KvParams p)
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
             const int64_t jc = min(jb + u, j1 - 1);
-            kr[u] = *reinterpret_cast<const f32x4 *>(kbase + jc * p.kv_rs);
-            vr[u] = *reinterpret_cast<const f32x4 *>(vbase + jc * p.kv_rs);
+            kr[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(kbase + jc * p.kv_rs));
+            vr[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(vbase + jc * p.kv_rs));
         }
 #pragma unroll
         for (int u = 0; u < kU; ++u) {

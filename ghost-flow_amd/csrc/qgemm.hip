@@ -861,7 +861,7 @@ __global__ __launch_bounds__(kThreads, QX ? 4 : 1) void qlinear_skinny_kernel(Sk
             const bool ok = s0 + u < st1 && off + kb < kl;
 #pragma unroll
             for (int d = 0; d < D; ++d)
-                w[u][d] = ok ? *reinterpret_cast<const i32x4 *>(wsrc[d] + off) : i32x4{0, 0, 0, 0};
+                w[u][d] = ok ? __builtin_nontemporal_load(reinterpret_cast<const i32x4 *>(wsrc[d] + off)) : i32x4{0, 0, 0, 0};
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
                 const int64_t row = mb * 16 + (lane & 15);
@@ -1179,7 +1179,7 @@ __global__ __launch_bounds__(64 * kWaves, (MB <= 2 && !DUAL) ? 2 : 1) void qline
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 __builtin_amdgcn_global_load_lds((glb_ptr)(wsrc[d][j] + min(i * kChunk + wcol[j], kl - 16)),
-                                                 (lds_ptr)(stage + 4 * j * kChunk), 16, 0, 0);
+                                                 (lds_ptr)(stage + 4 * j * kChunk), 16, 0, kNtHint);
         }
     };
 
