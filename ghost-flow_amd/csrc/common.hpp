@@ -129,6 +129,18 @@ typedef int i32x16 __attribute__((ext_vector_type(16)));
 // such as a weight whose every byte one workgroup consumes.
 constexpr int kNtHint = 2;
 
+// 16-byte partial-result traffic of the split-K protocol below: raw buffer
+// loads and stores with the sc1 cache bit, the bit an agent-scope relaxed
+// atomic load or store carries (global_load_dword / global_store_dword ...
+// sc1), so they complete at the device coherence point like those, four
+// dwords per instruction instead of one.  The buffer resource bounds every
+// access to `bytes` (the gfx9 raw-buffer word 3: 32-bit data format); `bytes`
+// must fit 32 bits.
+constexpr int kScDevice = 16;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_buffer(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+
 // ---- cross-lane sums without LDS round trips ---------------------------
 template <int CTRL>
 __device__ __forceinline__ float dpp_mov(float x) {

@@ -488,17 +488,26 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
             // let the last slice of the tile add the others' (integer, so
             // exact in any order) and run the epilogue.  The arrival
             // protocol is common.hpp's.
-            constexpr int REGS = FM * FN * 16;
+            constexpr int REGS = FM * FN * 16, R4 = REGS / 4;
             constexpr int NT = T::kNT;
-            int32_t *mine = p.part + ((int64_t)slice * nblk + bid) * (REGS * NT) + tid;
+            // 16-byte stores and loads at the coherence point (common.hpp):
+            // registers 4 q .. 4 q + 3 of thread t at [slot][q][t].
+            const __amdgpu_buffer_rsrc_t part_buf =
+                coherent_buffer(p.part, (uint32_t)((int64_t)p.slices * nblk * REGS * NT * 4));
+            auto part_off = [&](int64_t sl, int q4) {
+                return (uint32_t)((((sl * nblk + bid) * R4 + q4) * NT + tid) * 16);
+            };
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r)
-                        __hip_atomic_store(mine + ((i * FN + j) * 16 + r) * NT, acc[i][j][r], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
+                    for (int q4 = 0; q4 < 4; ++q4) {
+                        const i32x4 v = {acc[i][j][4 * q4], acc[i][j][4 * q4 + 1], acc[i][j][4 * q4 + 2],
+                                         acc[i][j][4 * q4 + 3]};
+                        __builtin_amdgcn_raw_buffer_store_b128(v, part_buf, part_off(slice, (i * FN + j) * 4 + q4),
+                                                               0, kScDevice);
+                    }
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             wait_vmcnt<0>();  // this thread's partial stores are complete
             // (the flag goes through the operand ring: after this barrier no
@@ -515,16 +524,15 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
             // of a group requested before the first add.
             constexpr int G = REGS >= 96 ? 1 : 96 / REGS;
             for (int j0 = 0; j0 < p.slices; j0 += G) {
-                int32_t t[G][REGS];
+                i32x4 t[G][R4];
 #pragma unroll
                 for (int g = 0; g < G; ++g) {
                     const int j = j0 + g;
                     const bool use = j < p.slices && j != slice;
-                    const int32_t *src = p.part + ((int64_t)(use ? j : slice) * nblk + bid) * (REGS * NT) + tid;
 #pragma unroll
-                    for (int r = 0; r < REGS; ++r)
-                        t[g][r] = use ? __hip_atomic_load(src + r * NT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                      : 0;
+                    for (int q4 = 0; q4 < R4; ++q4)
+                        t[g][q4] = use ? __builtin_amdgcn_raw_buffer_load_b128(part_buf, part_off(j, q4), 0, kScDevice)
+                                       : i32x4{0, 0, 0, 0};
                 }
 #pragma unroll
                 for (int g = 0; g < G; ++g)
@@ -533,9 +541,11 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
 #pragma unroll
                         for (int jj = 0; jj < FN; ++jj)
 #pragma unroll
-                            for (int r = 0; r < 16; ++r)
-                                acc[i][jj][r] = (int32_t)((uint32_t)acc[i][jj][r] +
-                                                          (uint32_t)t[g][(i * FN + jj) * 16 + r]);
+                            for (int r = 0; r < 16; ++r) {
+                                const i32x4 w = t[g][((i * FN + jj) * 16 + r) / 4];
+                                const int32_t e = w[r % 4];
+                                acc[i][jj][r] = (int32_t)((uint32_t)acc[i][jj][r] + (uint32_t)e);
+                            }
             }
             if (tid == 0) __hip_atomic_store(p.counters + bid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
