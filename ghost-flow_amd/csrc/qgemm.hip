@@ -1,4 +1,5 @@
-// qgemm.hip -- INT8 linear on CDNA4 i8 MFMA (v_mfma_i32_32x32x32_i8).
+// qgemm.hip -- INT8 linear on CDNA4 i8 MFMA (v_mfma_i32_16x16x64_i8; the generic
+// fallback for K % 64 != 0 on v_mfma_i32_32x32x32_i8).
 //
 //   raw[m,n] = sum_k qx[m,k] * qw[n,k]                       (exact int32)
 //   acc[m,n] = raw - zx * rowsum[n]                          (exact int32)
@@ -228,9 +229,14 @@ __global__ __launch_bounds__(kThreads) void qlinear_mfma_kernel(QParams p) {
 // ---- MFMA tiles fed by direct-to-LDS loads (M > 64) ------------------------------
 //
 // A workgroup owns a BM x BN output tile; its NWM x NWN waves each hold a
-// (BM/NWM) x (BN/NWN) sub-tile as v_mfma_i32_32x32x32_i8 accumulators.
+// (BM/NWM) x (BN/NWN) sub-tile as v_mfma_i32_16x16x64_i8 accumulators.
 // The dispatch runs 8 waves in a 2 x 4 grid: 256 x 256 tiles (M > 512)
-// give each wave 4 x 2 accumulators (128 registers), 128 x 128 tiles 2 x 1.
+// give each wave 8 x 4 accumulators (128 registers), 128 x 128 tiles 4 x 2.
+// The 16 x 16 x 64 form, rather than 32 x 32 x 32 (the same operations per
+// wave tile, the same LDS reads), because the clock holds up better under
+// it: a register-only loop of each on quantized-Gaussian operands sustained
+// 4277 against 3584 TOP/s (uniform random codes 4058 / 3254; all-zero
+// operands 4909 / 4924), and the int8 GEMMs at 4096 rows are power-bound.
 // Operands stream through rings of SA (A) and SB (B) slots of BK bytes of K,
 // filled with global_load_lds_dwordx4 (global memory straight into LDS, no
 // VGPR staging); all stages but the one being consumed are in flight.  At
@@ -294,8 +300,8 @@ struct Tile {
     static_assert(SB >= 2 && (SA == SB || SA == SB + 1), "ring slots");
     static constexpr int kNW = NWM * NWN, kNT = 64 * kNW;   // waves, threads
     static constexpr int kWM = BM / NWM, kWN = BN / NWN;     // wave sub-tile
-    static constexpr int kFM = kWM / 32, kFN = kWN / 32;     // accumulators per wave
-    static constexpr int kSteps = BK / 32;                   // MFMA k-steps per stage
+    static constexpr int kFM = kWM / 16, kFN = kWN / 16;     // 16 x 16 accumulators per wave
+    static constexpr int kSteps = BK / 64;                   // MFMA k-steps per stage
     static constexpr int kChunks = BK / 16;                  // 16-byte chunks per row
     static constexpr int kRowsPerLoad = 1024 / BK;           // rows filled by one load instruction
     static constexpr int kLA = BM * BK / (1024 * kNW), kLB = BN * BK / (1024 * kNW);  // loads per wave per stage
@@ -310,12 +316,12 @@ struct Tile {
     // The same before the first stage, after the prologue's requests.
     static constexpr int kWaitFirst = (SB - 1) * (kLA + kLB) + (SA - SB) * kLA;
     // Output staging: each wave converts half of its sub-tile (kWM/2 rows x
-    // kWN columns) at a time -- all of it when it is a single 32-row block;
-    // row stride kWN + 8 floats keeps the two row groups of one ds_write_b32
-    // on disjoint banks.
+    // kWN columns) at a time -- all of it when it is a single 16-row block;
+    // a row stride of kWN + 4 floats (4 rows apart: 16 banks apart) keeps
+    // the four row groups of one ds_write_b32 on disjoint banks.
     static constexpr int kOutPasses = kFM >= 2 ? 2 : 1;
     static constexpr int kOutRows = kWM / kOutPasses;
-    static constexpr int kOutStride = kWN + 8;
+    static constexpr int kOutStride = kWN + 4;
     static constexpr int kOut = kNW * kOutRows * kOutStride * 4;
     static constexpr int kLds = kRing > kOut ? kRing : kOut;
     static_assert(kLds <= 160 * 1024, "LDS per workgroup");
@@ -323,8 +329,9 @@ struct Tile {
 
 // DUAL (SwiGLU gate/up): the B tile's 32-row blocks alternate between
 // gate_proj and up_proj rows of the same BN / 2 output columns, so a wave's
-// accumulator blocks j = 0 / 1 hold gate / up of one 32-column group and the
-// epilogue writes silu(gate) * up straight from registers.
+// accumulator blocks j = 0, 1 hold gate and j = 2, 3 up of one 32-column
+// group (16 columns each) and the epilogue writes silu(gate) * up straight
+// from registers.
 template <int BM, int BN, int BK, int SA, int SB, int NWM, int NWN, bool X_PER_ROW, bool WANT_ACC, bool DUAL = false>
 __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
                              ((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kLds > 80 * 1024) ? 1 : 2)) void qlinear_tile_kernel(
@@ -401,38 +408,39 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
                                              (lds_ptr)(lb + (wave * (BN / NW) + j * RPL) * BK), 16, 0, 0);
     };
 
-    // Fragment address inside a stage: lane l reads row l%32 of a 32-row
-    // block, logical chunk 2*ks + l/32.  Blocks start at multiples of 32
-    // rows, so the swizzle depends on l only, and logical chunk 2*ks + h
-    // lands at offset foff0 ^ (ks * 32).
-    const int frow = lane & 31;
-    const int foff0 = frow * BK + (((lane >> 5) ^ swz<BK>(frow)) * 16);
+    // Fragment address inside a stage: lane l reads row l%16 of a 16-row
+    // block, logical chunk 4*ks + l/16 (the operand layout of
+    // v_mfma_i32_16x16x64_i8: 16 consecutive k bytes per lane).  Blocks
+    // start at multiples of 16 rows, so the swizzle depends on l only; the
+    // 16 lanes of one chunk then read 16 rows on 16 distinct 4-bank groups
+    // (BK = 128: even rows on banks 4 (c ^ s), odd rows 32 above; BK = 64:
+    // row 4a + b on 16 b + 4 (c ^ a)).
+    const int frow = lane & 15, fq = lane >> 4, fsw = swz<BK>(frow);
+    auto frag_off = [&](int ks) { return frow * BK + (((((ks << 2) | fq)) ^ fsw) << 4); };
 
     i32x4 af[2][FM], bf[2][FN];
     auto load_frags = [&](int buf, int t, int ks) {
         const int8_t *la = lds + (t % SA) * T::kABytes;
         const int8_t *lb = ring_b + (t % SB) * T::kBBytes;
-        const int fo = foff0 ^ (ks << 5);
+        const int fo = frag_off(ks);
 #pragma unroll
-        for (int i = 0; i < FM; ++i) af[buf][i] = *reinterpret_cast<const i32x4 *>(la + (wm0 + i * 32) * BK + fo);
+        for (int i = 0; i < FM; ++i) af[buf][i] = *reinterpret_cast<const i32x4 *>(la + (wm0 + i * 16) * BK + fo);
 #pragma unroll
-        for (int j = 0; j < FN; ++j) bf[buf][j] = *reinterpret_cast<const i32x4 *>(lb + (wn0 + j * 32) * BK + fo);
+        for (int j = 0; j < FN; ++j) bf[buf][j] = *reinterpret_cast<const i32x4 *>(lb + (wn0 + j * 16) * BK + fo);
     };
 
-    i32x16 acc[FM][FN];
+    i32x4 acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+        for (int j = 0; j < FN; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
 
     auto mfmas = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[buf][i], bf[buf][j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[buf][i], bf[buf][j], acc[i][j], 0, 0, 0);
     };
 
     // Stages t+SB of B and t+SA of A are issued into stage t's slots as soon
@@ -470,8 +478,13 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
         __builtin_amdgcn_s_barrier();
         issue_b(min(t + SB, nk - 1), t % SB);
         issue_a(min(t + SA, nk - 1), t % SA);
-        load_frags(0, t + 1, 0);
-        mfmas((T::kSteps - 1) & 1);
+        if constexpr (T::kSteps >= 2) {
+            load_frags(0, t + 1, 0);
+            mfmas((T::kSteps - 1) & 1);
+        } else {  // one k-step per stage (BK = 64): this stage's MFMAs, then the next stage's fragments
+            mfmas(0);
+            load_frags(0, t + 1, 0);
+        }
         interleave<T::kLPS, NR, NM>();
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -488,10 +501,10 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
             // let the last slice of the tile add the others' (integer, so
             // exact in any order) and run the epilogue.  The arrival
             // protocol is common.hpp's.
-            constexpr int REGS = FM * FN * 16, R4 = REGS / 4;
+            constexpr int REGS = FM * FN * 4, R4 = FM * FN;
             constexpr int NT = T::kNT;
             // 16-byte stores and loads at the coherence point (common.hpp):
-            // registers 4 q .. 4 q + 3 of thread t at [slot][q][t].
+            // accumulator block q = i FN + j of thread t at [slot][q][t].
             const __amdgpu_buffer_rsrc_t part_buf =
                 coherent_buffer(p.part, (uint32_t)((int64_t)p.slices * nblk * REGS * NT * 4));
             auto part_off = [&](int64_t sl, int q4) {
@@ -501,13 +514,8 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
             for (int i = 0; i < FM; ++i)
 #pragma unroll
                 for (int j = 0; j < FN; ++j)
-#pragma unroll
-                    for (int q4 = 0; q4 < 4; ++q4) {
-                        const i32x4 v = {acc[i][j][4 * q4], acc[i][j][4 * q4 + 1], acc[i][j][4 * q4 + 2],
-                                         acc[i][j][4 * q4 + 3]};
-                        __builtin_amdgcn_raw_buffer_store_b128(v, part_buf, part_off(slice, (i * FN + j) * 4 + q4),
-                                                               0, kScDevice);
-                    }
+                    __builtin_amdgcn_raw_buffer_store_b128(acc[i][j], part_buf, part_off(slice, i * FN + j), 0,
+                                                           kScDevice);
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             wait_vmcnt<0>();  // this thread's partial stores are complete
             // (the flag goes through the operand ring: after this barrier no
@@ -539,47 +547,61 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
 #pragma unroll
                     for (int i = 0; i < FM; ++i)
 #pragma unroll
-                        for (int jj = 0; jj < FN; ++jj)
+                        for (int jj = 0; jj < FN; ++jj) {
+                            const i32x4 w = t[g][i * FN + jj];
 #pragma unroll
-                            for (int r = 0; r < 16; ++r) {
-                                const i32x4 w = t[g][((i * FN + jj) * 16 + r) / 4];
-                                const int32_t e = w[r % 4];
+                            for (int r = 0; r < 4; ++r) {
+                                const int32_t e = w[r];
                                 acc[i][jj][r] = (int32_t)((uint32_t)acc[i][jj][r] + (uint32_t)e);
                             }
+                        }
             }
             if (tid == 0) __hip_atomic_store(p.counters + bid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 
     if constexpr (DUAL) {
-        // Lane l, register r of block (i, j): row 8*(r/4) + 4*(l/32) + r%4,
-        // column l%32 of the wave's 32-column group; j = 0 gate, j = 1 up.
-        const int64_t col = n0 + wn0 / 2 + (lane & 31);
-        const int64_t cc = min(col, p.n - 1);
+        // Lane l, register r of block (i, j): row 4*(l/16) + r, column l%16
+        // of the 16 x 16 block; blocks j < FN/2 are gate, j + FN/2 the up
+        // projection of the same columns.
+        constexpr int FG = FN / 2;
         const int32_t zx0 = p.zx ? (int32_t)p.zx[0] : 0;
         const float sx0 = p.sx[0];
-        const int32_t rs_g = p.zx ? p.rowsum[cc] : 0, rs_u = p.zx ? p.rowsum2[cc] : 0;
-        const float sc_g = sx0 * p.sw[cc], sc_u = sx0 * p.sw2[cc];
-        const float b_g = p.bias ? p.bias[cc] : 0.f, b_u = p.bias2 ? p.bias2[cc] : 0.f;
+        int64_t col[FG];
+        int32_t rs_g[FG], rs_u[FG];
+        float sc_g[FG], sc_u[FG], b_g[FG], b_u[FG];
+#pragma unroll
+        for (int j = 0; j < FG; ++j) {
+            col[j] = n0 + wn0 / 2 + j * 16 + (lane & 15);
+            const int64_t cc = min(col[j], p.n - 1);
+            rs_g[j] = p.zx ? p.rowsum[cc] : 0;
+            rs_u[j] = p.zx ? p.rowsum2[cc] : 0;
+            sc_g[j] = sx0 * p.sw[cc];
+            sc_u[j] = sx0 * p.sw2[cc];
+            b_g[j] = p.bias ? p.bias[cc] : 0.f;
+            b_u[j] = p.bias2 ? p.bias2[cc] : 0.f;
+        }
         float mn = INFINITY, mx = -INFINITY;
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t row = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                const int32_t ag = (int32_t)((uint32_t)acc[i][0][r] - (uint32_t)(zx0 * rs_g));
-                const int32_t au = (int32_t)((uint32_t)acc[i][1][r] - (uint32_t)(zx0 * rs_u));
-                float g = (float)ag * sc_g;
-                float u = (float)au * sc_u;
-                if (p.bias) g = g + b_g;
-                if (p.bias2) u = u + b_u;
-                const float h = silu_mul1(g, u);
-                if (row < p.m && col < p.n) {
-                    p.y[row * p.n + col] = h;
-                    mn = fminf(mn, h);
-                    mx = fmaxf(mx, h);
+            for (int j = 0; j < FG; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t row = m0 + wm0 + i * 16 + 4 * (lane >> 4) + r;
+                    const int32_t ag = (int32_t)((uint32_t)acc[i][j][r] - (uint32_t)(zx0 * rs_g[j]));
+                    const int32_t au = (int32_t)((uint32_t)acc[i][j + FG][r] - (uint32_t)(zx0 * rs_u[j]));
+                    float g = (float)ag * sc_g[j];
+                    float u = (float)au * sc_u[j];
+                    if (p.bias) g = g + b_g[j];
+                    if (p.bias2) u = u + b_u[j];
+                    const float h = silu_mul1(g, u);
+                    if (row < p.m && col[j] < p.n) {
+                        p.y[row * p.n + col[j]] = h;
+                        mn = fminf(mn, h);
+                        mx = fmaxf(mx, h);
+                    }
                 }
-            }
         wave_minmax(mn, mx);
         // Cross-wave fold through the (now idle) operand ring.
         wait_lgkm0();
@@ -597,7 +619,7 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
     }
 
     // Epilogue: lane l, register r of block (i, j) holds
-    // row 8*(r/4) + 4*(l/32) + r%4, column l%32 of that 32 x 32 block.
+    // row 4*(l/16) + r, column l%16 of that 16 x 16 block.
     // Per-tensor activation parameters are uniform; per-row ones are read
     // once per row.
     const int zx0 = (!X_PER_ROW && p.zx) ? (int)p.zx[0] : 0;
@@ -606,7 +628,7 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
     float swc[FN], bc[FN];
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-        const int64_t col = min(n0 + wn0 + j * 32 + (lane & 31), p.n - 1);
+        const int64_t col = min(n0 + wn0 + j * 16 + (lane & 15), p.n - 1);
         rs[j] = p.zx ? p.rowsum[col] : 0;
         swc[j] = p.y ? p.sw[col] : 0.f;
         bc[j] = p.bias ? p.bias[col] : 0.f;
@@ -617,7 +639,7 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
         a = acc[i][j][r];
         float sc;
         if (X_PER_ROW) {
-            const int64_t row = min(m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3), p.m - 1);
+            const int64_t row = min(m0 + wm0 + i * 16 + 4 * (lane >> 4) + r, p.m - 1);
             if (p.zx) a = (int32_t)((uint32_t)a - (uint32_t)((int32_t)p.zx[row] * rs[j]));
             sc = p.y ? p.sx[row] * swc[j] : 0.f;
         } else {
@@ -634,12 +656,12 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
         // straight from registers.
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
-            const int64_t col = n0 + wn0 + j * 32 + (lane & 31);
+            const int64_t col = n0 + wn0 + j * 16 + (lane & 15);
 #pragma unroll
             for (int i = 0; i < FM; ++i)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int64_t row = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t row = m0 + wm0 + i * 16 + 4 * (lane >> 4) + r;
                     int32_t a;
                     const float v = finish(i, j, r, a);
                     if (col < p.n && row < p.m) {
@@ -652,14 +674,14 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
     }
 
     // Output tile through LDS: each wave converts half of its sub-tile (all
-    // of a single 32-row block) at a time into its own region, then writes
+    // of a single 16-row block) at a time into its own region, then writes
     // whole row runs (WN floats) with 16-byte stores.
     constexpr int LPR = WN / 4;                // lanes per output row
     constexpr int RPI = 64 / LPR;              // rows per read instruction
     constexpr int PASSES = T::kOutPasses;
     constexpr int HALF = T::kOutRows;          // rows per pass
-    constexpr int BPP = FM / PASSES;           // 32-row blocks per pass
-    static_assert(BPP * PASSES == FM && BPP * 32 == HALF, "output passes cover the sub-tile");
+    constexpr int BPP = FM / PASSES;           // 16-row blocks per pass
+    static_assert(BPP * PASSES == FM && BPP * 16 == HALF, "output passes cover the sub-tile");
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();  // every wave is done with the operand ring
     float *lt = reinterpret_cast<float *>(lds) + wave * (HALF * T::kOutStride);
@@ -671,11 +693,11 @@ __global__ __launch_bounds__((Tile<BM, BN, BK, SA, SB, NWM, NWN>::kNT),
 #pragma unroll
             for (int j = 0; j < FN; ++j)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
+                for (int r = 0; r < 4; ++r) {
                     int32_t a;
                     const float v = finish(h * BPP + ii, j, r, a);
-                    const int lr = ii * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    lt[lr * T::kOutStride + j * 32 + (lane & 31)] = v;
+                    const int lr = ii * 16 + 4 * (lane >> 4) + r;
+                    lt[lr * T::kOutStride + j * 16 + (lane & 15)] = v;
                 }
         const int64_t col = n0 + wn0 + 4 * (lane % LPR);
 #pragma unroll
