@@ -345,6 +345,42 @@ class CpuRef:
                            f"oracle Tensor::matmul {n}^3 (2 operand copies + matmul_blocked + output copy); "
                            f"matmul_blocked on {rows}/{n} rows, {ext}: {full:.2f} s per call ({meas:.2f} s measured)")
 
+    def matmul_backward(self, m, k, n):
+        """matmul_backward's naive loops (backward.rs:131-160, restated by
+        gfo_matmul_backward): grad_a rows and grad_b rows are independent, so
+        each half is timed on a sample of its rows and scaled."""
+        np, L = self.np, self.L
+        ra, rb = min(m, 16), min(k, 4)  # (grad_b's loop reads a with stride k: ~0.2 s per row at 4096^2)
+        g = self._randn((m, n))
+        a = self._randn((m, k))
+        b = self._randn((k, n))
+        ga = np.empty((ra, k), np.float32)
+        t_a = self._t(lambda: L.gfo_matmul_backward(g[:ra], a[:ra], b, ra, k, n, ga.ctypes.data, None))
+        a_cols = np.ascontiguousarray(a[:, :rb])  # grad_b rows 0 .. rb-1 read these columns of a
+        gb = np.empty((rb, n), np.float32)
+        t_b = self._t(lambda: L.gfo_matmul_backward(g, a_cols, b[:rb], m, rb, n, None, gb.ctypes.data))
+        full = t_a * (m / ra) + t_b * (k / rb)
+        return self.result(4.0 * m * n * k / full / 1e12, "TFLOP/s", full,
+                           f"oracle matmul_backward m={m} k={k} n={n}: grad_a on {ra}/{m} rows ({t_a:.2f} s), "
+                           f"grad_b on {rb}/{k} rows ({t_b:.2f} s), extrapolated: {full:.1f} s per call")
+
+    def batched_matmul(self, batch, m, k, n):
+        """Tensor::matmul on [batch, m, k] @ [batch, k, n]: data_f32 of both
+        operands, batched_matmul's i-j-k loop on a sample of slices, the
+        output copy (the copies timed in full)."""
+        np, L = self.np, self.L
+        sl = min(batch, 4)
+        a = self._randn((sl, m, k))
+        b = self._randn((sl, k, n))
+        c = np.empty((sl, m, n), np.float32)
+        t_copy = self._copy_s(4 * batch * m * k) + self._copy_s(4 * batch * k * n) + self._copy_s(4 * batch * m * n)
+        t_mm = self._t(lambda: L.gfo_batched_matmul(a.reshape(-1), sl, b.reshape(-1), sl, c.reshape(-1), sl, m, k, n))
+        full = t_copy + t_mm * (batch / sl)
+        return self.result(2.0 * batch * m * n * k / full / 1e12, "TFLOP/s", full,
+                           f"oracle Tensor::matmul (batched_matmul) [{batch},{m},{k}] @ [{batch},{k},{n}]: operand and "
+                           f"output copies in full, the loop on {sl}/{batch} slices ({t_mm:.2f} s), extrapolated: "
+                           f"{full:.1f} s per call")
+
     def qlinear(self, m, n, k, per_tensor=True):
         """The reference's executable INT8 path: DynamicQuantization::
         quantize_activation (per tensor, asymmetric) of x, dequantize of x
@@ -654,6 +690,51 @@ def comp_sgemm(lib, torch, n):
     fl = 2.0 * n ** 3
     return {"name": f"sgemm_nn_{n}", "ms": ms, "value": fl / ms / 1e9, "unit": "TFLOP/s",
             "frac": fl / ms / 1e9 / (PEAK_F32 / 1e12), "bound": "mfma_f32"}
+
+
+def comp_matmul_backward(lib, torch, m, k, n):
+    """matmul_backward (ghostflow-autograd/src/backward.rs:131-160) of C = a @ b,
+    a [m, k], b [k, n]: grad_a = grad . b^T (NT) and grad_b = a^T . grad
+    (transposed A), one gfh_matmul_backward_f32 call, 2 x 2mnk FLOP."""
+    dev = torch.device("cuda:0")
+    g = torch.randn((m, n), device=dev)
+    a = torch.randn((m, k), device=dev)
+    b = torch.randn((k, n), device=dev)
+    ga = torch.empty((m, k), device=dev)
+    gb = torch.empty((k, n), device=dev)
+    s = torch.cuda.current_stream(dev).cuda_stream
+    L = lib.L
+    gp, ap, bp, gap, gbp = g.data_ptr(), a.data_ptr(), b.data_ptr(), ga.data_ptr(), gb.data_ptr()
+
+    def f(_):
+        L.gfh_matmul_backward_f32(gp, ap, bp, m, k, n, gap, gbp, s)
+    fl = 4.0 * m * n * k
+    reps = int(min(100, max(5, 1.0 / (fl / 50e12))))
+    ms = event_time_ms(torch, f, reps)
+    return {"name": f"matmul_backward_m{m}_k{k}_n{n}", "ms": ms, "value": fl / ms / 1e9, "unit": "TFLOP/s",
+            "frac": fl / ms / 1e9 / (PEAK_F32 / 1e12), "bound": "mfma_f32"}
+
+
+def comp_batched_matmul(lib, torch, batch, m, k, n):
+    """Tensor::matmul on 3-D operands (batched_matmul, matmul.rs:122-170):
+    [batch, m, k] @ [batch, k, n], the attention-score shape, through
+    gfh_sgemm_strided_batched."""
+    dev = torch.device("cuda:0")
+    a = torch.randn((batch, m, k), device=dev)
+    b = torch.randn((batch, k, n), device=dev)
+    c = torch.empty((batch, m, n), device=dev)
+    s = torch.cuda.current_stream(dev).cuda_stream
+    L = lib.L
+    ap, bp, cp = a.data_ptr(), b.data_ptr(), c.data_ptr()
+
+    def f(_):
+        L.gfh_sgemm_strided_batched(0, 0, m, n, k, 1.0, ap, k, m * k, batch, bp, n, k * n, batch, 0.0, cp, n, m * n,
+                                    batch, None, s)
+    fl = 2.0 * batch * m * n * k
+    reps = int(min(200, max(5, 1.0 / (fl / 50e12))))
+    ms = event_time_ms(torch, f, reps)
+    return {"name": f"batched_matmul_b{batch}_m{m}_k{k}_n{n}", "ms": ms, "value": fl / ms / 1e9,
+            "unit": "TFLOP/s", "frac": fl / ms / 1e9 / (PEAK_F32 / 1e12), "bound": "mfma_f32"}
 
 
 def comp_qlinear(lib, torch, m, n, k, per_tensor=True):
@@ -1130,7 +1211,7 @@ def run_components(lib, torch, only, cpu=None):
     4096] activation measured 24.9 us per call right after a CPU baseline,
     7.5 us without one)."""
     want = set(filter(None, only.split(","))) or {"sgemm", "qlinear", "gemv", "sdpa", "flash", "softmax",
-                                                  "quantize", "decode", "swiglu", "io"}
+                                                  "quantize", "decode", "swiglu", "io", "backward"}
     out = []
     pending = []  # (record, cpu_fn): CPU baselines, run after the GPU figures
 
@@ -1195,6 +1276,9 @@ def run_components(lib, torch, only, cpu=None):
             add(comp_swiglu, m, True, I=14336, cpu_fn=lambda m=m: cpu.swiglu(m, True, I=14336))
         for m in (1, 16):
             add(comp_swiglu, m, False, I=14336, cpu_fn=lambda m=m: cpu.swiglu(m, False, I=14336))
+    if "backward" in want:
+        add(comp_matmul_backward, 4096, 4096, 4096, cpu_fn=lambda: cpu.matmul_backward(4096, 4096, 4096))
+        add(comp_batched_matmul, 128, 512, 128, 512, cpu_fn=lambda: cpu.batched_matmul(128, 512, 128, 512))
     if "sgemm" in want:
         for n in (1024, 2048, 4096, 8192):
             add(comp_sgemm, n, cpu_fn=lambda n=n: cpu.sgemm(n))

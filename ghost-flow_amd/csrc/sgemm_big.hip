@@ -1,11 +1,15 @@
 // sgemm_big.hip -- fp32 GEMM on 256 x 256, 128 x 128 or 64 x 64 tiles fed by
 // direct-to-LDS loads:
-// C = alpha * A . op(B) (+ beta C) (+ bias) with A [m, k] row-major and B
-// either [n, k] (NT: Linear::forward's x . W^T with the reference's
-// [out, in] weight, ghostflow-nn/src/linear.rs:56-69) or [k, n] (NN:
-// Tensor::matmul, ghostflow-core/src/ops/matmul.rs:91-119).  gfh_sgemm
-// sends those calls here when the problem fills the GPU with such tiles;
-// the general tile kernel (sgemm.hip) serves everything else.
+// C = alpha * op(A) . op(B) (+ beta C) (+ bias) with A [m, k] or, transposed,
+// [k, m] row-major and B either [n, k] (NT: Linear::forward's x . W^T with
+// the reference's [out, in] weight, ghostflow-nn/src/linear.rs:56-69) or
+// [k, n] (NN: Tensor::matmul, ghostflow-core/src/ops/matmul.rs:91-119).  The
+// transposed A is matmul_backward's a^T . grad
+// (ghostflow-autograd/src/backward.rs:131-160); a batch of such products
+// runs as the grid's y dimension with batched_matmul's modulo slice indexing
+// (matmul.rs:122-170).  gfh_sgemm and gfh_sgemm_strided_batched send those
+// calls here when the problem fills the GPU with such tiles; the general
+// tile kernel (sgemm.hip) serves everything else.
 //
 // Design (one 512-thread workgroup = 8 wave64s, 2 x 4, per 256 x 256 tile;
 // 64 x 64 tiles run 2 x 2 waves twice over, as two wave sets that split
@@ -27,7 +31,9 @@
 //  * NN: the B stage is 32 k-rows of 256 columns; one load instruction
 //    fills one k-row (1 KB).  Rows sit 264 floats apart, so the B fragment
 //    -- 4 scalar reads of 4 consecutive k for column l % 32 -- puts lanes
-//    0-31 and 32-63 (4 rows apart) on disjoint halves of the 64 banks.
+//    0-31 and 32-63 (4 rows apart) on disjoint halves of the 64 banks.  A
+//    transposed A is staged and read the same way, in k-rows of the tile's
+//    C rows.
 //  * The loop body is branch-free: past the end of K the ring reloads the
 //    last stage into the slot just freed, so every s_waitcnt is a constant.
 //  * Epilogue: alpha * acc (+ beta C) (+ bias), separate f32 roundings as in
@@ -53,7 +59,7 @@ constexpr int kKGroups = BKB / 32;  // 8-float k-groups per stage
 // Geometry of a BM x BN tile on an NWM_ x NWN_ wave grid with an
 // STAGES_-deep ring: 256 x 256 and 128 x 128 on 2 x 4 waves and 2 stages,
 // 64 x 64 on 2 x 2 waves and 4 stages.
-template <int BM, int BN, bool NN, int NWM_ = 2, int NWN_ = 4, int STAGES_ = 2, int KS_ = 1>
+template <int BM, int BN, bool NN, int NWM_ = 2, int NWN_ = 4, int STAGES_ = 2, int KS_ = 1, bool TA_ = false>
 struct Geo {
     // KS wave sets share the tile: set s computes k-groups [s kKGroups / KS,
     // (s + 1) kKGroups / KS) of every stage into its own accumulators, which
@@ -70,12 +76,16 @@ struct Geo {
     static constexpr int kLA = BM * BKB / (1024 * NWT), kLB = BN * BKB / (1024 * NWT);
     static_assert(kLA * 1024 * NWT == BM * BKB && kLB * 1024 * NWT == BN * BKB, "whole load instructions per wave");
     static constexpr int kLPS = kLA + kLB;
-    static constexpr int kABytes = BM * BKB;
     // NN: a load instruction fills RPL k-rows of BN floats (1 KB); groups
     // of RPL rows sit 1024 + 32 RPL bytes apart, which puts rows 4 apart
-    // 32 banks apart.
+    // 32 banks apart.  A transposed A ([k, m] in memory, TA) is staged the
+    // same way, in k-rows of BM floats.
+    static constexpr bool TA = TA_;
     static constexpr int RPL = 1024 / (BN * 4);
     static constexpr int kGroupStride = 1024 + 32 * RPL;
+    static constexpr int RPLA = 1024 / (BM * 4);
+    static constexpr int kGroupStrideA = 1024 + 32 * RPLA;
+    static constexpr int kABytes = TA ? (32 / RPLA) * kGroupStrideA : BM * BKB;
     static constexpr int kBBytes = NN ? (32 / RPL) * kGroupStride : BN * BKB;
     static constexpr int kStageBytes = kABytes + kBBytes;
     static constexpr int kOutStride = WN + 8;  // floats per staged output row
@@ -89,8 +99,9 @@ struct Geo {
     static_assert(KS == 1 || NW * FM * FN * 16 * 64 * 4 <= kLds, "accumulator exchange fits the ring");
     static_assert(FM >= 1 && FN >= 1 && (FM == 1 || FM % 2 == 0), "wave sub-tile");
     static_assert((STAGES - 1) * kLPS < 64, "vmcnt is 6 bits");
-    // byte offset of k-row r inside an NN B stage
+    // byte offset of k-row r inside an NN B stage / a TA A stage
     static __device__ __forceinline__ int brow(int r) { return (r / RPL) * kGroupStride + (r % RPL) * BN * 4; }
+    static __device__ __forceinline__ int arow(int r) { return (r / RPLA) * kGroupStrideA + (r % RPLA) * BM * 4; }
 };
 
 typedef __attribute__((address_space(3))) void *lds_ptr;
@@ -101,6 +112,10 @@ struct BigParams {
     float *c;
     const float *bias;
     int64_t m, n, k, lda, ldb, ldc;
+    // batch z (blockIdx.y) takes A slice z % batch_a and B slice z % batch_b
+    // (batched_matmul's modulo indexing) and writes C slice z
+    int64_t stride_a, stride_b, stride_c;
+    int batch_a, batch_b;
     float alpha, beta;
     int tiles_m, tiles_n;
 };
@@ -128,10 +143,11 @@ __device__ __forceinline__ void interleave() {
     }
 }
 
-template <int BM, int BN, bool NN, int NWM_ = 2, int NWN_ = 4, int STAGES_ = 2, int KS_ = 1>
-__global__ __launch_bounds__((Geo<BM, BN, NN, NWM_, NWN_, STAGES_, KS_>::NT),
+template <int BM, int BN, bool NN, int NWM_ = 2, int NWN_ = 4, int STAGES_ = 2, int KS_ = 1, bool TA = false,
+          bool BATCH = false>
+__global__ __launch_bounds__((Geo<BM, BN, NN, NWM_, NWN_, STAGES_, KS_, TA>::NT),
                              (BM * BN <= 128 * 128) ? 2 : 1) void sgemm_big_kernel(BigParams p) {
-    using G = Geo<BM, BN, NN, NWM_, NWN_, STAGES_, KS_>;
+    using G = Geo<BM, BN, NN, NWM_, NWN_, STAGES_, KS_, TA>;
     constexpr int NWN = G::NWN, NW = G::NW, NWT = G::NWT, STAGES = G::STAGES, KS = G::KS;
     constexpr int KGP = kKGroups / KS;  // k-groups per stage of this wave's set
     constexpr int WM = G::WM, WN = G::WN, FM = G::FM, FN = G::FN;
@@ -157,19 +173,35 @@ __global__ __launch_bounds__((Geo<BM, BN, NN, NWM_, NWN_, STAGES_, KS_>::NT),
     const int in_group = bid - group * group_size;
     const int64_t m0 = (int64_t)(first_m + in_group % gm) * BM;
     const int64_t n0 = (int64_t)(in_group / gm) * BN;
+    const float *pa = p.a, *pb = p.b;
+    float *pc = p.c;
+    if constexpr (BATCH) {
+        const int bz = blockIdx.y;
+        pa += (bz % p.batch_a) * p.stride_a;
+        pb += (bz % p.batch_b) * p.stride_b;
+        pc += bz * p.stride_c;
+    }
 
     // Byte offsets, from the tile's first row, of this wave's load
     // instructions: instruction j covers tile rows wave * (BM / NW) + j * 8
     // .. + 7; lane l fills LDS slot l of that 1 KB run (row l / 8, chunk
     // l % 8) from logical chunk (l % 8) ^ swz(row).  Rows past m / n read
     // the last row (their products are never stored).
-    const char *a_base = reinterpret_cast<const char *>(p.a + m0 * p.lda);
-    const char *b_base = reinterpret_cast<const char *>(NN ? p.b + n0 : p.b + n0 * p.ldb);
+    const char *a_base = reinterpret_cast<const char *>(TA ? pa + m0 : pa + m0 * p.lda);
+    const char *b_base = reinterpret_cast<const char *>(NN ? pb + n0 : pb + n0 * p.ldb);
     int64_t a_off[kLA], b_off[kLB];
 #pragma unroll
     for (int j = 0; j < kLA; ++j) {
-        const int r = wave * (BM / NWT) + j * kRowsPerLoad + lane / 8;
-        a_off[j] = (min(m0 + r, p.m - 1) - m0) * p.lda * 4 + ((lane % 8) ^ swz(r)) * 16;
+        if (TA) {
+            // row group wave * kLA + j: k-row RPLA g + l / (64 / RPLA), rows
+            // m0 + 4 (l % (64 / RPLA)) .. + 3 of C (clamped below m; m % 4 == 0)
+            constexpr int LPRA = 64 / G::RPLA;
+            const int kr = (wave * kLA + j) * G::RPLA + lane / LPRA;
+            a_off[j] = (int64_t)kr * p.lda * 4 + (min(m0 + 4 * (lane % LPRA), p.m - 4) - m0) * 4;
+        } else {
+            const int r = wave * (BM / NWT) + j * kRowsPerLoad + lane / 8;
+            a_off[j] = (min(m0 + r, p.m - 1) - m0) * p.lda * 4 + ((lane % 8) ^ swz(r)) * 16;
+        }
     }
 #pragma unroll
     for (int j = 0; j < kLB; ++j) {
@@ -185,18 +217,20 @@ __global__ __launch_bounds__((Geo<BM, BN, NN, NWM_, NWN_, STAGES_, KS_>::NT),
             b_off[j] = (min(n0 + r, p.n - 1) - n0) * p.ldb * 4 + ((lane % 8) ^ swz(r)) * 16;
         }
     }
-    // bytes between consecutive stages of B in global memory
+    // bytes between consecutive stages of A / B in global memory
+    const int64_t a_stage = TA ? (int64_t)32 * p.lda * 4 : BKB;
     const int64_t b_stage = NN ? (int64_t)32 * p.ldb * 4 : BKB;
     const int nk = (int)(p.k / 32);
 
     auto issue = [&](int t, int slot) __attribute__((always_inline)) {
         char *la = lds + slot * kStageBytes;
         char *lb = la + kABytes;
-        const int64_t kb = (int64_t)t * BKB;
 #pragma unroll
-        for (int j = 0; j < kLA; ++j)
-            __builtin_amdgcn_global_load_lds((glb_ptr)(a_base + kb + a_off[j]),
-                                             (lds_ptr)(la + (wave * (BM / NWT) + j * kRowsPerLoad) * BKB), 16, 0, 0);
+        for (int j = 0; j < kLA; ++j) {
+            char *dst = TA ? la + (wave * kLA + j) * G::kGroupStrideA : la + (wave * (BM / NWT) + j * kRowsPerLoad) * BKB;
+            __builtin_amdgcn_global_load_lds((glb_ptr)(a_base + (int64_t)t * a_stage + a_off[j]), (lds_ptr)dst, 16, 0,
+                                             0);
+        }
 #pragma unroll
         for (int j = 0; j < kLB; ++j) {
             char *dst = NN ? lb + (wave * kLB + j) * G::kGroupStride : lb + (wave * (BN / NWT) + j * kRowsPerLoad) * BKB;
@@ -215,8 +249,18 @@ __global__ __launch_bounds__((Geo<BM, BN, NN, NWM_, NWN_, STAGES_, KS_>::NT),
         const char *la = lds + (t % STAGES) * kStageBytes;
         const char *lb = la + kABytes;
         const int fo = foff0 ^ (kg << 5);
+        if (TA) {
+            const int r0 = 8 * kg + 4 * (lane >> 5);
 #pragma unroll
-        for (int i = 0; i < FM; ++i) af[buf][i] = *reinterpret_cast<const f32x4 *>(la + (wm0 + i * 32) * BKB + fo);
+            for (int e = 0; e < 4; ++e) {
+                const float *fa = reinterpret_cast<const float *>(la + G::arow(r0 + e)) + (lane & 31);
+#pragma unroll
+                for (int i = 0; i < FM; ++i) af[buf][i][e] = fa[wm0 + i * 32];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < FM; ++i) af[buf][i] = *reinterpret_cast<const f32x4 *>(la + (wm0 + i * 32) * BKB + fo);
+        }
         if (NN) {
             const int r0 = 8 * kg + 4 * (lane >> 5);
 #pragma unroll
@@ -249,7 +293,7 @@ __global__ __launch_bounds__((Geo<BM, BN, NN, NWM_, NWN_, STAGES_, KS_>::NT),
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[buf][i][e], bf[buf][j][e], acc[i][j], 0, 0, 0);
     };
 
-    constexpr int NR = FM + (NN ? 4 : 1) * FN, NM = 4 * FM * FN;
+    constexpr int NR = (TA ? 4 : 1) * FM + (NN ? 4 : 1) * FN, NM = 4 * FM * FN;
     for (int t = 0; t < STAGES; ++t) issue(min(t, nk - 1), t);
     wait_vmcnt<(STAGES - 1) * kLPS>();
     __builtin_amdgcn_s_barrier();
@@ -315,7 +359,7 @@ __global__ __launch_bounds__((Geo<BM, BN, NN, NWM_, NWN_, STAGES_, KS_>::NT),
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();  // every wave is done with the operand ring
     float *lt = reinterpret_cast<float *>(lds) + wt * (HALF * kOutStride);
-    const bool vec_out = (p.ldc % 4) == 0 && (reinterpret_cast<uintptr_t>(p.c) & 15) == 0;
+    const bool vec_out = (p.ldc % 4) == 0 && (reinterpret_cast<uintptr_t>(pc) & 15) == 0;
 #pragma unroll
     for (int hf = 0; hf < PASSES; ++hf) {
         if (KS == 1 || ks == 0) {  // (set 1 only keeps the barriers)
@@ -335,7 +379,7 @@ __global__ __launch_bounds__((Geo<BM, BN, NN, NWM_, NWN_, STAGES_, KS_>::NT),
                 f32x4 v = *reinterpret_cast<const f32x4 *>(lt + lr * kOutStride + 4 * (lane % LPR));
                 const int64_t row = m0 + wm0 + hf * HALF + lr;
                 if (row >= p.m) continue;
-                float *dst = p.c + row * p.ldc + col;
+                float *dst = pc + row * p.ldc + col;
                 if (vec_out && col + 3 < p.n) {
                     if (p.beta != 0.f) {
                         const f32x4 c0 = *reinterpret_cast<const f32x4 *>(dst);
@@ -366,19 +410,54 @@ __global__ __launch_bounds__((Geo<BM, BN, NN, NWM_, NWN_, STAGES_, KS_>::NT),
 }  // namespace
 
 namespace {
-int64_t tiles_of(const SgemmDesc &d, int64_t t) { return ((d.m + t - 1) / t) * ((d.n + t - 1) / t); }
+// output tiles of side t over the whole batch
+int64_t tiles_of(const SgemmDesc &d, int64_t t) { return ((d.m + t - 1) / t) * ((d.n + t - 1) / t) * d.batch; }
+
+// One tile configuration in the four operand layouts (A as [m, k] or, with
+// trans_a, [k, m]; B as [k, n] or, with trans_b, [n, k]); batched products
+// take A as [m, k].
+template <int BM, int BN, int NWM, int NWN, int STAGES, int KS>
+void launch_layouts(bool trans_a, bool trans_b, bool batched, const BigParams &p, dim3 grid, hipStream_t s) {
+    constexpr int kThreads = Geo<BM, BN, false, NWM, NWN, STAGES, KS>::NT;
+    const dim3 block(kThreads);
+    if (batched) {
+        if (trans_b)
+            hipLaunchKernelGGL((sgemm_big_kernel<BM, BN, false, NWM, NWN, STAGES, KS, false, true>), grid, block, 0, s,
+                               p);
+        else
+            hipLaunchKernelGGL((sgemm_big_kernel<BM, BN, true, NWM, NWN, STAGES, KS, false, true>), grid, block, 0, s,
+                               p);
+    } else if (trans_a) {
+        if (trans_b)
+            hipLaunchKernelGGL((sgemm_big_kernel<BM, BN, false, NWM, NWN, STAGES, KS, true>), grid, block, 0, s, p);
+        else
+            hipLaunchKernelGGL((sgemm_big_kernel<BM, BN, true, NWM, NWN, STAGES, KS, true>), grid, block, 0, s, p);
+    } else {
+        if (trans_b)
+            hipLaunchKernelGGL((sgemm_big_kernel<BM, BN, false, NWM, NWN, STAGES, KS, false>), grid, block, 0, s, p);
+        else
+            hipLaunchKernelGGL((sgemm_big_kernel<BM, BN, true, NWM, NWN, STAGES, KS, false>), grid, block, 0, s, p);
+    }
+}
 }  // namespace
 
-// 256 x 256 tiles when there are at least 256 of them (one per CU), else
-// 128 x 128 tiles when those number 256, else 64 x 64 tiles on 2 x 2 waves
-// (at least 32 of them).  Measured against the register-staged tile kernel
-// (us): 1024^3 NN 31.3 -> 25.8, NT 29.5 -> 20.9; 1536^3 NN 120.5 -> 84.4;
-// 1024 x 1024 x 4096 NN 107.2 -> 86.6; 512 x 2048 x 1024 NT 29.5 -> 20.7.
+// 256 x 256 tiles when there are at least 256 of them (one per CU) and K is
+// at least 256, else 128 x 128 tiles when those number 256, else 64 x 64
+// tiles on 2 x 2 waves (at least 32 of them), counting the tiles of every
+// batch slice.
+// Measured against the register-staged tile kernel (us): 1024^3 NN 31.3 ->
+// 25.8, NT 29.5 -> 20.9; 1536^3 NN 120.5 -> 84.4; 1024 x 1024 x 4096 NN
+// 107.2 -> 86.6; 512 x 2048 x 1024 NT 29.5 -> 20.7.
 bool sgemm_big_fits(const SgemmDesc &d) {
-    if (d.trans_a || d.batch > 1 || d.batch_a > 1 || d.batch_b > 1) return false;
     if (d.k <= 0 || d.k % 32 != 0 || d.lda % 4 != 0 || d.ldb % 4 != 0) return false;
-    if (!d.trans_b && d.n % 4 != 0) return false;  // NN: whole 16-byte column groups
+    if (!d.trans_b && d.n % 4 != 0) return false;  // B as [k, n]: whole 16-byte column groups
+    if (d.trans_a && d.m % 4 != 0) return false;   // A as [k, m]: the same
     if (!aligned16(d.a) || !aligned16(d.b)) return false;
+    if (d.batch > 1 || d.batch_a > 1 || d.batch_b > 1) {
+        // A as [m, k]; every slice 16-byte aligned; the batch is the grid's
+        // y dimension
+        if (d.trans_a || d.stride_a % 4 != 0 || d.stride_b % 4 != 0 || d.batch > 65535) return false;
+    }
     if (d.m >= 128 && d.n >= 128 && tiles_of(d, 128) >= 256) return true;
     return d.m >= 64 && d.n >= 64 && tiles_of(d, 64) >= 32;
 }
@@ -395,45 +474,45 @@ int launch_sgemm_big(const SgemmDesc &d, hipStream_t s) {
     p.lda = d.lda;
     p.ldb = d.ldb;
     p.ldc = d.ldc;
+    p.stride_a = d.stride_a;
+    p.stride_b = d.stride_b;
+    p.stride_c = d.stride_c;
+    // (a slice count above the batch indexes like the batch itself)
+    const int64_t nb = std::max<int64_t>(d.batch, 1);
+    p.batch_a = (int)std::min(std::max<int64_t>(d.batch_a, 1), nb);
+    p.batch_b = (int)std::min(std::max<int64_t>(d.batch_b, 1), nb);
+    const bool batched = d.batch > 1 || d.batch_a > 1 || d.batch_b > 1;
     p.alpha = d.alpha;
     p.beta = d.beta;
+    // 256 x 256 tiles need K >= 256: below that a tile's epilogue outweighs
+    // its K loop, and 128 x 128 tiles, two workgroups per CU, overlap one
+    // tile's stores with the other's loop (batched 512 x 512 x 128 slices,
+    // 128 of them: 89.0 -> 85.8 us; 2048 x 2048 x 128: 1341 -> 1308 us).
     const int64_t t128 = tiles_of(d, 128);
-    const int t = (d.m >= 256 && d.n >= 256 && tiles_of(d, 256) >= 256) ? 256
-                  : (d.m >= 128 && d.n >= 128 && t128 >= 256)           ? 128
-                                                                         : 64;
+    const int t = (d.m >= 256 && d.n >= 256 && d.k >= 256 && tiles_of(d, 256) >= 256) ? 256
+                  : (d.m >= 128 && d.n >= 128 && t128 >= 256)                          ? 128
+                                                                                        : 64;
     p.tiles_m = (int)((d.m + t - 1) / t);
     p.tiles_n = (int)((d.n + t - 1) / t);
-    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n));
-    constexpr int kNT = Geo<128, 128, false>::NT;
-    constexpr int kNT64 = Geo<64, 64, false, 2, 2>::NT;
+    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n), (unsigned)std::max<int64_t>(d.batch, 1));
     if (t == 256) {
-        if (d.trans_b)
-            hipLaunchKernelGGL((sgemm_big_kernel<256, 256, false>), grid, dim3(kNT), 0, s, p);
-        else
-            hipLaunchKernelGGL((sgemm_big_kernel<256, 256, true>), grid, dim3(kNT), 0, s, p);
+        launch_layouts<256, 256, 2, 4, 2, 1>(d.trans_a, d.trans_b, batched, p, grid, s);
     } else if (t == 128) {
         // One round of tiles (one workgroup per CU): a 3-deep ring (2048^3 NN
         // 143.7 -> 133.7 us); more tiles: 2 stages, two workgroups per CU.
-        if (t128 <= 256) {
-            if (d.trans_b)
-                hipLaunchKernelGGL((sgemm_big_kernel<128, 128, false, 2, 4, 3>), grid, dim3(kNT), 0, s, p);
-            else
-                hipLaunchKernelGGL((sgemm_big_kernel<128, 128, true, 2, 4, 3>), grid, dim3(kNT), 0, s, p);
-        } else {
-            if (d.trans_b)
-                hipLaunchKernelGGL((sgemm_big_kernel<128, 128, false>), grid, dim3(kNT), 0, s, p);
-            else
-                hipLaunchKernelGGL((sgemm_big_kernel<128, 128, true>), grid, dim3(kNT), 0, s, p);
-        }
+        if (t128 <= 256)
+            launch_layouts<128, 128, 2, 4, 3, 1>(d.trans_a, d.trans_b, batched, p, grid, s);
+        else
+            launch_layouts<128, 128, 2, 4, 2, 1>(d.trans_a, d.trans_b, batched, p, grid, s);
     } else {
         // Two wave sets splitting each stage's k-groups, so each SIMD runs
         // two waves (1024^3 NN 24.1 -> 22.0 us, 1024 x 1024 x 4096 NN 86.3
         // -> 77.5 us; NT unchanged).  Ring depth: NT 4 stages, NN 2 (of
         // 2 / 3 / 4 / 6: NN 22.0 / 22.8 / 22.2 / 22.4 us at 1024^3).
         if (d.trans_b)
-            hipLaunchKernelGGL((sgemm_big_kernel<64, 64, false, 2, 2, 4, 2>), grid, dim3(2 * kNT64), 0, s, p);
+            launch_layouts<64, 64, 2, 2, 4, 2>(d.trans_a, true, batched, p, grid, s);
         else
-            hipLaunchKernelGGL((sgemm_big_kernel<64, 64, true, 2, 2, 2, 2>), grid, dim3(2 * kNT64), 0, s, p);
+            launch_layouts<64, 64, 2, 2, 2, 2>(d.trans_a, false, batched, p, grid, s);
     }
     return check_launch("sgemm (direct-to-LDS tiles)");
 }

@@ -192,17 +192,21 @@ def test_k_zero_gives_bias(torch_dev):
     assert to_np(out).tolist() == [list(range(6))] * 4
 
 
-@pytest.mark.parametrize("m,n,k", [(4096, 4096, 64), (4100, 4000, 96), (4352, 3900, 32), (2048, 2048, 64),
+@pytest.mark.parametrize("m,n,k", [(4096, 4096, 256), (4100, 4000, 288), (4352, 3900, 32), (2048, 2048, 64),
                                    (2100, 2000, 96), (1024, 4096, 32), (330, 700, 96), (1000, 520, 1024),
                                    (1024, 1024, 1024)])
 @pytest.mark.parametrize("tb", [True, False])
-def test_big_tiles_integer_exact(torch_dev, m, n, k, tb):
-    """NT (Linear's x . W^T) and NN (Tensor::matmul) shapes with K % 32 == 0
-    take the direct-to-LDS kernel: 256 x 256 tiles (the first three), 128 x
-    128 tiles with a 3-deep ring (one round of tiles: 2048^2, 1024 x 4096)
-    or 2 stages (2100 x 2000), and 64 x 64 tiles on 2 x 2 waves (the last
-    three) -- ragged m and n inside the last tiles, alpha, beta and bias, on
-    integer data (exact in any summation order)."""
+@pytest.mark.parametrize("ta", [False, True])
+def test_big_tiles_integer_exact(torch_dev, m, n, k, tb, ta):
+    """The four layouts with K % 32 == 0 (B as Linear's [n, k] weight or
+    Tensor::matmul's [k, n]; A as [m, k] or, transposed as matmul_backward's
+    a^T, [k, m]) take the direct-to-LDS kernel: 256 x 256 tiles (the first
+    two: K >= 256), 128 x 128 tiles with 2 stages (4352 x 3900, 2100 x 2000)
+    or a 3-deep ring (one round of tiles: 2048^2, 1024 x 4096), and 64 x 64
+    tiles on 2 x 2 waves (the last three) -- ragged m and n inside the last
+    tiles, alpha, beta and bias, on integer data (exact in any summation
+    order).  The reference is the oracle's Linear::forward, or for the
+    largest products the same sums in float64, which are exact here."""
     gh, O = _gh(), _oracle()
     rng = np.random.default_rng(m + n + k)
     a = rng.integers(-4, 5, size=(m, k)).astype(np.float32)
@@ -210,10 +214,55 @@ def test_big_tiles_integer_exact(torch_dev, m, n, k, tb):
     c0 = rng.integers(-4, 5, size=(m, n)).astype(np.float32)
     bias = rng.integers(-4, 5, size=(n,)).astype(np.float32)
     dc = to_dev(c0, torch_dev)
+    a_dev = to_dev(np.ascontiguousarray(a.T) if ta else a, torch_dev)
     b_dev = to_dev(w if tb else np.ascontiguousarray(w.T), torch_dev)
-    gh.sgemm(to_dev(a, torch_dev), b_dev, trans_b=tb, alpha=2.0, beta=-1.0, bias=to_dev(bias, torch_dev), out=dc)
-    ref = (2.0 * O.linear_forward(a, w) - c0 + bias).astype(np.float32)
+    gh.sgemm(a_dev, b_dev, trans_a=ta, trans_b=tb, alpha=2.0, beta=-1.0, bias=to_dev(bias, torch_dev), out=dc)
+    if m * n * k <= (1 << 30):
+        prod = O.linear_forward(a, w)
+    else:
+        prod = (a.astype(np.float64) @ w.astype(np.float64).T).astype(np.float32)
+    ref = (2.0 * prod - c0 + bias).astype(np.float32)
     np.testing.assert_array_equal(to_np(dc), ref)
+
+
+def _strided_batched(torch_dev, ta, tb, a, b, batch_a, batch_b, batch, m, n, k):
+    """gfh_sgemm_strided_batched on packed slices; returns C [batch, m, n]."""
+    import torch
+    gh = _gh()
+    L = gh.lib()
+    da, db = to_dev(a, torch_dev), to_dev(b, torch_dev)
+    dc = torch.full((batch, m, n), float("nan"), device=torch_dev)
+    st = torch.cuda.current_stream(torch_dev).cuda_stream
+    rc = L.gfh_sgemm_strided_batched(int(ta), int(tb), m, n, k, 1.0, da.data_ptr(), m if ta else k, m * k, batch_a,
+                                     db.data_ptr(), k if tb else n, k * n, batch_b, 0.0, dc.data_ptr(), n, m * n,
+                                     batch, None, st)
+    assert rc == 0, L.gfh_last_error()
+    return to_np(dc)
+
+
+@pytest.mark.parametrize("batch,batch_a,batch_b,m,n,k", [
+    (4, 4, 1, 2048, 2048, 256),   # 256 x 256 tiles, B shared by every slice
+    (16, 16, 16, 512, 512, 128),  # 128 x 128 tiles, one round (3-deep ring), the SDPA score shape
+    (32, 32, 32, 512, 512, 96),   # 128 x 128 tiles, 2 stages
+    (6, 3, 6, 256, 320, 96),      # 64 x 64 tiles, A slices taken modulo 3
+    (6, 6, 3, 300, 260, 64),      # 64 x 64 tiles, B slices modulo 3, ragged edges
+])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+def test_big_tiles_batched_modulo(torch_dev, batch, batch_a, batch_b, m, n, k, ta, tb):
+    """Strided-batched products: slice z multiplies A slice z % batch_a by B
+    slice z % batch_b (batched_matmul's modulo indexing, matmul.rs:148-149),
+    on integer data (exact in any order).  With A as [m, k] they run on the
+    direct-to-LDS kernel, the batch as its grid's y dimension; a transposed
+    A takes the general tile kernel."""
+    rng = np.random.default_rng(batch * 7 + m + n + k + 3 * ta + tb)
+    a = rng.integers(-4, 5, size=(batch_a, m, k)).astype(np.float32)
+    b = rng.integers(-4, 5, size=(batch_b, k, n)).astype(np.float32)
+    a_st = np.ascontiguousarray(a.transpose(0, 2, 1)) if ta else a
+    b_st = np.ascontiguousarray(b.transpose(0, 2, 1)) if tb else b
+    got = _strided_batched(torch_dev, ta, tb, a_st, b_st, batch_a, batch_b, batch, m, n, k)
+    for z in range(batch):
+        ref = (a[z % batch_a].astype(np.float64) @ b[z % batch_b].astype(np.float64)).astype(np.float32)
+        np.testing.assert_array_equal(got[z], ref, err_msg=f"slice {z}")
 
 
 @pytest.mark.parametrize("n", [2048, 4096])
