@@ -64,7 +64,21 @@ struct GemvParams {
     int64_t kslice;  // rows per slice: a multiple of 16, at most kMaxSlice
     int xvec;        // x rows 16-byte aligned and k % 4 == 0 (fp32 kernel: staged 4 rows per load)
     int off32;       // the weight is under 4 GB: byte offsets into it fit 32 bits
+    // gfh_sgemm's epilogue when it routes a product here (epi != 0):
+    // y = alpha * (x . W), then + beta * y, then + bias, each rounded
+    float alpha, beta;
+    const float *bias;
+    int epi;
 };
+
+// The value stored for batch row bi, column col of y, from the product v.
+__device__ __forceinline__ float gemv_out(const GemvParams &p, int64_t bi, int64_t col, float v) {
+    if (!p.epi) return v;
+    float o = p.alpha * v;
+    if (p.beta != 0.f) o = o + p.beta * p.y[bi * p.n + col];
+    if (p.bias) o = o + p.bias[col];
+    return o;
+}
 
 constexpr int kMaxSlice = 1024;  // int8 kernel
 
@@ -92,7 +106,7 @@ __device__ __forceinline__ void store_strip(const GemvParams &p, int64_t strip, 
         for (int t = threadIdx.x; t < MAXB * SCOLS; t += NT) {
             const int bi = t / SCOLS, c = t % SCOLS;
             if (bi >= nb || col0 + c >= p.n) continue;
-            p.y[bi * p.n + col0 + c] = value(bi, c);
+            p.y[bi * p.n + col0 + c] = gemv_out(p, bi, col0 + c, value(bi, c));
         }
         return;
     }
@@ -150,7 +164,7 @@ __device__ __forceinline__ void store_strip(const GemvParams &p, int64_t strip, 
     for (int o = 0; o < kOut; ++o)
         if (src[o]) {
             const int t = threadIdx.x + o * NT;
-            p.y[(t / SCOLS) * p.n + col0 + t % SCOLS] = v[o];
+            p.y[(t / SCOLS) * p.n + col0 + t % SCOLS] = gemv_out(p, t / SCOLS, col0 + t % SCOLS, v[o]);
         }
     if (threadIdx.x == 0) __hip_atomic_store(p.counters + strip, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -915,7 +929,16 @@ int for_batch_groups(const GemvParams &p, const float *x, float *y, int64_t b, F
 }  // namespace
 
 int launch_gemv_f32(const float *x, const float *w, float *y, int64_t b, int64_t k, int64_t n, hipStream_t s) {
+    return launch_gemv_f32_epi(x, w, y, b, k, n, 1.f, 0.f, nullptr, s);
+}
+
+int launch_gemv_f32_epi(const float *x, const float *w, float *y, int64_t b, int64_t k, int64_t n, float alpha,
+                        float beta, const float *bias, hipStream_t s) {
     GemvParams p{};
+    p.alpha = alpha;
+    p.beta = beta;
+    p.bias = bias;
+    p.epi = alpha != 1.f || beta != 0.f || bias != nullptr;
     p.w = w;
     p.k = k;
     p.n = n;

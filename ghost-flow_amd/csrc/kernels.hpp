@@ -105,6 +105,10 @@ int launch_qlinear_swiglu_i8(const QSwigluDesc &d, int *npart, hipStream_t s);
 
 // gemv.hip
 int launch_gemv_f32(const float *x, const float *w, float *y, int64_t b, int64_t k, int64_t n, hipStream_t s);
+// The same with gfh_sgemm's epilogue: y = alpha * (x . W) (+ beta * y) (+ bias),
+// each a separately rounded f32 operation.
+int launch_gemv_f32_epi(const float *x, const float *w, float *y, int64_t b, int64_t k, int64_t n, float alpha,
+                        float beta, const float *bias, hipStream_t s);
 int launch_gemv_w8(const float *x, const int8_t *qw, const float *scales, const int8_t *zps, float *y, int64_t b,
                    int64_t k, int64_t n, hipStream_t s);
 // Same computation with its split-K scratch in a static device array: no

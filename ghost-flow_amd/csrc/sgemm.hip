@@ -283,10 +283,22 @@ int launch_sgemm_nt_group(const SgemmDesc *d, int count, hipStream_t s) {
     return set_error(GFH_INVALID_SHAPE, "sgemm: these products do not share one launch");
 }
 
+// Tensor::matmul at decode batch sizes, x [m, k] . W [k, n] with m <= 16 and
+// packed rows: the decode GEMV (gemv.hip) streams W once per 8 rows of x,
+// with the same epilogue.  (W [4096, 14336]: 38-39 us at m = 1-8, where the
+// tile kernels took 106 us.)
+namespace {
+bool gemv_nn_fits(const SgemmDesc &d) {
+    return !d.trans_a && !d.trans_b && d.batch <= 1 && d.batch_a <= 1 && d.batch_b <= 1 && d.m >= 1 && d.m <= 16 &&
+           d.k > 0 && d.n > 0 && d.lda == d.k && d.ldb == d.n && d.ldc == d.n;
+}
+}  // namespace
+
 int launch_sgemm(const SgemmDesc &d, hipStream_t s) {
     // x . W^T with at most 8 rows of x: a tile of this kernel would leave
     // most of its MFMA rows empty and its grid far too small to stream W.
     if (gemv_nt_fits(d)) return launch_gemv_nt(d, s);
+    if (gemv_nn_fits(d)) return launch_gemv_f32_epi(d.a, d.b, d.c, d.m, d.k, d.n, d.alpha, d.beta, d.bias, s);
     // up to 64 rows: the weight streamed straight into f32 MFMA operands
     if (gemm_nt_skinny_fits(d)) return launch_gemm_nt_skinny(d, s);
     // NT / NN on 256 x 256 tiles fed by direct-to-LDS loads, when they fill the GPU

@@ -265,6 +265,23 @@ def test_big_tiles_batched_modulo(torch_dev, batch, batch_a, batch_b, m, n, k, t
         np.testing.assert_array_equal(got[z], ref, err_msg=f"slice {z}")
 
 
+@pytest.mark.parametrize("m", [1, 3, 8, 13, 16])
+def test_matmul_decode_rows(torch_dev, m):
+    """Tensor::matmul at decode batch sizes (x [m, k] . W [k, n], m <= 16)
+    runs on the decode GEMV kernel: bit-exact on integer data, and within
+    the GEMM bound on N(0, 1) data against the oracle's matmul_blocked."""
+    gh, O = _gh(), _oracle()
+    rng = np.random.default_rng(40 + m)
+    k, n = 1000, 4100
+    a = rng.integers(-8, 9, size=(m, k)).astype(np.float32)
+    b = rng.integers(-8, 9, size=(k, n)).astype(np.float32)
+    np.testing.assert_array_equal(to_np(gh.matmul(to_dev(a, torch_dev), to_dev(b, torch_dev))), O.matmul(a, b))
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    got = to_np(gh.matmul(to_dev(a, torch_dev), to_dev(b, torch_dev)))
+    assert np.abs(got - O.matmul(a, b)).max() <= gemm_tol(k, a, b)
+
+
 @pytest.mark.parametrize("n", [2048, 4096])
 def test_big_tiles_nn_random(torch_dev, n):
     """NN at n^3 on N(0,1) data (the sweep's shapes: 128 x 128 tiles at 2048,
