@@ -818,14 +818,16 @@ void launch_f32(const GemvParams &p, bool vec, hipStream_t s) {
     // Matrix cores for groups of 5-8 rows: W [4096, 14336] at 8 rows 46.1 ->
     // 44.6 us; at 4 rows both forms take 42.7 us.
     constexpr bool MF = MAXB >= 8;
-    if (vec && p.xvec && p.off32) {  // x streamed with the weights, no staging
-        if (nwg <= 256)
-            hipLaunchKernelGGL((gemv_f32_kernel<MAXB, U, true, 8, f32_max_rows<MAXB>(), MF, true>), dim3(nwg),
-                               dim3(512), 0, s, p);
-        else
-            hipLaunchKernelGGL((gemv_f32_kernel<MAXB, U, true, kWaves, f32_max_rows<MAXB>(), MF, true>), dim3(nwg),
-                               dim3(kThreads), 0, s, p);
-        return;
+    if constexpr (MAXB <= 8) {
+        if (vec && p.xvec && p.off32) {  // x streamed with the weights, no staging
+            if (nwg <= 256)
+                hipLaunchKernelGGL((gemv_f32_kernel<MAXB, U, true, 8, f32_max_rows<MAXB>(), MF, true>), dim3(nwg),
+                                   dim3(512), 0, s, p);
+            else
+                hipLaunchKernelGGL((gemv_f32_kernel<MAXB, U, true, kWaves, f32_max_rows<MAXB>(), MF, true>),
+                                   dim3(nwg), dim3(kThreads), 0, s, p);
+            return;
+        }
     }
     if constexpr (MAXB == 8) {
         if (vec && nwg <= 256 && p.kslice > f32_max_rows<8>()) {
@@ -839,7 +841,7 @@ void launch_f32(const GemvParams &p, bool vec, hipStream_t s) {
     else if (vec)
         hipLaunchKernelGGL((gemv_f32_kernel<MAXB, U, true, kWaves, f32_max_rows<MAXB>(), MF>), dim3(nwg),
                            dim3(kThreads), 0, s, p);
-    else
+    else if constexpr (MAXB <= 8)
         hipLaunchKernelGGL((gemv_f32_kernel<MAXB, U, false>), dim3(nwg), dim3(kThreads), 0, s, p);
 }
 
@@ -913,14 +915,14 @@ int set_slices(GemvParams &q, int64_t kslice, hipStream_t s, const SplitScratch 
     return GFH_SUCCESS;
 }
 
-// The batch is processed in groups of at most 8 rows.
+// The batch is processed in groups of at most `group` rows.
 template <typename F>
-int for_batch_groups(const GemvParams &p, const float *x, float *y, int64_t b, F launch_group) {
-    for (int64_t b0 = 0; b0 < b; b0 += 8) {
+int for_batch_groups(const GemvParams &p, const float *x, float *y, int64_t b, F launch_group, int64_t group = 8) {
+    for (int64_t b0 = 0; b0 < b; b0 += group) {
         GemvParams q = p;
         q.x = x + b0 * p.k;
         q.y = y + b0 * p.n;
-        q.b = (b - b0) < 8 ? (b - b0) : 8;
+        q.b = (b - b0) < group ? (b - b0) : group;
         GFH_TRY(launch_group(q));
     }
     return GFH_SUCCESS;
@@ -947,12 +949,15 @@ int launch_gemv_f32_epi(const float *x, const float *w, float *y, int64_t b, int
     p.xvec = (k % 4 == 0) && aligned16(x);
     // (64 rows of margin: a step's offsets are formed before the clamp to the last row)
     p.off32 = ((double)k + 64.0) * (double)n * 4.0 < 4294967296.0;
+    // 9-16 rows on the matrix cores in one launch (a 16-column B operand)
+    const int64_t group = (b > 8 && vec) ? 16 : 8;
     return for_batch_groups(p, x, y, b, [&](GemvParams &q) {
-        const int maxb = q.b == 1 ? 1 : q.b == 2 ? 2 : q.b <= 4 ? 4 : 8;
+        const int maxb = q.b == 1 ? 1 : q.b == 2 ? 2 : q.b <= 4 ? 4 : q.b <= 8 ? 8 : 16;
         int64_t max_rows = maxb == 1   ? f32_max_rows<1>()
                            : maxb == 2 ? f32_max_rows<2>()
                            : maxb == 4 ? f32_max_rows<4>()
-                                       : f32_max_rows<8>();
+                           : maxb == 8 ? f32_max_rows<8>()
+                                       : f32_max_rows<16>();
         // 8 batch rows: all of K <= 4096 in one slice when the strips alone
         // fill the GPU with one 8-wave workgroup per CU (W [4096, 14336]:
         // see kWideRows8), instead of 4 slices of 1024 rows.
@@ -965,10 +970,12 @@ int launch_gemv_f32_epi(const float *x, const float *w, float *y, int64_t b, int
             launch_f32<2>(q, vec, s);
         else if (maxb == 4)
             launch_f32<4>(q, vec, s);
-        else
+        else if (maxb == 8)
             launch_f32<8>(q, vec, s);
+        else
+            launch_f32<16>(q, vec, s);
         return check_launch("gemv_f32");
-    });
+    }, group);
 }
 
 namespace {
