@@ -488,10 +488,22 @@ int launch_sgemm_big(const SgemmDesc &d, hipStream_t s) {
     // its K loop, and 128 x 128 tiles, two workgroups per CU, overlap one
     // tile's stores with the other's loop (batched 512 x 512 x 128 slices,
     // 128 of them: 89.0 -> 85.8 us; 2048 x 2048 x 128: 1341 -> 1308 us).
-    const int64_t t128 = tiles_of(d, 128);
-    const int t = (d.m >= 256 && d.n >= 256 && d.k >= 256 && tiles_of(d, 256) >= 256) ? 256
-                  : (d.m >= 128 && d.n >= 128 && t128 >= 256)                          ? 128
-                                                                                        : 64;
+    // Between 256 x 256 and 128 x 128 tiles, the one with the shorter
+    // estimated time, in units of a 256 x 256 tile's K loop (one round of
+    // 256 of them): a round of 512 tiles of 128 x 128, two per CU, takes
+    // 0.54 of it (4096^3: 1001 against 930 us for twice the rounds), and up
+    // to 256 of them, one per CU, 0.28 (2048^3: 131 us at K = 2048).  The
+    // larger tile keeps near-ties.  Measured at N = 14336, K = 4096 (us):
+    // M = 768 747 on 128 x 128 (930 on 256 x 256), M = 1024 932 on 256 x 256
+    // (990), M = 1536 1492 on 128 x 128 (1852).
+    const int64_t t128 = tiles_of(d, 128), t256 = tiles_of(d, 256);
+    const bool ok256 = d.m >= 256 && d.n >= 256 && d.k >= 256;
+    const bool ok128 = d.m >= 128 && d.n >= 128 && t128 >= 256;
+    const double r256 = (double)((t256 + 255) / 256);
+    const int64_t rem128 = t128 % 512;
+    const double r128 = t128 <= 256 ? 0.28
+                                    : 0.54 * (double)(t128 / 512) + (rem128 == 0 ? 0.0 : rem128 <= 256 ? 0.28 : 0.54);
+    const int t = (ok256 && (!ok128 ? t256 >= 256 : r128 >= 0.95 * r256)) ? 256 : ok128 ? 128 : 64;
     p.tiles_m = (int)((d.m + t - 1) / t);
     p.tiles_n = (int)((d.n + t - 1) / t);
     const dim3 grid((unsigned)(p.tiles_m * p.tiles_n), (unsigned)std::max<int64_t>(d.batch, 1));
