@@ -118,6 +118,13 @@ struct BigParams {
     int batch_a, batch_b;
     float alpha, beta;
     int tiles_m, tiles_n;
+    // split K (unbatched): workgroup z * tiles + t computes tile t over
+    // stages [z kslice, (z + 1) kslice) of 32 k; each slice publishes its
+    // partial tile in part and the last to arrive sums all slices in slice
+    // order and runs the epilogue
+    int slices, kslice;
+    float *part;
+    int *counters;
 };
 
 __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
@@ -165,6 +172,11 @@ __global__ __launch_bounds__((Geo<BM, BN, NN, NWM_, NWN_, STAGES_, KS_, TA>::NT)
 
     const int nblk = p.tiles_m * p.tiles_n;
     int bid = blockIdx.x;
+    int slice = 0;
+    if (!BATCH && p.slices > 1) {
+        slice = bid / nblk;
+        bid -= slice * nblk;
+    }
     if ((nblk & 7) == 0) bid = (bid & 7) * (nblk >> 3) + (bid >> 3);
     const int group_size = kGroupM * p.tiles_n;
     const int group = bid / group_size;
@@ -187,8 +199,9 @@ __global__ __launch_bounds__((Geo<BM, BN, NN, NWM_, NWN_, STAGES_, KS_, TA>::NT)
     // .. + 7; lane l fills LDS slot l of that 1 KB run (row l / 8, chunk
     // l % 8) from logical chunk (l % 8) ^ swz(row).  Rows past m / n read
     // the last row (their products are never stored).
-    const char *a_base = reinterpret_cast<const char *>(TA ? pa + m0 : pa + m0 * p.lda);
-    const char *b_base = reinterpret_cast<const char *>(NN ? pb + n0 : pb + n0 * p.ldb);
+    const int64_t k_lo = (int64_t)slice * p.kslice * 32;  // first k of this workgroup's slice
+    const char *a_base = reinterpret_cast<const char *>(TA ? pa + k_lo * p.lda + m0 : pa + m0 * p.lda + k_lo);
+    const char *b_base = reinterpret_cast<const char *>(NN ? pb + k_lo * p.ldb + n0 : pb + n0 * p.ldb + k_lo);
     int64_t a_off[kLA], b_off[kLB];
 #pragma unroll
     for (int j = 0; j < kLA; ++j) {
@@ -220,7 +233,7 @@ __global__ __launch_bounds__((Geo<BM, BN, NN, NWM_, NWN_, STAGES_, KS_, TA>::NT)
     // bytes between consecutive stages of A / B in global memory
     const int64_t a_stage = TA ? (int64_t)32 * p.lda * 4 : BKB;
     const int64_t b_stage = NN ? (int64_t)32 * p.ldb * 4 : BKB;
-    const int nk = (int)(p.k / 32);
+    const int nk = (int)min((int64_t)p.kslice, p.k / 32 - (int64_t)slice * p.kslice);
 
     auto issue = [&](int t, int slot) __attribute__((always_inline)) {
         char *la = lds + slot * kStageBytes;
@@ -347,6 +360,76 @@ __global__ __launch_bounds__((Geo<BM, BN, NN, NWM_, NWN_, STAGES_, KS_, TA>::NT)
         }
     }
 
+    if (!BATCH && p.slices > 1) {
+        // Split K.  Every slice publishes its tile (register quad q of
+        // thread t at [slot][q][t]: 16-byte stores and loads, coalesced, at
+        // the device coherence point) and counts its arrival (the split-K
+        // protocol of common.hpp); the last to arrive sums all slices'
+        // partials in slice order, so the result does not depend on the
+        // order of arrival.  With two wave sets the tile is in set 0.
+        constexpr int R4 = FM * FN * 4, NTP = NW * 64;
+        const uint32_t part_bytes = (uint32_t)((int64_t)p.slices * nblk * R4 * NTP * 16);
+        const __amdgpu_buffer_rsrc_t part_buf = coherent_buffer(p.part, part_bytes);
+        const int tp = wt * 64 + lane;
+        auto part_off = [&](int sl, int q) { return (uint32_t)((((int64_t)sl * nblk + bid) * R4 + q) * NTP + tp) * 16; };
+        if (KS == 1 || ks == 0) {
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const f32x4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, v), part_buf,
+                                                               part_off(slice, (i * FN + j) * 4 + q), 0, kScDevice);
+                    }
+        }
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        wait_vmcnt<0>();  // this thread's partial stores are complete
+        __syncthreads();  // (the flag goes through the idle ring)
+        int *last_flag = reinterpret_cast<int *>(lds);
+        if (tid == 0)
+            *last_flag =
+                __hip_atomic_fetch_add(p.counters + bid, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == p.slices - 1;
+        __syncthreads();
+        if (!*last_flag) return;
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        if (KS == 1 || ks == 0) {
+            // slice 0 + slice 1 + ..., a block of 4 registers at a time with
+            // every slice's load of it requested before the first add
+            constexpr int GS = 8;
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int qq = (i * FN + j) * 4 + q;
+                        f32x4 tot = {0.f, 0.f, 0.f, 0.f};
+                        for (int s0 = 0; s0 < p.slices; s0 += GS) {
+                            i32x4 t[GS];
+#pragma unroll
+                            for (int g = 0; g < GS; ++g)
+                                t[g] = s0 + g < p.slices
+                                           ? __builtin_amdgcn_raw_buffer_load_b128(part_buf, part_off(s0 + g, qq), 0,
+                                                                                   kScDevice)
+                                           : i32x4{0, 0, 0, 0};
+#pragma unroll
+                            for (int g = 0; g < GS; ++g) {
+                                const f32x4 v = __builtin_bit_cast(f32x4, t[g]);
+                                if (s0 + g == 0)
+                                    tot = v;
+                                else if (s0 + g < p.slices)
+                                    tot = tot + v;
+                            }
+                        }
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) acc[i][j][4 * q + e] = tot[e];
+                    }
+        }
+        if (tid == 0) __hip_atomic_store(p.counters + bid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
     // Epilogue.  Lane l, register r of block (i, j): row 8 (r / 4) +
     // 4 (l / 32) + r % 4, column l % 32.  Each wave converts half of its
     // sub-tile at a time into its own LDS region, then writes whole row
@@ -459,8 +542,23 @@ bool sgemm_big_fits(const SgemmDesc &d) {
         if (d.trans_a || d.stride_a % 4 != 0 || d.stride_b % 4 != 0 || d.batch > 65535) return false;
     }
     if (d.m >= 128 && d.n >= 128 && tiles_of(d, 128) >= 256) return true;
-    return d.m >= 64 && d.n >= 64 && tiles_of(d, 64) >= 32;
+    if (d.m >= 64 && d.n >= 64 && tiles_of(d, 64) >= 32) return true;
+    // A few rows of an unbatched product with a long K: 64 x 64 tiles with K
+    // split over the CUs (split_k_slices).
+    return d.batch <= 1 && d.batch_a <= 1 && d.batch_b <= 1 && d.m >= 16 && d.n >= 64 && d.k >= 1024 &&
+           tiles_of(d, 64) >= 16;
 }
+
+namespace {
+// K slices for an unbatched launch of `tiles` workgroups over `stages`
+// stages of 32 k: enough to bring a launch of fewer than 256 tiles to about
+// one workgroup per CU, at most 8, each slice at least 8 stages.
+int split_k_slices(int64_t tiles, int64_t stages) {
+    if (tiles >= 256) return 1;
+    int64_t sl = std::min<int64_t>(std::min<int64_t>(8, 256 / std::max<int64_t>(tiles, 1)), stages / 8);
+    return (int)std::max<int64_t>(sl, 1);
+}
+}  // namespace
 
 int launch_sgemm_big(const SgemmDesc &d, hipStream_t s) {
     BigParams p{};
@@ -506,7 +604,24 @@ int launch_sgemm_big(const SgemmDesc &d, hipStream_t s) {
     const int t = (ok256 && (!ok128 ? t256 >= 256 : r128 >= 0.95 * r256)) ? 256 : ok128 ? 128 : 64;
     p.tiles_m = (int)((d.m + t - 1) / t);
     p.tiles_n = (int)((d.n + t - 1) / t);
-    const dim3 grid((unsigned)(p.tiles_m * p.tiles_n), (unsigned)std::max<int64_t>(d.batch, 1));
+    const int64_t nblk = (int64_t)p.tiles_m * p.tiles_n, stages = d.k / 32;
+    p.slices = 1;
+    p.kslice = (int)stages;
+    if (!batched) {
+        const int sl = split_k_slices(nblk, stages);
+        if (sl > 1) {
+            p.kslice = (int)((stages + sl - 1) / sl);
+            p.slices = (int)((stages + p.kslice - 1) / p.kslice);
+        }
+    }
+    if (p.slices > 1) {
+        // one partial tile per slice: t x t floats
+        void *ws = nullptr;
+        GFH_TRY(stream_workspace(s, sizeof(float) * (size_t)(p.slices * nblk) * t * t, &ws));
+        p.part = static_cast<float *>(ws);
+        GFH_TRY(stream_counters(s, (size_t)nblk, &p.counters));
+    }
+    const dim3 grid((unsigned)(nblk * p.slices), (unsigned)std::max<int64_t>(d.batch, 1));
     if (t == 256) {
         launch_layouts<256, 256, 2, 4, 2, 1>(d.trans_a, d.trans_b, batched, p, grid, s);
     } else if (t == 128) {

@@ -225,6 +225,48 @@ def test_big_tiles_integer_exact(torch_dev, m, n, k, tb, ta):
     np.testing.assert_array_equal(to_np(dc), ref)
 
 
+@pytest.mark.parametrize("m,n,k", [(32, 4096, 4096), (48, 1000, 2048), (64, 512, 4096), (100, 700, 3072),
+                                   (17, 4100, 1024), (128, 4096, 2048)])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+def test_big_tiles_split_k_integer_exact(torch_dev, m, n, k, ta, tb):
+    """Fewer than 256 tiles of 64 x 64 over a long K split K over the CUs
+    (2-8 slices whose partial tiles the last slice to arrive sums in slice
+    order): ragged m and n, alpha, beta and bias, on integer data (exact in
+    any order); the same call twice, so the arrival counters are back at
+    zero."""
+    gh = _gh()
+    rng = np.random.default_rng(m + 3 * n + k + 5 * ta + tb)
+    if ta and m % 4:
+        pytest.skip("a transposed A takes the tile kernels with m % 4 == 0")
+    a = rng.integers(-4, 5, size=(m, k)).astype(np.float32)
+    w = rng.integers(-4, 5, size=(n, k)).astype(np.float32)
+    c0 = rng.integers(-4, 5, size=(m, n)).astype(np.float32)
+    bias = rng.integers(-4, 5, size=(n,)).astype(np.float32)
+    a_dev = to_dev(np.ascontiguousarray(a.T) if ta else a, torch_dev)
+    b_dev = to_dev(w if tb else np.ascontiguousarray(w.T), torch_dev)
+    ref = (2.0 * (a.astype(np.float64) @ w.astype(np.float64).T) - c0 + bias).astype(np.float32)
+    for _ in range(2):
+        dc = to_dev(c0, torch_dev)
+        gh.sgemm(a_dev, b_dev, trans_a=bool(ta), trans_b=bool(tb), alpha=2.0, beta=-1.0, bias=to_dev(bias, torch_dev),
+                 out=dc)
+        np.testing.assert_array_equal(to_np(dc), ref)
+
+
+@pytest.mark.parametrize("m,n,k", [(32, 4096, 4096), (64, 512, 4096)])
+def test_big_tiles_split_k_random(torch_dev, m, n, k):
+    """Split K on N(0, 1) data against the oracle's matmul_blocked, within
+    the GEMM bound, and bit-identical on a second call (the slices are
+    summed in a fixed order whatever order they arrive in)."""
+    gh, O = _gh(), _oracle()
+    rng = np.random.default_rng(m + n)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    da, db = to_dev(a, torch_dev), to_dev(b, torch_dev)
+    got = to_np(gh.sgemm(da, db))
+    assert np.abs(got - O.matmul(a, b)).max() <= gemm_tol(k, a, b)
+    np.testing.assert_array_equal(to_np(gh.sgemm(da, db)), got)
+
+
 def _strided_batched(torch_dev, ta, tb, a, b, batch_a, batch_b, batch, m, n, k):
     """gfh_sgemm_strided_batched on packed slices; returns C [batch, m, n]."""
     import torch
