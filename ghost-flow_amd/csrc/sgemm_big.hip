@@ -601,7 +601,16 @@ int launch_sgemm_big(const SgemmDesc &d, hipStream_t s) {
     const int64_t rem128 = t128 % 512;
     const double r128 = t128 <= 256 ? 0.28
                                     : 0.54 * (double)(t128 / 512) + (rem128 == 0 ? 0.0 : rem128 <= 256 ? 0.28 : 0.54);
-    const int t = (ok256 && (!ok128 ? t256 >= 256 : r128 >= 0.95 * r256)) ? 256 : ok128 ? 128 : 64;
+    int t = (ok256 && (!ok128 ? t256 >= 256 : r128 >= 0.95 * r256)) ? 256 : ok128 ? 128 : 64;
+    // 32-255 tiles of 128 x 128 over a long K, with K split (split_k_slices),
+    // where they fill half again as many CUs as the 64 x 64 tiles do (768 x
+    // 768 x 8192: 252 workgroups of 128 x 128 against 144 of 64 x 64, 85.7
+    // against 147 us; where both fill the GPU, as at 1024 x 1024 x 4096,
+    // either tile takes 70-77 us).
+    if (t == 64 && !batched && d.m >= 128 && d.n >= 128 && t128 >= 32 && d.k >= 1024) {
+        const int64_t t64 = tiles_of(d, 64), stages = d.k / 32;
+        if (2 * t128 * split_k_slices(t128, stages) >= 3 * t64 * split_k_slices(t64, stages)) t = 128;
+    }
     p.tiles_m = (int)((d.m + t - 1) / t);
     p.tiles_n = (int)((d.n + t - 1) / t);
     const int64_t nblk = (int64_t)p.tiles_m * p.tiles_n, stages = d.k / 32;
@@ -627,7 +636,7 @@ int launch_sgemm_big(const SgemmDesc &d, hipStream_t s) {
     } else if (t == 128) {
         // One round of tiles (one workgroup per CU): a 3-deep ring (2048^3 NN
         // 143.7 -> 133.7 us); more tiles: 2 stages, two workgroups per CU.
-        if (t128 <= 256)
+        if (nblk * p.slices <= 256)
             launch_layouts<128, 128, 2, 4, 3, 1>(d.trans_a, d.trans_b, batched, p, grid, s);
         else
             launch_layouts<128, 128, 2, 4, 2, 1>(d.trans_a, d.trans_b, batched, p, grid, s);
