@@ -617,7 +617,24 @@ int launch_sgemm_big(const SgemmDesc &d, hipStream_t s) {
     p.slices = 1;
     p.kslice = (int)stages;
     if (!batched) {
-        const int sl = split_k_slices(nblk, stages);
+        int sl = split_k_slices(nblk, stages);
+        if (t == 128 && nblk > 256) {
+            // 128 x 128 tiles two per CU: the slice count (up to 4) with the
+            // shortest estimated time in the rounds model above, plus 0.03
+            // for publishing and summing partial tiles (N = 14336, K = 4096:
+            // M = 384, 336 tiles in 3 slices, 492 -> 340 us; M = 640, 560
+            // tiles in 4 slices, 736 -> 572 us)
+            double best = 1e30;
+            for (int c = 1; c <= 4 && stages / c >= 8; ++c) {
+                const int64_t tasks = nblk * c, rem = tasks % 512;
+                const double r = 0.54 * (double)(tasks / 512) + (rem == 0 ? 0.0 : rem <= 256 ? 0.28 : 0.54);
+                const double est = r / c + (c > 1 ? 0.03 : 0.0);
+                if (est < 0.97 * best) {
+                    best = est;
+                    sl = c;
+                }
+            }
+        }
         if (sl > 1) {
             p.kslice = (int)((stages + sl - 1) / sl);
             p.slices = (int)((stages + p.kslice - 1) / p.kslice);
