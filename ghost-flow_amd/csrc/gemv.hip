@@ -99,14 +99,17 @@ constexpr int f32_max_rows() { return MAXB >= 8 ? 1024 : 4096; }
 // writeback or invalidate is needed -- only that the partial stores have
 // completed (vmcnt 0) before the arrival is counted.  The counter is
 // returned to 0 by that last workgroup.
-template <int MAXB, int SCOLS, int NT = kThreads, typename F>
+// EPI: the fp32 kernel, whose callers may ask for gfh_sgemm's epilogue (the
+// int8 kernel never stores through it, and its 8-row form measured 8% slower
+// with the check compiled in).
+template <int MAXB, int SCOLS, int NT = kThreads, bool EPI = false, typename F>
 __device__ __forceinline__ void store_strip(const GemvParams &p, int64_t strip, int64_t slice, int64_t nb,
                                             int64_t col0, int *last_flag, F value) {
     if (p.slices == 1) {
         for (int t = threadIdx.x; t < MAXB * SCOLS; t += NT) {
             const int bi = t / SCOLS, c = t % SCOLS;
             if (bi >= nb || col0 + c >= p.n) continue;
-            p.y[bi * p.n + col0 + c] = gemv_out(p, bi, col0 + c, value(bi, c));
+            p.y[bi * p.n + col0 + c] = EPI ? gemv_out(p, bi, col0 + c, value(bi, c)) : value(bi, c);
         }
         return;
     }
@@ -164,7 +167,7 @@ __device__ __forceinline__ void store_strip(const GemvParams &p, int64_t strip, 
     for (int o = 0; o < kOut; ++o)
         if (src[o]) {
             const int t = threadIdx.x + o * NT;
-            p.y[(t / SCOLS) * p.n + col0 + t % SCOLS] = gemv_out(p, t / SCOLS, col0 + t % SCOLS, v[o]);
+            p.y[(t / SCOLS) * p.n + col0 + t % SCOLS] = EPI ? gemv_out(p, t / SCOLS, col0 + t % SCOLS, v[o]) : v[o];
         }
     if (threadIdx.x == 0) __hip_atomic_store(p.counters + strip, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -221,7 +224,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_f32_kernel(GemvParams p) {
     const int64_t s_lo = slice * p.kslice;
     const int rows = (int)min(p.kslice, p.k - s_lo);
     if (rows <= 0) {  // K == 0: y = 0, and no row may be read
-        store_strip<MAXB, SCOLS, NT>(p, strip, slice, nb, col0, &last_flag, [](int, int) { return 0.f; });
+        store_strip<MAXB, SCOLS, NT, true>(p, strip, slice, nb, col0, &last_flag, [](int, int) { return 0.f; });
         return;
     }
     const int rows_s = (rows + kStep - 1) / kStep * kStep;
@@ -471,7 +474,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_f32_kernel(GemvParams p) {
         for (int w2 = 1; w2 < NW; ++w2) v = v + red[w2][bi][c];
         return v;
     };
-    store_strip<MAXB, SCOLS, NT>(p, strip, slice, nb, col0, &last_flag, strip_value);
+    store_strip<MAXB, SCOLS, NT, true>(p, strip, slice, nb, col0, &last_flag, strip_value);
 }
 
 // ---- int8 weights on the matrix cores -------------------------------------------
