@@ -653,7 +653,7 @@ int launch_sgemm_big(const SgemmDesc &d, hipStream_t s) {
     } else if (t == 128) {
         // One round of tiles (one workgroup per CU): a 3-deep ring (2048^3 NN
         // 143.7 -> 133.7 us); more tiles: 2 stages, two workgroups per CU.
-        if (nblk * p.slices <= 256)
+        if (nblk * p.slices * nb <= 256)
             launch_layouts<128, 128, 2, 4, 3, 1>(d.trans_a, d.trans_b, batched, p, grid, s);
         else
             launch_layouts<128, 128, 2, 4, 2, 1>(d.trans_a, d.trans_b, batched, p, grid, s);
