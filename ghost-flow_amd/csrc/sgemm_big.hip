@@ -611,7 +611,10 @@ int launch_sgemm_big(const SgemmDesc &d, hipStream_t s) {
         const int64_t t64 = tiles_of(d, 64), stages = d.k / 32;
         if (2 * t128 * split_k_slices(t128, stages) >= 3 * t64 * split_k_slices(t64, stages)) t = 128;
     }
-    p.tiles_m = (int)((d.m + t - 1) / t);
+    // Up to 32 rows of an unbatched product: 32 x 64 tiles (two wave sets
+    // of 1 x 2 waves), so that half of each MFMA's rows is not padding.
+    const int tm = (t == 64 && !batched && d.m <= 32) ? 32 : t;
+    p.tiles_m = (int)((d.m + tm - 1) / tm);
     p.tiles_n = (int)((d.n + t - 1) / t);
     const int64_t nblk = (int64_t)p.tiles_m * p.tiles_n, stages = d.k / 32;
     p.slices = 1;
@@ -641,9 +644,9 @@ int launch_sgemm_big(const SgemmDesc &d, hipStream_t s) {
         }
     }
     if (p.slices > 1) {
-        // one partial tile per slice: t x t floats
+        // one partial tile per slice: tm x t floats
         void *ws = nullptr;
-        GFH_TRY(stream_workspace(s, sizeof(float) * (size_t)(p.slices * nblk) * t * t, &ws));
+        GFH_TRY(stream_workspace(s, sizeof(float) * (size_t)(p.slices * nblk) * tm * t, &ws));
         p.part = static_cast<float *>(ws);
         GFH_TRY(stream_counters(s, (size_t)nblk, &p.counters));
     }
@@ -657,6 +660,11 @@ int launch_sgemm_big(const SgemmDesc &d, hipStream_t s) {
             launch_layouts<128, 128, 2, 4, 3, 1>(d.trans_a, d.trans_b, batched, p, grid, s);
         else
             launch_layouts<128, 128, 2, 4, 2, 1>(d.trans_a, d.trans_b, batched, p, grid, s);
+    } else if (tm == 32) {
+        if (d.trans_b)
+            launch_layouts<32, 64, 1, 2, 4, 2>(d.trans_a, true, batched, p, grid, s);
+        else
+            launch_layouts<32, 64, 1, 2, 2, 2>(d.trans_a, false, batched, p, grid, s);
     } else {
         // Two wave sets splitting each stage's k-groups, so each SIMD runs
         // two waves (1024^3 NN 24.1 -> 22.0 us, 1024 x 1024 x 4096 NN 86.3

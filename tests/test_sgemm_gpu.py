@@ -226,16 +226,17 @@ def test_big_tiles_integer_exact(torch_dev, m, n, k, tb, ta):
 
 
 @pytest.mark.parametrize("m,n,k", [(32, 4096, 4096), (48, 1000, 2048), (64, 512, 4096), (100, 700, 3072),
-                                   (17, 4100, 1024), (128, 4096, 2048), (768, 760, 2048), (384, 11000, 1024)])
+                                   (17, 4100, 1024), (128, 4096, 2048), (768, 760, 2048), (384, 11000, 1024),
+                                   (24, 11008, 2048)])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
 def test_big_tiles_split_k_integer_exact(torch_dev, m, n, k, ta, tb):
     """Launches that split K over the CUs (2-8 slices whose partial tiles the
     last slice to arrive sums in slice order): fewer than 256 tiles of 64 x
-    64, 128 x 128 tiles where those fill more CUs (768 x 760), and 128 x 128
-    tiles two per CU that fill a partial round (384 x 11000: 258 tiles in 4
-    slices); ragged m and n, alpha, beta and bias, on integer data (exact in
-    any order); the same call twice, so the arrival counters are back at
-    zero."""
+    64 (32 x 64 up to 32 rows: 17, 24 and 32 rows here), 128 x 128 tiles
+    where those fill more CUs (768 x 760), and 128 x 128 tiles two per CU
+    that fill a partial round (384 x 11000: 258 tiles in 4 slices); ragged m
+    and n, alpha, beta and bias, on integer data (exact in any order); the
+    same call twice, so the arrival counters are back at zero."""
     gh = _gh()
     rng = np.random.default_rng(m + 3 * n + k + 5 * ta + tb)
     if ta and m % 4:
