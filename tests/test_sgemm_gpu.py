@@ -270,17 +270,20 @@ def test_big_tiles_split_k_random(torch_dev, m, n, k):
     np.testing.assert_array_equal(to_np(gh.sgemm(da, db)), got)
 
 
-def _strided_batched(torch_dev, ta, tb, a, b, batch_a, batch_b, batch, m, n, k):
-    """gfh_sgemm_strided_batched on packed slices; returns C [batch, m, n]."""
+def _strided_batched(torch_dev, ta, tb, a, b, batch_a, batch_b, batch, m, n, k, alpha=1.0, beta=0.0, c0=None,
+                     bias=None):
+    """gfh_sgemm_strided_batched on packed slices; returns C [batch, m, n]
+    (C starts as c0, or NaN when beta is 0)."""
     import torch
     gh = _gh()
     L = gh.lib()
     da, db = to_dev(a, torch_dev), to_dev(b, torch_dev)
-    dc = torch.full((batch, m, n), float("nan"), device=torch_dev)
+    dc = to_dev(c0, torch_dev) if c0 is not None else torch.full((batch, m, n), float("nan"), device=torch_dev)
+    dbias = to_dev(bias, torch_dev) if bias is not None else None
     st = torch.cuda.current_stream(torch_dev).cuda_stream
-    rc = L.gfh_sgemm_strided_batched(int(ta), int(tb), m, n, k, 1.0, da.data_ptr(), m if ta else k, m * k, batch_a,
-                                     db.data_ptr(), k if tb else n, k * n, batch_b, 0.0, dc.data_ptr(), n, m * n,
-                                     batch, None, st)
+    rc = L.gfh_sgemm_strided_batched(int(ta), int(tb), m, n, k, alpha, da.data_ptr(), m if ta else k, m * k, batch_a,
+                                     db.data_ptr(), k if tb else n, k * n, batch_b, beta, dc.data_ptr(), n, m * n,
+                                     batch, None if dbias is None else dbias.data_ptr(), st)
     assert rc == 0, L.gfh_last_error()
     return to_np(dc)
 
@@ -296,7 +299,8 @@ def _strided_batched(torch_dev, ta, tb, a, b, batch_a, batch_b, batch, m, n, k):
 def test_big_tiles_batched_modulo(torch_dev, batch, batch_a, batch_b, m, n, k, ta, tb):
     """Strided-batched products: slice z multiplies A slice z % batch_a by B
     slice z % batch_b (batched_matmul's modulo indexing, matmul.rs:148-149),
-    on integer data (exact in any order).  With A as [m, k] they run on the
+    on integer data (exact in any order), plain and with alpha, beta and
+    bias.  With A as [m, k] they run on the
     direct-to-LDS kernel, the batch as its grid's y dimension; a transposed
     A takes the general tile kernel."""
     rng = np.random.default_rng(batch * 7 + m + n + k + 3 * ta + tb)
@@ -308,6 +312,14 @@ def test_big_tiles_batched_modulo(torch_dev, batch, batch_a, batch_b, m, n, k, t
     for z in range(batch):
         ref = (a[z % batch_a].astype(np.float64) @ b[z % batch_b].astype(np.float64)).astype(np.float32)
         np.testing.assert_array_equal(got[z], ref, err_msg=f"slice {z}")
+    # alpha, beta (each slice's own C) and bias, separately rounded
+    c0 = rng.integers(-4, 5, size=(batch, m, n)).astype(np.float32)
+    bias = rng.integers(-4, 5, size=(n,)).astype(np.float32)
+    got = _strided_batched(torch_dev, ta, tb, a_st, b_st, batch_a, batch_b, batch, m, n, k, alpha=2.0, beta=-1.0,
+                           c0=c0, bias=bias)
+    for z in range(batch):
+        prod = (a[z % batch_a].astype(np.float64) @ b[z % batch_b].astype(np.float64)).astype(np.float32)
+        np.testing.assert_array_equal(got[z], (2.0 * prod - c0[z] + bias).astype(np.float32), err_msg=f"slice {z}")
 
 
 @pytest.mark.parametrize("m", [1, 3, 8, 13, 16])
