@@ -524,10 +524,10 @@ void launch_layouts(bool trans_a, bool trans_b, bool batched, const BigParams &p
 }
 }  // namespace
 
-// 256 x 256 tiles when there are at least 256 of them (one per CU) and K is
-// at least 256, else 128 x 128 tiles when those number 256, else 64 x 64
-// tiles on 2 x 2 waves (at least 32 of them), counting the tiles of every
-// batch slice.
+// Whether these tiles take the product: at least 256 tiles of 128 x 128 or
+// 32 of 64 x 64 (counting every batch slice), or, unbatched, 16 or more rows
+// with K >= 1024 and at least 16 tiles of 64 x 64 (split K then fills the
+// CUs).  launch_sgemm_big picks the tile size and the K split.
 // Measured against the register-staged tile kernel (us): 1024^3 NN 31.3 ->
 // 25.8, NT 29.5 -> 20.9; 1536^3 NN 120.5 -> 84.4; 1024 x 1024 x 4096 NN
 // 107.2 -> 86.6; 512 x 2048 x 1024 NT 29.5 -> 20.7.
